@@ -1,0 +1,126 @@
+"""Builds lib/libkvexp_hip.so (gfx950) in-tree.
+
+    python compressed-kv-attention_amd/build.py [--jobs N] [--asm]
+
+Every source is compiled with hipcc for gfx950 only, with the numeric flags
+the reference uses for its own code (-ffp-contract=off, no fast math), and
+with packed FP32 instructions disabled (-packed-fp32-ops target feature).
+``--asm`` also writes the device assembly of each kernel file to
+``_build/asm/`` for inspection.
+"""
+from __future__ import annotations
+
+import argparse
+import concurrent.futures as cf
+import os
+import shutil
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+LIB_DIR = os.path.join(HERE, "lib")
+LIB = os.path.join(LIB_DIR, "libkvexp_hip.so")
+OBJ_DIR = os.path.join(HERE, "_build", "obj")
+ASM_DIR = os.path.join(HERE, "_build", "asm")
+
+ARCH = "gfx950"
+SOURCES = [
+    "csrc/hip/codec_kernels.hip",
+    "csrc/hip/attention_kernels.hip",
+    "csrc/host/kvexp_hip_api.cpp",
+    "csrc/host/kvexp_cpp_api.cpp",
+]
+HEADERS = [
+    "csrc/hip/kvexp_device.h",
+    "csrc/hip/kvexp_expf.h",
+    "csrc/hip/kvexp_types.h",
+    "../include/kvexp_hip.h",
+    "../include/kvexp/attention.hpp",
+    "../include/kvexp/codec.hpp",
+    "../include/kvexp/bf16.hpp",
+]
+
+
+def hipcc() -> str:
+    for c in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
+        if c and os.path.exists(c):
+            return c
+    raise RuntimeError("hipcc not found (ROCm 7.x expected under /opt/rocm)")
+
+
+def common_flags() -> list[str]:
+    return [
+        f"--offload-arch={ARCH}",
+        "-O3",
+        "-std=c++17",
+        "-fPIC",
+        "-ffp-contract=off",
+        "-fno-fast-math",
+        "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+        "-Wall",
+        "-Wno-unused-command-line-argument",
+        f"-I{os.path.join(ROOT, 'include')}",
+        f"-I{os.path.join(HERE, 'csrc', 'hip')}",
+    ]
+
+
+def _newest(paths) -> float:
+    return max(os.path.getmtime(os.path.join(HERE, p)) for p in paths)
+
+
+def _compile(src: str, force: bool) -> str:
+    obj = os.path.join(OBJ_DIR, os.path.basename(src) + ".o")
+    dep_time = max(_newest([src]), _newest(HEADERS), os.path.getmtime(__file__))
+    if not force and os.path.exists(obj) and os.path.getmtime(obj) >= dep_time:
+        return obj
+    if src.endswith(".hip"):
+        cmd = [hipcc()] + common_flags() + ["-x", "hip"]
+    else:  # host-only translation unit: plain C++ against the HIP runtime headers
+        cmd = [hipcc()] + [f for f in common_flags() if not f.startswith("--offload-arch")] + ["-x", "c++"]
+        cmd = [c for c in cmd if c not in ("-Xclang", "-target-feature", "-packed-fp32-ops")]
+        cmd += ["-D__HIP_PLATFORM_AMD__=1", "-I/opt/rocm/include"]
+    cmd += ["-c", os.path.join(HERE, src), "-o", obj]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"compile failed: {src}\n{' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
+    return obj
+
+
+def _asm(src: str) -> None:
+    os.makedirs(ASM_DIR, exist_ok=True)
+    out = os.path.join(ASM_DIR, os.path.basename(src) + ".s")
+    cmd = [hipcc()] + common_flags() + ["-x", "hip", "--cuda-device-only", "-S",
+                                         os.path.join(HERE, src), "-o", out]
+    subprocess.run(cmd, check=True, capture_output=True, text=True)
+
+
+def build(force: bool = True, jobs: int = 4, asm: bool = False) -> str:
+    """Compiles every source (``force``: even when up to date) and links the library."""
+    os.makedirs(OBJ_DIR, exist_ok=True)
+    os.makedirs(LIB_DIR, exist_ok=True)
+    with cf.ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:
+        objs = list(ex.map(lambda s: _compile(s, force), SOURCES))
+        if asm:
+            list(ex.map(_asm, [s for s in SOURCES if s.endswith(".hip")]))
+    tmp = LIB + ".tmp"
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp] + objs
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"link failed\n{' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
+    os.replace(tmp, LIB)
+    return LIB
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--jobs", type=int, default=4)
+    ap.add_argument("--asm", action="store_true")
+    ap.add_argument("--incremental", action="store_true", help="skip up-to-date objects")
+    a = ap.parse_args()
+    print(build(force=not a.incremental, jobs=a.jobs, asm=a.asm))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

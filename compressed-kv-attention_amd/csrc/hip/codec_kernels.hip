@@ -1,0 +1,368 @@
+// gfx950 kernels for the XKV container: block decode and the encoder.
+//
+// Decode (reference src/codec.cpp:166-174 via XkvReader::read_next,
+// include/kvexp/scan.hpp:125-155): one workgroup per block. A coded element
+// is bf16_from_delta(base[d], code, sm) unless its code is the all-ones
+// sentinel, in which case it is the next escape word of the block in scan
+// order; the escape rank of each element comes from a workgroup prefix sum
+// of per-thread sentinel counts.
+//
+// Encode (reference src/codec.cpp:18-164), three launches:
+//   1. per block: exponent histogram per channel, the smallest base that
+//      covers the most exponents for 2- and 4-bit windows, escape counts,
+//      and the mode choice with the reference's tie rules;
+//   2. one workgroup: prefix sum of block sizes -> block byte offsets and
+//      first tokens (the block index the attention kernels read);
+//   3. per block: header, base, sign/mantissa bytes, packed codes, escapes.
+#include "kvexp_device.h"
+#include "kvexp_types.h"
+
+namespace kvexp_dev {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / kWave;
+
+// ----------------------------------------------------------------- decode --
+__global__ __launch_bounds__(kThreads) void decode_blocks_kernel(const uint8_t *__restrict__ blob, uint64_t bytes,
+                                                                const int64_t *__restrict__ offs,
+                                                                const int32_t *__restrict__ first, int seq, int dim,
+                                                                uint16_t *__restrict__ out,
+                                                                uint32_t *__restrict__ status) {
+    __shared__ int scan_tmp[kWaves];
+    const int b = int(blockIdx.x);
+    const int t0 = first[b];
+    const int want = first[b + 1] - t0;
+    const int64_t off = offs[b];
+    BlockHdr h;
+    const uint32_t st = check_block(blob, bytes, off, dim, want, &h);
+    if (st != 0u) {
+        if (threadIdx.x == 0) atomicOr(status, st);
+        return;
+    }
+    const int rows = min(want, seq - t0);
+    if (rows <= 0) return;
+    const uint8_t *p = blob + off + 8;
+    uint16_t *o = out + size_t(t0) * size_t(dim);
+    const int total = rows * dim;
+    if (h.mode == 0) {
+        for (int i = int(threadIdx.x); i < total; i += kThreads) o[i] = uint16_t(load_u16_any(p + 2 * i));
+        return;
+    }
+    const bool four = h.mode == 4;
+    const uint8_t *base = p;
+    const uint8_t *sm = p + dim;
+    const uint8_t *codes = sm + size_t(h.n_tokens) * size_t(dim);
+    const uint8_t *esc = codes + exp_payload_bytes(h.n_tokens, dim, h.mode);
+    const int units = total / 4; // dim % 4 == 0
+    int carry = 0;
+    uint32_t bad = 0;
+    for (int r = 0; r < units; r += kThreads) {
+        const int u = r + int(threadIdx.x);
+        const bool act = u < units;
+        uint32_t smw = 0, cw = 0;
+        int cnt = 0;
+        if (act) {
+            smw = load_u32_any(sm + 4 * size_t(u));
+            cw = four ? load_u16_any(codes + 2 * size_t(u)) : uint32_t(codes[u]);
+            cnt = four ? sentinels4(cw) : sentinels2(cw);
+        }
+        int rank = carry;
+        if (h.n_escape > 0) {
+            int tot = 0;
+            rank += block_excl_scan<kWaves>(cnt, scan_tmp, &tot);
+            carry += tot;
+        }
+        if (act) {
+            const int e0 = 4 * u;
+            const int d0 = e0 % dim;
+            uint32_t v[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const uint32_t code = four ? (cw >> (4 * k)) & 15u : (cw >> (2 * k)) & 3u;
+                const uint32_t sentinel = four ? 15u : 3u;
+                if (code == sentinel) {
+                    if (rank < h.n_escape) {
+                        v[k] = load_u16_any(esc + 2 * size_t(rank));
+                    } else {
+                        v[k] = 0;
+                        bad = kStEscape;
+                    }
+                    ++rank;
+                } else {
+                    v[k] = bf16_join(uint32_t(base[d0 + k]) + code, (smw >> (8 * k)) & 0xFFu);
+                }
+            }
+            uint2 w;
+            w.x = v[0] | (v[1] << 16);
+            w.y = v[2] | (v[3] << 16);
+            *reinterpret_cast<uint2 *>(o + e0) = w;
+        }
+    }
+    if (bad) atomicOr(status, bad);
+}
+
+// ------------------------------------------------------------ encode: stats --
+// bases: [n_blocks][2][dim] (2-bit window base, 4-bit window base).
+__global__ __launch_bounds__(kThreads) void encode_stats_kernel(const uint16_t *__restrict__ kv, int seq, int dim,
+                                                               int bt, EncBlockMeta *__restrict__ meta,
+                                                               uint8_t *__restrict__ bases) {
+    __shared__ uint32_t hist[kWaves][256];
+    __shared__ uint32_t pre[kWaves][257];
+    __shared__ int esc_part[kWaves][2];
+    const int b = int(blockIdx.x);
+    const int t0 = b * bt;
+    const int n = min(bt, seq - t0);
+    const int lane = lane_id();
+    const int w = int(threadIdx.x) >> 6;
+    const uint16_t *src = kv + size_t(t0) * size_t(dim);
+    int esc2 = 0, esc4 = 0;
+    for (int d = w; d < dim; d += kWaves) { // dim % 4 == 0: every wave runs dim/4 rounds
+#pragma unroll
+        for (int i = 0; i < 4; ++i) hist[w][4 * lane + i] = 0u;
+        __syncthreads();
+        for (int t = lane; t < n; t += kWave) atomicAdd(&hist[w][(src[size_t(t) * dim + d] >> 7) & 0xFFu], 1u);
+        __syncthreads();
+        uint32_t h4[4], run = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            run += hist[w][4 * lane + i];
+            h4[i] = run;
+        }
+        const int excl = wave_scan_add(int(run)) - int(run);
+        if (lane == 0) pre[w][0] = 0u;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) pre[w][4 * lane + i + 1] = uint32_t(excl) + h4[i];
+        __syncthreads();
+#pragma unroll
+        for (int bi = 0; bi < 2; ++bi) {
+            const int width = bi == 0 ? 3 : 15; // codes 0..2^bits-2
+            int key = -1;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int base = 4 * lane + i;
+                if (base <= 256 - width) {
+                    const int cov = int(pre[w][base + width] - pre[w][base]);
+                    key = max(key, (cov << 9) | (511 - base)); // most covered, then smallest base
+                }
+            }
+            for (int o = 32; o > 0; o >>= 1) key = max(key, __shfl_xor(key, o));
+            const int cov = key >> 9;
+            const int base = 511 - (key & 511);
+            if (lane == 0) {
+                bases[(size_t(b) * 2 + size_t(bi)) * size_t(dim) + size_t(d)] = uint8_t(base);
+                if (bi == 0)
+                    esc2 += n - cov;
+                else
+                    esc4 += n - cov;
+            }
+        }
+        __syncthreads();
+    }
+    if (lane == 0) {
+        esc_part[w][0] = esc2;
+        esc_part[w][1] = esc4;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        int e2 = 0, e4 = 0;
+        for (int i = 0; i < kWaves; ++i) {
+            e2 += esc_part[i][0];
+            e4 += esc_part[i][1];
+        }
+        // codec.cpp:94-103: raw, then 2-bit, then 4-bit; replace when smaller,
+        // or on a tie when the best is not raw and has more escapes (or equal
+        // escapes and more bits).
+        int best_mode = 0, best_esc = 0;
+        int64_t best_bytes = block_bytes(0, n, 0, dim);
+        const int cand_esc[2] = {e2, e4};
+#pragma unroll
+        for (int bi = 0; bi < 2; ++bi) {
+            const int mode = bi == 0 ? 2 : 4;
+            const int64_t by = block_bytes(mode, n, cand_esc[bi], dim);
+            const bool smaller = by < best_bytes;
+            const bool tie_win = by == best_bytes && best_mode != 0 &&
+                                 (cand_esc[bi] < best_esc || (cand_esc[bi] == best_esc && mode < best_mode));
+            if (smaller || tie_win) {
+                best_mode = mode;
+                best_bytes = by;
+                best_esc = cand_esc[bi];
+            }
+        }
+        EncBlockMeta m;
+        m.bytes = best_bytes;
+        m.mode = best_mode;
+        m.n_escape = best_esc;
+        meta[b] = m;
+    }
+}
+
+// ------------------------------------------------------------- encode: scan --
+// offs[i] = sum of block sizes before block i (n_blocks + 1 entries);
+// first[i] = i * bt, first[n_blocks] = seq.
+__global__ __launch_bounds__(1024) void encode_scan_kernel(const EncBlockMeta *__restrict__ meta, int n_blocks,
+                                                          int bt, int seq, int64_t *__restrict__ offs,
+                                                          int32_t *__restrict__ first) {
+    __shared__ long long wave_tot[16];
+    __shared__ long long carry_s;
+    const int tid = int(threadIdx.x);
+    const int lane = lane_id();
+    const int w = tid >> 6;
+    if (tid == 0) carry_s = 0;
+    __syncthreads();
+    for (int r = 0; r < n_blocks; r += 1024) {
+        const int i = r + tid;
+        long long v = i < n_blocks ? meta[i].bytes : 0;
+        long long incl = v;
+        for (int o = 1; o < kWave; o <<= 1) {
+            const long long y = __shfl_up(incl, o);
+            if (lane >= o) incl += y;
+        }
+        if (lane == kWave - 1) wave_tot[w] = incl;
+        __syncthreads();
+        long long base = carry_s;
+        long long tot = 0;
+        for (int k = 0; k < 16; ++k) {
+            base += (k < w) ? wave_tot[k] : 0;
+            tot += wave_tot[k];
+        }
+        if (i < n_blocks) {
+            offs[i] = base + incl - v;
+            first[i] = i * bt;
+        }
+        __syncthreads();
+        if (tid == 0) carry_s += tot;
+        __syncthreads();
+    }
+    if (tid == 0) {
+        offs[n_blocks] = carry_s;
+        first[n_blocks] = seq;
+    }
+}
+
+// ------------------------------------------------------------ encode: write --
+__global__ __launch_bounds__(kThreads) void encode_write_kernel(const uint16_t *__restrict__ kv, int seq, int dim,
+                                                               int bt, const EncBlockMeta *__restrict__ meta,
+                                                               const uint8_t *__restrict__ bases,
+                                                               const int64_t *__restrict__ offs,
+                                                               uint8_t *__restrict__ out,
+                                                               uint32_t *__restrict__ status) {
+    __shared__ int scan_tmp[kWaves];
+    const int b = int(blockIdx.x);
+    const int t0 = b * bt;
+    const int n = min(bt, seq - t0);
+    const EncBlockMeta m = meta[b];
+    uint8_t *p = out + offs[b];
+    const uint16_t *src = kv + size_t(t0) * size_t(dim);
+    const int total = n * dim;
+    if (threadIdx.x == 0) {
+        p[0] = uint8_t(m.mode);
+        p[1] = uint8_t(n);
+        const int ne = m.mode == 0 ? 0 : m.n_escape;
+        p[2] = uint8_t(ne & 0xFF);
+        p[3] = uint8_t(ne >> 8);
+        p[4] = uint8_t(dim & 0xFF);
+        p[5] = uint8_t(dim >> 8);
+        p[6] = 0;
+        p[7] = 0;
+    }
+    p += 8;
+    if (m.mode == 0) {
+        for (int i = int(threadIdx.x); i < total; i += kThreads) {
+            const uint16_t h = src[i];
+            p[2 * i] = uint8_t(h & 0xFF);
+            p[2 * i + 1] = uint8_t(h >> 8);
+        }
+        return;
+    }
+    const bool four = m.mode == 4;
+    const int width = four ? 15 : 3;
+    const uint8_t *bsrc = bases + (size_t(b) * 2 + (four ? 1 : 0)) * size_t(dim);
+    for (int d = int(threadIdx.x); d < dim; d += kThreads) p[d] = bsrc[d];
+    uint8_t *sm = p + dim;
+    uint8_t *codes = sm + size_t(total);
+    uint8_t *esc = codes + exp_payload_bytes(n, dim, m.mode);
+    const int units = total / 4;
+    int carry = 0;
+    for (int r = 0; r < units; r += kThreads) {
+        const int u = r + int(threadIdx.x);
+        const bool act = u < units;
+        uint32_t c[4] = {0, 0, 0, 0};
+        uint32_t hv[4] = {0, 0, 0, 0};
+        int cnt = 0;
+        if (act) {
+            const int e0 = 4 * u;
+            const int d0 = e0 % dim;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const uint32_t h = src[e0 + k];
+                hv[k] = h;
+                sm[e0 + k] = uint8_t(((h >> 8) & 0x80u) | (h & 0x7Fu));
+                const int delta = int((h >> 7) & 0xFFu) - int(bsrc[d0 + k]);
+                if (delta >= 0 && delta < width) {
+                    c[k] = uint32_t(delta);
+                } else {
+                    c[k] = uint32_t(width);
+                    ++cnt;
+                }
+            }
+            if (four) {
+                codes[2 * u] = uint8_t(c[0] | (c[1] << 4));
+                codes[2 * u + 1] = uint8_t(c[2] | (c[3] << 4));
+            } else {
+                codes[u] = uint8_t(c[0] | (c[1] << 2) | (c[2] << 4) | (c[3] << 6));
+            }
+        }
+        int tot = 0;
+        int rank = carry + block_excl_scan<kWaves>(cnt, scan_tmp, &tot);
+        carry += tot;
+        if (act && cnt) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                if (c[k] == uint32_t(width)) {
+                    if (rank < m.n_escape) {
+                        esc[2 * rank] = uint8_t(hv[k] & 0xFF);
+                        esc[2 * rank + 1] = uint8_t(hv[k] >> 8);
+                    }
+                    ++rank;
+                }
+            }
+        }
+    }
+    if (threadIdx.x == 0 && carry != m.n_escape) atomicOr(status, kStEscape);
+}
+
+__global__ __launch_bounds__(256) void expf_kernel(const float *__restrict__ x, float *__restrict__ y, size_t n) {
+    const size_t i = size_t(blockIdx.x) * 256u + threadIdx.x;
+    if (i < n) y[i] = kvexp_expf(x[i]);
+}
+
+} // namespace kvexp_dev
+
+// ---------------------------------------------------------------- launchers --
+namespace kvexp_launch {
+using namespace kvexp_dev;
+
+hipError_t decode(const uint8_t *blob, uint64_t bytes, const int64_t *offs, const int32_t *first, int n_blocks,
+                  int seq, int dim, uint16_t *out, uint32_t *status, hipStream_t s) {
+    if (n_blocks <= 0) return hipSuccess;
+    hipLaunchKernelGGL(decode_blocks_kernel, dim3(n_blocks), dim3(kThreads), 0, s, blob, bytes, offs, first, seq,
+                       dim, out, status);
+    return hipGetLastError();
+}
+
+hipError_t encode(const uint16_t *kv, int seq, int dim, int bt, int n_blocks, EncBlockMeta *meta, uint8_t *bases,
+                  int64_t *offs, int32_t *first, uint8_t *out, uint32_t *status, hipStream_t s) {
+    hipLaunchKernelGGL(encode_stats_kernel, dim3(n_blocks), dim3(kThreads), 0, s, kv, seq, dim, bt, meta, bases);
+    hipLaunchKernelGGL(encode_scan_kernel, dim3(1), dim3(1024), 0, s, meta, n_blocks, bt, seq, offs, first);
+    hipLaunchKernelGGL(encode_write_kernel, dim3(n_blocks), dim3(kThreads), 0, s, kv, seq, dim, bt, meta, bases,
+                       offs, out, status);
+    return hipGetLastError();
+}
+
+hipError_t expf(const float *x, float *y, size_t n, hipStream_t s) {
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(expf_kernel, dim3(unsigned((n + 255) / 256)), dim3(256), 0, s, x, y, n);
+    return hipGetLastError();
+}
+
+} // namespace kvexp_launch

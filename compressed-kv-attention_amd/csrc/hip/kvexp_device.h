@@ -1,0 +1,166 @@
+// Device helpers shared by the gfx950 kernels: container header checks, byte
+// loads at any alignment, BF16 field assembly and wave64 scans (DPP).
+//
+// Container format (reference include/kvexp/codec.hpp:12-36): blocks of
+//   u8 mode (0 raw, 2, 4) | u8 n_tokens | u16 n_escape | u16 head_dim | u16 0
+// then raw BF16 rows, or base[dim], sm[n*dim], packed codes, u16 escapes.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "kvexp_expf.h"
+#include "kvexp_types.h"
+
+namespace kvexp_dev {
+
+constexpr int kMaxDim = 256;
+constexpr int kWave = 64;
+
+__device__ __forceinline__ uint32_t f32_bits(float x) { return __float_as_uint(x); }
+__device__ __forceinline__ float bits_f32(uint32_t u) { return __uint_as_float(u); }
+__device__ __forceinline__ float bf16_f32(uint32_t b) { return __uint_as_float(b << 16); }
+
+// BF16 from an exponent (wrapping modulo 256, bf16.hpp:35-37) and a
+// sign/mantissa byte (sign in bit 7).
+__device__ __forceinline__ uint32_t bf16_join(uint32_t exponent, uint32_t sm) {
+    return ((sm & 0x80u) << 8) | ((exponent & 0xFFu) << 7) | (sm & 0x7Fu);
+}
+
+// The four bytes [p, p+4) at any alignment, little-endian. Reads only the
+// aligned dwords that hold those bytes, so a caller whose four bytes lie
+// inside a buffer never touches a page outside it.
+__device__ __forceinline__ uint32_t load_u32_any(const uint8_t *p) {
+    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+    const uint32_t sh = uint32_t(a & 3u);
+    const uint32_t *w = reinterpret_cast<const uint32_t *>(a & ~uintptr_t(3));
+    const uint32_t lo = w[0];
+    if (sh == 0) return lo;
+    const uint32_t hi = w[1];
+    return uint32_t(((uint64_t(hi) << 32) | lo) >> (sh * 8u));
+}
+
+__device__ __forceinline__ uint32_t load_u8(const uint8_t *p) { return *p; }
+__device__ __forceinline__ uint32_t load_u16_any(const uint8_t *p) {
+    return uint32_t(p[0]) | (uint32_t(p[1]) << 8);
+}
+
+struct BlockHdr {
+    int mode, n_tokens, n_escape, dim;
+};
+
+__device__ __forceinline__ BlockHdr read_hdr(const uint8_t *p) {
+    BlockHdr h;
+    h.mode = p[0];
+    h.n_tokens = p[1];
+    h.n_escape = int(load_u16_any(p + 2));
+    h.dim = int(load_u16_any(p + 4));
+    return h;
+}
+
+__host__ __device__ __forceinline__ int exp_payload_bytes(int n, int dim, int bits) {
+    return (n * dim * bits + 7) / 8;
+}
+
+// Byte size of a block from its header, or -1 when the mode is unknown.
+__host__ __device__ __forceinline__ int64_t block_bytes(int mode, int n, int n_escape, int dim) {
+    if (mode == 0) return 8 + 2 * int64_t(n) * dim;
+    if (mode != 2 && mode != 4) return -1;
+    return 8 + int64_t(dim) + int64_t(n) * dim + exp_payload_bytes(n, dim, mode) + 2 * int64_t(n_escape);
+}
+
+// Status bits for the block at byte `off` of a container of `bytes` bytes
+// that should hold `want_tokens` tokens of `dim` channels (0 = valid).
+__device__ __forceinline__ uint32_t check_block(const uint8_t *blob, uint64_t bytes, int64_t off, int dim,
+                                                int want_tokens, BlockHdr *out) {
+    if (off < 0 || uint64_t(off) + 8u > bytes) return kStHeader;
+    const BlockHdr h = read_hdr(blob + off);
+    *out = h;
+    if (h.dim != dim || h.n_tokens <= 0) return kStHeader;
+    if (h.n_tokens != want_tokens) return kStIndex;
+    const int64_t sz = block_bytes(h.mode, h.n_tokens, h.n_escape, dim);
+    if (sz < 0) return kStMode;
+    if (uint64_t(off) + uint64_t(sz) > bytes) return kStTruncated;
+    return 0u;
+}
+
+// ------------------------------------------------------------- DPP scans --
+// dpp_ctrl encodings (GFX9): row_shr:n = 0x110 + n, wave_shr:1 = 0x138,
+// row_bcast:15 = 0x142, row_bcast:31 = 0x143.
+template <int CTRL, int ROW_MASK = 0xf, bool BOUND_CTRL = false>
+__device__ __forceinline__ float dpp_f32(float old, float src) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(old), __float_as_int(src), CTRL, ROW_MASK,
+                                                      0xf, BOUND_CTRL));
+}
+template <int CTRL, int ROW_MASK = 0xf, bool BOUND_CTRL = false>
+__device__ __forceinline__ int dpp_i32(int old, int src) {
+    return __builtin_amdgcn_update_dpp(old, src, CTRL, ROW_MASK, 0xf, BOUND_CTRL);
+}
+
+// Inclusive prefix maximum over the 64 lanes (IEEE maxNum: NaN lanes are
+// ignored, as `(m < s) ? s : m` ignores a NaN score).
+__device__ __forceinline__ float wave_scan_max(float x) {
+    const float ninf = -__builtin_inff();
+    x = fmaxf(x, dpp_f32<0x111>(ninf, x));
+    x = fmaxf(x, dpp_f32<0x112>(ninf, x));
+    x = fmaxf(x, dpp_f32<0x114>(ninf, x));
+    x = fmaxf(x, dpp_f32<0x118>(ninf, x));
+    x = fmaxf(x, dpp_f32<0x142, 0xa>(ninf, x));
+    x = fmaxf(x, dpp_f32<0x143, 0xc>(ninf, x));
+    return x;
+}
+
+// Value of lane - 1 (lane 0 gets `first`).
+__device__ __forceinline__ float wave_shift_up(float x, float first) { return dpp_f32<0x138>(first, x); }
+
+// Inclusive prefix sum of ints over the 64 lanes.
+__device__ __forceinline__ int wave_scan_add(int x) {
+    x += dpp_i32<0x111>(0, x);
+    x += dpp_i32<0x112>(0, x);
+    x += dpp_i32<0x114>(0, x);
+    x += dpp_i32<0x118>(0, x);
+    x += dpp_i32<0x142, 0xa>(0, x);
+    x += dpp_i32<0x143, 0xc>(0, x);
+    return x;
+}
+
+__device__ __forceinline__ int lane_id() { return int(__lane_id()); }
+
+__device__ __forceinline__ float readlane_f32(float x, int lane) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), lane));
+}
+
+// Exclusive prefix sum over a workgroup of NW waves. `tmp` holds NW ints in
+// LDS. Returns the prefix and writes the workgroup total to *total. Every
+// thread of the workgroup must call it.
+template <int NW>
+__device__ __forceinline__ int block_excl_scan(int v, int *tmp, int *total) {
+    const int incl = wave_scan_add(v);
+    const int lane = lane_id();
+    const int wave = int(threadIdx.x) >> 6;
+    if (lane == kWave - 1) tmp[wave] = incl;
+    __syncthreads();
+    int base = 0, tot = 0;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+        const int t = tmp[w];
+        base += (w < wave) ? t : 0;
+        tot += t;
+    }
+    __syncthreads();
+    *total = tot;
+    return base + incl - v;
+}
+
+// Number of 4-bit codes equal to 15 (sentinels) in a dword of 8 codes.
+__device__ __forceinline__ int sentinels4(uint32_t x) {
+    uint32_t a = x & (x >> 1);
+    a = a & (a >> 2);
+    return __builtin_popcount(a & 0x11111111u);
+}
+// Number of 2-bit codes equal to 3 (sentinels) in a dword of 16 codes.
+__device__ __forceinline__ int sentinels2(uint32_t x) {
+    return __builtin_popcount(x & (x >> 1) & 0x55555555u);
+}
+
+} // namespace kvexp_dev

@@ -1,0 +1,131 @@
+/* Single-precision exp that returns glibc 2.35's expf bits.
+ *
+ * The reference computes every softmax coefficient with std::exp(float)
+ * (src/softmax.hpp:10-11,20-21), i.e. glibc's expf. Matching the reference
+ * output bit for bit on the GPU therefore needs the same function, so this
+ * is a restatement of glibc 2.35's expf (sysdeps/ieee754/flt-32/e_expf.c,
+ * the published ARM optimized-routines algorithm):
+ *
+ *   x * 32/ln2 = k + r, |r| <= 1/2, k integer (round to nearest even via the
+ *   1.5*2^52 shift);
+ *   exp(x) = 2^(k/32) * 2^(r/32) ~= s * (1 + C2 r + C1 r^2 + C0 r^3),
+ *   s = 2^(k/32) read from a 32-entry table of 2^(i/32) rounded to double,
+ *   stored minus (i << 47) so that adding k << 47 forms s directly.
+ *
+ * Evaluated in double precision, then rounded to float once. The table below
+ * is 2^(i/32) correctly rounded, computed from first principles; C0..C2 are
+ * the published minimax coefficients (scaled by 32^-3, 32^-2, 32^-1).
+ *
+ * glibc on x86-64 runs an FMA-compiled copy of this code on FMA-capable CPUs
+ * (the __expf_fma ifunc variant); KVEXP_EXPF_FORM selects which operations are
+ * fused so the result equals that build. An exhaustive comparison over all
+ * 2^32 inputs against the host libm pins the choice (tests/test_expf.py).
+ *
+ *   form 0: no fused operation
+ *   form 1: the three polynomial steps fused
+ *   form 2: form 1, plus x*32/ln2 fused into both uses (shift add, remainder)
+ *
+ * The header compiles as C or C++ on the host (gcc) and as HIP device code.
+ */
+#ifndef KVEXP_EXPF_H
+#define KVEXP_EXPF_H
+
+#include <stdint.h>
+#include <string.h>
+
+#ifndef KVEXP_EXPF_FORM
+#define KVEXP_EXPF_FORM 2
+#endif
+
+#if defined(__HIPCC__)
+#define KVEXP_HD __host__ __device__ static inline __attribute__((always_inline))
+#define KVEXP_EXP_TABLE_QUAL static __constant__ __device__
+#else
+#define KVEXP_HD static inline
+#define KVEXP_EXP_TABLE_QUAL static const
+#endif
+
+KVEXP_EXP_TABLE_QUAL uint64_t kvexp_exp2_32_table[32] = {
+    0x3ff0000000000000ull, 0x3fefd9b0d3158574ull, 0x3fefb5586cf9890full, 0x3fef9301d0125b51ull,
+    0x3fef72b83c7d517bull, 0x3fef54873168b9aaull, 0x3fef387a6e756238ull, 0x3fef1e9df51fdee1ull,
+    0x3fef06fe0a31b715ull, 0x3feef1a7373aa9cbull, 0x3feedea64c123422ull, 0x3feece086061892dull,
+    0x3feebfdad5362a27ull, 0x3feeb42b569d4f82ull, 0x3feeab07dd485429ull, 0x3feea47eb03a5585ull,
+    0x3feea09e667f3bcdull, 0x3fee9f75e8ec5f74ull, 0x3feea11473eb0187ull, 0x3feea589994cce13ull,
+    0x3feeace5422aa0dbull, 0x3feeb737b0cdc5e5ull, 0x3feec49182a3f090ull, 0x3feed503b23e255dull,
+    0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,
+    0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull,
+};
+
+#define KVEXP_EXP_INVLN2N (0x1.71547652b82fep+0 * 32.0)
+#define KVEXP_EXP_SHIFT 0x1.8p+52
+#define KVEXP_EXP_C0 (0x1.c6af84b912394p-5 / 32.0 / 32.0 / 32.0)
+#define KVEXP_EXP_C1 (0x1.ebfce50fac4f3p-3 / 32.0 / 32.0)
+#define KVEXP_EXP_C2 (0x1.62e42ff0c52d6p-1 / 32.0)
+
+KVEXP_HD uint32_t kvexp_f32_bits(float x) {
+    uint32_t u;
+    memcpy(&u, &x, 4);
+    return u;
+}
+KVEXP_HD uint64_t kvexp_f64_bits(double x) {
+    uint64_t u;
+    memcpy(&u, &x, 8);
+    return u;
+}
+KVEXP_HD double kvexp_f64_from(uint64_t u) {
+    double x;
+    memcpy(&x, &u, 8);
+    return x;
+}
+
+#if defined(__HIPCC__)
+#define KVEXP_FMA64(a, b, c) __builtin_fma((a), (b), (c))
+#else
+#define KVEXP_FMA64(a, b, c) __builtin_fma((a), (b), (c))
+#endif
+
+/* The reduction and polynomial, for |x| < 88 (no special case). */
+KVEXP_HD float kvexp_expf_core(float x) {
+    const double xd = (double)x;
+#if KVEXP_EXPF_FORM >= 2
+    double kd = KVEXP_FMA64(KVEXP_EXP_INVLN2N, xd, KVEXP_EXP_SHIFT);
+    const uint64_t ki = kvexp_f64_bits(kd);
+    kd -= KVEXP_EXP_SHIFT;
+    const double r = KVEXP_FMA64(KVEXP_EXP_INVLN2N, xd, -kd);
+#else
+    const double z = KVEXP_EXP_INVLN2N * xd;
+    double kd = z + KVEXP_EXP_SHIFT;
+    const uint64_t ki = kvexp_f64_bits(kd);
+    kd -= KVEXP_EXP_SHIFT;
+    const double r = z - kd;
+#endif
+    const uint64_t t = kvexp_exp2_32_table[ki & 31u] + (ki << 47);
+    const double s = kvexp_f64_from(t);
+    const double r2 = r * r;
+#if KVEXP_EXPF_FORM >= 1
+    const double p = KVEXP_FMA64(KVEXP_EXP_C0, r, KVEXP_EXP_C1);
+    double y = KVEXP_FMA64(KVEXP_EXP_C2, r, 1.0);
+    y = KVEXP_FMA64(p, r2, y);
+#else
+    const double p = KVEXP_EXP_C0 * r + KVEXP_EXP_C1;
+    double y = KVEXP_EXP_C2 * r + 1.0;
+    y = p * r2 + y;
+#endif
+    return (float)(y * s);
+}
+
+/* expf with glibc's special cases: -inf -> +0, NaN/+inf -> x + x,
+ * x > 0x1.62e42ep6 -> +inf, x < -0x1.9fe368p6 -> +0. */
+KVEXP_HD float kvexp_expf(float x) {
+    const uint32_t ux = kvexp_f32_bits(x);
+    const uint32_t abstop = (ux >> 20) & 0x7ffu;
+    if (abstop >= 0x42bu) { /* |x| >= 88, or x is Inf/NaN */
+        if (ux == 0xff800000u) return 0.0f;
+        if (abstop >= 0x7f8u) return x + x;
+        if (x > 0x1.62e42ep6f) return __builtin_inff();
+        if (x < -0x1.9fe368p6f) return 0.0f;
+    }
+    return kvexp_expf_core(x);
+}
+
+#endif /* KVEXP_EXPF_H */

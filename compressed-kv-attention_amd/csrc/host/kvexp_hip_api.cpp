@@ -1,0 +1,624 @@
+// C ABI of the gfx950 backend (include/kvexp_hip.h).
+//
+// Host-side responsibilities: argument validation with the reference's
+// exception classes and messages, the host walk of block headers, split
+// planning (token_bounds, dispatch.cpp:17-23, with the block-alignment rule
+// of scan.hpp:107-109), device descriptors and workspace, and mapping the
+// kernels' status word back to errors. All arithmetic runs in the kernels.
+#include "kvexp_hip.h"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstring>
+#include <mutex>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "../hip/kvexp_types.h"
+
+using kvexp_dev::EncBlockMeta;
+using kvexp_dev::HeadDev;
+using kvexp_dev::WorkItem;
+
+namespace kvexp_launch {
+hipError_t decode(const uint8_t *blob, uint64_t bytes, const int64_t *offs, const int32_t *first, int n_blocks,
+                  int seq, int dim, uint16_t *out, uint32_t *status, hipStream_t s);
+hipError_t encode(const uint16_t *kv, int seq, int dim, int bt, int n_blocks, EncBlockMeta *meta, uint8_t *bases,
+                  int64_t *offs, int32_t *first, uint8_t *out, uint32_t *status, hipStream_t s);
+hipError_t attention(bool xkv, int order, const HeadDev *heads, const WorkItem *items, int n_items,
+                     const int32_t *merge_ids, int n_merge, const uint16_t *q, float *out, float *lse, float *ws,
+                     int dim, uint32_t *status, hipStream_t s);
+size_t attention_lds_bytes(int dim);
+hipError_t expf(const float *x, float *y, size_t n, hipStream_t s);
+} // namespace kvexp_launch
+
+namespace {
+
+constexpr int kMaxQPerLaunch = 8;
+constexpr int kMaxDim = 256;
+
+thread_local std::string g_error;
+
+int set_error(int code, const std::string &msg) {
+    g_error = msg;
+    return code;
+}
+int ok() {
+    g_error.clear();
+    return KVEXP_HIP_OK;
+}
+
+struct HipFail {
+    hipError_t err;
+    const char *what;
+};
+
+#define HIPX(call)                                                                                                    \
+    do {                                                                                                              \
+        hipError_t e_ = (call);                                                                                       \
+        if (e_ != hipSuccess) throw HipFail{e_, #call};                                                               \
+    } while (0)
+
+struct KvexpFail {
+    int code;
+    std::string msg;
+};
+
+[[noreturn]] void fail(int code, const std::string &msg) { throw KvexpFail{code, msg}; }
+
+template <class F> int guarded(F &&fn) {
+    try {
+        fn();
+        return ok();
+    } catch (const KvexpFail &f) {
+        return set_error(f.code, f.msg);
+    } catch (const HipFail &h) {
+        return set_error(KVEXP_HIP_DEVICE_ERROR, std::string(h.what) + ": " + hipGetErrorString(h.err));
+    } catch (const std::bad_alloc &) {
+        return set_error(KVEXP_HIP_DEVICE_ERROR, "host allocation failed");
+    } catch (const std::exception &e) {
+        return set_error(KVEXP_HIP_LOGIC_ERROR, e.what());
+    }
+}
+
+// Device allocation released on scope exit unless kept.
+struct DevBuf {
+    void *p = nullptr;
+    DevBuf() = default;
+    explicit DevBuf(size_t n) {
+        if (n) HIPX(hipMalloc(&p, n));
+    }
+    DevBuf(const DevBuf &) = delete;
+    DevBuf &operator=(const DevBuf &) = delete;
+    DevBuf(DevBuf &&o) noexcept : p(o.p) { o.p = nullptr; }
+    DevBuf &operator=(DevBuf &&o) noexcept {
+        std::swap(p, o.p);
+        return *this;
+    }
+    ~DevBuf() {
+        if (p) (void)hipFree(p);
+    }
+    template <class T> T *as() const { return static_cast<T *>(p); }
+};
+
+// --------------------------------------------------------- host block walk --
+struct HostBlock {
+    int mode, n_tokens, n_escape;
+    size_t next;
+};
+
+inline unsigned rd16(const uint8_t *p) { return unsigned(p[0]) | (unsigned(p[1]) << 8); }
+
+// parse_block (scan.hpp:28-66): validation order and messages.
+HostBlock parse_block_host(const uint8_t *blob, size_t bytes, size_t at, int dim) {
+    if (bytes - at < 8) fail(KVEXP_HIP_FORMAT_ERROR, "truncated xkv block header");
+    const uint8_t *p = blob + at;
+    HostBlock b{p[0], p[1], int(rd16(p + 2)), 0};
+    const int hdim = int(rd16(p + 4));
+    if (hdim != dim || b.n_tokens <= 0) fail(KVEXP_HIP_FORMAT_ERROR, "xkv block dimension or length mismatch");
+    const size_t body = at + 8;
+    if (b.mode == 0) {
+        const size_t nb = size_t(b.n_tokens) * size_t(dim) * 2u;
+        if (bytes - body < nb) fail(KVEXP_HIP_FORMAT_ERROR, "truncated raw xkv block");
+        b.next = body + nb;
+        return b;
+    }
+    if (b.mode != 2 && b.mode != 4) fail(KVEXP_HIP_FORMAT_ERROR, "unknown xkv block mode");
+    const size_t need = size_t(dim) + size_t(b.n_tokens) * size_t(dim) +
+                        size_t((b.n_tokens * dim * b.mode + 7) / 8) + size_t(b.n_escape) * 2u;
+    if (bytes - body < need) fail(KVEXP_HIP_FORMAT_ERROR, "truncated coded xkv block");
+    b.next = body + need;
+    return b;
+}
+
+// Blocks that a reader consuming `seq` tokens touches, then the eager parse of
+// the following header (scan.hpp:144-151, 176-189).
+void walk_index(const uint8_t *blob, size_t bytes, int dim, int seq, std::vector<int64_t> &off,
+                std::vector<int32_t> &first) {
+    off.clear();
+    first.clear();
+    size_t at = 0;
+    int64_t tok = 0;
+    while (at < bytes) {
+        const HostBlock b = parse_block_host(blob, bytes, at, dim);
+        if (tok >= seq) break;
+        off.push_back(int64_t(at));
+        first.push_back(int32_t(tok));
+        tok += b.n_tokens;
+        at = b.next;
+    }
+    off.push_back(int64_t(at));
+    first.push_back(int32_t(std::min<int64_t>(tok, INT32_MAX)));
+}
+
+// token_bounds (dispatch.cpp:17-23).
+void token_bounds(int seq, int tile, int tid, int n, int &a, int &b) {
+    const int ntiles = (seq + tile - 1) / tile;
+    const int b0 = int((long long)tid * ntiles / n);
+    const int b1 = int((long long)(tid + 1) * ntiles / n);
+    a = std::min(seq, b0 * tile);
+    b = std::min(seq, b1 * tile);
+}
+
+std::string status_message(uint32_t st) {
+    using namespace kvexp_dev;
+    if (st & kStHeader) return "xkv block dimension or length mismatch";
+    if (st & kStMode) return "unknown xkv block mode";
+    if (st & kStTruncated) return "truncated coded xkv block";
+    if (st & kStIndex) return "xkv block index does not match the container";
+    if (st & kStEscape) return "xkv escape stream overrun";
+    return "xkv container error";
+}
+
+} // namespace
+
+// ================================================================ context ==
+struct kvexp_hip_ctx {
+    int device = 0;
+    DevBuf status; // uint32 status word
+    // encoder scratch, grown on demand
+    DevBuf enc_meta, enc_bases, enc_off, enc_first;
+    size_t enc_meta_cap = 0, enc_bases_cap = 0, enc_index_cap = 0;
+    int cu_count = 0;
+};
+
+struct kvexp_hip_plan {
+    kvexp_hip_ctx *ctx = nullptr;
+    int n_heads = 0, n_q = 0, dim = 0, order = 0;
+    bool xkv = false;
+    DevBuf heads, items, merge_ids, ws, status;
+    int n_dev_heads = 0, n_items = 0, n_merge = 0;
+};
+
+namespace {
+struct DeviceGuard {
+    int prev = -1;
+    explicit DeviceGuard(int dev) {
+        HIPX(hipGetDevice(&prev));
+        if (prev != dev) HIPX(hipSetDevice(dev));
+    }
+    ~DeviceGuard() {
+        int cur = -1;
+        if (hipGetDevice(&cur) == hipSuccess && cur != prev && prev >= 0) (void)hipSetDevice(prev);
+    }
+};
+
+void grow(DevBuf &buf, size_t &cap, size_t need) {
+    if (need <= cap) return;
+    DevBuf nb(need);
+    buf = std::move(nb);
+    cap = need;
+}
+
+void check_status_word(uint32_t *d_status, hipStream_t s) {
+    uint32_t st = 0;
+    HIPX(hipMemcpyAsync(&st, d_status, sizeof st, hipMemcpyDeviceToHost, s));
+    HIPX(hipStreamSynchronize(s));
+    if (st != 0u) {
+        HIPX(hipMemsetAsync(d_status, 0, sizeof(uint32_t), s));
+        HIPX(hipStreamSynchronize(s));
+        fail(KVEXP_HIP_FORMAT_ERROR, status_message(st));
+    }
+}
+} // namespace
+
+extern "C" {
+
+const char *kvexp_hip_status_string(int status) {
+    switch (status) {
+    case KVEXP_HIP_OK: return "ok";
+    case KVEXP_HIP_INVALID_ARGUMENT: return "invalid argument";
+    case KVEXP_HIP_FORMAT_ERROR: return "container or split format error";
+    case KVEXP_HIP_LOGIC_ERROR: return "internal consistency error";
+    case KVEXP_HIP_UNSUPPORTED: return "unsupported shape or option";
+    case KVEXP_HIP_DEVICE_ERROR: return "HIP runtime error";
+    case KVEXP_HIP_CAPACITY: return "output buffer too small";
+    default: return "unknown status";
+    }
+}
+
+const char *kvexp_hip_last_error(void) { return g_error.c_str(); }
+
+const char *kvexp_hip_version(void) { return "kvexp-amd 0.1 (gfx950)"; }
+
+int kvexp_hip_ctx_create(int device, kvexp_hip_ctx **out) {
+    return guarded([&] {
+        if (out == nullptr) fail(KVEXP_HIP_INVALID_ARGUMENT, "kvexp_hip_ctx_create: null output");
+        *out = nullptr;
+        int n = 0;
+        HIPX(hipGetDeviceCount(&n));
+        if (device < 0 || device >= n) fail(KVEXP_HIP_INVALID_ARGUMENT, "kvexp_hip_ctx_create: no such device");
+        DeviceGuard g(device);
+        hipDeviceProp_t prop;
+        HIPX(hipGetDeviceProperties(&prop, device));
+        if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+            fail(KVEXP_HIP_UNSUPPORTED, std::string("kvexp-amd is built for gfx950, device is ") + prop.gcnArchName);
+        auto *c = new kvexp_hip_ctx();
+        c->device = device;
+        c->cu_count = prop.multiProcessorCount;
+        try {
+            c->status = DevBuf(sizeof(uint32_t));
+            HIPX(hipMemset(c->status.p, 0, sizeof(uint32_t)));
+        } catch (...) {
+            delete c;
+            throw;
+        }
+        *out = c;
+    });
+}
+
+int kvexp_hip_ctx_destroy(kvexp_hip_ctx *ctx) {
+    return guarded([&] {
+        if (ctx == nullptr) return;
+        DeviceGuard g(ctx->device);
+        delete ctx;
+    });
+}
+
+// ============================================================ size model ==
+int kvexp_hip_exp_payload_bytes(int n, int dim, int bits) { return (n * dim * bits + 7) / 8; }
+int kvexp_hip_coded_block_bytes(int n, int dim, int bits, int esc) {
+    return 8 + dim + n * dim + kvexp_hip_exp_payload_bytes(n, dim, bits) + 2 * esc;
+}
+int kvexp_hip_raw_block_bytes(int n, int dim) { return 8 + 2 * n * dim; }
+int kvexp_hip_block_count(int seq, int bt) {
+    if (seq <= 0 || bt <= 0) return 0;
+    return (seq + bt - 1) / bt;
+}
+int64_t kvexp_hip_encode_bound(int seq, int dim, int bt) {
+    if (seq <= 0 || dim <= 0 || bt <= 0) return 0;
+    return int64_t(kvexp_hip_block_count(seq, bt)) * 8 + 2 * int64_t(seq) * dim;
+}
+
+// ================================================================= index ==
+int kvexp_hip_build_index(const uint8_t *blob, size_t bytes, int dim, int seq, int64_t *offsets,
+                          int32_t *first_token, int capacity, int *n_blocks) {
+    return guarded([&] {
+        if ((blob == nullptr && bytes) || offsets == nullptr || first_token == nullptr || n_blocks == nullptr)
+            fail(KVEXP_HIP_INVALID_ARGUMENT, "kvexp_hip_build_index: null argument");
+        std::vector<int64_t> off;
+        std::vector<int32_t> first;
+        walk_index(blob, bytes, dim, seq, off, first);
+        const int nb = int(off.size()) - 1;
+        *n_blocks = nb;
+        if (nb > capacity) fail(KVEXP_HIP_CAPACITY, "kvexp_hip_build_index: capacity below the block count");
+        std::memcpy(offsets, off.data(), off.size() * sizeof(int64_t));
+        std::memcpy(first_token, first.data(), first.size() * sizeof(int32_t));
+    });
+}
+
+// ================================================================= codec ==
+int kvexp_hip_encode(kvexp_hip_ctx *ctx, const uint16_t *d_kv, int seq, int dim, int bt, uint8_t *d_out,
+                     size_t capacity, int64_t *d_offsets, int32_t *d_first_token, size_t *bytes_out, void *stream) {
+    return guarded([&] {
+        if (ctx == nullptr) fail(KVEXP_HIP_INVALID_ARGUMENT, "kvexp_hip_encode: null context");
+        // codec.cpp:40-52
+        if (d_kv == nullptr || seq <= 0 || dim <= 0 || bt <= 0)
+            fail(KVEXP_HIP_INVALID_ARGUMENT, "encode_bf16: empty input");
+        if (dim % 4 != 0 || dim > kMaxDim)
+            fail(KVEXP_HIP_INVALID_ARGUMENT, "encode_bf16: head_dim must be a multiple of 4 and at most 256");
+        if (bt > 255) fail(KVEXP_HIP_INVALID_ARGUMENT, "encode_bf16: block_tokens must fit in a byte");
+        if (int64_t(bt) * dim > 65535)
+            fail(KVEXP_HIP_INVALID_ARGUMENT, "encode_bf16: block escape count would not fit in u16");
+        if (d_out == nullptr) fail(KVEXP_HIP_INVALID_ARGUMENT, "kvexp_hip_encode: null output");
+        if (int64_t(capacity) < kvexp_hip_encode_bound(seq, dim, bt))
+            fail(KVEXP_HIP_CAPACITY, "kvexp_hip_encode: capacity below kvexp_hip_encode_bound");
+        DeviceGuard g(ctx->device);
+        hipStream_t s = static_cast<hipStream_t>(stream);
+        const int nb = kvexp_hip_block_count(seq, bt);
+        grow(ctx->enc_meta, ctx->enc_meta_cap, size_t(nb) * sizeof(EncBlockMeta));
+        grow(ctx->enc_bases, ctx->enc_bases_cap, size_t(nb) * 2u * size_t(dim));
+        int64_t *offs = d_offsets;
+        int32_t *first = d_first_token;
+        if (offs == nullptr || first == nullptr) {
+            const size_t need = size_t(nb + 1) * (sizeof(int64_t) + sizeof(int32_t));
+            if (need > ctx->enc_index_cap) {
+                ctx->enc_off = DevBuf(size_t(nb + 1) * sizeof(int64_t));
+                ctx->enc_first = DevBuf(size_t(nb + 1) * sizeof(int32_t));
+                ctx->enc_index_cap = need;
+            }
+            if (offs == nullptr) offs = ctx->enc_off.as<int64_t>();
+            if (first == nullptr) first = ctx->enc_first.as<int32_t>();
+        }
+        HIPX(kvexp_launch::encode(d_kv, seq, dim, bt, nb, ctx->enc_meta.as<EncBlockMeta>(),
+                                  ctx->enc_bases.as<uint8_t>(), offs, first, d_out, ctx->status.as<uint32_t>(), s));
+        if (bytes_out != nullptr) {
+            int64_t total = 0;
+            uint32_t st = 0;
+            HIPX(hipMemcpyAsync(&total, offs + nb, sizeof total, hipMemcpyDeviceToHost, s));
+            HIPX(hipMemcpyAsync(&st, ctx->status.p, sizeof st, hipMemcpyDeviceToHost, s));
+            HIPX(hipStreamSynchronize(s));
+            if (st != 0u) {
+                HIPX(hipMemset(ctx->status.p, 0, sizeof(uint32_t)));
+                fail(KVEXP_HIP_LOGIC_ERROR, "escape count drifted from the size model");
+            }
+            *bytes_out = size_t(total);
+        }
+    });
+}
+
+int kvexp_hip_decode(kvexp_hip_ctx *ctx, const uint8_t *d_blob, size_t bytes, const int64_t *d_offsets,
+                     const int32_t *d_first_token, int n_blocks, int seq, int dim, uint16_t *d_out, int check,
+                     void *stream) {
+    return guarded([&] {
+        if (ctx == nullptr) fail(KVEXP_HIP_INVALID_ARGUMENT, "kvexp_hip_decode: null context");
+        if (seq < 0 || dim <= 0 || n_blocks < 0) fail(KVEXP_HIP_INVALID_ARGUMENT, "kvexp_hip_decode: bad shape");
+        if (dim % 4 != 0 || dim > kMaxDim)
+            fail(KVEXP_HIP_INVALID_ARGUMENT, "kvexp_hip_decode: head_dim must be a multiple of 4 and at most 256");
+        if (seq == 0) return;
+        if (d_blob == nullptr || d_offsets == nullptr || d_first_token == nullptr || d_out == nullptr)
+            fail(KVEXP_HIP_INVALID_ARGUMENT, "kvexp_hip_decode: null argument");
+        DeviceGuard g(ctx->device);
+        hipStream_t s = static_cast<hipStream_t>(stream);
+        if (check) {
+            int32_t have = 0;
+            HIPX(hipMemcpyAsync(&have, d_first_token + n_blocks, sizeof have, hipMemcpyDeviceToHost, s));
+            HIPX(hipStreamSynchronize(s));
+            if (have < seq) fail(KVEXP_HIP_FORMAT_ERROR, "xkv decode ran out of blocks");
+        }
+        HIPX(kvexp_launch::decode(d_blob, bytes, d_offsets, d_first_token, n_blocks, seq, dim, d_out,
+                                  ctx->status.as<uint32_t>(), s));
+        if (check) check_status_word(ctx->status.as<uint32_t>(), s);
+    });
+}
+
+// ============================================================= attention ==
+int kvexp_hip_suggest_splits(kvexp_hip_ctx *ctx, int n_heads, int seq, int split_tokens) {
+    if (ctx == nullptr || n_heads <= 0 || seq <= 0 || split_tokens <= 0) return 1;
+    const int tiles = (seq + split_tokens - 1) / split_tokens;
+    // about two resident workgroups per CU over the whole launch
+    const int target = std::max(1, (2 * ctx->cu_count + n_heads - 1) / n_heads);
+    return std::max(1, std::min(tiles, target));
+}
+
+int kvexp_hip_plan_create(kvexp_hip_ctx *ctx, const kvexp_hip_head *heads, int n_heads, int n_q, int dim,
+                          int split_tokens, int order, kvexp_hip_plan **out) {
+    return guarded([&] {
+        if (out == nullptr) fail(KVEXP_HIP_INVALID_ARGUMENT, "kvexp_hip_plan_create: null output");
+        *out = nullptr;
+        if (ctx == nullptr || heads == nullptr || n_heads <= 0 || n_q <= 0 || dim <= 0 || split_tokens <= 0)
+            fail(KVEXP_HIP_INVALID_ARGUMENT, "attention_decode: bad argument");
+        if (order != KVEXP_HIP_ORDER_SCALAR && order != KVEXP_HIP_ORDER_DPBF16)
+            fail(KVEXP_HIP_INVALID_ARGUMENT, "kvexp_hip_plan_create: unknown score order");
+        // attention_scalar.cpp:47-49 / attention_avx512.cpp:155-157
+        if (order == KVEXP_HIP_ORDER_SCALAR && (dim % 8 != 0 || dim > kMaxDim))
+            fail(KVEXP_HIP_INVALID_ARGUMENT, "scalar attention: bad shape");
+        if (order == KVEXP_HIP_ORDER_DPBF16 && (dim % 32 != 0 || dim > kMaxDim))
+            fail(KVEXP_HIP_INVALID_ARGUMENT, "avx512 attention: head_dim must be a multiple of 32");
+        DeviceGuard g(ctx->device);
+
+        const bool xkv = heads[0].k_xkv != nullptr;
+        std::vector<HeadDev> hv;
+        std::vector<WorkItem> items;
+        std::vector<int32_t> merge;
+        int ws_slots = 0;
+        std::vector<int32_t> kfirst, vfirst;
+        for (int h = 0; h < n_heads; ++h) {
+            const kvexp_hip_head &H = heads[h];
+            const bool raw = H.k_raw != nullptr, x = H.k_xkv != nullptr;
+            if (H.seq <= 0) fail(KVEXP_HIP_INVALID_ARGUMENT, "attention_decode: bad argument");
+            if (raw == x || (H.v_raw != nullptr) != raw || (H.v_xkv != nullptr) != x)
+                fail(KVEXP_HIP_INVALID_ARGUMENT, "attention_decode: pass raw K and V or xkv K and V, not both");
+            if (x != xkv) fail(KVEXP_HIP_UNSUPPORTED, "kvexp_hip_plan_create: one plan holds raw or XKV heads, not both");
+            const int ntiles = (H.seq + split_tokens - 1) / split_tokens;
+            const int n_splits = std::min(std::max(1, H.n_splits), ntiles);
+            if (x) {
+                if (H.k_offsets == nullptr || H.v_offsets == nullptr || H.k_first_token == nullptr ||
+                    H.v_first_token == nullptr || H.k_n_blocks <= 0 || H.v_n_blocks <= 0)
+                    fail(KVEXP_HIP_INVALID_ARGUMENT, "kvexp_hip_plan_create: XKV head without a block index");
+                kfirst.resize(size_t(H.k_n_blocks) + 1);
+                vfirst.resize(size_t(H.v_n_blocks) + 1);
+                HIPX(hipMemcpy(kfirst.data(), H.k_first_token, kfirst.size() * 4, hipMemcpyDeviceToHost));
+                HIPX(hipMemcpy(vfirst.data(), H.v_first_token, vfirst.size() * 4, hipMemcpyDeviceToHost));
+                if (kfirst.back() < H.seq || vfirst.back() < H.seq)
+                    fail(KVEXP_HIP_FORMAT_ERROR, "xkv ran out of tokens");
+            }
+            // query rows in groups of <= 8 per device head, same splits
+            for (int q0 = 0; q0 < n_q; q0 += kMaxQPerLaunch) {
+                HeadDev d{};
+                d.kx = H.k_xkv;
+                d.vx = H.v_xkv;
+                d.kbytes = H.k_bytes;
+                d.vbytes = H.v_bytes;
+                d.koff = H.k_offsets;
+                d.voff = H.v_offsets;
+                d.kfirst = H.k_first_token;
+                d.vfirst = H.v_first_token;
+                d.kraw = H.k_raw;
+                d.vraw = H.v_raw;
+                d.seq = H.seq;
+                d.n_splits = n_splits;
+                d.ws_base = ws_slots;
+                d.q_row = h * n_q + q0;
+                d.n_q = std::min(kMaxQPerLaunch, n_q - q0);
+                const int dh = int(hv.size());
+                for (int sp = 0; sp < n_splits; ++sp) {
+                    WorkItem wi{};
+                    wi.head = dh;
+                    wi.split = sp;
+                    token_bounds(H.seq, split_tokens, sp, n_splits, wi.tok_begin, wi.tok_end);
+                    wi.kblk = wi.vblk = -1;
+                    if (x) {
+                        auto kit = std::lower_bound(kfirst.begin(), kfirst.end() - 1, wi.tok_begin);
+                        auto vit = std::lower_bound(vfirst.begin(), vfirst.end() - 1, wi.tok_begin);
+                        if (kit == kfirst.end() - 1 || *kit != wi.tok_begin || vit == vfirst.end() - 1 ||
+                            *vit != wi.tok_begin)
+                            fail(KVEXP_HIP_FORMAT_ERROR, "token split is not aligned to an encoded block");
+                        wi.kblk = int(kit - kfirst.begin());
+                        wi.vblk = int(vit - vfirst.begin());
+                    }
+                    items.push_back(wi);
+                }
+                if (n_splits > 1) {
+                    merge.push_back(dh);
+                    ws_slots += n_splits;
+                }
+                hv.push_back(d);
+            }
+        }
+        auto *p = new kvexp_hip_plan();
+        try {
+            p->ctx = ctx;
+            p->n_heads = n_heads;
+            p->n_q = n_q;
+            p->dim = dim;
+            p->order = order;
+            p->xkv = xkv;
+            p->n_dev_heads = int(hv.size());
+            p->n_items = int(items.size());
+            p->n_merge = int(merge.size());
+            p->heads = DevBuf(hv.size() * sizeof(HeadDev));
+            p->items = DevBuf(items.size() * sizeof(WorkItem));
+            p->merge_ids = DevBuf(std::max<size_t>(1, merge.size()) * sizeof(int32_t));
+            const size_t slot_floats = size_t(kMaxQPerLaunch) * size_t(dim + 2);
+            p->ws = DevBuf(std::max<size_t>(1, size_t(ws_slots)) * slot_floats * sizeof(float));
+            p->status = DevBuf(sizeof(uint32_t));
+            HIPX(hipMemcpy(p->heads.p, hv.data(), hv.size() * sizeof(HeadDev), hipMemcpyHostToDevice));
+            HIPX(hipMemcpy(p->items.p, items.data(), items.size() * sizeof(WorkItem), hipMemcpyHostToDevice));
+            if (!merge.empty())
+                HIPX(hipMemcpy(p->merge_ids.p, merge.data(), merge.size() * sizeof(int32_t), hipMemcpyHostToDevice));
+            HIPX(hipMemset(p->status.p, 0, sizeof(uint32_t)));
+        } catch (...) {
+            delete p;
+            throw;
+        }
+        *out = p;
+    });
+}
+
+int kvexp_hip_plan_destroy(kvexp_hip_plan *plan) {
+    return guarded([&] {
+        if (plan == nullptr) return;
+        DeviceGuard g(plan->ctx->device);
+        delete plan;
+    });
+}
+
+int kvexp_hip_attention_run(kvexp_hip_plan *plan, const uint16_t *d_q, float *d_out, float *d_lse, int check,
+                            void *stream) {
+    return guarded([&] {
+        if (plan == nullptr || d_q == nullptr || d_out == nullptr)
+            fail(KVEXP_HIP_INVALID_ARGUMENT, "attention_decode: bad argument");
+        DeviceGuard g(plan->ctx->device);
+        hipStream_t s = static_cast<hipStream_t>(stream);
+        HIPX(kvexp_launch::attention(plan->xkv, plan->order, plan->heads.as<HeadDev>(), plan->items.as<WorkItem>(),
+                                     plan->n_items, plan->merge_ids.as<int32_t>(), plan->n_merge, d_q, d_out, d_lse,
+                                     plan->ws.as<float>(), plan->dim, plan->status.as<uint32_t>(), s));
+        if (check) check_status_word(plan->status.as<uint32_t>(), s);
+    });
+}
+
+int kvexp_hip_plan_status(kvexp_hip_plan *plan, void *stream) {
+    return guarded([&] {
+        if (plan == nullptr) fail(KVEXP_HIP_INVALID_ARGUMENT, "kvexp_hip_plan_status: null plan");
+        DeviceGuard g(plan->ctx->device);
+        check_status_word(plan->status.as<uint32_t>(), static_cast<hipStream_t>(stream));
+    });
+}
+
+int kvexp_hip_attention_decode_host(kvexp_hip_ctx *ctx, int order, const uint16_t *q, const uint16_t *k_raw,
+                                    const uint16_t *v_raw, const uint8_t *k_xkv, size_t k_bytes,
+                                    const uint8_t *v_xkv, size_t v_bytes, float *out, int n_q, int dim, int seq,
+                                    int n_threads, int split_tokens) {
+    return guarded([&] {
+        // dispatch.cpp:31-38
+        if (q == nullptr || out == nullptr || n_q <= 0 || dim <= 0 || seq <= 0 || split_tokens <= 0)
+            fail(KVEXP_HIP_INVALID_ARGUMENT, "attention_decode: bad argument");
+        const bool raw = k_raw != nullptr, x = k_xkv != nullptr;
+        if (raw == x || (v_raw != nullptr) != raw || (v_xkv != nullptr) != x)
+            fail(KVEXP_HIP_INVALID_ARGUMENT, "attention_decode: pass raw K and V or xkv K and V, not both");
+        if (ctx == nullptr) fail(KVEXP_HIP_INVALID_ARGUMENT, "kvexp_hip_attention_decode_host: null context");
+        if (order == KVEXP_HIP_ORDER_SCALAR && (dim % 8 != 0 || dim > kMaxDim))
+            fail(KVEXP_HIP_INVALID_ARGUMENT, "scalar attention: bad shape");
+        if (order == KVEXP_HIP_ORDER_DPBF16 && (dim % 32 != 0 || dim > kMaxDim))
+            fail(KVEXP_HIP_INVALID_ARGUMENT, "avx512 attention: head_dim must be a multiple of 32");
+        DeviceGuard g(ctx->device);
+        const size_t qn = size_t(n_q) * size_t(dim);
+        DevBuf dq(qn * 2), dout(qn * 4);
+        HIPX(hipMemcpy(dq.p, q, qn * 2, hipMemcpyHostToDevice));
+        kvexp_hip_head H{};
+        H.seq = seq;
+        H.n_splits = n_threads;
+        DevBuf dk, dv, kio, kif, vio, vif;
+        if (raw) {
+            const size_t nb = size_t(seq) * size_t(dim) * 2u;
+            dk = DevBuf(nb);
+            dv = DevBuf(nb);
+            HIPX(hipMemcpy(dk.p, k_raw, nb, hipMemcpyHostToDevice));
+            HIPX(hipMemcpy(dv.p, v_raw, nb, hipMemcpyHostToDevice));
+            H.k_raw = dk.as<uint16_t>();
+            H.v_raw = dv.as<uint16_t>();
+        } else {
+            std::vector<int64_t> ko, vo;
+            std::vector<int32_t> kf, vf;
+            walk_index(k_xkv, k_bytes, dim, seq, ko, kf);
+            walk_index(v_xkv, v_bytes, dim, seq, vo, vf);
+            if (kf.back() < seq || vf.back() < seq)
+                fail(KVEXP_HIP_FORMAT_ERROR, "xkv ran out of tokens");
+            dk = DevBuf(std::max<size_t>(k_bytes, 4));
+            dv = DevBuf(std::max<size_t>(v_bytes, 4));
+            HIPX(hipMemcpy(dk.p, k_xkv, k_bytes, hipMemcpyHostToDevice));
+            HIPX(hipMemcpy(dv.p, v_xkv, v_bytes, hipMemcpyHostToDevice));
+            kio = DevBuf(ko.size() * 8);
+            kif = DevBuf(kf.size() * 4);
+            vio = DevBuf(vo.size() * 8);
+            vif = DevBuf(vf.size() * 4);
+            HIPX(hipMemcpy(kio.p, ko.data(), ko.size() * 8, hipMemcpyHostToDevice));
+            HIPX(hipMemcpy(kif.p, kf.data(), kf.size() * 4, hipMemcpyHostToDevice));
+            HIPX(hipMemcpy(vio.p, vo.data(), vo.size() * 8, hipMemcpyHostToDevice));
+            HIPX(hipMemcpy(vif.p, vf.data(), vf.size() * 4, hipMemcpyHostToDevice));
+            H.k_xkv = dk.as<uint8_t>();
+            H.v_xkv = dv.as<uint8_t>();
+            H.k_bytes = k_bytes;
+            H.v_bytes = v_bytes;
+            H.k_offsets = kio.as<int64_t>();
+            H.v_offsets = vio.as<int64_t>();
+            H.k_first_token = kif.as<int32_t>();
+            H.v_first_token = vif.as<int32_t>();
+            H.k_n_blocks = int(ko.size()) - 1;
+            H.v_n_blocks = int(vo.size()) - 1;
+        }
+        kvexp_hip_plan *plan = nullptr;
+        int rc = kvexp_hip_plan_create(ctx, &H, 1, n_q, dim, split_tokens, order, &plan);
+        if (rc) fail(rc, g_error);
+        rc = kvexp_hip_attention_run(plan, dq.as<uint16_t>(), dout.as<float>(), nullptr, 1, nullptr);
+        const std::string msg = g_error;
+        kvexp_hip_plan_destroy(plan);
+        if (rc) fail(rc, msg);
+        HIPX(hipMemcpy(out, dout.p, qn * 4, hipMemcpyDeviceToHost));
+    });
+}
+
+int kvexp_hip_expf(kvexp_hip_ctx *ctx, const float *d_x, float *d_y, size_t n, void *stream) {
+    return guarded([&] {
+        if (ctx == nullptr || (n && (d_x == nullptr || d_y == nullptr)))
+            fail(KVEXP_HIP_INVALID_ARGUMENT, "kvexp_hip_expf: null argument");
+        if (n > (size_t(1) << 40)) fail(KVEXP_HIP_INVALID_ARGUMENT, "kvexp_hip_expf: n too large");
+        DeviceGuard g(ctx->device);
+        HIPX(kvexp_launch::expf(d_x, d_y, n, static_cast<hipStream_t>(stream)));
+    });
+}
+
+} // extern "C"

@@ -1,0 +1,292 @@
+"""Python access to the kvexp-amd C ABI (include/kvexp_hip.h) over torch device memory.
+
+The library ``lib/libkvexp_hip.so`` is built in-tree by ``build.py``; importing
+this module does not build it, and every entry point raises if it is missing
+(there is no CPU fallback). Tensors are torch CUDA(ROCm) tensors; BF16 data is
+carried as ``torch.int16`` / ``torch.bfloat16`` bits.
+
+Errors are :class:`KvexpHipError` with the C ABI status and the reference-style
+message (``invalid_argument`` / ``runtime_error`` / ``logic_error`` kinds).
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import re
+from dataclasses import dataclass
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.dirname(HERE)
+ROOT = os.path.dirname(PKG)
+LIB_PATH = os.path.join(PKG, "lib", "libkvexp_hip.so")
+HEADER = os.path.join(ROOT, "include", "kvexp_hip.h")
+
+ORDER_SCALAR = 0
+ORDER_DPBF16 = 1
+
+_KIND = {1: "invalid_argument", 2: "runtime_error", 3: "logic_error", 4: "unsupported", 5: "device_error",
+         6: "capacity"}
+
+_lib = None
+
+
+class KvexpHipError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"{_KIND.get(code, code)}: {msg}")
+        self.code = code
+        self.kind = _KIND.get(code, str(code))
+        self.msg = msg
+
+
+class _Head(C.Structure):
+    _fields_ = [
+        ("k_xkv", C.c_void_p), ("v_xkv", C.c_void_p),
+        ("k_bytes", C.c_uint64), ("v_bytes", C.c_uint64),
+        ("k_offsets", C.c_void_p), ("v_offsets", C.c_void_p),
+        ("k_first_token", C.c_void_p), ("v_first_token", C.c_void_p),
+        ("k_n_blocks", C.c_int32), ("v_n_blocks", C.c_int32),
+        ("k_raw", C.c_void_p), ("v_raw", C.c_void_p),
+        ("seq", C.c_int32), ("n_splits", C.c_int32),
+    ]
+
+
+def declared_symbols() -> list[str]:
+    """Names of the functions include/kvexp_hip.h declares."""
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(kvexp_hip_\w+)\s*\(", text)))
+
+
+def lib() -> C.CDLL:
+    """Loads the library (raises FileNotFoundError when it was not built)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise FileNotFoundError(f"{LIB_PATH} is missing: run compressed-kv-attention_amd/build.py")
+    L = C.CDLL(LIB_PATH)
+    vp, sz, i32, i64 = C.c_void_p, C.c_size_t, C.c_int, C.c_int64
+    L.kvexp_hip_status_string.restype = C.c_char_p
+    L.kvexp_hip_status_string.argtypes = [i32]
+    L.kvexp_hip_last_error.restype = C.c_char_p
+    L.kvexp_hip_version.restype = C.c_char_p
+    L.kvexp_hip_ctx_create.argtypes = [i32, C.POINTER(vp)]
+    L.kvexp_hip_ctx_destroy.argtypes = [vp]
+    for f in ("kvexp_hip_exp_payload_bytes", "kvexp_hip_coded_block_bytes", "kvexp_hip_raw_block_bytes",
+              "kvexp_hip_block_count"):
+        getattr(L, f).restype = i32
+    L.kvexp_hip_encode_bound.restype = i64
+    L.kvexp_hip_encode_bound.argtypes = [i32, i32, i32]
+    L.kvexp_hip_build_index.argtypes = [vp, sz, i32, i32, vp, vp, i32, C.POINTER(i32)]
+    L.kvexp_hip_encode.argtypes = [vp, vp, i32, i32, i32, vp, sz, vp, vp, C.POINTER(sz), vp]
+    L.kvexp_hip_decode.argtypes = [vp, vp, sz, vp, vp, i32, i32, i32, vp, i32, vp]
+    L.kvexp_hip_plan_create.argtypes = [vp, C.POINTER(_Head), i32, i32, i32, i32, i32, C.POINTER(vp)]
+    L.kvexp_hip_plan_destroy.argtypes = [vp]
+    L.kvexp_hip_suggest_splits.argtypes = [vp, i32, i32, i32]
+    L.kvexp_hip_attention_run.argtypes = [vp, vp, vp, vp, i32, vp]
+    L.kvexp_hip_plan_status.argtypes = [vp, vp]
+    L.kvexp_hip_attention_decode_host.argtypes = [vp, i32, vp, vp, vp, vp, sz, vp, sz, vp, i32, i32, i32, i32, i32]
+    L.kvexp_hip_expf.argtypes = [vp, vp, vp, sz, vp]
+    _lib = L
+    return L
+
+
+def check(rc: int) -> None:
+    if rc != 0:
+        raise KvexpHipError(rc, lib().kvexp_hip_last_error().decode())
+
+
+def _ptr(t) -> int | None:
+    if t is None:
+        return None
+    return int(t.data_ptr())
+
+
+def _stream(stream):
+    import torch
+
+    if stream is None:
+        return C.c_void_p(torch.cuda.current_stream().cuda_stream)
+    return C.c_void_p(stream.cuda_stream if hasattr(stream, "cuda_stream") else int(stream))
+
+
+# ----------------------------------------------------------------- host-only --
+def encode_bound(seq: int, dim: int, block: int = 128) -> int:
+    return int(lib().kvexp_hip_encode_bound(seq, dim, block))
+
+
+def build_index(blob, dim: int, seq: int):
+    """Host walk of a host container (numpy uint8) -> (offsets int64, first int32) numpy arrays."""
+    import numpy as np
+
+    blob = np.ascontiguousarray(blob, dtype=np.uint8)
+    cap = blob.size // 8 + 2
+    off = np.zeros(cap + 1, dtype=np.int64)
+    first = np.zeros(cap + 1, dtype=np.int32)
+    nb = C.c_int(0)
+    check(lib().kvexp_hip_build_index(blob.ctypes.data_as(C.c_void_p), blob.size, dim, seq,
+                                      off.ctypes.data_as(C.c_void_p), first.ctypes.data_as(C.c_void_p), cap,
+                                      C.byref(nb)))
+    return off[: nb.value + 1].copy(), first[: nb.value + 1].copy()
+
+
+# ------------------------------------------------------------------- device --
+@dataclass
+class Encoded:
+    """A device container and its block index."""
+    blob: "object"     # torch.uint8 [capacity]
+    nbytes: int
+    offsets: "object"  # torch.int64 [n_blocks + 1]
+    first: "object"    # torch.int32 [n_blocks + 1]
+    seq: int
+    dim: int
+    block: int
+
+    @property
+    def n_blocks(self) -> int:
+        return int(self.offsets.numel()) - 1
+
+
+class Context:
+    """One device context (workspace + status word)."""
+
+    def __init__(self, device: int = 0):
+        import torch
+
+        if not torch.cuda.is_available():
+            raise RuntimeError("kvexp_amd needs a ROCm GPU (torch.cuda.is_available() is False)")
+        self.device = device
+        h = C.c_void_p()
+        check(lib().kvexp_hip_ctx_create(device, C.byref(h)))
+        self.h = h
+
+    def close(self) -> None:
+        if getattr(self, "h", None):
+            lib().kvexp_hip_ctx_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    # codec ------------------------------------------------------------------
+    def encode(self, kv, seq: int, dim: int, block: int = 128, stream=None, sync_size: bool = True) -> Encoded:
+        """kv: device tensor holding [seq, dim] BF16 bits (int16/bfloat16)."""
+        import torch
+
+        dev = torch.device("cuda", self.device)
+        cap = max(encode_bound(seq, dim, block), 1)
+        nb = max(lib().kvexp_hip_block_count(seq, block), 0)
+        blob = torch.empty(cap, dtype=torch.uint8, device=dev)
+        offs = torch.empty(nb + 1, dtype=torch.int64, device=dev)
+        first = torch.empty(nb + 1, dtype=torch.int32, device=dev)
+        n = C.c_size_t(0)
+        check(lib().kvexp_hip_encode(self.h, _ptr(kv), seq, dim, block, _ptr(blob), cap, _ptr(offs), _ptr(first),
+                                     C.byref(n) if sync_size else None, _stream(stream)))
+        return Encoded(blob, int(n.value) if sync_size else -1, offs, first, seq, dim, block)
+
+    def upload(self, blob_np, dim: int, seq: int, block: int = 128) -> Encoded:
+        """A host container (numpy uint8) to the device, with its host-built index."""
+        import torch
+
+        off, first = build_index(blob_np, dim, seq)
+        dev = torch.device("cuda", self.device)
+        b = torch.from_numpy(blob_np.copy()).to(dev) if blob_np.size else torch.zeros(4, dtype=torch.uint8, device=dev)
+        return Encoded(b, int(blob_np.size), torch.from_numpy(off).to(dev), torch.from_numpy(first).to(dev), seq, dim,
+                       block)
+
+    def decode(self, enc: Encoded, seq: int | None = None, out=None, check_errors: bool = True, stream=None):
+        import torch
+
+        seq = enc.seq if seq is None else seq
+        if out is None:
+            out = torch.empty(max(seq * enc.dim, 1), dtype=torch.int16, device=torch.device("cuda", self.device))
+        check(lib().kvexp_hip_decode(self.h, _ptr(enc.blob), enc.nbytes, _ptr(enc.offsets), _ptr(enc.first),
+                                     enc.n_blocks, seq, enc.dim, _ptr(out), 1 if check_errors else 0,
+                                     _stream(stream)))
+        return out[: seq * enc.dim]
+
+    # attention --------------------------------------------------------------
+    def plan(self, heads: list, n_q: int, dim: int, split: int = 128, order: int = ORDER_SCALAR) -> "Plan":
+        """heads: dicts with 'seq', 'splits' and either 'k'/'v' (raw device tensors) or
+        'kx'/'vx' (Encoded)."""
+        arr = (_Head * len(heads))()
+        keep = []
+        for i, h in enumerate(heads):
+            H = arr[i]
+            H.seq = int(h["seq"])
+            H.n_splits = int(h.get("splits", 1))
+            if "kx" in h:
+                kx, vx = h["kx"], h["vx"]
+                keep += [kx, vx]
+                H.k_xkv, H.v_xkv = _ptr(kx.blob), _ptr(vx.blob)
+                H.k_bytes, H.v_bytes = kx.nbytes, vx.nbytes
+                H.k_offsets, H.v_offsets = _ptr(kx.offsets), _ptr(vx.offsets)
+                H.k_first_token, H.v_first_token = _ptr(kx.first), _ptr(vx.first)
+                H.k_n_blocks, H.v_n_blocks = kx.n_blocks, vx.n_blocks
+            else:
+                keep += [h["k"], h["v"]]
+                H.k_raw, H.v_raw = _ptr(h["k"]), _ptr(h["v"])
+        p = C.c_void_p()
+        check(lib().kvexp_hip_plan_create(self.h, arr, len(heads), n_q, dim, split, order, C.byref(p)))
+        return Plan(self, p, len(heads), n_q, dim, keep)
+
+    def expf(self, x, out=None, stream=None):
+        import torch
+
+        if out is None:
+            out = torch.empty_like(x)
+        check(lib().kvexp_hip_expf(self.h, _ptr(x), _ptr(out), x.numel(), _stream(stream)))
+        return out
+
+    def suggest_splits(self, n_heads: int, seq: int, split: int = 128) -> int:
+        return int(lib().kvexp_hip_suggest_splits(self.h, n_heads, seq, split))
+
+    def attention_decode_host(self, order, q, k=None, v=None, kx=None, vx=None, *, n_q, dim, seq, threads=1,
+                              split=128):
+        """The Backend::Hip entry with host numpy buffers (reference argument list)."""
+        import numpy as np
+
+        def np_ptr(a):
+            return None if a is None else a.ctypes.data_as(C.c_void_p)
+
+        q = np.ascontiguousarray(q, dtype=np.uint16)
+        k = None if k is None else np.ascontiguousarray(k, dtype=np.uint16)
+        v = None if v is None else np.ascontiguousarray(v, dtype=np.uint16)
+        kx = None if kx is None else np.ascontiguousarray(kx, dtype=np.uint8)
+        vx = None if vx is None else np.ascontiguousarray(vx, dtype=np.uint8)
+        out = np.zeros(max(n_q * dim, 1), dtype=np.float32)
+        check(lib().kvexp_hip_attention_decode_host(
+            self.h, order, np_ptr(q), np_ptr(k), np_ptr(v), np_ptr(kx), 0 if kx is None else kx.size, np_ptr(vx),
+            0 if vx is None else vx.size, np_ptr(out), n_q, dim, seq, threads, split))
+        return out[: n_q * dim]
+
+
+class Plan:
+    def __init__(self, ctx: Context, h, n_heads: int, n_q: int, dim: int, keep):
+        self.ctx, self.h, self.n_heads, self.n_q, self.dim, self._keep = ctx, h, n_heads, n_q, dim, keep
+
+    def run(self, q, out=None, lse=None, check_errors: bool = False, stream=None):
+        import torch
+
+        if out is None:
+            out = torch.empty(self.n_heads * self.n_q * self.dim, dtype=torch.float32, device=q.device)
+        check(lib().kvexp_hip_attention_run(self.h, _ptr(q), _ptr(out), _ptr(lse), 1 if check_errors else 0,
+                                            _stream(stream)))
+        return out
+
+    def status(self, stream=None) -> None:
+        check(lib().kvexp_hip_plan_status(self.h, _stream(stream)))
+
+    def close(self) -> None:
+        if getattr(self, "h", None):
+            lib().kvexp_hip_plan_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -1,0 +1,168 @@
+/* kvexp-amd: C ABI of the MI355X (gfx950) backend for kvexp's fused
+ * compressed-KV decode attention.
+ *
+ * Plain pointers and sizes only; no HIP or torch types cross this boundary
+ * (streams are passed as `void *` holding a hipStream_t, NULL = default
+ * stream). Every entry point returns a status code (0 = success) and never
+ * lets a C++ exception escape; kvexp_hip_last_error() returns the calling
+ * thread's message for the last failure, worded like the reference's
+ * exception text where the reference defines one.
+ *
+ * Device pointers are marked d_*. The caller owns every buffer. Entry points
+ * that take a stream are stream-ordered and do not synchronise unless stated.
+ *
+ * Reference interfaces each entry point replaces (paths in the reference):
+ *   kvexp_hip_attention_decode_host  kvexp::attention_decode
+ *                                    include/kvexp/attention.hpp:58-61,
+ *                                    src/dispatch.cpp:27-104 (Backend::Hip case)
+ *   kvexp_hip_attention_run          the per-thread range plugin
+ *                                    detail::range_<isa> (src/detail.hpp:9-19)
+ *                                    plus merge_state/finalize_state
+ *                                    (src/softmax.hpp:16-41), batched over heads
+ *   kvexp_hip_encode                 kvexp::encode_bf16 (include/kvexp/codec.hpp:45-46,
+ *                                    src/codec.cpp:39-164)
+ *   kvexp_hip_decode                 kvexp::decode_bf16 (include/kvexp/codec.hpp:48,
+ *                                    src/codec.cpp:166-174)
+ *   kvexp_hip_build_index            the header walk of XkvReader::seek / open_xkv
+ *                                    (include/kvexp/scan.hpp:94-123,192-218)
+ *   kvexp_hip_*_block_bytes          include/kvexp/bf16.hpp:39-49
+ */
+#ifndef KVEXP_HIP_H
+#define KVEXP_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ------------------------------------------------------------- status ---- */
+enum {
+    KVEXP_HIP_OK = 0,
+    KVEXP_HIP_INVALID_ARGUMENT = 1, /* reference: std::invalid_argument */
+    KVEXP_HIP_FORMAT_ERROR = 2,     /* reference: std::runtime_error (container, split) */
+    KVEXP_HIP_LOGIC_ERROR = 3,      /* reference: std::logic_error */
+    KVEXP_HIP_UNSUPPORTED = 4,      /* shape or option this build does not run */
+    KVEXP_HIP_DEVICE_ERROR = 5,     /* a HIP runtime call failed */
+    KVEXP_HIP_CAPACITY = 6          /* an output buffer is too small */
+};
+
+const char *kvexp_hip_status_string(int status);
+/* Message of the calling thread's last failure ("" after a success). */
+const char *kvexp_hip_last_error(void);
+/* Library version string and the gfx target it was built for. */
+const char *kvexp_hip_version(void);
+
+/* ------------------------------------------------------------ context ---- */
+/* A context binds one device and owns its workspace (partial softmax states,
+ * head/work descriptors, a status word). Contexts are independent; one
+ * context may be used from one host thread at a time. */
+typedef struct kvexp_hip_ctx kvexp_hip_ctx;
+
+int kvexp_hip_ctx_create(int device, kvexp_hip_ctx **out);
+int kvexp_hip_ctx_destroy(kvexp_hip_ctx *ctx);
+
+/* --------------------------------------------------------- size model ---- */
+/* include/kvexp/bf16.hpp:39-49 */
+int kvexp_hip_exp_payload_bytes(int n_tokens, int dim, int bits);
+int kvexp_hip_coded_block_bytes(int n_tokens, int dim, int bits, int n_escape);
+int kvexp_hip_raw_block_bytes(int n_tokens, int dim);
+/* Largest container encode_bf16 can emit for [seq, dim] (every block raw). */
+int64_t kvexp_hip_encode_bound(int seq, int dim, int block_tokens);
+int kvexp_hip_block_count(int seq, int block_tokens);
+
+/* ------------------------------------------------------- block index ---- */
+/* Host walk of a host-resident container: byte offset and first token of
+ * each block that a reader consuming `seq` tokens touches, plus one terminal
+ * entry (next byte offset, token count). Arrays hold capacity + 1 entries.
+ * Validation and messages follow parse_block (scan.hpp:28-66), including the
+ * eager parse of the header after the last block used (scan.hpp:144-151). */
+int kvexp_hip_build_index(const uint8_t *blob, size_t bytes, int dim, int seq, int64_t *offsets,
+                          int32_t *first_token, int capacity, int *n_blocks);
+
+/* ------------------------------------------------------------- codec ---- */
+/* Encodes d_kv [seq, dim] BF16 (token-major) into d_out, byte-identical to
+ * encode_bf16. d_out needs kvexp_hip_encode_bound() bytes. Writes the block
+ * index (n_blocks + 1 entries each) to d_offsets / d_first_token when they
+ * are non-NULL. The container size is written to *bytes_out (host) after a
+ * synchronisation of `stream` when bytes_out is non-NULL; it is also
+ * d_offsets[n_blocks] when d_offsets is given. */
+int kvexp_hip_encode(kvexp_hip_ctx *ctx, const uint16_t *d_kv, int seq, int dim, int block_tokens,
+                     uint8_t *d_out, size_t capacity, int64_t *d_offsets, int32_t *d_first_token,
+                     size_t *bytes_out, void *stream);
+
+/* Decodes seq tokens of a device container into d_out [seq, dim] BF16,
+ * bit-identical to decode_bf16. d_offsets / d_first_token is the block index
+ * (n_blocks + 1 entries) of that container. Synchronises `stream` and
+ * reports container format errors (bad header, escape overrun) when
+ * `check` is non-zero. */
+int kvexp_hip_decode(kvexp_hip_ctx *ctx, const uint8_t *d_blob, size_t bytes, const int64_t *d_offsets,
+                     const int32_t *d_first_token, int n_blocks, int seq, int dim, uint16_t *d_out,
+                     int check, void *stream);
+
+/* --------------------------------------------------------- attention ---- */
+/* Score order of the QK dot product (bit-for-bit with one reference backend):
+ *   KVEXP_HIP_ORDER_SCALAR: 8 strided FMA lanes then ((l0+l4)+(l1+l5))+((l2+l6)+(l3+l7)),
+ *                           as attention_scalar.cpp and attention_avx2.cpp;
+ *   KVEXP_HIP_ORDER_DPBF16: VDPBF16PS pairs (odd element first, DAZ/FTZ) over 32-element
+ *                           steps and a 16-lane pairwise tree, as attention_avx512.cpp. */
+enum { KVEXP_HIP_ORDER_SCALAR = 0, KVEXP_HIP_ORDER_DPBF16 = 1 };
+
+/* One KV head: either XKV containers with their device block indexes, or raw
+ * [seq, dim] BF16 arrays (exactly one of the two, for K and V alike). */
+typedef struct kvexp_hip_head {
+    const uint8_t *k_xkv, *v_xkv;             /* device containers, or NULL */
+    uint64_t k_bytes, v_bytes;
+    const int64_t *k_offsets, *v_offsets;     /* device block index (n_blocks + 1) */
+    const int32_t *k_first_token, *v_first_token;
+    int32_t k_n_blocks, v_n_blocks;
+    const uint16_t *k_raw, *v_raw;            /* device [seq, dim] BF16, or NULL */
+    int32_t seq;                              /* tokens attended (> 0) */
+    int32_t n_splits;                         /* sequence splits, as attention_decode's n_threads */
+} kvexp_hip_head;
+
+/* A plan fixes the heads, the split of each head and the kernel choice; it
+ * owns the device-side descriptors, so running it launches kernels and
+ * copies nothing from the host. Splits follow token_bounds
+ * (dispatch.cpp:17-23) over `split_tokens`-token tiles with
+ * min(max(1, n_splits), tiles) parts; XKV split starts must fall on block
+ * starts of both K and V (else "token split is not aligned to an encoded
+ * block"). Creating a plan reads the device first_token arrays (one
+ * synchronous copy per tensor). */
+typedef struct kvexp_hip_plan kvexp_hip_plan;
+
+int kvexp_hip_plan_create(kvexp_hip_ctx *ctx, const kvexp_hip_head *heads, int n_heads, int n_q, int dim,
+                          int split_tokens, int order, kvexp_hip_plan **out);
+int kvexp_hip_plan_destroy(kvexp_hip_plan *plan);
+/* Suggested n_splits for a head of `seq` tokens so that a plan over
+ * `n_heads` such heads fills the device (one wave group per split). */
+int kvexp_hip_suggest_splits(kvexp_hip_ctx *ctx, int n_heads, int seq, int split_tokens);
+
+/* Runs a plan: d_q is [n_heads, n_q, dim] BF16; d_out [n_heads, n_q, dim]
+ * FP32 is fully overwritten; d_lse (nullable) [n_heads, n_q] receives
+ * m + log(l) per query row. With `check` non-zero the call synchronises
+ * `stream` and reports container format errors found by the kernels. */
+int kvexp_hip_attention_run(kvexp_hip_plan *plan, const uint16_t *d_q, float *d_out, float *d_lse, int check,
+                            void *stream);
+/* Reads and clears the plan's status word (synchronises `stream`). */
+int kvexp_hip_plan_status(kvexp_hip_plan *plan, void *stream);
+
+/* The Backend::Hip case of attention_decode: the reference argument list
+ * with host pointers. Copies the inputs to the device, builds indexes and a
+ * plan with n_splits = n_threads, runs it and copies `out` back. */
+int kvexp_hip_attention_decode_host(kvexp_hip_ctx *ctx, int order, const uint16_t *q, const uint16_t *k_raw,
+                                    const uint16_t *v_raw, const uint8_t *k_xkv, size_t k_bytes,
+                                    const uint8_t *v_xkv, size_t v_bytes, float *out, int n_q, int dim, int seq,
+                                    int n_threads, int split_tokens);
+
+/* ------------------------------------------------------------ numerics ---- */
+/* d_y[i] = exp(d_x[i]) with the kernels' exp, which returns the bits of the
+ * reference's std::exp(float) (glibc 2.35 expf). No reference counterpart:
+ * it lets a caller check that function on its own. */
+int kvexp_hip_expf(kvexp_hip_ctx *ctx, const float *d_x, float *d_y, size_t n, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* KVEXP_HIP_H */

@@ -259,6 +259,32 @@ class Reference:
             0 if vx is None else vx.size, _p(out), n_q, dim, seq, threads, split))
         return out[: n_q * dim]
 
+    def attention_heads(self, backend, q, ks, vs, *, xkv: bool, n_q: int, dim: int, seq: int, split: int = 128,
+                        omp_threads: int = 1, out=None):
+        """The reference bench's model_heads scope: OpenMP over heads, one thread per head.
+        ks/vs: lists of uint16 arrays (raw) or uint8 containers (xkv). Returns out."""
+        be = BACKENDS[backend] if isinstance(backend, str) else int(backend)
+        L = self.L
+        if not hasattr(L, "_heads_typed"):
+            vp, i32 = C.c_void_p, C.c_int
+            L.kvexp_ref_attention_heads.argtypes = [i32, i32, i32, vp, vp, vp, vp, vp, vp, vp, vp, i32, i32, i32,
+                                                    i32]
+            L._heads_typed = True
+        H = len(ks)
+        kp = (C.c_void_p * H)(*[a.ctypes.data for a in ks])
+        vpp = (C.c_void_p * H)(*[a.ctypes.data for a in vs])
+        q = _u16(q)
+        if out is None:
+            out = np.zeros(H * n_q * dim, dtype=np.float32)
+        if xkv:
+            kb = np.array([a.size for a in ks], dtype=np.uint64)
+            vb = np.array([a.size for a in vs], dtype=np.uint64)
+            args = [None, None, C.cast(kp, C.c_void_p), _p(kb), C.cast(vpp, C.c_void_p), _p(vb)]
+        else:
+            args = [C.cast(kp, C.c_void_p), C.cast(vpp, C.c_void_p), None, None, None, None]
+        self._check(L.kvexp_ref_attention_heads(be, H, omp_threads, _p(q), *args, _p(out), n_q, dim, seq, split))
+        return out
+
 
 def reference_or_none():
     try:

@@ -16,6 +16,7 @@
 #include "kvexp/codec.hpp"
 
 #include <cstring>
+#include <omp.h>
 #include <stdexcept>
 #include <string>
 
@@ -93,6 +94,41 @@ int kvexp_ref_attention(int backend, const uint16_t *q, const uint16_t *k_raw, c
         }
         kvexp::attention_decode(be, q, k_raw, v_raw, k_xkv, k_bytes, v_xkv, v_bytes, out, n_q, dim,
                                 seq, n_threads, split_tokens);
+    });
+}
+
+// The reference bench's `model_heads` scope (src/bench.cpp:711-728): OpenMP over
+// independent KV heads, each head attention_decode with one thread. Head h
+// reads q + h*n_q*dim and writes out + h*n_q*dim; XKV inputs when k_xkv is set.
+int kvexp_ref_attention_heads(int backend, int n_heads, int omp_threads, const uint16_t *q,
+                              const uint16_t *const *k_raw, const uint16_t *const *v_raw,
+                              const uint8_t *const *k_xkv, const uint64_t *k_bytes,
+                              const uint8_t *const *v_xkv, const uint64_t *v_bytes, float *out, int n_q,
+                              int dim, int seq, int split_tokens) {
+    return guarded([&] {
+        kvexp::Backend be = backend == 2 ? kvexp::Backend::Avx512Bf16
+                                         : (backend == 1 ? kvexp::Backend::Avx2 : kvexp::Backend::Scalar);
+        int failed = 0;
+        omp_set_dynamic(0);
+#pragma omp parallel for schedule(static) num_threads(omp_threads)
+        for (int h = 0; h < n_heads; ++h) {
+            const size_t qo = size_t(h) * size_t(n_q) * size_t(dim);
+            try {
+                if (k_xkv != nullptr) {
+                    kvexp::attention_decode(be, q + qo, nullptr, nullptr, k_xkv[h], k_bytes[h], v_xkv[h],
+                                            v_bytes[h], out + qo, n_q, dim, seq, 1, split_tokens);
+                } else {
+                    kvexp::attention_decode(be, q + qo, k_raw[h], v_raw[h], nullptr, 0, nullptr, 0, out + qo,
+                                            n_q, dim, seq, 1, split_tokens);
+                }
+            } catch (...) {
+#pragma omp atomic write
+                failed = 1;
+            }
+        }
+        if (failed) {
+            throw std::runtime_error("kvexp_ref_attention_heads: a head failed");
+        }
     });
 }
 

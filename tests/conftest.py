@@ -5,7 +5,8 @@ import numpy as np
 import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-for p in (ROOT, os.path.join(ROOT, "oracle"), os.path.join(ROOT, "tests")):
+for p in (ROOT, os.path.join(ROOT, "oracle"), os.path.join(ROOT, "tests"),
+          os.path.join(ROOT, "compressed-kv-attention_amd")):
     if p not in sys.path:
         sys.path.insert(0, p)
 
@@ -50,3 +51,32 @@ def bits_equal(a: np.ndarray, b: np.ndarray) -> bool:
         return False
     na, nb = np.isnan(a), np.isnan(b)
     return bool(np.array_equal(na, nb) and np.array_equal(a[~na].view(np.uint32), b[~nb].view(np.uint32)))
+
+
+@pytest.fixture(scope="session")
+def ctx():
+    """A kvexp_amd context on cuda:0 (GPU tests only)."""
+    import torch
+
+    import kvexp_amd
+
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    c = kvexp_amd.Context(0)
+    yield c
+    torch.cuda.synchronize()
+    c.close()
+
+
+def say(*a):
+    """Progress line that names the case before a GPU step (flushed)."""
+    print("[gpu-case]", *a, flush=True)
+
+
+def to_dev(a, dtype=None):
+    import torch
+
+    t = torch.from_numpy(np.ascontiguousarray(a))
+    if dtype is not None:
+        t = t.view(dtype)
+    return t.to("cuda:0")

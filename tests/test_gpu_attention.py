@@ -1,0 +1,188 @@
+"""GPU fused decode attention (kvexp_hip_attention_run and the Backend::Hip host
+entry) against the reference.
+
+Parity, as stated for this path:
+  (2) XKV and raw GPU results are bit-identical (same kernel order).
+  (3) FP32 outputs match the reference scalar/AVX2 path (KVEXP_HIP_ORDER_SCALAR)
+      and AVX-512 path (KVEXP_HIP_ORDER_DPBF16) within max relative error
+      1e-5 per element. The kernels repeat the reference's operations one for
+      one, so for the same split these tests assert bit equality, which
+      implies the 1e-5 bound (asserted separately as well).
+Expected values come from the reference's golden outputs (tests/golden) and
+from the oracle, which is pinned to the compiled reference.
+"""
+import numpy as np
+import pytest
+
+from conftest import bits_equal, say, to_dev
+from kvdata import bf16_from_f32, random_kv
+
+pytestmark = pytest.mark.gpu
+
+ORDER = {"scalar": 0, "avx2": 0, "avx512": 1}
+REL_TOL = 1e-5
+
+
+def max_rel_err(got, want) -> float:
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    both_nan = np.isnan(got) & np.isnan(want)
+    same_inf = np.isinf(got) & np.isinf(want) & (np.sign(got) == np.sign(want))
+    ok = both_nan | same_inf
+    d = np.abs(got - want)
+    denom = np.maximum(np.abs(want), np.finfo(np.float32).tiny)
+    rel = np.where(ok, 0.0, d / denom)
+    rel = np.where(np.isnan(rel), np.inf, rel)
+    return float(rel.max()) if rel.size else 0.0
+
+
+def run_gpu(ctx, order, q, heads_np, n_q, dim, split, xkv, with_lse=False):
+    """heads_np: list of dicts (k, v uint16, seq, splits); returns out (and lse)."""
+    import torch
+
+    block = split
+    heads = []
+    for h in heads_np:
+        if xkv:
+            kx = ctx.encode(to_dev(h["k"], torch.int16), h["seq"], dim, h.get("block", block))
+            vx = ctx.encode(to_dev(h["v"], torch.int16), h["seq"], dim, h.get("block", block))
+            heads.append(dict(kx=kx, vx=vx, seq=h["seq"], splits=h["splits"]))
+        else:
+            heads.append(dict(k=to_dev(h["k"], torch.int16), v=to_dev(h["v"], torch.int16), seq=h["seq"],
+                              splits=h["splits"]))
+    plan = ctx.plan(heads, n_q, dim, split, order)
+    dq = to_dev(q, torch.int16)
+    lse = torch.empty(len(heads) * n_q, dtype=torch.float32, device="cuda:0") if with_lse else None
+    out = plan.run(dq, lse=lse, check_errors=True)
+    res = out.cpu().numpy()
+    plan.close()
+    return (res, lse.cpu().numpy()) if with_lse else res
+
+
+def test_golden_outputs(ctx, golden):
+    """Every reference golden output (scalar, AVX2, AVX-512; thread counts as
+    splits), from raw and from XKV inputs."""
+    z, man = golden
+    for c in man["attn"]:
+        n = c["name"]
+        q, k, v = z[f"attn/{n}/q"], z[f"attn/{n}/k"], z[f"attn/{n}/v"]
+        for be in c["backends"]:
+            for th in c["threads"]:
+                say("golden attention", n, be, th)
+                want = z[f"attn/{n}/{be}/t{th}"]
+                heads = [dict(k=k, v=v, seq=c["seq"], splits=th)]
+                for xkv in (False, True):
+                    got = run_gpu(ctx, ORDER[be], q, heads, c["n_q"], c["dim"], c["block"], xkv)
+                    assert bits_equal(got, want), (n, be, th, xkv)
+                    assert max_rel_err(got, want) <= REL_TOL
+
+
+def _case(rng, trial):
+    dim = int(rng.choice([8, 16, 32, 64, 96, 128, 192, 256]))
+    n_q = int(rng.choice([1, 2, 4, 7, 8, 11, 16]))
+    seq = int(rng.integers(1, 1400))
+    blocks = [b for b in (16, 64, 100, 128, 255) if b * dim <= 65535]
+    block = int(rng.choice(blocks))
+    kind = trial % 4
+    if kind == 0:
+        k = random_kv(rng, seq, dim, spread_lo=-6, spread_hi=4, outliers=min(2, dim))
+    elif kind == 1:
+        x = rng.uniform(1.0, 7.9, seq * dim) * np.where(rng.random(seq * dim) < .5, -1, 1)
+        k = bf16_from_f32(x.astype(np.float32) * 0.25)
+    elif kind == 2:
+        k = rng.integers(0, 65536, seq * dim, dtype=np.uint16)
+        k[(k & 0x7F80) == 0x7F80] &= 0x3FFF
+        k = bf16_from_f32(np.clip(np.nan_to_num((k.astype(np.uint32) << 16).view(np.float32)), -8, 8))
+    else:
+        k = random_kv(rng, seq, dim, specials=True, wide=True)
+    v = random_kv(rng, seq, dim, sigma=0.5, specials=trial % 5 == 0)
+    q = random_kv(rng, n_q, dim, spread_lo=-1, spread_hi=1)
+    splits = int(rng.integers(1, 9))
+    return dim, n_q, seq, block, q, k, v, splits
+
+
+def test_random_against_oracle(ctx, oracle):
+    rng = np.random.default_rng(2024)
+    for trial in range(48):
+        dim, n_q, seq, block, q, k, v, splits = _case(rng, trial)
+        for be in ("scalar", "avx512"):
+            if be == "avx512" and dim % 32:
+                continue
+            say("random attention", trial, be, dict(dim=dim, n_q=n_q, seq=seq, block=block, splits=splits))
+            want = oracle.attention(be, q, k, v, n_q=n_q, dim=dim, seq=seq, threads=splits, split=block)
+            heads = [dict(k=k, v=v, seq=seq, splits=splits)]
+            raw = run_gpu(ctx, ORDER[be], q, heads, n_q, dim, block, False)
+            xkv = run_gpu(ctx, ORDER[be], q, heads, n_q, dim, block, True)
+            assert bits_equal(raw, xkv), (trial, be)
+            assert bits_equal(raw, want), (trial, be, max_rel_err(raw, want))
+
+
+def test_many_heads_variable_length(ctx, oracle):
+    """A batched plan over heads of different lengths and split counts (the
+    shape of BASELINE config 3, shortened), with LSE."""
+    rng = np.random.default_rng(77)
+    dim, n_q, block = 64, 7, 128
+    heads = []
+    for h in range(20):
+        seq = int(round(np.exp(rng.uniform(np.log(40), np.log(3000)))))
+        heads.append(dict(k=random_kv(rng, seq, dim, spread_lo=-6, spread_hi=4, outliers=2),
+                          v=random_kv(rng, seq, dim, sigma=0.5), seq=seq, splits=int(rng.integers(1, 12))))
+    q = random_kv(rng, len(heads) * n_q, dim)
+    say("variable-length plan", len(heads))
+    want, lse_want = oracle.attention_heads("scalar", q, [dict(k=h["k"], v=h["v"], seq=h["seq"], threads=h["splits"])
+                                                          for h in heads], n_q=n_q, dim=dim, split=block,
+                                            with_lse=True)
+    raw, lse_raw = run_gpu(ctx, 0, q, heads, n_q, dim, block, False, with_lse=True)
+    xkv, lse_x = run_gpu(ctx, 0, q, heads, n_q, dim, block, True, with_lse=True)
+    assert bits_equal(raw, xkv) and bits_equal(lse_raw, lse_x)
+    assert bits_equal(raw, want)
+    # LSE = m + log(l): no reference output; device log vs glibc logf within 2 ulp-ish
+    assert np.allclose(lse_raw, lse_want, rtol=1e-6, atol=1e-6)
+
+
+def test_host_entry_backend_hip(ctx, oracle, golden):
+    """kvexp_hip_attention_decode_host: the attention_decode argument list with
+    host pointers (the Backend::Hip case of dispatch.cpp)."""
+    z, man = golden
+    c = next(c for c in man["attn"] if c["name"].startswith("qwen_like"))
+    n = c["name"]
+    q, k, v = z[f"attn/{n}/q"], z[f"attn/{n}/k"], z[f"attn/{n}/v"]
+    kx = oracle.encode(k, c["seq"], c["dim"], c["block"])
+    vx = oracle.encode(v, c["seq"], c["dim"], c["block"])
+    for be in ("scalar", "avx512"):
+        for th in c["threads"]:
+            say("host entry", be, th)
+            kw = dict(n_q=c["n_q"], dim=c["dim"], seq=c["seq"], threads=th, split=c["block"])
+            want = z[f"attn/{n}/{be}/t{th}"]
+            assert bits_equal(ctx.attention_decode_host(ORDER[be], q, k, v, **kw), want)
+            assert bits_equal(ctx.attention_decode_host(ORDER[be], q, kx=kx, vx=vx, **kw), want)
+
+
+def test_split_and_argument_errors(ctx, oracle):
+    import kvexp_amd
+
+    rng = np.random.default_rng(8)
+    q, k, v = random_kv(rng, 2, 64), random_kv(rng, 300, 64), random_kv(rng, 300, 64)
+    kx, vx = oracle.encode(k, 300, 64, 128), oracle.encode(v, 300, 64, 128)
+
+    def err(fn):
+        with pytest.raises(kvexp_amd.KvexpHipError) as ei:
+            fn()
+        return ei.value.kind, ei.value.msg
+
+    H = ctx.attention_decode_host
+    say("error paths")
+    assert err(lambda: H(0, q, kx=kx, vx=vx, n_q=2, dim=64, seq=300, split=100, threads=2)) == (
+        "runtime_error", "token split is not aligned to an encoded block")
+    assert err(lambda: H(0, q, kx=kx, vx=vx, n_q=2, dim=64, seq=400)) == ("runtime_error", "xkv ran out of tokens")
+    assert err(lambda: H(0, q, k, v, kx=kx, vx=vx, n_q=2, dim=64, seq=300)) == (
+        "invalid_argument", "attention_decode: pass raw K and V or xkv K and V, not both")
+    assert err(lambda: H(0, q, k, v, n_q=2, dim=60, seq=300)) == ("invalid_argument", "scalar attention: bad shape")
+    assert err(lambda: H(1, q, k, v, n_q=2, dim=48, seq=300)) == (
+        "invalid_argument", "avx512 attention: head_dim must be a multiple of 32")
+    assert err(lambda: H(0, q, k, v, n_q=0, dim=64, seq=300)) == ("invalid_argument", "attention_decode: bad argument")
+    assert err(lambda: H(0, q, kx=kx[:-40], vx=vx, n_q=2, dim=64, seq=300)) == (
+        "runtime_error", "truncated coded xkv block")
+    # one thread reads from token 0: any split works
+    out = H(0, q, kx=kx, vx=vx, n_q=2, dim=64, seq=300, split=100, threads=1)
+    assert bits_equal(out, oracle.attention("scalar", q, k, v, n_q=2, dim=64, seq=300, split=100, threads=1))
