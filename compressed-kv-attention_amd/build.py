@@ -28,6 +28,7 @@ ARCH = "gfx950"
 SOURCES = [
     "csrc/hip/codec_kernels.hip",
     "csrc/hip/attention_kernels.hip",
+    "csrc/hip/attention_wave.hip",
     "csrc/host/kvexp_hip_api.cpp",
     "csrc/host/kvexp_cpp_api.cpp",
 ]

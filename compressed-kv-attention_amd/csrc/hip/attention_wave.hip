@@ -1,0 +1,591 @@
+// gfx950 fused decode attention, head_dim 64, scalar/AVX2 score order:
+// one wave64 per split, no workgroup barriers on the hot path.
+//
+// A split [tok_begin, tok_end) of one KV head is processed in chunks of up to
+// 64 tokens that never cross a K or V block. Per chunk the wave:
+//   1. decodes the chunk's K rows (lane = token) from registers loaded one
+//      chunk ahead into a BF16 tile in its own LDS slice: a coded element is
+//      (sm & 0x80) << 8 | (base + code) << 7 | (sm & 0x7F), built two at a
+//      time with v_perm_b32 / v_lshl_add_u32 / v_bfi_b32 on packed pairs;
+//      escape words are then written over their elements using the plan's
+//      escape-position index, so no sentinel search runs here;
+//   2. computes the G scores of each token (lane = token) in the reference
+//      order: 8 strided FMA chains over the 64 channels, q widened from BF16
+//      scalar registers, then the ((l0+l4)+(l1+l5))+((l2+l6)+(l3+l7)) tree;
+//   3. decodes the V rows into the same tile;
+//   4. turns scores into alpha = exp(m_prev - m), e = exp(s - m) with an
+//      exact DPP prefix maximum and the glibc-identical expf (table in LDS);
+//   5. folds the chunk's tokens in order (lane = channel):
+//      acc = fma(e, v, acc * alpha), l = fma(l, alpha, e); alpha == 1 for a
+//      whole chunk skips the multiply, which is exact.
+// Splits of a head are merged left to right (merge_state order) by the wave
+// that finishes last, chosen with an atomic counter per head; the merge is
+// followed by out = acc * (1/l).
+//
+// Every float operation is the reference's (attention_scalar.cpp:19-85,
+// softmax.hpp:8-41, dispatch.cpp:98-103), so outputs equal the reference's
+// bits for the same split, and the raw instantiation equals the XKV one.
+#include "kvexp_device.h"
+#include "kvexp_types.h"
+
+namespace kvexp_dev {
+namespace wave {
+
+constexpr int kD = 64;          // head_dim of this kernel
+constexpr int kChunk = 64;      // tokens per chunk (one per lane)
+constexpr int kTileStride = 144; // bytes per tile row: 64 BF16 + 16 (conflict-free 16-byte rows)
+constexpr int kWavesPerWg = 4;
+constexpr int kSlotQ = 8;       // partial-state slot: m[8], l[8], acc[8][64]
+
+struct WaveLds {
+    uint8_t tile[kChunk * kTileStride];
+    float e[kChunk][8];
+    float a[kChunk][8];
+    uint32_t bp[kD / 2]; // base pair words of the block being decoded
+};
+
+struct WgLds {
+    uint64_t exptab[32];
+    WaveLds w[kWavesPerWg];
+};
+
+// Position of one tensor inside its XKV container (all fields wave-uniform).
+struct Cursor {
+    const uint8_t *blob;
+    uint64_t bytes;
+    const int64_t *offs;
+    const int32_t *first;
+    const int32_t *esc0;
+    const uint16_t *escpos;
+    const uint8_t *blk; // current block
+    int b, t0, t1;      // block index and its token range
+    int mode, ntok, nesc;
+    int eb;             // index of the block's first escape in escpos
+    int ecur;           // escapes of this block already written
+};
+
+// Enters block b: reads its 8-byte header with aligned (scalar) dword loads
+// and checks it against the index (dim, token count, mode, payload inside the
+// container, escape count). Every block of a valid container is >= 12 bytes.
+__device__ __forceinline__ uint32_t open_block(Cursor &c, int b) {
+    c.b = b;
+    c.t0 = c.first[b];
+    c.t1 = c.first[b + 1];
+    const int64_t off = c.offs[b];
+    c.blk = c.blob + off;
+    c.mode = 0;
+    c.ntok = 0;
+    c.nesc = 0;
+    c.eb = c.esc0[b];
+    c.ecur = 0;
+    if (off < 0 || uint64_t(off) + 12u > c.bytes) return kStHeader;
+    const uintptr_t a = reinterpret_cast<uintptr_t>(c.blk);
+    const uint32_t *w = reinterpret_cast<const uint32_t *>(a & ~uintptr_t(3));
+    const uint32_t sh = uint32_t(a & 3u) * 8u;
+    const uint32_t w0 = w[0], w1 = w[1], w2 = w[2];
+    const uint32_t d0 = uint32_t(((uint64_t(w1) << 32) | w0) >> sh);
+    const uint32_t d1 = uint32_t(((uint64_t(w2) << 32) | w1) >> sh);
+    const int mode = int(d0 & 0xFFu), ntok = int((d0 >> 8) & 0xFFu), nesc = int(d0 >> 16);
+    const int dim = int(d1 & 0xFFFFu);
+    c.mode = mode;
+    c.ntok = ntok;
+    c.nesc = mode == 0 ? 0 : nesc;
+    if (dim != kD || ntok <= 0) return kStHeader;
+    if (ntok != c.t1 - c.t0) return kStIndex;
+    const int64_t sz = block_bytes(mode, ntok, nesc, kD);
+    if (sz < 0) return kStMode;
+    if (uint64_t(off) + uint64_t(sz) > c.bytes) return kStTruncated;
+    if (c.esc0[b + 1] - c.eb != c.nesc) return kStIndex;
+    return 0u;
+}
+
+// Global-memory loads (address space 1, so they are issued as global_load_*
+// and counted on the vector-memory counter only). Addresses need only 2-byte
+// alignment: gfx950 under ROCm runs in unaligned-access mode.
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4), aligned(2)));
+typedef const __attribute__((address_space(1))) u32x4 g_u32x4;
+typedef const __attribute__((address_space(1))) uint16_t g_u16;
+
+// Constant address space (4): uniform loads from it are scalar loads.
+typedef float f8 __attribute__((ext_vector_type(8)));
+typedef const __attribute__((address_space(4))) f8 c_f8;
+
+__device__ __forceinline__ uint4 ld16(const uint8_t *p) {
+    const u32x4 v = *(g_u32x4 *)(p);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint32_t ldu16(const uint8_t *p) { return *(g_u16 *)(p); }
+
+// Loads rows [r0 + lane] of the cursor's block (lanes < rows) into R.
+__device__ __forceinline__ void load_rows(const Cursor &c, int r0, int rows, uint4 (&R)[8]) {
+    const int lane = lane_id();
+    if (lane >= rows) return;
+    const int r = r0 + lane;
+    const uint8_t *p = c.blk + 8;
+    if (c.mode == 0) {
+        const uint8_t *row = p + size_t(r) * (2 * kD);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) R[i] = ld16(row + 16 * i);
+        return;
+    }
+    const uint8_t *sm = p + kD + size_t(r) * kD;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) R[i] = ld16(sm + 16 * i);
+    const uint8_t *codes = p + kD + size_t(c.ntok) * kD;
+    if (c.mode == 4) {
+        R[4] = ld16(codes + size_t(r) * (kD / 2));
+        R[5] = ld16(codes + size_t(r) * (kD / 2) + 16);
+    } else {
+        R[4] = ld16(codes + size_t(r) * (kD / 4));
+    }
+}
+
+__device__ __forceinline__ uint32_t comp(const uint4 &v, int i) {
+    return i == 0 ? v.x : (i == 1 ? v.y : (i == 2 ? v.z : v.w));
+}
+
+// Base pair words of the block into LDS: word p = base[2p] << 7 | base[2p+1] << 23
+// (lane p < 32 builds word p).
+__device__ __forceinline__ void base_pairs(const uint8_t *base, uint32_t *bp) {
+    const int lane = lane_id();
+    if (lane < kD / 2) {
+        const uint32_t two = ldu16(base + 2 * lane);
+        bp[lane] = ((two & 0xFFu) << 7) | ((two >> 8) << 23);
+    }
+}
+
+// One BF16 pair from two sign/mantissa bytes (positions lb, lb+1 of sw), two
+// codes (byte p of lo and hi) and the channel pair's base word.
+__device__ __forceinline__ uint32_t pair4(uint32_t sw, int lb, uint32_t lo, uint32_t hi, int p, uint32_t bpw) {
+    const uint32_t code16 = __builtin_amdgcn_perm(hi, lo, 0x0c000c00u | (uint32_t(4 + p) << 16) | uint32_t(p));
+    const uint32_t t = (code16 << 7) + bpw; // exponent pair at bits 14:7 / 30:23
+    const uint32_t hb = uint32_t(lb + 1);
+    const uint32_t s = __builtin_amdgcn_perm(sw, sw, (hb << 24) | (hb << 16) | (uint32_t(lb) << 8) | uint32_t(lb));
+    return (s & 0x807F807Fu) | (t & ~0x807F807Fu);
+}
+
+// Decodes the lane's row held in R (cursor's block mode) into its tile row.
+__device__ __forceinline__ void decode_row(const Cursor &c, const uint4 (&R)[8], const uint32_t *bp, uint8_t *row) {
+    uint4 *dst = reinterpret_cast<uint4 *>(row);
+    if (c.mode == 0) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) dst[i] = R[i];
+        return;
+    }
+#pragma unroll
+    for (int dg = 0; dg < 8; ++dg) {
+        const uint32_t s0 = comp(R[dg >> 1], (dg & 1) * 2);
+        const uint32_t s1 = comp(R[dg >> 1], (dg & 1) * 2 + 1);
+        uint32_t lo, hi;
+        if (c.mode == 4) {
+            const uint32_t cw = comp(R[4 + (dg >> 2)], dg & 3);
+            lo = cw & 0x0F0F0F0Fu;
+            hi = (cw >> 4) & 0x0F0F0F0Fu;
+        } else {
+            // 16 two-bit codes per dword; octet dg uses 16 bits.
+            const uint32_t cw = comp(R[4], dg >> 1) >> (16 * (dg & 1));
+            // byte p of lo/hi: codes 2p and 2p+1 of the octet
+            lo = (cw & 3u) | (((cw >> 4) & 3u) << 8) | (((cw >> 8) & 3u) << 16) | (((cw >> 12) & 3u) << 24);
+            hi = ((cw >> 2) & 3u) | (((cw >> 6) & 3u) << 8) | (((cw >> 10) & 3u) << 16) | (((cw >> 14) & 3u) << 24);
+        }
+        const uint4 b4 = *reinterpret_cast<const uint4 *>(bp + 4 * dg);
+        uint4 o;
+        o.x = pair4(s0, 0, lo, hi, 0, b4.x);
+        o.y = pair4(s0, 2, lo, hi, 1, b4.y);
+        o.z = pair4(s1, 0, lo, hi, 2, b4.z);
+        o.w = pair4(s1, 2, lo, hi, 3, b4.w);
+        dst[dg] = o;
+    }
+}
+
+// Writes the escape words of rows [r0, r0 + n) of the cursor's block over
+// their elements in the tile (positions ascend, so they form a prefix of the
+// block's remaining escapes).
+__device__ __forceinline__ void patch_escapes(Cursor &c, int r0, int n, uint8_t *tile) {
+    if (c.nesc == 0) return;
+    const int lane = lane_id();
+    const int lim = (r0 + n) * kD;
+    const uint8_t *esc = c.blk + 8 + kD + size_t(c.ntok) * kD + exp_payload_bytes(c.ntok, kD, c.mode);
+    while (true) {
+        const int k = c.ecur + lane;
+        int pos = 0x7fffffff;
+        if (k < c.nesc) pos = int(*(g_u16 *)(c.escpos + c.eb + k));
+        const bool in = pos < lim;
+        const int cnt = __popcll(__ballot(in));
+        const int row = pos / kD - r0, col = pos % kD;
+        if (in && row >= 0) { // row < n by the sort order; row >= 0 guards a damaged index
+            const uint32_t val = ldu16(esc + 2 * size_t(k));
+            *reinterpret_cast<uint16_t *>(tile + row * kTileStride + col * 2) = uint16_t(val);
+        }
+        c.ecur += cnt;
+        if (cnt < kWave) break;
+    }
+}
+
+__device__ __forceinline__ void wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+}
+
+__device__ __forceinline__ float lo_f32(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float hi_f32(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
+
+// Scores of the lane's tile row for G query rows (scalar/AVX2 order).
+// qa is the address of the head's query rows widened to FP32 ([8][64],
+// written by q_widen_kernel before this launch). Stage st = dg * G + g
+// multiplies channels 8dg..8dg+7 of row g; its eight q values arrive by one
+// scalar load issued two stages earlier, whose address is tied (through an
+// empty asm) to that earlier stage's FMA results, so at most two stages of q
+// are live in scalar registers and no load is hoisted out of the chunk loop.
+template <int G>
+__device__ __forceinline__ void scores(const uint8_t *row, uint64_t qa, float (&s)[G]) {
+    constexpr int NS = 8 * G;
+    float c[G][8];
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) c[g][j] = 0.0f;
+    f8 qb[2];
+    qb[0] = *(const c_f8 *)(qa);
+    if (NS > 1) qb[1] = *(const c_f8 *)(qa + ((1 % G) * kD + 8 * (1 / G)) * 4);
+    float k[8];
+#pragma unroll
+    for (int st = 0; st < NS; ++st) {
+        const int dg = st / G, g = st % G;
+        if (g == 0) {
+            const uint4 kb = *reinterpret_cast<const uint4 *>(row + 16 * dg);
+            k[0] = lo_f32(kb.x); k[1] = hi_f32(kb.x); k[2] = lo_f32(kb.y); k[3] = hi_f32(kb.y);
+            k[4] = lo_f32(kb.z); k[5] = hi_f32(kb.z); k[6] = lo_f32(kb.w); k[7] = hi_f32(kb.w);
+        }
+        const f8 q = qb[st & 1];
+        c[g][0] = fmaf(q.s0, k[0], c[g][0]);
+        c[g][1] = fmaf(q.s1, k[1], c[g][1]);
+        c[g][2] = fmaf(q.s2, k[2], c[g][2]);
+        c[g][3] = fmaf(q.s3, k[3], c[g][3]);
+        c[g][4] = fmaf(q.s4, k[4], c[g][4]);
+        c[g][5] = fmaf(q.s5, k[5], c[g][5]);
+        c[g][6] = fmaf(q.s6, k[6], c[g][6]);
+        c[g][7] = fmaf(q.s7, k[7], c[g][7]);
+        if (st + 2 < NS) {
+            const int n2 = st + 2;
+            uint64_t a2 = qa + uint64_t(((n2 % G) * kD + 8 * (n2 / G)) * 4);
+            asm volatile("" : "+s"(a2), "+v"(c[g][0]), "+v"(c[g][1]), "+v"(c[g][2]), "+v"(c[g][3]), "+v"(c[g][4]),
+                         "+v"(c[g][5]), "+v"(c[g][6]), "+v"(c[g][7]));
+            qb[st & 1] = *(const c_f8 *)(a2);
+        }
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        const float a = (c[g][0] + c[g][4]) + (c[g][1] + c[g][5]);
+        const float b = (c[g][2] + c[g][6]) + (c[g][3] + c[g][7]);
+        s[g] = a + b;
+    }
+}
+
+// q32[h][g][d] = FP32 of query row q_row + g of device head h (rows >= n_q
+// left alone). One workgroup per device head.
+__global__ __launch_bounds__(256) void q_widen_kernel(const HeadDev *__restrict__ heads,
+                                                     const uint16_t *__restrict__ q_all, float *__restrict__ q32) {
+    const HeadDev hd = heads[blockIdx.x];
+    for (int i = int(threadIdx.x); i < hd.n_q * kD; i += 256)
+        q32[size_t(blockIdx.x) * kSlotQ * kD + i] = __uint_as_float(uint32_t(q_all[size_t(hd.q_row) * kD + i]) << 16);
+}
+
+template <int G, bool XKV>
+__global__ __launch_bounds__(kWavesPerWg * 64) void attn_wave_kernel(
+    const HeadDev *__restrict__ heads, const WorkItem *__restrict__ items, int n_items,
+    const float *__restrict__ q32_all, float *__restrict__ out_all, float *__restrict__ lse_all,
+    float *__restrict__ ws, int *__restrict__ counters, uint32_t *__restrict__ status) {
+    __shared__ WgLds L;
+    if (threadIdx.x < 32) L.exptab[threadIdx.x] = kvexp_exp2_32_table[threadIdx.x];
+    __syncthreads();
+
+    const int lane = lane_id();
+    const int w = int(threadIdx.x) >> 6;
+    const int item = __builtin_amdgcn_readfirstlane(int(blockIdx.x) * kWavesPerWg + w);
+    if (item >= n_items) return;
+    WaveLds &S = L.w[w];
+    const uint64_t *tab = L.exptab;
+    const WorkItem wi = items[item];
+    const HeadDev hd = heads[wi.head];
+    const float *q32 = q32_all + size_t(wi.head) * kSlotQ * kD;
+
+    float acc[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) acc[g] = 0.0f;
+    float mvec = -__builtin_inff(); // lane g < G holds m of query row g
+    float lvec = 0.0f;              // lane g < G holds l of query row g
+
+    uint32_t bad = 0;
+    Cursor kc{}, vc{};
+    uint4 RK[8], RV[8];
+    int t = wi.tok_begin;
+    if (XKV) {
+        kc.blob = hd.kx;
+        kc.bytes = hd.kbytes;
+        kc.offs = hd.koff;
+        kc.first = hd.kfirst;
+        kc.esc0 = hd.kesc0;
+        kc.escpos = hd.kescpos;
+        vc.blob = hd.vx;
+        vc.bytes = hd.vbytes;
+        vc.offs = hd.voff;
+        vc.first = hd.vfirst;
+        vc.esc0 = hd.vesc0;
+        vc.escpos = hd.vescpos;
+        bad |= open_block(kc, wi.kblk);
+        bad |= open_block(vc, wi.vblk);
+        if (kc.t0 != t || vc.t0 != t) bad |= kStIndex;
+        if (bad == 0u) {
+            load_rows(kc, 0, min(kChunk, min(kc.t1, wi.tok_end) - t), RK);
+            load_rows(vc, 0, min(kChunk, min(vc.t1, wi.tok_end) - t), RV);
+        }
+    } else {
+        const int rows = min(kChunk, wi.tok_end - t);
+        if (lane < rows) {
+            const uint8_t *kr = reinterpret_cast<const uint8_t *>(hd.kraw + size_t(t + lane) * kD);
+            const uint8_t *vr = reinterpret_cast<const uint8_t *>(hd.vraw + size_t(t + lane) * kD);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                RK[i] = ld16(kr + 16 * i);
+                RV[i] = ld16(vr + 16 * i);
+            }
+        }
+    }
+    uint8_t *my_row = S.tile + lane * kTileStride;
+
+    while (t < wi.tok_end && bad == 0u) {
+        int n = min(kChunk, wi.tok_end - t);
+        if (XKV) n = min(n, min(kc.t1 - t, vc.t1 - t));
+        const int tn = t + n;
+
+        // 1. K rows -> tile; prefetch the next chunk's K rows
+        if (XKV) {
+            if (kc.mode != 0) {
+                base_pairs(kc.blk + 8, S.bp);
+                wave_sync();
+            }
+            decode_row(kc, RK, S.bp, my_row);
+            wave_sync();
+            patch_escapes(kc, t - kc.t0, n, S.tile);
+            if (tn < wi.tok_end) {
+                if (tn >= kc.t1) bad |= open_block(kc, kc.b + 1);
+                if (bad == 0u) load_rows(kc, tn - kc.t0, min(kChunk, min(kc.t1, wi.tok_end) - tn), RK);
+            }
+        } else {
+            uint4 *dst = reinterpret_cast<uint4 *>(my_row);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) dst[i] = RK[i];
+            if (tn < wi.tok_end && lane < min(kChunk, wi.tok_end - tn)) {
+                const uint8_t *kr = reinterpret_cast<const uint8_t *>(hd.kraw + size_t(tn + lane) * kD);
+#pragma unroll
+                for (int i = 0; i < 8; ++i) RK[i] = ld16(kr + 16 * i);
+            }
+        }
+        wave_sync();
+
+        // 2. scores, lane = token (an opaque copy of the q address per chunk
+        // keeps the q loads inside the loop)
+        float s[G];
+        uint64_t qa = reinterpret_cast<uint64_t>(q32);
+        asm volatile("" : "+s"(qa));
+        scores<G>(my_row, qa, s);
+        wave_sync();
+
+        // 3. V rows -> tile; prefetch the next chunk's V rows
+        if (XKV) {
+            if (vc.mode != 0) {
+                base_pairs(vc.blk + 8, S.bp);
+                wave_sync();
+            }
+            decode_row(vc, RV, S.bp, my_row);
+            wave_sync();
+            patch_escapes(vc, t - vc.t0, n, S.tile);
+            if (tn < wi.tok_end) {
+                if (tn >= vc.t1) bad |= open_block(vc, vc.b + 1);
+                if (bad == 0u) load_rows(vc, tn - vc.t0, min(kChunk, min(vc.t1, wi.tok_end) - tn), RV);
+            }
+        } else {
+            uint4 *dst = reinterpret_cast<uint4 *>(my_row);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) dst[i] = RV[i];
+            if (tn < wi.tok_end && lane < min(kChunk, wi.tok_end - tn)) {
+                const uint8_t *vr = reinterpret_cast<const uint8_t *>(hd.vraw + size_t(tn + lane) * kD);
+#pragma unroll
+                for (int i = 0; i < 8; ++i) RV[i] = ld16(vr + 16 * i);
+            }
+        }
+
+        // 4. softmax coefficients, lane = token
+        bool resc = false;
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            const float mg = readlane_f32(mvec, g);
+            const float mi = fmaxf(wave_scan_max(s[g]), mg);
+            const float mp = wave_shift_up(mi, mg);
+            const float d = mp - mi;
+            float alpha = 1.0f;
+            if (!(d == 0.0f)) alpha = kvexp_expf_tab(d, tab);
+            const float e = kvexp_expf_tab(s[g] - mi, tab);
+            S.e[lane][g] = e;
+            S.a[lane][g] = alpha;
+            resc |= __ballot(lane < n && !(alpha == 1.0f)) != 0;
+            const float mn = readlane_f32(mi, n - 1);
+            mvec = lane == g ? mn : mvec;
+        }
+        wave_sync();
+
+        // 5. ordered fold, lane = channel
+        const uint16_t *vt = reinterpret_cast<const uint16_t *>(S.tile);
+        if (!resc) {
+#pragma unroll 4
+            for (int tok = 0; tok < n; ++tok) {
+                const float v = __uint_as_float(uint32_t(vt[tok * (kTileStride / 2) + lane]) << 16);
+                const float4 e0 = *reinterpret_cast<const float4 *>(&S.e[tok][0]);
+                const float4 e1 = *reinterpret_cast<const float4 *>(&S.e[tok][4]);
+                const float ev[8] = {e0.x, e0.y, e0.z, e0.w, e1.x, e1.y, e1.z, e1.w};
+#pragma unroll
+                for (int g = 0; g < G; ++g) acc[g] = fmaf(ev[g], v, acc[g]);
+                lvec = lvec + S.e[tok][lane & 7];
+            }
+        } else {
+#pragma unroll 2
+            for (int tok = 0; tok < n; ++tok) {
+                const float v = __uint_as_float(uint32_t(vt[tok * (kTileStride / 2) + lane]) << 16);
+                const float4 e0 = *reinterpret_cast<const float4 *>(&S.e[tok][0]);
+                const float4 e1 = *reinterpret_cast<const float4 *>(&S.e[tok][4]);
+                const float4 a0 = *reinterpret_cast<const float4 *>(&S.a[tok][0]);
+                const float4 a1 = *reinterpret_cast<const float4 *>(&S.a[tok][4]);
+                const float ev[8] = {e0.x, e0.y, e0.z, e0.w, e1.x, e1.y, e1.z, e1.w};
+                const float av[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+#pragma unroll
+                for (int g = 0; g < G; ++g) acc[g] = fmaf(ev[g], v, acc[g] * av[g]);
+                lvec = fmaf(lvec, S.a[tok][lane & 7], S.e[tok][lane & 7]);
+            }
+        }
+        wave_sync();
+        t = tn;
+    }
+    if (bad) {
+        if (lane == 0) atomicOr(status, bad);
+    }
+
+    // ---- epilogue --------------------------------------------------------------
+    const float mv = mvec;
+    if (hd.n_splits == 1) {
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            const float l = readlane_f32(lvec, g);
+            out_all[(size_t(hd.q_row) + g) * kD + lane] = acc[g] * (1.0f / l);
+        }
+        if (lse_all != nullptr && lane < G) lse_all[hd.q_row + lane] = mv + logf(lvec);
+        return;
+    }
+    const size_t slot_f = size_t(kSlotQ) * (kD + 2);
+    float *slot = ws + size_t(hd.ws_base + wi.split) * slot_f;
+    if (lane < G) {
+        slot[lane] = mv;
+        slot[kSlotQ + lane] = lvec;
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g) slot[2 * kSlotQ + g * kD + lane] = acc[g];
+    __threadfence();
+    int prev = 0;
+    if (lane == 0) prev = atomicAdd(&counters[wi.head], 1);
+    prev = __builtin_amdgcn_readfirstlane(prev);
+    if (prev != hd.n_splits - 1) return;
+
+    // ---- the last split of this head: ordered merge (softmax.hpp:16-30) -----
+    __threadfence();
+    const float *slots = ws + size_t(hd.ws_base) * slot_f;
+    float a[G], mf[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        a[g] = __builtin_nontemporal_load(slots + 2 * kSlotQ + g * kD + lane);
+        mf[g] = __builtin_nontemporal_load(slots + g);
+    }
+    float lf = lane < G ? __builtin_nontemporal_load(slots + kSlotQ + lane) : 0.0f;
+    for (int s0 = 1; s0 < hd.n_splits; s0 += kChunk) {
+        const int cnt = min(kChunk, hd.n_splits - s0);
+        // lane = split s0 + lane: running maximum and the two exponentials
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            const float ms = lane < cnt ? __builtin_nontemporal_load(slots + size_t(s0 + lane) * slot_f + g)
+                                        : -__builtin_inff();
+            const float mm = fmaxf(wave_scan_max(ms), mf[g]);
+            const float mprev = wave_shift_up(mm, mf[g]);
+            S.e[lane][g] = kvexp_expf_tab(mprev - mm, tab);
+            S.a[lane][g] = kvexp_expf_tab(ms - mm, tab);
+            mf[g] = readlane_f32(mm, cnt - 1);
+        }
+        wave_sync();
+        for (int j = 0; j < cnt; ++j) {
+            const float *sl = slots + size_t(s0 + j) * slot_f;
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                const float ab = __builtin_nontemporal_load(sl + 2 * kSlotQ + g * kD + lane);
+                a[g] = fmaf(a[g], S.e[j][g], ab * S.a[j][g]);
+            }
+            const float lb = lane < G ? __builtin_nontemporal_load(sl + kSlotQ + lane) : 0.0f;
+            lf = fmaf(lf, S.e[j][lane & 7], lb * S.a[j][lane & 7]);
+        }
+        wave_sync();
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        const float l = readlane_f32(lf, g);
+        out_all[(size_t(hd.q_row) + g) * kD + lane] = a[g] * (1.0f / l);
+    }
+    float mfl = -__builtin_inff();
+#pragma unroll
+    for (int g = 0; g < G; ++g) mfl = lane == g ? mf[g] : mfl;
+    if (lse_all != nullptr && lane < G) lse_all[hd.q_row + lane] = mfl + logf(lf);
+    if (lane == 0) counters[wi.head] = 0;
+}
+
+} // namespace wave
+} // namespace kvexp_dev
+
+namespace kvexp_launch {
+using namespace kvexp_dev;
+
+template <int G, bool XKV>
+static hipError_t launch_wave_g(const HeadDev *heads, const WorkItem *items, int n_items, const float *q,
+                                float *out, float *lse, float *ws, int *counters, uint32_t *status, hipStream_t s) {
+    const int grid = (n_items + wave::kWavesPerWg - 1) / wave::kWavesPerWg;
+    hipLaunchKernelGGL((wave::attn_wave_kernel<G, XKV>), dim3(grid), dim3(wave::kWavesPerWg * 64), 0, s, heads,
+                       items, n_items, q, out, lse, ws, counters, status);
+    return hipGetLastError();
+}
+
+template <bool XKV>
+static hipError_t launch_wave_x(int G, const HeadDev *heads, const WorkItem *items, int n_items, const float *q,
+                                float *out, float *lse, float *ws, int *counters, uint32_t *status, hipStream_t s) {
+    switch (G) {
+    case 1: return launch_wave_g<1, XKV>(heads, items, n_items, q, out, lse, ws, counters, status, s);
+    case 2: return launch_wave_g<2, XKV>(heads, items, n_items, q, out, lse, ws, counters, status, s);
+    case 3: return launch_wave_g<3, XKV>(heads, items, n_items, q, out, lse, ws, counters, status, s);
+    case 4: return launch_wave_g<4, XKV>(heads, items, n_items, q, out, lse, ws, counters, status, s);
+    case 5: return launch_wave_g<5, XKV>(heads, items, n_items, q, out, lse, ws, counters, status, s);
+    case 6: return launch_wave_g<6, XKV>(heads, items, n_items, q, out, lse, ws, counters, status, s);
+    case 7: return launch_wave_g<7, XKV>(heads, items, n_items, q, out, lse, ws, counters, status, s);
+    case 8: return launch_wave_g<8, XKV>(heads, items, n_items, q, out, lse, ws, counters, status, s);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+// Items with the same G; counters: one per device head, zero between runs.
+hipError_t q_widen(const HeadDev *heads, int n_heads, const uint16_t *q, float *q32, hipStream_t s) {
+    hipLaunchKernelGGL(wave::q_widen_kernel, dim3(n_heads), dim3(256), 0, s, heads, q, q32);
+    return hipGetLastError();
+}
+
+hipError_t attention_wave(bool xkv, int G, const HeadDev *heads, const WorkItem *items, int n_items,
+                          const float *q, float *out, float *lse, float *ws, int *counters, uint32_t *status,
+                          hipStream_t s) {
+    if (n_items <= 0) return hipSuccess;
+    return xkv ? launch_wave_x<true>(G, heads, items, n_items, q, out, lse, ws, counters, status, s)
+               : launch_wave_x<false>(G, heads, items, n_items, q, out, lse, ws, counters, status, s);
+}
+
+} // namespace kvexp_launch

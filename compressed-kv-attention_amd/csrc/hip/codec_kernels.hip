@@ -331,6 +331,84 @@ __global__ __launch_bounds__(kThreads) void encode_write_kernel(const uint16_t *
     if (threadIdx.x == 0 && carry != m.n_escape) atomicOr(status, kStEscape);
 }
 
+// -------------------------------------------------- escape-position index --
+// esc0[b] = escape words in blocks before b (raw blocks count 0), one
+// workgroup per tensor.
+__global__ __launch_bounds__(kThreads) void esc_start_kernel(const EscJob *__restrict__ jobs,
+                                                            uint32_t *__restrict__ status) {
+    __shared__ int scan_tmp[kWaves];
+    const EscJob j = jobs[blockIdx.x];
+    int carry = 0;
+    for (int r = 0; r < j.n_blocks; r += kThreads) {
+        const int b = r + int(threadIdx.x);
+        int ne = 0;
+        if (b < j.n_blocks) {
+            const int64_t off = j.offs[b];
+            if (off >= 0 && uint64_t(off) + 8u <= j.bytes) {
+                const BlockHdr h = read_hdr(j.blob + off);
+                ne = h.mode == 0 ? 0 : h.n_escape;
+            } else {
+                atomicOr(status, kStHeader);
+            }
+        }
+        int tot = 0;
+        const int excl = block_excl_scan<kWaves>(ne, scan_tmp, &tot);
+        if (b < j.n_blocks) j.esc0[b] = carry + excl;
+        carry += tot;
+    }
+    if (threadIdx.x == 0) j.esc0[j.n_blocks] = carry;
+}
+
+// Element index of every escape of one block (one workgroup per block;
+// `blocks` lists (job, block) pairs).
+__global__ __launch_bounds__(kThreads) void esc_pos_kernel(const EscJob *__restrict__ jobs,
+                                                          const int2 *__restrict__ blocks,
+                                                          uint32_t *__restrict__ status) {
+    __shared__ int scan_tmp[kWaves];
+    const int2 jb = blocks[blockIdx.x];
+    const EscJob j = jobs[jb.x];
+    const int b = jb.y;
+    const int dim = j.dim;
+    const int64_t off = j.offs[b];
+    if (off < 0 || uint64_t(off) + 8u > j.bytes) return;
+    const BlockHdr h = read_hdr(j.blob + off);
+    if (h.mode == 0 || h.n_escape == 0) return;
+    const int64_t sz = block_bytes(h.mode, h.n_tokens, h.n_escape, dim);
+    if (sz < 0 || h.dim != dim || uint64_t(off) + uint64_t(sz) > j.bytes) {
+        if (threadIdx.x == 0) atomicOr(status, kStTruncated);
+        return;
+    }
+    const bool four = h.mode == 4;
+    const uint8_t *codes = j.blob + off + 8 + dim + size_t(h.n_tokens) * size_t(dim);
+    uint16_t *pos = j.pos + j.esc0[b];
+    const int units = (h.n_tokens * dim) / 4;
+    int carry = 0;
+    for (int r = 0; r < units; r += kThreads) {
+        const int u = r + int(threadIdx.x);
+        const bool act = u < units;
+        uint32_t cw = 0;
+        int cnt = 0;
+        if (act) {
+            cw = four ? load_u16_any(codes + 2 * size_t(u)) : uint32_t(codes[u]);
+            cnt = four ? sentinels4(cw) : sentinels2(cw);
+        }
+        int tot = 0;
+        int rank = carry + block_excl_scan<kWaves>(cnt, scan_tmp, &tot);
+        carry += tot;
+        if (act && cnt) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const uint32_t code = four ? (cw >> (4 * k)) & 15u : (cw >> (2 * k)) & 3u;
+                if (code == (four ? 15u : 3u)) {
+                    if (rank < h.n_escape) pos[rank] = uint16_t(4 * u + k);
+                    ++rank;
+                }
+            }
+        }
+    }
+    if (threadIdx.x == 0 && carry != h.n_escape) atomicOr(status, kStEscape);
+}
+
 __global__ __launch_bounds__(256) void expf_kernel(const float *__restrict__ x, float *__restrict__ y, size_t n) {
     const size_t i = size_t(blockIdx.x) * 256u + threadIdx.x;
     if (i < n) y[i] = kvexp_expf(x[i]);
@@ -356,6 +434,18 @@ hipError_t encode(const uint16_t *kv, int seq, int dim, int bt, int n_blocks, En
     hipLaunchKernelGGL(encode_scan_kernel, dim3(1), dim3(1024), 0, s, meta, n_blocks, bt, seq, offs, first);
     hipLaunchKernelGGL(encode_write_kernel, dim3(n_blocks), dim3(kThreads), 0, s, kv, seq, dim, bt, meta, bases,
                        offs, out, status);
+    return hipGetLastError();
+}
+
+hipError_t esc_start(const EscJob *jobs, int n_jobs, uint32_t *status, hipStream_t s) {
+    if (n_jobs <= 0) return hipSuccess;
+    hipLaunchKernelGGL(esc_start_kernel, dim3(n_jobs), dim3(kThreads), 0, s, jobs, status);
+    return hipGetLastError();
+}
+
+hipError_t esc_pos(const EscJob *jobs, const int2 *blocks, int n_blocks, uint32_t *status, hipStream_t s) {
+    if (n_blocks <= 0) return hipSuccess;
+    hipLaunchKernelGGL(esc_pos_kernel, dim3(n_blocks), dim3(kThreads), 0, s, jobs, blocks, status);
     return hipGetLastError();
 }
 

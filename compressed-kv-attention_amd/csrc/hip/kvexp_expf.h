@@ -78,14 +78,11 @@ KVEXP_HD double kvexp_f64_from(uint64_t u) {
     return x;
 }
 
-#if defined(__HIPCC__)
 #define KVEXP_FMA64(a, b, c) __builtin_fma((a), (b), (c))
-#else
-#define KVEXP_FMA64(a, b, c) __builtin_fma((a), (b), (c))
-#endif
 
-/* The reduction and polynomial, for |x| < 88 (no special case). */
-KVEXP_HD float kvexp_expf_core(float x) {
+/* The reduction and polynomial, for |x| < 88 (no special case), reading
+ * 2^(i/32) from `tab` (a copy of kvexp_exp2_32_table, e.g. in LDS). */
+KVEXP_HD float kvexp_expf_core_tab(float x, const uint64_t *tab) {
     const double xd = (double)x;
 #if KVEXP_EXPF_FORM >= 2
     double kd = KVEXP_FMA64(KVEXP_EXP_INVLN2N, xd, KVEXP_EXP_SHIFT);
@@ -99,7 +96,7 @@ KVEXP_HD float kvexp_expf_core(float x) {
     kd -= KVEXP_EXP_SHIFT;
     const double r = z - kd;
 #endif
-    const uint64_t t = kvexp_exp2_32_table[ki & 31u] + (ki << 47);
+    const uint64_t t = tab[ki & 31u] + (ki << 47);
     const double s = kvexp_f64_from(t);
     const double r2 = r * r;
 #if KVEXP_EXPF_FORM >= 1
@@ -116,16 +113,21 @@ KVEXP_HD float kvexp_expf_core(float x) {
 
 /* expf with glibc's special cases: -inf -> +0, NaN/+inf -> x + x,
  * x > 0x1.62e42ep6 -> +inf, x < -0x1.9fe368p6 -> +0. */
-KVEXP_HD float kvexp_expf(float x) {
+KVEXP_HD float kvexp_expf_tab(float x, const uint64_t *tab) {
     const uint32_t ux = kvexp_f32_bits(x);
     const uint32_t abstop = (ux >> 20) & 0x7ffu;
-    if (abstop >= 0x42bu) { /* |x| >= 88, or x is Inf/NaN */
+    if (abstop >= 0x42bu) {
         if (ux == 0xff800000u) return 0.0f;
         if (abstop >= 0x7f8u) return x + x;
         if (x > 0x1.62e42ep6f) return __builtin_inff();
         if (x < -0x1.9fe368p6f) return 0.0f;
     }
-    return kvexp_expf_core(x);
+    return kvexp_expf_core_tab(x, tab);
 }
+
+/* The reduction and polynomial with the built-in table. */
+KVEXP_HD float kvexp_expf_core(float x) { return kvexp_expf_core_tab(x, kvexp_exp2_32_table); }
+
+KVEXP_HD float kvexp_expf(float x) { return kvexp_expf_tab(x, kvexp_exp2_32_table); }
 
 #endif /* KVEXP_EXPF_H */

@@ -22,12 +22,28 @@ struct HeadDev {
     const int64_t *koff, *voff;  // block byte offsets (n_blocks + 1)
     const int32_t *kfirst, *vfirst; // block first tokens (n_blocks + 1)
     const uint16_t *kraw, *vraw; // [seq, dim] BF16 (raw heads)
+    // Escape-position index (plan-owned, XKV heads of the wave kernel):
+    // block b's escape words are entries [esc0[b], esc0[b+1]) and escpos[k]
+    // is the element index (row * dim + channel) of entry k inside its block.
+    const int32_t *kesc0, *vesc0;
+    const uint16_t *kescpos, *vescpos;
     int32_t seq;
     int32_t n_splits;            // work items of this head, in merge order
     int32_t ws_base;             // first partial-state slot of this head
     int32_t q_row;               // first query row of this head in d_q / d_out
     int32_t n_q;                 // query rows of this head (<= 8)
     int32_t pad;
+};
+
+// One tensor (container + block index) for the escape-position index builders.
+struct EscJob {
+    const uint8_t *blob;
+    uint64_t bytes;
+    const int64_t *offs;
+    int32_t *esc0;      // out: n_blocks + 1 entries
+    uint16_t *pos;      // out: esc0[n_blocks] entries
+    int32_t n_blocks;
+    int32_t dim;
 };
 
 // One split: tokens [tok_begin, tok_end) of a head; for XKV the blocks that

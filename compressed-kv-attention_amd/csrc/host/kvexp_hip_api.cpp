@@ -32,6 +32,12 @@ hipError_t attention(bool xkv, int order, const HeadDev *heads, const WorkItem *
                      int dim, uint32_t *status, hipStream_t s);
 size_t attention_lds_bytes(int dim);
 hipError_t expf(const float *x, float *y, size_t n, hipStream_t s);
+hipError_t esc_start(const kvexp_dev::EscJob *jobs, int n_jobs, uint32_t *status, hipStream_t s);
+hipError_t esc_pos(const kvexp_dev::EscJob *jobs, const int2 *blocks, int n_blocks, uint32_t *status, hipStream_t s);
+hipError_t q_widen(const HeadDev *heads, int n_heads, const uint16_t *q, float *q32, hipStream_t s);
+hipError_t attention_wave(bool xkv, int G, const HeadDev *heads, const WorkItem *items, int n_items,
+                          const float *q, float *out, float *lse, float *ws, int *counters, uint32_t *status,
+                          hipStream_t s);
 } // namespace kvexp_launch
 
 namespace {
@@ -188,8 +194,12 @@ struct kvexp_hip_plan {
     kvexp_hip_ctx *ctx = nullptr;
     int n_heads = 0, n_q = 0, dim = 0, order = 0;
     bool xkv = false;
+    bool wave = false; // one-wave-per-split kernel (dim 64, scalar order)
     DevBuf heads, items, merge_ids, ws, status;
+    DevBuf counters, esc0, escpos, q32; // wave kernel: merge counters, escape-position index, FP32 q
     int n_dev_heads = 0, n_items = 0, n_merge = 0;
+    // wave kernel: items sorted by query-row count G; group_start[G] .. group_start[G+1]
+    int group_start[10] = {0};
 };
 
 namespace {
@@ -222,6 +232,64 @@ void check_status_word(uint32_t *d_status, hipStream_t s) {
         fail(KVEXP_HIP_FORMAT_ERROR, status_message(st));
     }
 }
+// Escape-position index of every XKV tensor of a plan: per block the first
+// escape's index (esc0) and per escape its element index inside the block.
+// Built on the device from the containers, once per plan; the device heads
+// of one user head share it.
+void build_escape_index(kvexp_hip_plan &p, const kvexp_hip_head *heads, int n_heads, int n_q, int dim,
+                        std::vector<HeadDev> &hv) {
+    std::vector<kvexp_dev::EscJob> jobs;
+    std::vector<size_t> e0_at;
+    size_t e0_total = 0;
+    for (int h = 0; h < n_heads; ++h) {
+        for (int kv = 0; kv < 2; ++kv) {
+            kvexp_dev::EscJob j{};
+            j.blob = kv ? heads[h].v_xkv : heads[h].k_xkv;
+            j.bytes = kv ? heads[h].v_bytes : heads[h].k_bytes;
+            j.offs = kv ? heads[h].v_offsets : heads[h].k_offsets;
+            j.n_blocks = kv ? heads[h].v_n_blocks : heads[h].k_n_blocks;
+            j.dim = dim;
+            e0_at.push_back(e0_total);
+            e0_total += size_t(j.n_blocks) + 1;
+            jobs.push_back(j);
+        }
+    }
+    p.esc0 = DevBuf(e0_total * sizeof(int32_t));
+    for (size_t i = 0; i < jobs.size(); ++i) jobs[i].esc0 = p.esc0.as<int32_t>() + e0_at[i];
+    DevBuf djobs(jobs.size() * sizeof(kvexp_dev::EscJob));
+    HIPX(hipMemcpy(djobs.p, jobs.data(), jobs.size() * sizeof(kvexp_dev::EscJob), hipMemcpyHostToDevice));
+    uint32_t *st = p.ctx->status.as<uint32_t>();
+    HIPX(kvexp_launch::esc_start(djobs.as<kvexp_dev::EscJob>(), int(jobs.size()), st, nullptr));
+    std::vector<int32_t> e0(e0_total);
+    HIPX(hipMemcpy(e0.data(), p.esc0.p, e0_total * sizeof(int32_t), hipMemcpyDeviceToHost));
+    size_t pos_total = 0;
+    std::vector<size_t> pos_at;
+    std::vector<int2> blocks;
+    for (size_t i = 0; i < jobs.size(); ++i) {
+        pos_at.push_back(pos_total);
+        pos_total += size_t(e0[e0_at[i] + size_t(jobs[i].n_blocks)]);
+        for (int b = 0; b < jobs[i].n_blocks; ++b) blocks.push_back(make_int2(int(i), b));
+    }
+    p.escpos = DevBuf(std::max<size_t>(pos_total, 1) * sizeof(uint16_t));
+    for (size_t i = 0; i < jobs.size(); ++i) jobs[i].pos = p.escpos.as<uint16_t>() + pos_at[i];
+    HIPX(hipMemcpy(djobs.p, jobs.data(), jobs.size() * sizeof(kvexp_dev::EscJob), hipMemcpyHostToDevice));
+    DevBuf dblocks(std::max<size_t>(blocks.size(), 1) * sizeof(int2));
+    HIPX(hipMemcpy(dblocks.p, blocks.data(), blocks.size() * sizeof(int2), hipMemcpyHostToDevice));
+    HIPX(kvexp_launch::esc_pos(djobs.as<kvexp_dev::EscJob>(), dblocks.as<int2>(), int(blocks.size()), st, nullptr));
+    HIPX(hipDeviceSynchronize());
+    check_status_word(st, nullptr);
+    const int per_head = (n_q + kMaxQPerLaunch - 1) / kMaxQPerLaunch;
+    for (int h = 0; h < n_heads; ++h) {
+        for (int c = 0; c < per_head; ++c) {
+            HeadDev &d = hv[size_t(h * per_head + c)];
+            d.kesc0 = jobs[size_t(2 * h)].esc0;
+            d.kescpos = jobs[size_t(2 * h)].pos;
+            d.vesc0 = jobs[size_t(2 * h + 1)].esc0;
+            d.vescpos = jobs[size_t(2 * h + 1)].pos;
+        }
+    }
+}
+
 } // namespace
 
 extern "C" {
@@ -388,8 +456,9 @@ int kvexp_hip_decode(kvexp_hip_ctx *ctx, const uint8_t *d_blob, size_t bytes, co
 int kvexp_hip_suggest_splits(kvexp_hip_ctx *ctx, int n_heads, int seq, int split_tokens) {
     if (ctx == nullptr || n_heads <= 0 || seq <= 0 || split_tokens <= 0) return 1;
     const int tiles = (seq + split_tokens - 1) / split_tokens;
-    // about two resident workgroups per CU over the whole launch
-    const int target = std::max(1, (2 * ctx->cu_count + n_heads - 1) / n_heads);
+    // about 12 resident single-wave splits per CU (the head_dim-64 kernel's
+    // LDS occupancy) over the whole launch
+    const int target = std::max(1, (12 * ctx->cu_count + n_heads - 1) / n_heads);
     return std::max(1, std::min(tiles, target));
 }
 
@@ -486,9 +555,24 @@ int kvexp_hip_plan_create(kvexp_hip_ctx *ctx, const kvexp_hip_head *heads, int n
             p->dim = dim;
             p->order = order;
             p->xkv = xkv;
+            p->wave = dim == 64 && order == KVEXP_HIP_ORDER_SCALAR;
             p->n_dev_heads = int(hv.size());
             p->n_items = int(items.size());
             p->n_merge = int(merge.size());
+            if (p->wave) {
+                // items grouped by G (one launch per distinct G)
+                std::stable_sort(items.begin(), items.end(), [&](const WorkItem &a, const WorkItem &b) {
+                    return hv[size_t(a.head)].n_q < hv[size_t(b.head)].n_q;
+                });
+                for (int G = 0; G <= 8; ++G)
+                    p->group_start[G + 1] =
+                        int(std::count_if(items.begin(), items.end(),
+                                          [&](const WorkItem &w) { return hv[size_t(w.head)].n_q <= G; }));
+                p->counters = DevBuf(hv.size() * sizeof(int));
+                p->q32 = DevBuf(hv.size() * size_t(kMaxQPerLaunch) * size_t(dim) * sizeof(float));
+                HIPX(hipMemset(p->counters.p, 0, hv.size() * sizeof(int)));
+                if (xkv) build_escape_index(*p, heads, n_heads, n_q, dim, hv);
+            }
             p->heads = DevBuf(hv.size() * sizeof(HeadDev));
             p->items = DevBuf(items.size() * sizeof(WorkItem));
             p->merge_ids = DevBuf(std::max<size_t>(1, merge.size()) * sizeof(int32_t));
@@ -523,9 +607,23 @@ int kvexp_hip_attention_run(kvexp_hip_plan *plan, const uint16_t *d_q, float *d_
             fail(KVEXP_HIP_INVALID_ARGUMENT, "attention_decode: bad argument");
         DeviceGuard g(plan->ctx->device);
         hipStream_t s = static_cast<hipStream_t>(stream);
-        HIPX(kvexp_launch::attention(plan->xkv, plan->order, plan->heads.as<HeadDev>(), plan->items.as<WorkItem>(),
-                                     plan->n_items, plan->merge_ids.as<int32_t>(), plan->n_merge, d_q, d_out, d_lse,
-                                     plan->ws.as<float>(), plan->dim, plan->status.as<uint32_t>(), s));
+        if (plan->wave) {
+            HIPX(kvexp_launch::q_widen(plan->heads.as<HeadDev>(), plan->n_dev_heads, d_q, plan->q32.as<float>(), s));
+            for (int G = 1; G <= 8; ++G) {
+                const int b = plan->group_start[G], e = plan->group_start[G + 1];
+                if (e > b)
+                    HIPX(kvexp_launch::attention_wave(plan->xkv, G, plan->heads.as<HeadDev>(),
+                                                      plan->items.as<WorkItem>() + b, e - b, plan->q32.as<float>(),
+                                                      d_out, d_lse,
+                                                      plan->ws.as<float>(), plan->counters.as<int>(),
+                                                      plan->status.as<uint32_t>(), s));
+            }
+        } else {
+            HIPX(kvexp_launch::attention(plan->xkv, plan->order, plan->heads.as<HeadDev>(),
+                                         plan->items.as<WorkItem>(), plan->n_items, plan->merge_ids.as<int32_t>(),
+                                         plan->n_merge, d_q, d_out, d_lse, plan->ws.as<float>(), plan->dim,
+                                         plan->status.as<uint32_t>(), s));
+        }
         if (check) check_status_word(plan->status.as<uint32_t>(), s);
     });
 }
