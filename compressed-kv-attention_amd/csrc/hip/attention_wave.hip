@@ -18,9 +18,9 @@
 //   5. folds the chunk's tokens in order (lane = channel):
 //      acc = fma(e, v, acc * alpha), l = fma(l, alpha, e); alpha == 1 for a
 //      whole chunk skips the multiply, which is exact.
-// Splits of a head are merged left to right (merge_state order) by the wave
-// that finishes last, chosen with an atomic counter per head; the merge is
-// followed by out = acc * (1/l).
+// A head cut into several splits leaves one partial state (m, l, acc) per
+// split; wave_merge_kernel, launched after the split kernels, folds them left
+// to right (merge_state order) and finalizes out = acc * (1/l).
 //
 // Every float operation is the reference's (attention_scalar.cpp:19-85,
 // softmax.hpp:8-41, dispatch.cpp:98-103), so outputs equal the reference's
@@ -36,6 +36,8 @@ constexpr int kChunk = 64;      // tokens per chunk (one per lane)
 constexpr int kTileStride = 144; // bytes per tile row: 64 BF16 + 16 (conflict-free 16-byte rows)
 constexpr int kWavesPerWg = 4;
 constexpr int kSlotQ = 8;       // partial-state slot: m[8], l[8], acc[8][64]
+constexpr int kSlotFloats = kSlotQ * (kD + 2);
+constexpr int kMergeBatch = 16; // split slots whose loads are in flight together in the merge
 
 struct WaveLds {
     uint8_t tile[kChunk * kTileStride];
@@ -295,7 +297,7 @@ template <int G, bool XKV>
 __global__ __launch_bounds__(kWavesPerWg * 64) void attn_wave_kernel(
     const HeadDev *__restrict__ heads, const WorkItem *__restrict__ items, int n_items,
     const float *__restrict__ q32_all, float *__restrict__ out_all, float *__restrict__ lse_all,
-    float *__restrict__ ws, int *__restrict__ counters, uint32_t *__restrict__ status) {
+    float *__restrict__ ws, uint32_t *__restrict__ status) {
     __shared__ WgLds L;
     if (threadIdx.x < 32) L.exptab[threadIdx.x] = kvexp_exp2_32_table[threadIdx.x];
     __syncthreads();
@@ -359,7 +361,7 @@ __global__ __launch_bounds__(kWavesPerWg * 64) void attn_wave_kernel(
         if (XKV) n = min(n, min(kc.t1 - t, vc.t1 - t));
         const int tn = t + n;
 
-        // 1. K rows -> tile; prefetch the next chunk's K rows
+        // 1. K rows -> tile
         if (XKV) {
             if (kc.mode != 0) {
                 base_pairs(kc.blk + 8, S.bp);
@@ -368,28 +370,30 @@ __global__ __launch_bounds__(kWavesPerWg * 64) void attn_wave_kernel(
             decode_row(kc, RK, S.bp, my_row);
             wave_sync();
             patch_escapes(kc, t - kc.t0, n, S.tile);
-            if (tn < wi.tok_end) {
-                if (tn >= kc.t1) bad |= open_block(kc, kc.b + 1);
-                if (bad == 0u) load_rows(kc, tn - kc.t0, min(kChunk, min(kc.t1, wi.tok_end) - tn), RK);
-            }
         } else {
             uint4 *dst = reinterpret_cast<uint4 *>(my_row);
 #pragma unroll
             for (int i = 0; i < 8; ++i) dst[i] = RK[i];
-            if (tn < wi.tok_end && lane < min(kChunk, wi.tok_end - tn)) {
-                const uint8_t *kr = reinterpret_cast<const uint8_t *>(hd.kraw + size_t(tn + lane) * kD);
-#pragma unroll
-                for (int i = 0; i < 8; ++i) RK[i] = ld16(kr + 16 * i);
-            }
         }
         wave_sync();
 
         // 2. scores, lane = token (an opaque copy of the q address per chunk
-        // keeps the q loads inside the loop)
+        // keeps the q loads inside the loop); then the next chunk's K rows are
+        // requested, so RK is not live across the score registers
         float s[G];
         uint64_t qa = reinterpret_cast<uint64_t>(q32);
         asm volatile("" : "+s"(qa));
         scores<G>(my_row, qa, s);
+        if (XKV) {
+            if (tn < wi.tok_end) {
+                if (tn >= kc.t1) bad |= open_block(kc, kc.b + 1);
+                if (bad == 0u) load_rows(kc, tn - kc.t0, min(kChunk, min(kc.t1, wi.tok_end) - tn), RK);
+            }
+        } else if (tn < wi.tok_end && lane < min(kChunk, wi.tok_end - tn)) {
+            const uint8_t *kr = reinterpret_cast<const uint8_t *>(hd.kraw + size_t(tn + lane) * kD);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) RK[i] = ld16(kr + 16 * i);
+        }
         wave_sync();
 
         // 3. V rows -> tile; prefetch the next chunk's V rows
@@ -416,21 +420,34 @@ __global__ __launch_bounds__(kWavesPerWg * 64) void attn_wave_kernel(
             }
         }
 
-        // 4. softmax coefficients, lane = token
-        bool resc = false;
+        // 4. softmax coefficients, lane = token. All G rows are computed
+        // together without branches (independent chains the scheduler can
+        // interleave); alpha is only needed when some token of the chunk
+        // raises a running maximum.
+        float mi[G], d[G], ev[8];
+        bool nz = false;
 #pragma unroll
         for (int g = 0; g < G; ++g) {
             const float mg = readlane_f32(mvec, g);
-            const float mi = fmaxf(wave_scan_max(s[g]), mg);
-            const float mp = wave_shift_up(mi, mg);
-            const float d = mp - mi;
-            float alpha = 1.0f;
-            if (!(d == 0.0f)) alpha = kvexp_expf_tab(d, tab);
-            const float e = kvexp_expf_tab(s[g] - mi, tab);
-            S.e[lane][g] = e;
-            S.a[lane][g] = alpha;
-            resc |= __ballot(lane < n && !(alpha == 1.0f)) != 0;
-            const float mn = readlane_f32(mi, n - 1);
+            mi[g] = fmaxf(wave_scan_max(s[g]), mg);
+            d[g] = wave_shift_up(mi[g], mg) - mi[g];
+            nz |= !(d[g] == 0.0f);
+        }
+#pragma unroll
+        for (int g = 0; g < 8; ++g) ev[g] = g < G ? kvexp_expf_tab_nb(s[g < G ? g : 0] - mi[g < G ? g : 0], tab) : 0.0f;
+        *reinterpret_cast<float4 *>(&S.e[lane][0]) = make_float4(ev[0], ev[1], ev[2], ev[3]);
+        if (G > 4) *reinterpret_cast<float4 *>(&S.e[lane][4]) = make_float4(ev[4], ev[5], ev[6], ev[7]);
+        const bool resc = __ballot(lane < n && nz) != 0;
+        if (resc) {
+            float av[8];
+#pragma unroll
+            for (int g = 0; g < 8; ++g) av[g] = g < G ? kvexp_expf_tab_nb(d[g < G ? g : 0], tab) : 1.0f;
+            *reinterpret_cast<float4 *>(&S.a[lane][0]) = make_float4(av[0], av[1], av[2], av[3]);
+            if (G > 4) *reinterpret_cast<float4 *>(&S.a[lane][4]) = make_float4(av[4], av[5], av[6], av[7]);
+        }
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            const float mn = readlane_f32(mi[g], n - 1);
             mvec = lane == g ? mn : mvec;
         }
         wave_sync();
@@ -481,66 +498,65 @@ __global__ __launch_bounds__(kWavesPerWg * 64) void attn_wave_kernel(
         if (lse_all != nullptr && lane < G) lse_all[hd.q_row + lane] = mv + logf(lvec);
         return;
     }
-    const size_t slot_f = size_t(kSlotQ) * (kD + 2);
-    float *slot = ws + size_t(hd.ws_base + wi.split) * slot_f;
+    float *slot = ws + size_t(hd.ws_base + wi.split) * kSlotFloats;
     if (lane < G) {
         slot[lane] = mv;
         slot[kSlotQ + lane] = lvec;
     }
 #pragma unroll
     for (int g = 0; g < G; ++g) slot[2 * kSlotQ + g * kD + lane] = acc[g];
-    __threadfence();
-    int prev = 0;
-    if (lane == 0) prev = atomicAdd(&counters[wi.head], 1);
-    prev = __builtin_amdgcn_readfirstlane(prev);
-    if (prev != hd.n_splits - 1) return;
+}
 
-    // ---- the last split of this head: ordered merge (softmax.hpp:16-30) -----
-    __threadfence();
-    const float *slots = ws + size_t(hd.ws_base) * slot_f;
-    float a[G], mf[G];
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-        a[g] = __builtin_nontemporal_load(slots + 2 * kSlotQ + g * kD + lane);
-        mf[g] = __builtin_nontemporal_load(slots + g);
-    }
-    float lf = lane < G ? __builtin_nontemporal_load(slots + kSlotQ + lane) : 0.0f;
-    for (int s0 = 1; s0 < hd.n_splits; s0 += kChunk) {
-        const int cnt = min(kChunk, hd.n_splits - s0);
+// Ordered merge of a head's split states (softmax.hpp:16-30 merge_state,
+// left to right in split order), then out = acc * (1/l) and lse = m + log l.
+// One wave per (device head, query row): lane = channel. A separate launch,
+// so the slots written by the split kernel are visible without fences.
+__global__ __launch_bounds__(kWavesPerWg * 64) void wave_merge_kernel(
+    const HeadDev *__restrict__ heads, const int2 *__restrict__ mitems, int n_mitems, float *__restrict__ out_all,
+    float *__restrict__ lse_all, const float *__restrict__ ws) {
+    __shared__ uint64_t tab[32];
+    if (threadIdx.x < 32) tab[threadIdx.x] = kvexp_exp2_32_table[threadIdx.x];
+    __syncthreads();
+    const int lane = lane_id();
+    const int mi = __builtin_amdgcn_readfirstlane(int(blockIdx.x) * kWavesPerWg + (int(threadIdx.x) >> 6));
+    if (mi >= n_mitems) return;
+    const int2 it = mitems[mi];
+    const HeadDev hd = heads[it.x];
+    const int g = it.y;
+    const float *slots = ws + size_t(hd.ws_base) * kSlotFloats;
+    const int n = hd.n_splits;
+    float a = slots[2 * kSlotQ + g * kD + lane];
+    float mf = slots[g];
+    float lf = slots[kSlotQ + g];
+    for (int s0 = 1; s0 < n; s0 += 64) {
+        const int cnt = min(64, n - s0);
         // lane = split s0 + lane: running maximum and the two exponentials
+        const float *ls = slots + size_t(s0 + min(lane, cnt - 1)) * kSlotFloats;
+        const float ms = lane < cnt ? ls[g] : -__builtin_inff();
+        const float lb = ls[kSlotQ + g];
+        const float mm = fmaxf(wave_scan_max(ms), mf);
+        const float mprev = wave_shift_up(mm, mf);
+        const float e1 = kvexp_expf_tab(mprev - mm, tab); // scale of the running state
+        const float e2 = kvexp_expf_tab(ms - mm, tab);    // scale of split s0 + lane
+        mf = readlane_f32(mm, cnt - 1);
+        for (int j0 = 0; j0 < cnt; j0 += kMergeBatch) {
+            float ab[kMergeBatch];
 #pragma unroll
-        for (int g = 0; g < G; ++g) {
-            const float ms = lane < cnt ? __builtin_nontemporal_load(slots + size_t(s0 + lane) * slot_f + g)
-                                        : -__builtin_inff();
-            const float mm = fmaxf(wave_scan_max(ms), mf[g]);
-            const float mprev = wave_shift_up(mm, mf[g]);
-            S.e[lane][g] = kvexp_expf_tab(mprev - mm, tab);
-            S.a[lane][g] = kvexp_expf_tab(ms - mm, tab);
-            mf[g] = readlane_f32(mm, cnt - 1);
-        }
-        wave_sync();
-        for (int j = 0; j < cnt; ++j) {
-            const float *sl = slots + size_t(s0 + j) * slot_f;
+            for (int jj = 0; jj < kMergeBatch; ++jj)
+                ab[jj] = slots[size_t(s0 + min(j0 + jj, cnt - 1)) * kSlotFloats + 2 * kSlotQ + g * kD + lane];
 #pragma unroll
-            for (int g = 0; g < G; ++g) {
-                const float ab = __builtin_nontemporal_load(sl + 2 * kSlotQ + g * kD + lane);
-                a[g] = fmaf(a[g], S.e[j][g], ab * S.a[j][g]);
+            for (int jj = 0; jj < kMergeBatch; ++jj) {
+                const int j = j0 + jj;
+                if (j < cnt) {
+                    const float x1 = readlane_f32(e1, j), x2 = readlane_f32(e2, j);
+                    a = fmaf(a, x1, ab[jj] * x2);
+                    lf = fmaf(lf, x1, readlane_f32(lb, j) * x2);
+                }
             }
-            const float lb = lane < G ? __builtin_nontemporal_load(sl + kSlotQ + lane) : 0.0f;
-            lf = fmaf(lf, S.e[j][lane & 7], lb * S.a[j][lane & 7]);
         }
-        wave_sync();
     }
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-        const float l = readlane_f32(lf, g);
-        out_all[(size_t(hd.q_row) + g) * kD + lane] = a[g] * (1.0f / l);
-    }
-    float mfl = -__builtin_inff();
-#pragma unroll
-    for (int g = 0; g < G; ++g) mfl = lane == g ? mf[g] : mfl;
-    if (lse_all != nullptr && lane < G) lse_all[hd.q_row + lane] = mfl + logf(lf);
-    if (lane == 0) counters[wi.head] = 0;
+    out_all[(size_t(hd.q_row) + g) * kD + lane] = a * (1.0f / lf);
+    if (lse_all != nullptr && lane == 0) lse_all[hd.q_row + g] = mf + logf(lf);
 }
 
 } // namespace wave
@@ -551,41 +567,48 @@ using namespace kvexp_dev;
 
 template <int G, bool XKV>
 static hipError_t launch_wave_g(const HeadDev *heads, const WorkItem *items, int n_items, const float *q,
-                                float *out, float *lse, float *ws, int *counters, uint32_t *status, hipStream_t s) {
+                                float *out, float *lse, float *ws, uint32_t *status, hipStream_t s) {
     const int grid = (n_items + wave::kWavesPerWg - 1) / wave::kWavesPerWg;
     hipLaunchKernelGGL((wave::attn_wave_kernel<G, XKV>), dim3(grid), dim3(wave::kWavesPerWg * 64), 0, s, heads,
-                       items, n_items, q, out, lse, ws, counters, status);
+                       items, n_items, q, out, lse, ws, status);
     return hipGetLastError();
 }
 
 template <bool XKV>
 static hipError_t launch_wave_x(int G, const HeadDev *heads, const WorkItem *items, int n_items, const float *q,
-                                float *out, float *lse, float *ws, int *counters, uint32_t *status, hipStream_t s) {
+                                float *out, float *lse, float *ws, uint32_t *status, hipStream_t s) {
     switch (G) {
-    case 1: return launch_wave_g<1, XKV>(heads, items, n_items, q, out, lse, ws, counters, status, s);
-    case 2: return launch_wave_g<2, XKV>(heads, items, n_items, q, out, lse, ws, counters, status, s);
-    case 3: return launch_wave_g<3, XKV>(heads, items, n_items, q, out, lse, ws, counters, status, s);
-    case 4: return launch_wave_g<4, XKV>(heads, items, n_items, q, out, lse, ws, counters, status, s);
-    case 5: return launch_wave_g<5, XKV>(heads, items, n_items, q, out, lse, ws, counters, status, s);
-    case 6: return launch_wave_g<6, XKV>(heads, items, n_items, q, out, lse, ws, counters, status, s);
-    case 7: return launch_wave_g<7, XKV>(heads, items, n_items, q, out, lse, ws, counters, status, s);
-    case 8: return launch_wave_g<8, XKV>(heads, items, n_items, q, out, lse, ws, counters, status, s);
+    case 1: return launch_wave_g<1, XKV>(heads, items, n_items, q, out, lse, ws, status, s);
+    case 2: return launch_wave_g<2, XKV>(heads, items, n_items, q, out, lse, ws, status, s);
+    case 3: return launch_wave_g<3, XKV>(heads, items, n_items, q, out, lse, ws, status, s);
+    case 4: return launch_wave_g<4, XKV>(heads, items, n_items, q, out, lse, ws, status, s);
+    case 5: return launch_wave_g<5, XKV>(heads, items, n_items, q, out, lse, ws, status, s);
+    case 6: return launch_wave_g<6, XKV>(heads, items, n_items, q, out, lse, ws, status, s);
+    case 7: return launch_wave_g<7, XKV>(heads, items, n_items, q, out, lse, ws, status, s);
+    case 8: return launch_wave_g<8, XKV>(heads, items, n_items, q, out, lse, ws, status, s);
     default: return hipErrorInvalidValue;
     }
 }
 
-// Items with the same G; counters: one per device head, zero between runs.
 hipError_t q_widen(const HeadDev *heads, int n_heads, const uint16_t *q, float *q32, hipStream_t s) {
     hipLaunchKernelGGL(wave::q_widen_kernel, dim3(n_heads), dim3(256), 0, s, heads, q, q32);
     return hipGetLastError();
 }
 
+hipError_t wave_merge(const HeadDev *heads, const int2 *mitems, int n_mitems, float *out, float *lse, const float *ws,
+                      hipStream_t s) {
+    if (n_mitems <= 0) return hipSuccess;
+    const int grid = (n_mitems + wave::kWavesPerWg - 1) / wave::kWavesPerWg;
+    hipLaunchKernelGGL(wave::wave_merge_kernel, dim3(grid), dim3(wave::kWavesPerWg * 64), 0, s, heads, mitems, n_mitems,
+                       out, lse, ws);
+    return hipGetLastError();
+}
+
 hipError_t attention_wave(bool xkv, int G, const HeadDev *heads, const WorkItem *items, int n_items,
-                          const float *q, float *out, float *lse, float *ws, int *counters, uint32_t *status,
-                          hipStream_t s) {
+                          const float *q, float *out, float *lse, float *ws, uint32_t *status, hipStream_t s) {
     if (n_items <= 0) return hipSuccess;
-    return xkv ? launch_wave_x<true>(G, heads, items, n_items, q, out, lse, ws, counters, status, s)
-               : launch_wave_x<false>(G, heads, items, n_items, q, out, lse, ws, counters, status, s);
+    return xkv ? launch_wave_x<true>(G, heads, items, n_items, q, out, lse, ws, status, s)
+               : launch_wave_x<false>(G, heads, items, n_items, q, out, lse, ws, status, s);
 }
 
 } // namespace kvexp_launch

@@ -409,9 +409,15 @@ __global__ __launch_bounds__(kThreads) void esc_pos_kernel(const EscJob *__restr
     if (threadIdx.x == 0 && carry != h.n_escape) atomicOr(status, kStEscape);
 }
 
+// y = expf(x) in the form the attention kernels evaluate it: even threads use
+// the branching special cases with the constant-memory table, odd threads the
+// branch-free form with the table copied to LDS (both must equal glibc).
 __global__ __launch_bounds__(256) void expf_kernel(const float *__restrict__ x, float *__restrict__ y, size_t n) {
+    __shared__ uint64_t tab[32];
+    if (threadIdx.x < 32) tab[threadIdx.x] = kvexp_exp2_32_table[threadIdx.x];
+    __syncthreads();
     const size_t i = size_t(blockIdx.x) * 256u + threadIdx.x;
-    if (i < n) y[i] = kvexp_expf(x[i]);
+    if (i < n) y[i] = (threadIdx.x & 1) ? kvexp_expf_tab_nb(x[i], tab) : kvexp_expf(x[i]);
 }
 
 } // namespace kvexp_dev

@@ -125,6 +125,21 @@ KVEXP_HD float kvexp_expf_tab(float x, const uint64_t *tab) {
     return kvexp_expf_core_tab(x, tab);
 }
 
+/* kvexp_expf_tab without branches: the reduction and polynomial run for every
+ * input (the table index is always in range) and the special cases are
+ * selected afterwards, so the result is the same for every x. */
+KVEXP_HD float kvexp_expf_tab_nb(float x, const uint64_t *tab) {
+    const float core = kvexp_expf_core_tab(x, tab);
+    const uint32_t ux = kvexp_f32_bits(x);
+    const uint32_t abstop = (ux >> 20) & 0x7ffu;
+    float special = core;
+    special = x < -0x1.9fe368p6f ? 0.0f : special;
+    special = x > 0x1.62e42ep6f ? __builtin_inff() : special;
+    special = abstop >= 0x7f8u ? x + x : special;
+    special = ux == 0xff800000u ? 0.0f : special;
+    return abstop >= 0x42bu ? special : core;
+}
+
 /* The reduction and polynomial with the built-in table. */
 KVEXP_HD float kvexp_expf_core(float x) { return kvexp_expf_core_tab(x, kvexp_exp2_32_table); }
 

@@ -36,8 +36,9 @@ hipError_t esc_start(const kvexp_dev::EscJob *jobs, int n_jobs, uint32_t *status
 hipError_t esc_pos(const kvexp_dev::EscJob *jobs, const int2 *blocks, int n_blocks, uint32_t *status, hipStream_t s);
 hipError_t q_widen(const HeadDev *heads, int n_heads, const uint16_t *q, float *q32, hipStream_t s);
 hipError_t attention_wave(bool xkv, int G, const HeadDev *heads, const WorkItem *items, int n_items,
-                          const float *q, float *out, float *lse, float *ws, int *counters, uint32_t *status,
-                          hipStream_t s);
+                          const float *q, float *out, float *lse, float *ws, uint32_t *status, hipStream_t s);
+hipError_t wave_merge(const HeadDev *heads, const int2 *mitems, int n_mitems, float *out, float *lse, const float *ws,
+                      hipStream_t s);
 } // namespace kvexp_launch
 
 namespace {
@@ -196,7 +197,8 @@ struct kvexp_hip_plan {
     bool xkv = false;
     bool wave = false; // one-wave-per-split kernel (dim 64, scalar order)
     DevBuf heads, items, merge_ids, ws, status;
-    DevBuf counters, esc0, escpos, q32; // wave kernel: merge counters, escape-position index, FP32 q
+    DevBuf mitems, esc0, escpos, q32; // wave kernel: merge work (head, row), escape-position index, FP32 q
+    int n_mitems = 0;
     int n_dev_heads = 0, n_items = 0, n_merge = 0;
     // wave kernel: items sorted by query-row count G; group_start[G] .. group_start[G+1]
     int group_start[10] = {0};
@@ -568,9 +570,14 @@ int kvexp_hip_plan_create(kvexp_hip_ctx *ctx, const kvexp_hip_head *heads, int n
                     p->group_start[G + 1] =
                         int(std::count_if(items.begin(), items.end(),
                                           [&](const WorkItem &w) { return hv[size_t(w.head)].n_q <= G; }));
-                p->counters = DevBuf(hv.size() * sizeof(int));
                 p->q32 = DevBuf(hv.size() * size_t(kMaxQPerLaunch) * size_t(dim) * sizeof(float));
-                HIPX(hipMemset(p->counters.p, 0, hv.size() * sizeof(int)));
+                std::vector<int2> mi;
+                for (int32_t dh : merge)
+                    for (int g = 0; g < hv[size_t(dh)].n_q; ++g) mi.push_back(make_int2(dh, g));
+                p->n_mitems = int(mi.size());
+                p->mitems = DevBuf(std::max<size_t>(1, mi.size()) * sizeof(int2));
+                if (!mi.empty())
+                    HIPX(hipMemcpy(p->mitems.p, mi.data(), mi.size() * sizeof(int2), hipMemcpyHostToDevice));
                 if (xkv) build_escape_index(*p, heads, n_heads, n_q, dim, hv);
             }
             p->heads = DevBuf(hv.size() * sizeof(HeadDev));
@@ -615,9 +622,10 @@ int kvexp_hip_attention_run(kvexp_hip_plan *plan, const uint16_t *d_q, float *d_
                     HIPX(kvexp_launch::attention_wave(plan->xkv, G, plan->heads.as<HeadDev>(),
                                                       plan->items.as<WorkItem>() + b, e - b, plan->q32.as<float>(),
                                                       d_out, d_lse,
-                                                      plan->ws.as<float>(), plan->counters.as<int>(),
-                                                      plan->status.as<uint32_t>(), s));
+                                                      plan->ws.as<float>(), plan->status.as<uint32_t>(), s));
             }
+            HIPX(kvexp_launch::wave_merge(plan->heads.as<HeadDev>(), plan->mitems.as<int2>(), plan->n_mitems, d_out,
+                                          d_lse, plan->ws.as<float>(), s));
         } else {
             HIPX(kvexp_launch::attention(plan->xkv, plan->order, plan->heads.as<HeadDev>(),
                                          plan->items.as<WorkItem>(), plan->n_items, plan->merge_ids.as<int32_t>(),

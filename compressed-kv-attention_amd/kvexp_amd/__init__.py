@@ -58,13 +58,17 @@ def declared_symbols() -> list[str]:
 
 
 def lib() -> C.CDLL:
-    """Loads the library (raises FileNotFoundError when it was not built)."""
+    """Loads the library (raises FileNotFoundError when it was not built).
+
+    KVEXP_HIP_LIBRARY, when set, names another build of the same library.
+    """
     global _lib
     if _lib is not None:
         return _lib
-    if not os.path.exists(LIB_PATH):
-        raise FileNotFoundError(f"{LIB_PATH} is missing: run compressed-kv-attention_amd/build.py")
-    L = C.CDLL(LIB_PATH)
+    path = os.environ.get("KVEXP_HIP_LIBRARY", LIB_PATH)
+    if not os.path.exists(path):
+        raise FileNotFoundError(f"{path} is missing: run compressed-kv-attention_amd/build.py")
+    L = C.CDLL(path)
     vp, sz, i32, i64 = C.c_void_p, C.c_size_t, C.c_int, C.c_int64
     L.kvexp_hip_status_string.restype = C.c_char_p
     L.kvexp_hip_status_string.argtypes = [i32]

@@ -1,5 +1,6 @@
 /* Exhaustive comparison of the device expf restatement (compiled here for the
- * host) with the host libm expf over every float bit pattern in [lo, hi).
+ * host; both the branching and the branch-free form) with the host libm expf
+ * over every float bit pattern in [lo, hi).
  * Usage: expf_exhaustive FORM_UNUSED lo hi   (the form is fixed at compile time)
  * Prints: "<mismatches> <first mismatching bits or -1>". */
 #include <math.h>
@@ -22,11 +23,12 @@ int main(int argc, char **argv) {
         uint32_t b = (uint32_t)u;
         float x;
         memcpy(&x, &b, 4);
-        float a = expf(x), d = kvexp_expf(x);
-        uint32_t ua, ud;
+        float a = expf(x), d = kvexp_expf(x), e = kvexp_expf_tab_nb(x, kvexp_exp2_32_table);
+        uint32_t ua, ud, ue;
         memcpy(&ua, &a, 4);
         memcpy(&ud, &d, 4);
-        if (ua != ud && !(isnan(a) && isnan(d))) {
+        memcpy(&ue, &e, 4);
+        if ((ua != ud && !(isnan(a) && isnan(d))) || (ua != ue && !(isnan(a) && isnan(e)))) {
             ++bad;
 #pragma omp critical
             if (first < 0 || u < first) first = u;
