@@ -15,12 +15,16 @@ Each timed step reads a different copy of the containers (--copies, default 4,
 Infinity Cache.
 
 Prints one JSON line. value = container bytes per step / seconds per step
-(GB/s, 1e9). roofline.achieved = algorithmic bytes of one launch (all K/V
-container bytes + Q + output) / the average step duration measured with HIP
-events on the stream the kernels run on. cpu_baseline = the reference library
-(oracle/_ref, compiled from the reference sources) running its model_heads
-scope (OpenMP over KV heads, AVX-512 BF16 when the host has it, else AVX2) on
-a bounded sample of the same step.
+(GB/s, 1e9), the step being all kernels of one run (q widening, split
+kernel, merge). roofline.achieved = algorithmic bytes of one split-kernel
+launch (all K/V container bytes + Q + output) / that kernel's average
+duration, measured with HIP events the library records around the split
+kernel on the run's stream (kvexp_hip_plan_timing). roofline.traffic = HBM
+bytes per launch from the committed counter summary
+profiles/attn_wave_c2_traffic.md (null when absent). cpu_baseline = the
+reference library (oracle/_ref, compiled from the reference sources) running
+its model_heads scope (OpenMP over KV heads, AVX-512 BF16 when the host has
+it, else AVX2) on a bounded sample of the same step.
 """
 from __future__ import annotations
 
@@ -41,6 +45,32 @@ def log(*a):
     print("[bench]", *a, file=sys.stderr, flush=True)
 
 
+def measured_traffic():
+    """HBM bytes per launch of the split kernel from the committed counter
+    summary (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, scaled by a plain copy
+    kernel of known size), or None when there is none."""
+    path = os.path.join(ROOT, "profiles", "attn_wave_c2_traffic.md")
+    try:
+        for line in open(path):
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":", 1)[1].strip())
+    except OSError:
+        pass
+    return None
+
+
+def copy_probe(torch, dev):
+    """Three device-to-device copies of 256 MiB: the known-size kernel the
+    FETCH_SIZE / WRITE_SIZE counters are scaled by."""
+    n = 256 << 20
+    src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"copy probe: 3 copies of {n} bytes")
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -51,6 +81,8 @@ def main() -> int:
     ap.add_argument("--splits", type=int, default=0, help="splits per KV head (0 = library suggestion)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=0)
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="also run a 256 MiB device copy (counter calibration under rocprofv3 --pmc)")
     a = ap.parse_args()
     if a.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
@@ -146,15 +178,30 @@ def main() -> int:
         per = [s.elapsed_time(e) for s, e in ev]
         return wall / steps * 1e3, float(np.mean(per)), float(np.median(per))
 
+    for p in xkv_plans:
+        p.timing(True)
     ms_x, ev_mean_x, ev_med_x = timed(xkv_plans, out_x, a.steps, a.warmup)
+    kern_ms, kern_runs = 0.0, 0
+    for p in xkv_plans:
+        t_ms, t_runs = p.kernel_time()
+        p.timing(False)
+        kern_ms += t_ms
+        kern_runs += t_runs
+    # the warmup runs are recorded too; every run launches the same kernels
+    kern_avg_ms = kern_ms / max(1, kern_runs)
     ms_r, ev_mean_r, ev_med_r = timed(raw_plans, out_r, max(10, a.steps // 2), a.warmup)
-    log(f"xkv {ms_x * 1e3:.1f} us/step (events mean {ev_mean_x * 1e3:.1f}), raw {ms_r * 1e3:.1f} us/step")
+    log(f"xkv {ms_x * 1e3:.1f} us/step (events mean {ev_mean_x * 1e3:.1f}, split kernel "
+        f"{kern_avg_ms * 1e3:.1f} over {kern_runs} runs), raw {ms_r * 1e3:.1f} us/step")
 
     q_bytes = H * G * D * 2
     out_bytes = H * G * D * 4
     algo_bytes = container + q_bytes + out_bytes
-    achieved = algo_bytes / (ev_mean_x * 1e-3) / 1e9
+    achieved = algo_bytes / (kern_avg_ms * 1e-3) / 1e9
+    traffic = measured_traffic()
     value = container / (ms_x * 1e-3) / 1e9
+
+    if a.copy_probe:
+        copy_probe(torch, dev)
 
     # ---- CPU baseline: the reference library, model_heads scope -------------------
     cpu = None
@@ -216,7 +263,9 @@ def main() -> int:
         "xkv_bit_equal_raw": bit_equal,
         "block_modes": stats,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None},
+                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
+                     "kernel": "attn_wave_kernel<7, true>", "kernel_us": round(kern_avg_ms * 1e3, 2),
+                     "algorithmic_bytes": algo_bytes},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

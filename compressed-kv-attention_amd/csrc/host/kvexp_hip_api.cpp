@@ -202,6 +202,17 @@ struct kvexp_hip_plan {
     int n_dev_heads = 0, n_items = 0, n_merge = 0;
     // wave kernel: items sorted by query-row count G; group_start[G] .. group_start[G+1]
     int group_start[10] = {0};
+    // split-kernel timing: one event pair per run while enabled
+    bool timing = false;
+    std::vector<std::pair<hipEvent_t, hipEvent_t>> events;
+    void clear_events() {
+        for (auto &e : events) {
+            (void)hipEventDestroy(e.first);
+            (void)hipEventDestroy(e.second);
+        }
+        events.clear();
+    }
+    ~kvexp_hip_plan() { clear_events(); }
 };
 
 namespace {
@@ -458,9 +469,10 @@ int kvexp_hip_decode(kvexp_hip_ctx *ctx, const uint8_t *d_blob, size_t bytes, co
 int kvexp_hip_suggest_splits(kvexp_hip_ctx *ctx, int n_heads, int seq, int split_tokens) {
     if (ctx == nullptr || n_heads <= 0 || seq <= 0 || split_tokens <= 0) return 1;
     const int tiles = (seq + split_tokens - 1) / split_tokens;
-    // about 12 resident single-wave splits per CU (the head_dim-64 kernel's
-    // LDS occupancy) over the whole launch
-    const int target = std::max(1, (12 * ctx->cu_count + n_heads - 1) / n_heads);
+    // about 24 single-wave splits per CU over the whole launch: two to three
+    // rounds of the head_dim-64 kernel's 8-12 resident waves per CU, so the
+    // dispatcher can even out splits that finish at different times
+    const int target = std::max(1, (24 * ctx->cu_count + n_heads - 1) / n_heads);
     return std::max(1, std::min(tiles, target));
 }
 
@@ -614,8 +626,18 @@ int kvexp_hip_attention_run(kvexp_hip_plan *plan, const uint16_t *d_q, float *d_
             fail(KVEXP_HIP_INVALID_ARGUMENT, "attention_decode: bad argument");
         DeviceGuard g(plan->ctx->device);
         hipStream_t s = static_cast<hipStream_t>(stream);
+        hipEvent_t ev0 = nullptr, ev1 = nullptr;
+        if (plan->timing) {
+            HIPX(hipEventCreate(&ev0));
+            if (hipEventCreate(&ev1) != hipSuccess) {
+                (void)hipEventDestroy(ev0);
+                fail(KVEXP_HIP_DEVICE_ERROR, "hipEventCreate failed");
+            }
+            plan->events.emplace_back(ev0, ev1);
+        }
         if (plan->wave) {
             HIPX(kvexp_launch::q_widen(plan->heads.as<HeadDev>(), plan->n_dev_heads, d_q, plan->q32.as<float>(), s));
+            if (ev0) HIPX(hipEventRecord(ev0, s));
             for (int G = 1; G <= 8; ++G) {
                 const int b = plan->group_start[G], e = plan->group_start[G + 1];
                 if (e > b)
@@ -624,15 +646,44 @@ int kvexp_hip_attention_run(kvexp_hip_plan *plan, const uint16_t *d_q, float *d_
                                                       d_out, d_lse,
                                                       plan->ws.as<float>(), plan->status.as<uint32_t>(), s));
             }
+            if (ev1) HIPX(hipEventRecord(ev1, s));
             HIPX(kvexp_launch::wave_merge(plan->heads.as<HeadDev>(), plan->mitems.as<int2>(), plan->n_mitems, d_out,
                                           d_lse, plan->ws.as<float>(), s));
         } else {
+            if (ev0) HIPX(hipEventRecord(ev0, s));
             HIPX(kvexp_launch::attention(plan->xkv, plan->order, plan->heads.as<HeadDev>(),
                                          plan->items.as<WorkItem>(), plan->n_items, plan->merge_ids.as<int32_t>(),
                                          plan->n_merge, d_q, d_out, d_lse, plan->ws.as<float>(), plan->dim,
                                          plan->status.as<uint32_t>(), s));
+            if (ev1) HIPX(hipEventRecord(ev1, s));
         }
         if (check) check_status_word(plan->status.as<uint32_t>(), s);
+    });
+}
+
+int kvexp_hip_plan_timing(kvexp_hip_plan *plan, int enable) {
+    return guarded([&] {
+        if (plan == nullptr) fail(KVEXP_HIP_INVALID_ARGUMENT, "kvexp_hip_plan_timing: null plan");
+        DeviceGuard g(plan->ctx->device);
+        plan->timing = enable != 0;
+    });
+}
+
+int kvexp_hip_plan_kernel_time(kvexp_hip_plan *plan, double *ms, int *runs) {
+    return guarded([&] {
+        if (plan == nullptr || ms == nullptr || runs == nullptr)
+            fail(KVEXP_HIP_INVALID_ARGUMENT, "kvexp_hip_plan_kernel_time: bad argument");
+        DeviceGuard g(plan->ctx->device);
+        double total = 0.0;
+        for (auto &e : plan->events) {
+            HIPX(hipEventSynchronize(e.second));
+            float t = 0.0f;
+            HIPX(hipEventElapsedTime(&t, e.first, e.second));
+            total += double(t);
+        }
+        *ms = total;
+        *runs = int(plan->events.size());
+        plan->clear_events();
     });
 }
 

@@ -89,6 +89,8 @@ def lib() -> C.CDLL:
     L.kvexp_hip_suggest_splits.argtypes = [vp, i32, i32, i32]
     L.kvexp_hip_attention_run.argtypes = [vp, vp, vp, vp, i32, vp]
     L.kvexp_hip_plan_status.argtypes = [vp, vp]
+    L.kvexp_hip_plan_timing.argtypes = [vp, i32]
+    L.kvexp_hip_plan_kernel_time.argtypes = [vp, C.POINTER(C.c_double), C.POINTER(C.c_int)]
     L.kvexp_hip_attention_decode_host.argtypes = [vp, i32, vp, vp, vp, vp, sz, vp, sz, vp, i32, i32, i32, i32, i32]
     L.kvexp_hip_expf.argtypes = [vp, vp, vp, sz, vp]
     _lib = L
@@ -283,6 +285,16 @@ class Plan:
 
     def status(self, stream=None) -> None:
         check(lib().kvexp_hip_plan_status(self.h, _stream(stream)))
+
+    def timing(self, enable: bool = True) -> None:
+        """Records a HIP event pair around the split kernels of every later run."""
+        check(lib().kvexp_hip_plan_timing(self.h, 1 if enable else 0))
+
+    def kernel_time(self) -> tuple[float, int]:
+        """(summed split-kernel ms, runs) since timing was enabled or last read; clears the record."""
+        ms, runs = C.c_double(0.0), C.c_int(0)
+        check(lib().kvexp_hip_plan_kernel_time(self.h, C.byref(ms), C.byref(runs)))
+        return ms.value, runs.value
 
     def close(self) -> None:
         if getattr(self, "h", None):

@@ -148,6 +148,15 @@ int kvexp_hip_attention_run(kvexp_hip_plan *plan, const uint16_t *d_q, float *d_
 /* Reads and clears the plan's status word (synchronises `stream`). */
 int kvexp_hip_plan_status(kvexp_hip_plan *plan, void *stream);
 
+/* Split-kernel timing. No counterpart in the reference (its bench times the
+ * whole call); it lets a benchmark time the dominant kernel alone. With
+ * `enable` non-zero every later run records a HIP event pair around its
+ * split-kernel launches on the run's stream; kvexp_hip_plan_kernel_time
+ * waits for the recorded pairs, returns their summed time in ms and the
+ * number of runs, and clears the record. */
+int kvexp_hip_plan_timing(kvexp_hip_plan *plan, int enable);
+int kvexp_hip_plan_kernel_time(kvexp_hip_plan *plan, double *ms, int *runs);
+
 /* The Backend::Hip case of attention_decode: the reference argument list
  * with host pointers. Copies the inputs to the device, builds indexes and a
  * plan with n_splits = n_threads, runs it and copies `out` back. */
