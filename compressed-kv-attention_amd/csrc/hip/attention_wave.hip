@@ -37,7 +37,7 @@ constexpr int kTileStride = 144; // bytes per tile row: 64 BF16 + 16 (conflict-f
 constexpr int kWavesPerWg = 4;
 constexpr int kSlotQ = 8;       // partial-state slot: m[8], l[8], acc[8][64]
 constexpr int kSlotFloats = kSlotQ * (kD + 2);
-constexpr int kMergeBatch = 16; // split slots whose loads are in flight together in the merge
+constexpr int kMergeBatch = 32; // split slots whose loads are in flight together in the merge
 
 struct WaveLds {
     uint8_t tile[kChunk * kTileStride];
@@ -422,14 +422,17 @@ __global__ __launch_bounds__(kWavesPerWg * 64) void attn_wave_kernel(
 
         // 4. softmax coefficients, lane = token. All G rows are computed
         // together without branches (independent chains the scheduler can
-        // interleave); alpha is only needed when some token of the chunk
+        // interleave); alpha is only computed when some token of the chunk
         // raises a running maximum.
         float mi[G], d[G], ev[8];
         bool nz = false;
 #pragma unroll
+        for (int g = 0; g < G; ++g) mi[g] = s[g];
+        wave_scan_max_rows<G>(mi);
+#pragma unroll
         for (int g = 0; g < G; ++g) {
             const float mg = readlane_f32(mvec, g);
-            mi[g] = fmaxf(wave_scan_max(s[g]), mg);
+            mi[g] = fmaxf(mi[g], mg);
             d[g] = wave_shift_up(mi[g], mg) - mi[g];
             nz |= !(d[g] == 0.0f);
         }
@@ -437,8 +440,9 @@ __global__ __launch_bounds__(kWavesPerWg * 64) void attn_wave_kernel(
         for (int g = 0; g < 8; ++g) ev[g] = g < G ? kvexp_expf_tab_nb(s[g < G ? g : 0] - mi[g < G ? g : 0], tab) : 0.0f;
         *reinterpret_cast<float4 *>(&S.e[lane][0]) = make_float4(ev[0], ev[1], ev[2], ev[3]);
         if (G > 4) *reinterpret_cast<float4 *>(&S.e[lane][4]) = make_float4(ev[4], ev[5], ev[6], ev[7]);
-        const bool resc = __ballot(lane < n && nz) != 0;
-        if (resc) {
+        // tokens (bits) where some row's running maximum moves: alpha != 1
+        const uint64_t rmask0 = __ballot(lane < n && nz);
+        if (rmask0 != 0) {
             float av[8];
 #pragma unroll
             for (int g = 0; g < 8; ++g) av[g] = g < G ? kvexp_expf_tab_nb(d[g < G ? g : 0], tab) : 1.0f;
@@ -452,11 +456,17 @@ __global__ __launch_bounds__(kWavesPerWg * 64) void attn_wave_kernel(
         }
         wave_sync();
 
-        // 5. ordered fold, lane = channel
+        // 5. ordered fold, lane = channel. Runs of tokens whose alpha is 1 for
+        // every row take acc = fma(e, v, acc), l = l + e (exact: alpha is
+        // exactly 1); a token that moves a running maximum also scales by
+        // alpha: acc = fma(e, v, acc * alpha), l = fma(l, alpha, e).
         const uint16_t *vt = reinterpret_cast<const uint16_t *>(S.tile);
-        if (!resc) {
+        uint64_t rmask = rmask0;
+        int tok = 0;
+        while (true) {
+            const int stop = rmask != 0 ? int(__builtin_ctzll(rmask)) : n;
 #pragma unroll 4
-            for (int tok = 0; tok < n; ++tok) {
+            for (; tok < stop; ++tok) {
                 const float v = __uint_as_float(uint32_t(vt[tok * (kTileStride / 2) + lane]) << 16);
                 const float4 e0 = *reinterpret_cast<const float4 *>(&S.e[tok][0]);
                 const float4 e1 = *reinterpret_cast<const float4 *>(&S.e[tok][4]);
@@ -465,9 +475,8 @@ __global__ __launch_bounds__(kWavesPerWg * 64) void attn_wave_kernel(
                 for (int g = 0; g < G; ++g) acc[g] = fmaf(ev[g], v, acc[g]);
                 lvec = lvec + S.e[tok][lane & 7];
             }
-        } else {
-#pragma unroll 2
-            for (int tok = 0; tok < n; ++tok) {
+            if (stop >= n) break;
+            {
                 const float v = __uint_as_float(uint32_t(vt[tok * (kTileStride / 2) + lane]) << 16);
                 const float4 e0 = *reinterpret_cast<const float4 *>(&S.e[tok][0]);
                 const float4 e1 = *reinterpret_cast<const float4 *>(&S.e[tok][4]);
@@ -479,6 +488,8 @@ __global__ __launch_bounds__(kWavesPerWg * 64) void attn_wave_kernel(
                 for (int g = 0; g < G; ++g) acc[g] = fmaf(ev[g], v, acc[g] * av[g]);
                 lvec = fmaf(lvec, S.a[tok][lane & 7], S.e[tok][lane & 7]);
             }
+            rmask &= rmask - 1;
+            tok = stop + 1;
         }
         wave_sync();
         t = tn;
@@ -528,30 +539,28 @@ __global__ __launch_bounds__(kWavesPerWg * 64) void wave_merge_kernel(
     float a = slots[2 * kSlotQ + g * kD + lane];
     float mf = slots[g];
     float lf = slots[kSlotQ + g];
-    for (int s0 = 1; s0 < n; s0 += 64) {
-        const int cnt = min(64, n - s0);
+    for (int s0 = 1; s0 < n; s0 += kMergeBatch) {
+        const int cnt = min(kMergeBatch, n - s0);
+        // every load of the batch is issued before any use (indices clamped)
+        float ab[kMergeBatch];
+#pragma unroll
+        for (int j = 0; j < kMergeBatch; ++j)
+            ab[j] = slots[size_t(s0 + min(j, cnt - 1)) * kSlotFloats + 2 * kSlotQ + g * kD + lane];
         // lane = split s0 + lane: running maximum and the two exponentials
         const float *ls = slots + size_t(s0 + min(lane, cnt - 1)) * kSlotFloats;
         const float ms = lane < cnt ? ls[g] : -__builtin_inff();
         const float lb = ls[kSlotQ + g];
         const float mm = fmaxf(wave_scan_max(ms), mf);
         const float mprev = wave_shift_up(mm, mf);
-        const float e1 = kvexp_expf_tab(mprev - mm, tab); // scale of the running state
-        const float e2 = kvexp_expf_tab(ms - mm, tab);    // scale of split s0 + lane
+        const float e1 = kvexp_expf_tab_nb(mprev - mm, tab); // scale of the running state
+        const float e2 = kvexp_expf_tab_nb(ms - mm, tab);    // scale of split s0 + lane
         mf = readlane_f32(mm, cnt - 1);
-        for (int j0 = 0; j0 < cnt; j0 += kMergeBatch) {
-            float ab[kMergeBatch];
 #pragma unroll
-            for (int jj = 0; jj < kMergeBatch; ++jj)
-                ab[jj] = slots[size_t(s0 + min(j0 + jj, cnt - 1)) * kSlotFloats + 2 * kSlotQ + g * kD + lane];
-#pragma unroll
-            for (int jj = 0; jj < kMergeBatch; ++jj) {
-                const int j = j0 + jj;
-                if (j < cnt) {
-                    const float x1 = readlane_f32(e1, j), x2 = readlane_f32(e2, j);
-                    a = fmaf(a, x1, ab[jj] * x2);
-                    lf = fmaf(lf, x1, readlane_f32(lb, j) * x2);
-                }
+        for (int j = 0; j < kMergeBatch; ++j) {
+            if (j < cnt) {
+                const float x1 = readlane_f32(e1, j), x2 = readlane_f32(e2, j);
+                a = fmaf(a, x1, ab[j] * x2);
+                lf = fmaf(lf, x1, readlane_f32(lb, j) * x2);
             }
         }
     }

@@ -110,6 +110,72 @@ __device__ __forceinline__ float wave_scan_max(float x) {
     return x;
 }
 
+// wave_scan_max of G values at once with the maximum fused into the DPP
+// read (v_max_f32_dpp, one instruction per step and value), as one asm block
+// so that its DPP hazards are under its own control: s_nop 1 before the
+// first step (the inputs were written by the compiler's code just before) and
+// after the last (a DPP read of a result may follow), and between steps when
+// fewer than three values separate a write from the next read of the same
+// VGPR (gfx9 needs two wait states between a VALU write and a DPP read).
+// The inputs must not be signalling NaNs (they are arithmetic results or
+// -inf), so the plain v_max_f32 needs no quieting. Lanes without a source
+// lane keep their value, which is max(x, -inf).
+#define KVEXP_DPPMAX(i, C) "v_max_f32_dpp %" #i ", %" #i ", %" #i " " C "\n"
+#define KVEXP_DPPMAX_ROW1(C) KVEXP_DPPMAX(0, C)
+#define KVEXP_DPPMAX_ROW2(C) KVEXP_DPPMAX_ROW1(C) KVEXP_DPPMAX(1, C)
+#define KVEXP_DPPMAX_ROW3(C) KVEXP_DPPMAX_ROW2(C) KVEXP_DPPMAX(2, C)
+#define KVEXP_DPPMAX_ROW4(C) KVEXP_DPPMAX_ROW3(C) KVEXP_DPPMAX(3, C)
+#define KVEXP_DPPMAX_ROW5(C) KVEXP_DPPMAX_ROW4(C) KVEXP_DPPMAX(4, C)
+#define KVEXP_DPPMAX_ROW6(C) KVEXP_DPPMAX_ROW5(C) KVEXP_DPPMAX(5, C)
+#define KVEXP_DPPMAX_ROW7(C) KVEXP_DPPMAX_ROW6(C) KVEXP_DPPMAX(6, C)
+#define KVEXP_DPPMAX_ROW8(C) KVEXP_DPPMAX_ROW7(C) KVEXP_DPPMAX(7, C)
+#define KVEXP_DPPMAX_SCAN(N, PAD)                                                             \
+    "s_nop 1\n" KVEXP_DPPMAX_ROW##N("row_shr:1 row_mask:0xf bank_mask:0xf") PAD            \
+        KVEXP_DPPMAX_ROW##N("row_shr:2 row_mask:0xf bank_mask:0xf") PAD                     \
+        KVEXP_DPPMAX_ROW##N("row_shr:4 row_mask:0xf bank_mask:0xf") PAD                     \
+        KVEXP_DPPMAX_ROW##N("row_shr:8 row_mask:0xf bank_mask:0xf") PAD                     \
+        KVEXP_DPPMAX_ROW##N("row_bcast:15 row_mask:0xa bank_mask:0xf") PAD                  \
+        KVEXP_DPPMAX_ROW##N("row_bcast:31 row_mask:0xc bank_mask:0xf") "s_nop 1\n"
+
+template <int G>
+__device__ __forceinline__ void wave_scan_max_rows(float (&x)[G]);
+template <>
+__device__ __forceinline__ void wave_scan_max_rows<1>(float (&x)[1]) {
+    asm volatile(KVEXP_DPPMAX_SCAN(1, "s_nop 1\n") : "+v"(x[0]));
+}
+template <>
+__device__ __forceinline__ void wave_scan_max_rows<2>(float (&x)[2]) {
+    asm volatile(KVEXP_DPPMAX_SCAN(2, "s_nop 0\n") : "+v"(x[0]), "+v"(x[1]));
+}
+template <>
+__device__ __forceinline__ void wave_scan_max_rows<3>(float (&x)[3]) {
+    asm volatile(KVEXP_DPPMAX_SCAN(3, "") : "+v"(x[0]), "+v"(x[1]), "+v"(x[2]));
+}
+template <>
+__device__ __forceinline__ void wave_scan_max_rows<4>(float (&x)[4]) {
+    asm volatile(KVEXP_DPPMAX_SCAN(4, "") : "+v"(x[0]), "+v"(x[1]), "+v"(x[2]), "+v"(x[3]));
+}
+template <>
+__device__ __forceinline__ void wave_scan_max_rows<5>(float (&x)[5]) {
+    asm volatile(KVEXP_DPPMAX_SCAN(5, "") : "+v"(x[0]), "+v"(x[1]), "+v"(x[2]), "+v"(x[3]), "+v"(x[4]));
+}
+template <>
+__device__ __forceinline__ void wave_scan_max_rows<6>(float (&x)[6]) {
+    asm volatile(KVEXP_DPPMAX_SCAN(6, "")
+                 : "+v"(x[0]), "+v"(x[1]), "+v"(x[2]), "+v"(x[3]), "+v"(x[4]), "+v"(x[5]));
+}
+template <>
+__device__ __forceinline__ void wave_scan_max_rows<7>(float (&x)[7]) {
+    asm volatile(KVEXP_DPPMAX_SCAN(7, "")
+                 : "+v"(x[0]), "+v"(x[1]), "+v"(x[2]), "+v"(x[3]), "+v"(x[4]), "+v"(x[5]), "+v"(x[6]));
+}
+template <>
+__device__ __forceinline__ void wave_scan_max_rows<8>(float (&x)[8]) {
+    asm volatile(KVEXP_DPPMAX_SCAN(8, "")
+                 : "+v"(x[0]), "+v"(x[1]), "+v"(x[2]), "+v"(x[3]), "+v"(x[4]), "+v"(x[5]), "+v"(x[6]),
+                   "+v"(x[7]));
+}
+
 // Value of lane - 1 (lane 0 gets `first`).
 __device__ __forceinline__ float wave_shift_up(float x, float first) { return dpp_f32<0x138>(first, x); }
 
