@@ -51,62 +51,25 @@ struct WgLds {
     WaveLds w[kWavesPerWg];
 };
 
-// Position of one tensor inside its XKV container (all fields wave-uniform).
-struct Cursor {
-    const uint8_t *blob;
-    uint64_t bytes;
-    const int64_t *offs;
-    const int32_t *first;
-    const int32_t *esc0;
-    const uint16_t *escpos;
-    const uint8_t *blk; // current block
-    int b, t0, t1;      // block index and its token range
-    int mode, ntok, nesc;
-    int eb;             // index of the block's first escape in escpos
-    int ecur;           // escapes of this block already written
-};
-
-// Enters block b: reads its 8-byte header with aligned (scalar) dword loads
-// and checks it against the index (dim, token count, mode, payload inside the
-// container, escape count). Every block of a valid container is >= 12 bytes.
-__device__ __forceinline__ uint32_t open_block(Cursor &c, int b) {
-    c.b = b;
-    c.t0 = c.first[b];
-    c.t1 = c.first[b + 1];
-    const int64_t off = c.offs[b];
-    c.blk = c.blob + off;
-    c.mode = 0;
-    c.ntok = 0;
-    c.nesc = 0;
-    c.eb = c.esc0[b];
-    c.ecur = 0;
-    if (off < 0 || uint64_t(off) + 12u > c.bytes) return kStHeader;
-    const uintptr_t a = reinterpret_cast<uintptr_t>(c.blk);
-    const uint32_t *w = reinterpret_cast<const uint32_t *>(a & ~uintptr_t(3));
-    const uint32_t sh = uint32_t(a & 3u) * 8u;
-    const uint32_t w0 = w[0], w1 = w[1], w2 = w[2];
-    const uint32_t d0 = uint32_t(((uint64_t(w1) << 32) | w0) >> sh);
-    const uint32_t d1 = uint32_t(((uint64_t(w2) << 32) | w1) >> sh);
-    const int mode = int(d0 & 0xFFu), ntok = int((d0 >> 8) & 0xFFu), nesc = int(d0 >> 16);
-    const int dim = int(d1 & 0xFFFFu);
-    c.mode = mode;
-    c.ntok = ntok;
-    c.nesc = mode == 0 ? 0 : nesc;
-    if (dim != kD || ntok <= 0) return kStHeader;
-    if (ntok != c.t1 - c.t0) return kStIndex;
-    const int64_t sz = block_bytes(mode, ntok, nesc, kD);
-    if (sz < 0) return kStMode;
-    if (uint64_t(off) + uint64_t(sz) > c.bytes) return kStTruncated;
-    if (c.esc0[b + 1] - c.eb != c.nesc) return kStIndex;
-    return 0u;
-}
-
 // Global-memory loads (address space 1, so they are issued as global_load_*
 // and counted on the vector-memory counter only). Addresses need only 2-byte
 // alignment: gfx950 under ROCm runs in unaligned-access mode.
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4), aligned(2)));
 typedef const __attribute__((address_space(1))) u32x4 g_u32x4;
 typedef const __attribute__((address_space(1))) uint16_t g_u16;
+
+// A copy of *p read through the constant address space (4): uniform loads
+// from it are scalar loads. For descriptors written by earlier launches only
+// (the scalar cache is coherent across launches). The host pass of this file
+// only needs the declaration to compile.
+template <class T>
+__device__ __forceinline__ T load_scalar(const T *p) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    return *(const __attribute__((address_space(4))) T *)(p);
+#else
+    return *p;
+#endif
+}
 
 // Constant address space (4): uniform loads from it are scalar loads.
 typedef float f8 __attribute__((ext_vector_type(8)));
@@ -117,6 +80,45 @@ __device__ __forceinline__ uint4 ld16(const uint8_t *p) {
     return make_uint4(v.x, v.y, v.z, v.w);
 }
 __device__ __forceinline__ uint32_t ldu16(const uint8_t *p) { return *(g_u16 *)(p); }
+
+// Position of one tensor inside its XKV container. The scalar fields are
+// wave-uniform; epos / eval hold the current block's first 64 escapes (lane
+// k: element index and word of escape k; epos = ~0 past the last).
+struct Cursor {
+    const BlockDesc *desc;
+    const uint16_t *escpos;
+    const uint8_t *blk; // current block's header
+    int b, t0, t1;      // block index and its token range
+    int mode, ntok, nesc;
+    int eb;             // index of the block's first escape in escpos
+    uint32_t epos, eval;
+};
+
+__device__ __forceinline__ const uint8_t *esc_words(const Cursor &c) {
+    return c.blk + 8 + kD + size_t(c.ntok) * kD + exp_payload_bytes(c.ntok, kD, c.mode);
+}
+
+// Enters block b, whose first token is t0: one scalar load of its
+// descriptor (checked against the container when the plan was built), then
+// the positions and words of its first 64 escapes.
+__device__ __forceinline__ void open_block(Cursor &c, int b, int t0) {
+    const BlockDesc d = load_scalar(c.desc + b);
+    c.b = b;
+    c.blk = d.data;
+    c.mode = int(d.meta & 0xFFu);
+    c.ntok = int((d.meta >> 8) & 0xFFu);
+    c.nesc = int(d.meta >> 16);
+    c.eb = d.esc0;
+    c.t0 = t0;
+    c.t1 = t0 + c.ntok;
+    c.epos = 0xFFFFFFFFu;
+    c.eval = 0u;
+    const int lane = lane_id();
+    if (lane < c.nesc) {
+        c.epos = *(g_u16 *)(c.escpos + c.eb + lane);
+        c.eval = ldu16(esc_words(c) + 2 * lane);
+    }
+}
 
 // Loads rows [r0 + lane] of the cursor's block (lanes < rows) into R.
 __device__ __forceinline__ void load_rows(const Cursor &c, int r0, int rows, uint4 (&R)[8]) {
@@ -201,26 +203,28 @@ __device__ __forceinline__ void decode_row(const Cursor &c, const uint4 (&R)[8],
 }
 
 // Writes the escape words of rows [r0, r0 + n) of the cursor's block over
-// their elements in the tile (positions ascend, so they form a prefix of the
-// block's remaining escapes).
-__device__ __forceinline__ void patch_escapes(Cursor &c, int r0, int n, uint8_t *tile) {
+// their elements in the tile: the first 64 escapes from the registers loaded
+// with the block, any further ones (blocks with more than 64) loaded here in
+// windows of 64. Positions ascend within a block.
+__device__ __forceinline__ void patch_escapes(const Cursor &c, int r0, int n, uint8_t *tile) {
     if (c.nesc == 0) return;
+    const uint32_t lo = uint32_t(r0 * kD), hi = uint32_t((r0 + n) * kD);
+    if (c.epos >= lo && c.epos < hi) {
+        const uint32_t row = c.epos / kD - uint32_t(r0), col = c.epos % kD;
+        *reinterpret_cast<uint16_t *>(tile + row * kTileStride + col * 2) = uint16_t(c.eval);
+    }
+    if (c.nesc <= kWave) return;
     const int lane = lane_id();
-    const int lim = (r0 + n) * kD;
-    const uint8_t *esc = c.blk + 8 + kD + size_t(c.ntok) * kD + exp_payload_bytes(c.ntok, kD, c.mode);
-    while (true) {
-        const int k = c.ecur + lane;
-        int pos = 0x7fffffff;
-        if (k < c.nesc) pos = int(*(g_u16 *)(c.escpos + c.eb + k));
-        const bool in = pos < lim;
-        const int cnt = __popcll(__ballot(in));
-        const int row = pos / kD - r0, col = pos % kD;
-        if (in && row >= 0) { // row < n by the sort order; row >= 0 guards a damaged index
-            const uint32_t val = ldu16(esc + 2 * size_t(k));
-            *reinterpret_cast<uint16_t *>(tile + row * kTileStride + col * 2) = uint16_t(val);
+    const uint8_t *esc = esc_words(c);
+    for (int k0 = kWave; k0 < c.nesc; k0 += kWave) {
+        const int k = k0 + lane;
+        uint32_t pos = 0xFFFFFFFFu;
+        if (k < c.nesc) pos = *(g_u16 *)(c.escpos + c.eb + k);
+        if (pos >= lo && pos < hi) {
+            const uint32_t row = pos / kD - uint32_t(r0), col = pos % kD;
+            *reinterpret_cast<uint16_t *>(tile + row * kTileStride + col * 2) = uint16_t(ldu16(esc + 2 * size_t(k)));
         }
-        c.ecur += cnt;
-        if (cnt < kWave) break;
+        if (uint32_t(__builtin_amdgcn_readfirstlane(int(pos))) >= hi) break; // lane 0 holds the window's first
     }
 }
 
@@ -297,7 +301,7 @@ template <int G, bool XKV>
 __global__ __launch_bounds__(kWavesPerWg * 64) void attn_wave_kernel(
     const HeadDev *__restrict__ heads, const WorkItem *__restrict__ items, int n_items,
     const float *__restrict__ q32_all, float *__restrict__ out_all, float *__restrict__ lse_all,
-    float *__restrict__ ws, uint32_t *__restrict__ status) {
+    float *__restrict__ ws) {
     __shared__ WgLds L;
     if (threadIdx.x < 32) L.exptab[threadIdx.x] = kvexp_exp2_32_table[threadIdx.x];
     __syncthreads();
@@ -308,8 +312,8 @@ __global__ __launch_bounds__(kWavesPerWg * 64) void attn_wave_kernel(
     if (item >= n_items) return;
     WaveLds &S = L.w[w];
     const uint64_t *tab = L.exptab;
-    const WorkItem wi = items[item];
-    const HeadDev hd = heads[wi.head];
+    const WorkItem wi = load_scalar(items + item);
+    const HeadDev hd = load_scalar(heads + wi.head);
     const float *q32 = q32_all + size_t(wi.head) * kSlotQ * kD;
 
     float acc[G];
@@ -318,30 +322,18 @@ __global__ __launch_bounds__(kWavesPerWg * 64) void attn_wave_kernel(
     float mvec = -__builtin_inff(); // lane g < G holds m of query row g
     float lvec = 0.0f;              // lane g < G holds l of query row g
 
-    uint32_t bad = 0;
     Cursor kc{}, vc{};
     uint4 RK[8], RV[8];
     int t = wi.tok_begin;
     if (XKV) {
-        kc.blob = hd.kx;
-        kc.bytes = hd.kbytes;
-        kc.offs = hd.koff;
-        kc.first = hd.kfirst;
-        kc.esc0 = hd.kesc0;
+        kc.desc = hd.kdesc;
         kc.escpos = hd.kescpos;
-        vc.blob = hd.vx;
-        vc.bytes = hd.vbytes;
-        vc.offs = hd.voff;
-        vc.first = hd.vfirst;
-        vc.esc0 = hd.vesc0;
+        vc.desc = hd.vdesc;
         vc.escpos = hd.vescpos;
-        bad |= open_block(kc, wi.kblk);
-        bad |= open_block(vc, wi.vblk);
-        if (kc.t0 != t || vc.t0 != t) bad |= kStIndex;
-        if (bad == 0u) {
-            load_rows(kc, 0, min(kChunk, min(kc.t1, wi.tok_end) - t), RK);
-            load_rows(vc, 0, min(kChunk, min(vc.t1, wi.tok_end) - t), RV);
-        }
+        open_block(kc, wi.kblk, t);
+        open_block(vc, wi.vblk, t);
+        load_rows(kc, 0, min(kChunk, min(kc.t1, wi.tok_end) - t), RK);
+        load_rows(vc, 0, min(kChunk, min(vc.t1, wi.tok_end) - t), RV);
     } else {
         const int rows = min(kChunk, wi.tok_end - t);
         if (lane < rows) {
@@ -356,9 +348,10 @@ __global__ __launch_bounds__(kWavesPerWg * 64) void attn_wave_kernel(
     }
     uint8_t *my_row = S.tile + lane * kTileStride;
 
-    while (t < wi.tok_end && bad == 0u) {
+    while (t < wi.tok_end) {
         int n = min(kChunk, wi.tok_end - t);
         if (XKV) n = min(n, min(kc.t1 - t, vc.t1 - t));
+        if (n <= 0) break; // unreachable with plan-checked descriptors (n_tokens > 0)
         const int tn = t + n;
 
         // 1. K rows -> tile
@@ -386,8 +379,8 @@ __global__ __launch_bounds__(kWavesPerWg * 64) void attn_wave_kernel(
         scores<G>(my_row, qa, s);
         if (XKV) {
             if (tn < wi.tok_end) {
-                if (tn >= kc.t1) bad |= open_block(kc, kc.b + 1);
-                if (bad == 0u) load_rows(kc, tn - kc.t0, min(kChunk, min(kc.t1, wi.tok_end) - tn), RK);
+                if (tn >= kc.t1) open_block(kc, kc.b + 1, kc.t1);
+                load_rows(kc, tn - kc.t0, min(kChunk, min(kc.t1, wi.tok_end) - tn), RK);
             }
         } else if (tn < wi.tok_end && lane < min(kChunk, wi.tok_end - tn)) {
             const uint8_t *kr = reinterpret_cast<const uint8_t *>(hd.kraw + size_t(tn + lane) * kD);
@@ -406,8 +399,8 @@ __global__ __launch_bounds__(kWavesPerWg * 64) void attn_wave_kernel(
             wave_sync();
             patch_escapes(vc, t - vc.t0, n, S.tile);
             if (tn < wi.tok_end) {
-                if (tn >= vc.t1) bad |= open_block(vc, vc.b + 1);
-                if (bad == 0u) load_rows(vc, tn - vc.t0, min(kChunk, min(vc.t1, wi.tok_end) - tn), RV);
+                if (tn >= vc.t1) open_block(vc, vc.b + 1, vc.t1);
+                load_rows(vc, tn - vc.t0, min(kChunk, min(vc.t1, wi.tok_end) - tn), RV);
             }
         } else {
             uint4 *dst = reinterpret_cast<uint4 *>(my_row);
@@ -494,9 +487,6 @@ __global__ __launch_bounds__(kWavesPerWg * 64) void attn_wave_kernel(
         wave_sync();
         t = tn;
     }
-    if (bad) {
-        if (lane == 0) atomicOr(status, bad);
-    }
 
     // ---- epilogue --------------------------------------------------------------
     const float mv = mvec;
@@ -576,25 +566,25 @@ using namespace kvexp_dev;
 
 template <int G, bool XKV>
 static hipError_t launch_wave_g(const HeadDev *heads, const WorkItem *items, int n_items, const float *q,
-                                float *out, float *lse, float *ws, uint32_t *status, hipStream_t s) {
+                                float *out, float *lse, float *ws, hipStream_t s) {
     const int grid = (n_items + wave::kWavesPerWg - 1) / wave::kWavesPerWg;
     hipLaunchKernelGGL((wave::attn_wave_kernel<G, XKV>), dim3(grid), dim3(wave::kWavesPerWg * 64), 0, s, heads,
-                       items, n_items, q, out, lse, ws, status);
+                       items, n_items, q, out, lse, ws);
     return hipGetLastError();
 }
 
 template <bool XKV>
 static hipError_t launch_wave_x(int G, const HeadDev *heads, const WorkItem *items, int n_items, const float *q,
-                                float *out, float *lse, float *ws, uint32_t *status, hipStream_t s) {
+                                float *out, float *lse, float *ws, hipStream_t s) {
     switch (G) {
-    case 1: return launch_wave_g<1, XKV>(heads, items, n_items, q, out, lse, ws, status, s);
-    case 2: return launch_wave_g<2, XKV>(heads, items, n_items, q, out, lse, ws, status, s);
-    case 3: return launch_wave_g<3, XKV>(heads, items, n_items, q, out, lse, ws, status, s);
-    case 4: return launch_wave_g<4, XKV>(heads, items, n_items, q, out, lse, ws, status, s);
-    case 5: return launch_wave_g<5, XKV>(heads, items, n_items, q, out, lse, ws, status, s);
-    case 6: return launch_wave_g<6, XKV>(heads, items, n_items, q, out, lse, ws, status, s);
-    case 7: return launch_wave_g<7, XKV>(heads, items, n_items, q, out, lse, ws, status, s);
-    case 8: return launch_wave_g<8, XKV>(heads, items, n_items, q, out, lse, ws, status, s);
+    case 1: return launch_wave_g<1, XKV>(heads, items, n_items, q, out, lse, ws, s);
+    case 2: return launch_wave_g<2, XKV>(heads, items, n_items, q, out, lse, ws, s);
+    case 3: return launch_wave_g<3, XKV>(heads, items, n_items, q, out, lse, ws, s);
+    case 4: return launch_wave_g<4, XKV>(heads, items, n_items, q, out, lse, ws, s);
+    case 5: return launch_wave_g<5, XKV>(heads, items, n_items, q, out, lse, ws, s);
+    case 6: return launch_wave_g<6, XKV>(heads, items, n_items, q, out, lse, ws, s);
+    case 7: return launch_wave_g<7, XKV>(heads, items, n_items, q, out, lse, ws, s);
+    case 8: return launch_wave_g<8, XKV>(heads, items, n_items, q, out, lse, ws, s);
     default: return hipErrorInvalidValue;
     }
 }
@@ -614,10 +604,10 @@ hipError_t wave_merge(const HeadDev *heads, const int2 *mitems, int n_mitems, fl
 }
 
 hipError_t attention_wave(bool xkv, int G, const HeadDev *heads, const WorkItem *items, int n_items,
-                          const float *q, float *out, float *lse, float *ws, uint32_t *status, hipStream_t s) {
+                          const float *q, float *out, float *lse, float *ws, hipStream_t s) {
     if (n_items <= 0) return hipSuccess;
-    return xkv ? launch_wave_x<true>(G, heads, items, n_items, q, out, lse, ws, status, s)
-               : launch_wave_x<false>(G, heads, items, n_items, q, out, lse, ws, status, s);
+    return xkv ? launch_wave_x<true>(G, heads, items, n_items, q, out, lse, ws, s)
+               : launch_wave_x<false>(G, heads, items, n_items, q, out, lse, ws, s);
 }
 
 } // namespace kvexp_launch

@@ -333,7 +333,10 @@ __global__ __launch_bounds__(kThreads) void encode_write_kernel(const uint16_t *
 
 // -------------------------------------------------- escape-position index --
 // esc0[b] = escape words in blocks before b (raw blocks count 0), one
-// workgroup per tensor.
+// workgroup per tensor. With j.desc set, every block is also checked against
+// the index (header inside the container, head_dim, n_tokens equal to the
+// index's token count, known mode, payload inside the container) and its
+// descriptor written.
 __global__ __launch_bounds__(kThreads) void esc_start_kernel(const EscJob *__restrict__ jobs,
                                                             uint32_t *__restrict__ status) {
     __shared__ int scan_tmp[kWaves];
@@ -342,18 +345,33 @@ __global__ __launch_bounds__(kThreads) void esc_start_kernel(const EscJob *__res
     for (int r = 0; r < j.n_blocks; r += kThreads) {
         const int b = r + int(threadIdx.x);
         int ne = 0;
+        BlockHdr h{};
+        uint32_t st = 0;
+        int64_t off = 0;
         if (b < j.n_blocks) {
-            const int64_t off = j.offs[b];
-            if (off >= 0 && uint64_t(off) + 8u <= j.bytes) {
-                const BlockHdr h = read_hdr(j.blob + off);
-                ne = h.mode == 0 ? 0 : h.n_escape;
+            off = j.offs[b];
+            if (j.desc != nullptr) {
+                st = check_block(j.blob, j.bytes, off, j.dim, j.first[b + 1] - j.first[b], &h);
+            } else if (off >= 0 && uint64_t(off) + 8u <= j.bytes) {
+                h = read_hdr(j.blob + off);
             } else {
-                atomicOr(status, kStHeader);
+                st = kStHeader;
             }
+            if (st != 0u) atomicOr(status, st);
+            else ne = h.mode == 0 ? 0 : h.n_escape;
         }
         int tot = 0;
         const int excl = block_excl_scan<kWaves>(ne, scan_tmp, &tot);
-        if (b < j.n_blocks) j.esc0[b] = carry + excl;
+        if (b < j.n_blocks) {
+            j.esc0[b] = carry + excl;
+            if (j.desc != nullptr) {
+                BlockDesc d;
+                d.data = j.blob + off;
+                d.esc0 = carry + excl;
+                d.meta = st != 0u ? 0u : uint32_t(h.mode) | (uint32_t(h.n_tokens) << 8) | (uint32_t(ne) << 16);
+                j.desc[b] = d;
+            }
+        }
         carry += tot;
     }
     if (threadIdx.x == 0) j.esc0[j.n_blocks] = carry;

@@ -22,10 +22,11 @@ struct HeadDev {
     const int64_t *koff, *voff;  // block byte offsets (n_blocks + 1)
     const int32_t *kfirst, *vfirst; // block first tokens (n_blocks + 1)
     const uint16_t *kraw, *vraw; // [seq, dim] BF16 (raw heads)
-    // Escape-position index (plan-owned, XKV heads of the wave kernel):
-    // block b's escape words are entries [esc0[b], esc0[b+1]) and escpos[k]
-    // is the element index (row * dim + channel) of entry k inside its block.
-    const int32_t *kesc0, *vesc0;
+    // Plan-owned, XKV heads of the wave kernel: validated block descriptors
+    // and the escape-position index (block b's escape words are entries
+    // [desc[b].esc0, desc[b].esc0 + n_escape) and escpos[k] is the element
+    // index (row * dim + channel) of entry k inside its block).
+    const struct BlockDesc *kdesc, *vdesc;
     const uint16_t *kescpos, *vescpos;
     int32_t seq;
     int32_t n_splits;            // work items of this head, in merge order
@@ -35,13 +36,23 @@ struct HeadDev {
     int32_t pad;
 };
 
-// One tensor (container + block index) for the escape-position index builders.
+// One block of a container as the wave kernel reads it, built and checked
+// against the block index once per plan (esc_start_kernel).
+struct BlockDesc {
+    const uint8_t *data; // the block's header
+    int32_t esc0;        // index of its first escape in the tensor's escape-position index
+    uint32_t meta;       // mode | n_tokens << 8 | n_escape << 16 (n_escape 0 for raw blocks)
+};
+
+// One tensor (container + block index) for the plan-time builders.
 struct EscJob {
     const uint8_t *blob;
     uint64_t bytes;
     const int64_t *offs;
-    int32_t *esc0;      // out: n_blocks + 1 entries
-    uint16_t *pos;      // out: esc0[n_blocks] entries
+    const int32_t *first; // block first tokens (n_blocks + 1)
+    int32_t *esc0;        // out: n_blocks + 1 entries
+    uint16_t *pos;        // out: esc0[n_blocks] entries
+    BlockDesc *desc;      // out: n_blocks entries (nullable)
     int32_t n_blocks;
     int32_t dim;
 };

@@ -36,7 +36,7 @@ hipError_t esc_start(const kvexp_dev::EscJob *jobs, int n_jobs, uint32_t *status
 hipError_t esc_pos(const kvexp_dev::EscJob *jobs, const int2 *blocks, int n_blocks, uint32_t *status, hipStream_t s);
 hipError_t q_widen(const HeadDev *heads, int n_heads, const uint16_t *q, float *q32, hipStream_t s);
 hipError_t attention_wave(bool xkv, int G, const HeadDev *heads, const WorkItem *items, int n_items,
-                          const float *q, float *out, float *lse, float *ws, uint32_t *status, hipStream_t s);
+                          const float *q, float *out, float *lse, float *ws, hipStream_t s);
 hipError_t wave_merge(const HeadDev *heads, const int2 *mitems, int n_mitems, float *out, float *lse, const float *ws,
                       hipStream_t s);
 } // namespace kvexp_launch
@@ -197,7 +197,8 @@ struct kvexp_hip_plan {
     bool xkv = false;
     bool wave = false; // one-wave-per-split kernel (dim 64, scalar order)
     DevBuf heads, items, merge_ids, ws, status;
-    DevBuf mitems, esc0, escpos, q32; // wave kernel: merge work (head, row), escape-position index, FP32 q
+    // wave kernel: merge work (head, row), escape-position index, block descriptors, FP32 q
+    DevBuf mitems, esc0, escpos, desc, q32;
     int n_mitems = 0;
     int n_dev_heads = 0, n_items = 0, n_merge = 0;
     // wave kernel: items sorted by query-row count G; group_start[G] .. group_start[G+1]
@@ -245,10 +246,12 @@ void check_status_word(uint32_t *d_status, hipStream_t s) {
         fail(KVEXP_HIP_FORMAT_ERROR, status_message(st));
     }
 }
-// Escape-position index of every XKV tensor of a plan: per block the first
-// escape's index (esc0) and per escape its element index inside the block.
-// Built on the device from the containers, once per plan; the device heads
-// of one user head share it.
+// Block descriptors and escape-position index of every XKV tensor of a plan:
+// per block its address, first escape index and header fields (checked
+// against the block index; a mismatch fails the plan with the matching
+// format error), and per escape its element index inside the block. Built on
+// the device from the containers, once per plan; the device heads of one
+// user head share it.
 void build_escape_index(kvexp_hip_plan &p, const kvexp_hip_head *heads, int n_heads, int n_q, int dim,
                         std::vector<HeadDev> &hv) {
     std::vector<kvexp_dev::EscJob> jobs;
@@ -260,6 +263,7 @@ void build_escape_index(kvexp_hip_plan &p, const kvexp_hip_head *heads, int n_he
             j.blob = kv ? heads[h].v_xkv : heads[h].k_xkv;
             j.bytes = kv ? heads[h].v_bytes : heads[h].k_bytes;
             j.offs = kv ? heads[h].v_offsets : heads[h].k_offsets;
+            j.first = kv ? heads[h].v_first_token : heads[h].k_first_token;
             j.n_blocks = kv ? heads[h].v_n_blocks : heads[h].k_n_blocks;
             j.dim = dim;
             e0_at.push_back(e0_total);
@@ -268,7 +272,11 @@ void build_escape_index(kvexp_hip_plan &p, const kvexp_hip_head *heads, int n_he
         }
     }
     p.esc0 = DevBuf(e0_total * sizeof(int32_t));
-    for (size_t i = 0; i < jobs.size(); ++i) jobs[i].esc0 = p.esc0.as<int32_t>() + e0_at[i];
+    p.desc = DevBuf(e0_total * sizeof(kvexp_dev::BlockDesc));
+    for (size_t i = 0; i < jobs.size(); ++i) {
+        jobs[i].esc0 = p.esc0.as<int32_t>() + e0_at[i];
+        jobs[i].desc = p.desc.as<kvexp_dev::BlockDesc>() + e0_at[i];
+    }
     DevBuf djobs(jobs.size() * sizeof(kvexp_dev::EscJob));
     HIPX(hipMemcpy(djobs.p, jobs.data(), jobs.size() * sizeof(kvexp_dev::EscJob), hipMemcpyHostToDevice));
     uint32_t *st = p.ctx->status.as<uint32_t>();
@@ -295,9 +303,9 @@ void build_escape_index(kvexp_hip_plan &p, const kvexp_hip_head *heads, int n_he
     for (int h = 0; h < n_heads; ++h) {
         for (int c = 0; c < per_head; ++c) {
             HeadDev &d = hv[size_t(h * per_head + c)];
-            d.kesc0 = jobs[size_t(2 * h)].esc0;
+            d.kdesc = jobs[size_t(2 * h)].desc;
             d.kescpos = jobs[size_t(2 * h)].pos;
-            d.vesc0 = jobs[size_t(2 * h + 1)].esc0;
+            d.vdesc = jobs[size_t(2 * h + 1)].desc;
             d.vescpos = jobs[size_t(2 * h + 1)].pos;
         }
     }
@@ -644,7 +652,7 @@ int kvexp_hip_attention_run(kvexp_hip_plan *plan, const uint16_t *d_q, float *d_
                     HIPX(kvexp_launch::attention_wave(plan->xkv, G, plan->heads.as<HeadDev>(),
                                                       plan->items.as<WorkItem>() + b, e - b, plan->q32.as<float>(),
                                                       d_out, d_lse,
-                                                      plan->ws.as<float>(), plan->status.as<uint32_t>(), s));
+                                                      plan->ws.as<float>(), s));
             }
             if (ev1) HIPX(hipEventRecord(ev1, s));
             HIPX(kvexp_launch::wave_merge(plan->heads.as<HeadDev>(), plan->mitems.as<int2>(), plan->n_mitems, d_out,

@@ -140,6 +140,61 @@ def test_many_heads_variable_length(ctx, oracle):
     assert np.allclose(lse_raw, lse_want, rtol=1e-6, atol=1e-6)
 
 
+def _escape_heavy_kv(rng, seq, dim, frac, narrow=False):
+    """K with a fraction `frac` of elements pushed 2^8..2^14 away from their
+    channel's exponent window, so that coded blocks carry many escapes
+    (`narrow`: values within three binades, so blocks pick 2-bit codes)."""
+    if narrow:
+        x = (rng.uniform(1.0, 7.9, (seq, dim)) * rng.choice([-0.25, 0.25], (seq, dim))).astype(np.float32)
+        k = bf16_from_f32(x.reshape(-1))
+    else:
+        k = random_kv(rng, seq, dim, spread_lo=-3, spread_hi=3)
+    x = (k.astype(np.uint32) << 16).view(np.float32).reshape(seq, dim).copy()
+    hit = rng.random((seq, dim)) < frac
+    x[hit] *= np.exp2(rng.integers(8, 15, size=int(hit.sum())) * rng.choice([-1, 1], size=int(hit.sum())))
+    return bf16_from_f32(x.reshape(-1))
+
+
+def _max_block_escapes(oracle, blob, dim, seq):
+    offs, first = oracle.block_index(blob, dim, seq)
+    hdr = np.asarray(blob)[np.asarray(offs[:-1])[:, None] + np.arange(4)[None, :]].astype(np.int64)
+    coded = hdr[:, 0] != 0
+    esc = hdr[:, 2] | (hdr[:, 3] << 8)
+    return int(esc[coded].max()) if coded.any() else 0
+
+
+def test_wave_kernel_groups_and_escapes(ctx, oracle):
+    """The head_dim-64 one-wave kernel for every query-row count G it is
+    instantiated for, on containers whose blocks carry from 0 to several
+    hundred escapes (blocks with more than 64 read the escape index in
+    windows), block sizes that do and do not split into 64-token chunks,
+    ragged lengths and several splits per head."""
+    rng = np.random.default_rng(4242)
+    dim = 64
+    seen_big = False
+    cases = [(1, 128, 0.05, False), (2, 255, 0.02, False), (3, 100, 0.0, False), (7, 128, 0.3, False),
+             (8, 64, 0.01, False), (5, 128, 0.002, True), (7, 255, 0.1, True), (11, 128, 0.05, False),
+             (4, 128, 0.6, False), (6, 128, 0.0, True)]
+    for trial, (n_q, block, frac, narrow) in enumerate(cases):
+        heads = []
+        for h in range(3):
+            seq = int(rng.integers(1, 1500))
+            k = _escape_heavy_kv(rng, seq, dim, frac, narrow)
+            v = _escape_heavy_kv(rng, seq, dim, frac / 2, narrow)
+            heads.append(dict(k=k, v=v, seq=seq, splits=int(rng.integers(1, 7)), block=block))
+            if frac:
+                seen_big |= _max_block_escapes(oracle, oracle.encode(k, seq, dim, block), dim, seq) > 64
+        q = random_kv(rng, len(heads) * n_q, dim, spread_lo=-1, spread_hi=1)
+        say("wave kernel", trial, dict(n_q=n_q, block=block, frac=frac, narrow=narrow, seqs=[h["seq"] for h in heads]))
+        want = oracle.attention_heads("scalar", q, [dict(k=h["k"], v=h["v"], seq=h["seq"], threads=h["splits"])
+                                                    for h in heads], n_q=n_q, dim=dim, split=block)
+        raw = run_gpu(ctx, 0, q, heads, n_q, dim, block, False)
+        xkv = run_gpu(ctx, 0, q, heads, n_q, dim, block, True)
+        assert bits_equal(raw, xkv), trial
+        assert bits_equal(raw, want), (trial, max_rel_err(raw, want))
+    assert seen_big
+
+
 def test_host_entry_backend_hip(ctx, oracle, golden):
     """kvexp_hip_attention_decode_host: the attention_decode argument list with
     host pointers (the Backend::Hip case of dispatch.cpp)."""
