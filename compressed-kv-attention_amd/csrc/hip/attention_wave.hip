@@ -37,7 +37,7 @@ constexpr int kTileStride = 144; // bytes per tile row: 64 BF16 + 16 (conflict-f
 constexpr int kWavesPerWg = 4;
 constexpr int kSlotQ = 8;       // partial-state slot: m[8], l[8], acc[8][64]
 constexpr int kSlotFloats = kSlotQ * (kD + 2);
-constexpr int kMergeBatch = 32; // split slots whose loads are in flight together in the merge
+constexpr int kMergeBatch = 128; // split slots whose loads are in flight together in the merge
 
 struct WaveLds {
     uint8_t tile[kChunk * kTileStride];
@@ -536,21 +536,30 @@ __global__ __launch_bounds__(kWavesPerWg * 64) void wave_merge_kernel(
 #pragma unroll
         for (int j = 0; j < kMergeBatch; ++j)
             ab[j] = slots[size_t(s0 + min(j, cnt - 1)) * kSlotFloats + 2 * kSlotQ + g * kD + lane];
-        // lane = split s0 + lane: running maximum and the two exponentials
-        const float *ls = slots + size_t(s0 + min(lane, cnt - 1)) * kSlotFloats;
-        const float ms = lane < cnt ? ls[g] : -__builtin_inff();
-        const float lb = ls[kSlotQ + g];
-        const float mm = fmaxf(wave_scan_max(ms), mf);
-        const float mprev = wave_shift_up(mm, mf);
-        const float e1 = kvexp_expf_tab_nb(mprev - mm, tab); // scale of the running state
-        const float e2 = kvexp_expf_tab_nb(ms - mm, tab);    // scale of split s0 + lane
-        mf = readlane_f32(mm, cnt - 1);
+        float ms[kMergeBatch / 64], lb[kMergeBatch / 64];
 #pragma unroll
-        for (int j = 0; j < kMergeBatch; ++j) {
-            if (j < cnt) {
-                const float x1 = readlane_f32(e1, j), x2 = readlane_f32(e2, j);
-                a = fmaf(a, x1, ab[j] * x2);
-                lf = fmaf(lf, x1, readlane_f32(lb, j) * x2);
+        for (int h = 0; h < kMergeBatch / 64; ++h) {
+            const int j = 64 * h + lane;
+            const float *ls = slots + size_t(s0 + min(j, cnt - 1)) * kSlotFloats;
+            ms[h] = j < cnt ? ls[g] : -__builtin_inff();
+            lb[h] = ls[kSlotQ + g];
+        }
+#pragma unroll
+        for (int h = 0; h < kMergeBatch / 64; ++h) {
+            if (64 * h >= cnt) break;
+            // lane = split s0 + 64h + lane: running maximum and the two exponentials
+            const float mm = fmaxf(wave_scan_max(ms[h]), mf);
+            const float mprev = wave_shift_up(mm, mf);
+            const float e1 = kvexp_expf_tab_nb(mprev - mm, tab); // scale of the running state
+            const float e2 = kvexp_expf_tab_nb(ms[h] - mm, tab); // scale of split s0 + 64h + lane
+            mf = readlane_f32(mm, min(64, cnt - 64 * h) - 1);
+#pragma unroll
+            for (int jj = 0; jj < 64; ++jj) {
+                if (64 * h + jj < cnt) {
+                    const float x1 = readlane_f32(e1, jj), x2 = readlane_f32(e2, jj);
+                    a = fmaf(a, x1, ab[64 * h + jj] * x2);
+                    lf = fmaf(lf, x1, readlane_f32(lb[h], jj) * x2);
+                }
             }
         }
     }
