@@ -41,8 +41,7 @@ constexpr int kMergeBatch = 128; // split slots whose loads are in flight togeth
 
 struct WaveLds {
     uint8_t tile[kChunk * kTileStride];
-    float e[kChunk][8];
-    float a[kChunk][8];
+    float e[kChunk][8];  // e of token t, row g
     uint32_t bp[kD / 2]; // base pair words of the block being decoded
 };
 
@@ -433,14 +432,13 @@ __global__ __launch_bounds__(kWavesPerWg * 64) void attn_wave_kernel(
         for (int g = 0; g < 8; ++g) ev[g] = g < G ? kvexp_expf_tab_nb(s[g < G ? g : 0] - mi[g < G ? g : 0], tab) : 0.0f;
         *reinterpret_cast<float4 *>(&S.e[lane][0]) = make_float4(ev[0], ev[1], ev[2], ev[3]);
         if (G > 4) *reinterpret_cast<float4 *>(&S.e[lane][4]) = make_float4(ev[4], ev[5], ev[6], ev[7]);
-        // tokens (bits) where some row's running maximum moves: alpha != 1
+        // tokens (bits) where some row's running maximum moves: alpha != 1;
+        // alpha stays in registers (lane = token) for the few tokens that need it
         const uint64_t rmask0 = __ballot(lane < n && nz);
+        float alpha[G];
         if (rmask0 != 0) {
-            float av[8];
 #pragma unroll
-            for (int g = 0; g < 8; ++g) av[g] = g < G ? kvexp_expf_tab_nb(d[g < G ? g : 0], tab) : 1.0f;
-            *reinterpret_cast<float4 *>(&S.a[lane][0]) = make_float4(av[0], av[1], av[2], av[3]);
-            if (G > 4) *reinterpret_cast<float4 *>(&S.a[lane][4]) = make_float4(av[4], av[5], av[6], av[7]);
+            for (int g = 0; g < G; ++g) alpha[g] = kvexp_expf_tab_nb(d[g], tab);
         }
 #pragma unroll
         for (int g = 0; g < G; ++g) {
@@ -473,13 +471,16 @@ __global__ __launch_bounds__(kWavesPerWg * 64) void attn_wave_kernel(
                 const float v = __uint_as_float(uint32_t(vt[tok * (kTileStride / 2) + lane]) << 16);
                 const float4 e0 = *reinterpret_cast<const float4 *>(&S.e[tok][0]);
                 const float4 e1 = *reinterpret_cast<const float4 *>(&S.e[tok][4]);
-                const float4 a0 = *reinterpret_cast<const float4 *>(&S.a[tok][0]);
-                const float4 a1 = *reinterpret_cast<const float4 *>(&S.a[tok][4]);
                 const float ev[8] = {e0.x, e0.y, e0.z, e0.w, e1.x, e1.y, e1.z, e1.w};
-                const float av[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+                float av[G];
+#pragma unroll
+                for (int g = 0; g < G; ++g) av[g] = readlane_f32(alpha[g], tok);
 #pragma unroll
                 for (int g = 0; g < G; ++g) acc[g] = fmaf(ev[g], v, acc[g] * av[g]);
-                lvec = fmaf(lvec, S.a[tok][lane & 7], S.e[tok][lane & 7]);
+                float al = av[0]; // lane g < G: alpha of row g
+#pragma unroll
+                for (int g = 1; g < G; ++g) al = lane == g ? av[g] : al;
+                lvec = fmaf(lvec, al, S.e[tok][lane & 7]);
             }
             rmask &= rmask - 1;
             tok = stop + 1;
