@@ -37,6 +37,7 @@ constexpr int kTileStride = 144; // bytes per tile row: 64 BF16 + 16 (conflict-f
 constexpr int kWavesPerWg = 4;
 constexpr int kSlotQ = 8;       // partial-state slot: m[8], l[8], acc[8][64]
 constexpr int kSlotFloats = kSlotQ * (kD + 2);
+constexpr int kRowRegs = 6;     // 16-byte registers per prefetched XKV row (coded rows need at most 6)
 constexpr int kMergeBatch = 128; // split slots whose loads are in flight together in the merge
 
 struct WaveLds {
@@ -120,15 +121,15 @@ __device__ __forceinline__ void open_block(Cursor &c, int b, int t0) {
 }
 
 // Loads rows [r0 + lane] of the cursor's block (lanes < rows) into R.
-__device__ __forceinline__ void load_rows(const Cursor &c, int r0, int rows, uint4 (&R)[8]) {
+__device__ __forceinline__ void load_rows(const Cursor &c, int r0, int rows, uint4 (&R)[kRowRegs]) {
     const int lane = lane_id();
     if (lane >= rows) return;
     const int r = r0 + lane;
     const uint8_t *p = c.blk + 8;
-    if (c.mode == 0) {
+    if (c.mode == 0) { // the first 96 of the row's 128 bytes; decode_row loads the rest
         const uint8_t *row = p + size_t(r) * (2 * kD);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) R[i] = ld16(row + 16 * i);
+        for (int i = 0; i < kRowRegs; ++i) R[i] = ld16(row + 16 * i);
         return;
     }
     const uint8_t *sm = p + kD + size_t(r) * kD;
@@ -168,11 +169,18 @@ __device__ __forceinline__ uint32_t pair4(uint32_t sw, int lb, uint32_t lo, uint
 }
 
 // Decodes the lane's row held in R (cursor's block mode) into its tile row.
-__device__ __forceinline__ void decode_row(const Cursor &c, const uint4 (&R)[8], const uint32_t *bp, uint8_t *row) {
+__device__ __forceinline__ void decode_row(const Cursor &c, const uint4 (&R)[kRowRegs], const uint32_t *bp,
+                                           uint8_t *row, int r0, int rows) {
     uint4 *dst = reinterpret_cast<uint4 *>(row);
     if (c.mode == 0) {
+        const int lane = lane_id();
+        if (lane < rows) {
+            const uint8_t *src = c.blk + 8 + size_t(r0 + lane) * (2 * kD);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) dst[i] = R[i];
+            for (int i = 0; i < kRowRegs; ++i) dst[i] = R[i];
+            dst[6] = ld16(src + 96);
+            dst[7] = ld16(src + 112);
+        }
         return;
     }
 #pragma unroll
@@ -296,8 +304,11 @@ __global__ __launch_bounds__(256) void q_widen_kernel(const HeadDev *__restrict_
         q32[size_t(blockIdx.x) * kSlotQ * kD + i] = __uint_as_float(uint32_t(q_all[size_t(hd.q_row) * kD + i]) << 16);
 }
 
+// XKV instantiations are held to three waves per SIMD (168 VGPRs; a few
+// loop-invariant lane addresses then live in scratch and are reloaded only
+// on the rare paths that use them); LDS allows three workgroups per CU.
 template <int G, bool XKV>
-__global__ __launch_bounds__(kWavesPerWg * 64) void attn_wave_kernel(
+__global__ __launch_bounds__(kWavesPerWg * 64) __attribute__((amdgpu_waves_per_eu(XKV ? 3 : 2))) void attn_wave_kernel(
     const HeadDev *__restrict__ heads, const WorkItem *__restrict__ items, int n_items,
     const float *__restrict__ q32_all, float *__restrict__ out_all, float *__restrict__ lse_all,
     float *__restrict__ ws) {
@@ -322,9 +333,9 @@ __global__ __launch_bounds__(kWavesPerWg * 64) void attn_wave_kernel(
     float lvec = 0.0f;              // lane g < G holds l of query row g
 
     Cursor kc{}, vc{};
-    uint4 RK[8], RV[8];
+    uint4 RK[XKV ? kRowRegs : 8], RV[XKV ? kRowRegs : 8];
     int t = wi.tok_begin;
-    if (XKV) {
+    if constexpr (XKV) {
         kc.desc = hd.kdesc;
         kc.escpos = hd.kescpos;
         vc.desc = hd.vdesc;
@@ -349,17 +360,17 @@ __global__ __launch_bounds__(kWavesPerWg * 64) void attn_wave_kernel(
 
     while (t < wi.tok_end) {
         int n = min(kChunk, wi.tok_end - t);
-        if (XKV) n = min(n, min(kc.t1 - t, vc.t1 - t));
+        if constexpr (XKV) n = min(n, min(kc.t1 - t, vc.t1 - t));
         if (n <= 0) break; // unreachable with plan-checked descriptors (n_tokens > 0)
         const int tn = t + n;
 
         // 1. K rows -> tile
-        if (XKV) {
+        if constexpr (XKV) {
             if (kc.mode != 0) {
                 base_pairs(kc.blk + 8, S.bp);
                 wave_sync();
             }
-            decode_row(kc, RK, S.bp, my_row);
+            decode_row(kc, RK, S.bp, my_row, t - kc.t0, n);
             wave_sync();
             patch_escapes(kc, t - kc.t0, n, S.tile);
         } else {
@@ -370,36 +381,28 @@ __global__ __launch_bounds__(kWavesPerWg * 64) void attn_wave_kernel(
         wave_sync();
 
         // 2. scores, lane = token (an opaque copy of the q address per chunk
-        // keeps the q loads inside the loop); then the next chunk's K rows are
-        // requested, so RK is not live across the score registers
+        // keeps the q loads inside the loop)
         float s[G];
         uint64_t qa = reinterpret_cast<uint64_t>(q32);
         asm volatile("" : "+s"(qa));
         scores<G>(my_row, qa, s);
-        if (XKV) {
-            if (tn < wi.tok_end) {
-                if (tn >= kc.t1) open_block(kc, kc.b + 1, kc.t1);
-                load_rows(kc, tn - kc.t0, min(kChunk, min(kc.t1, wi.tok_end) - tn), RK);
-            }
-        } else if (tn < wi.tok_end && lane < min(kChunk, wi.tok_end - tn)) {
-            const uint8_t *kr = reinterpret_cast<const uint8_t *>(hd.kraw + size_t(tn + lane) * kD);
-#pragma unroll
-            for (int i = 0; i < 8; ++i) RK[i] = ld16(kr + 16 * i);
-        }
         wave_sync();
 
-        // 3. V rows -> tile; prefetch the next chunk's V rows
-        if (XKV) {
+        // 3. V rows -> tile; request the next chunk's V and K rows (RK and RV
+        // are then not live across the score and decode registers)
+        if constexpr (XKV) {
             if (vc.mode != 0) {
                 base_pairs(vc.blk + 8, S.bp);
                 wave_sync();
             }
-            decode_row(vc, RV, S.bp, my_row);
+            decode_row(vc, RV, S.bp, my_row, t - vc.t0, n);
             wave_sync();
             patch_escapes(vc, t - vc.t0, n, S.tile);
             if (tn < wi.tok_end) {
                 if (tn >= vc.t1) open_block(vc, vc.b + 1, vc.t1);
                 load_rows(vc, tn - vc.t0, min(kChunk, min(vc.t1, wi.tok_end) - tn), RV);
+                if (tn >= kc.t1) open_block(kc, kc.b + 1, kc.t1);
+                load_rows(kc, tn - kc.t0, min(kChunk, min(kc.t1, wi.tok_end) - tn), RK);
             }
         } else {
             uint4 *dst = reinterpret_cast<uint4 *>(my_row);
@@ -407,8 +410,12 @@ __global__ __launch_bounds__(kWavesPerWg * 64) void attn_wave_kernel(
             for (int i = 0; i < 8; ++i) dst[i] = RV[i];
             if (tn < wi.tok_end && lane < min(kChunk, wi.tok_end - tn)) {
                 const uint8_t *vr = reinterpret_cast<const uint8_t *>(hd.vraw + size_t(tn + lane) * kD);
+                const uint8_t *kr = reinterpret_cast<const uint8_t *>(hd.kraw + size_t(tn + lane) * kD);
 #pragma unroll
-                for (int i = 0; i < 8; ++i) RV[i] = ld16(vr + 16 * i);
+                for (int i = 0; i < 8; ++i) {
+                    RV[i] = ld16(vr + 16 * i);
+                    RK[i] = ld16(kr + 16 * i);
+                }
             }
         }
 
