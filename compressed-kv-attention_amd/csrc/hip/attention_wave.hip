@@ -85,37 +85,37 @@ __device__ __forceinline__ uint32_t ldu16(const uint8_t *p) { return *(g_u16 *)(
 // wave-uniform; epos / eval hold the current block's first 64 escapes (lane
 // k: element index and word of escape k; epos = ~0 past the last).
 struct Cursor {
-    const BlockDesc *desc;
-    const uint16_t *escpos;
-    const uint8_t *blk; // current block's header
-    int b, t0, t1;      // block index and its token range
-    int mode, ntok, nesc;
-    int eb;             // index of the block's first escape in escpos
+    const BlockDesc *d;  // descriptor of the current block (the next one follows it)
+    const uint8_t *blk;  // current block's header
+    const uint16_t *esc; // its escape positions
+    int t0, t1;          // its token range
+    uint32_t meta;       // mode | n_tokens << 8 | n_escape << 16
     uint32_t epos, eval;
+    __device__ int mode() const { return int(meta & 0xFFu); }
+    __device__ int ntok() const { return int((meta >> 8) & 0xFFu); }
+    __device__ int nesc() const { return int(meta >> 16); }
 };
 
 __device__ __forceinline__ const uint8_t *esc_words(const Cursor &c) {
-    return c.blk + 8 + kD + size_t(c.ntok) * kD + exp_payload_bytes(c.ntok, kD, c.mode);
+    return c.blk + 8 + kD + size_t(c.ntok()) * kD + exp_payload_bytes(c.ntok(), kD, c.mode());
 }
 
-// Enters block b, whose first token is t0: one scalar load of its
-// descriptor (checked against the container when the plan was built), then
-// the positions and words of its first 64 escapes.
-__device__ __forceinline__ void open_block(Cursor &c, int b, int t0) {
-    const BlockDesc d = load_scalar(c.desc + b);
-    c.b = b;
-    c.blk = d.data;
-    c.mode = int(d.meta & 0xFFu);
-    c.ntok = int((d.meta >> 8) & 0xFFu);
-    c.nesc = int(d.meta >> 16);
-    c.eb = d.esc0;
+// Enters the block of descriptor d, whose first token is t0: one scalar load
+// of the descriptor (checked against the container when the plan was built),
+// then the positions and words of the block's first 64 escapes.
+__device__ __forceinline__ void open_block(Cursor &c, const BlockDesc *d, int t0) {
+    const BlockDesc bd = load_scalar(d);
+    c.d = d;
+    c.blk = bd.data;
+    c.esc = bd.esc;
+    c.meta = __builtin_amdgcn_readfirstlane(bd.meta);
     c.t0 = t0;
-    c.t1 = t0 + c.ntok;
+    c.t1 = t0 + c.ntok();
     c.epos = 0xFFFFFFFFu;
     c.eval = 0u;
     const int lane = lane_id();
-    if (lane < c.nesc) {
-        c.epos = *(g_u16 *)(c.escpos + c.eb + lane);
+    if (lane < c.nesc()) {
+        c.epos = *(g_u16 *)(c.esc + lane);
         c.eval = ldu16(esc_words(c) + 2 * lane);
     }
 }
@@ -126,7 +126,7 @@ __device__ __forceinline__ void load_rows(const Cursor &c, int r0, int rows, uin
     if (lane >= rows) return;
     const int r = r0 + lane;
     const uint8_t *p = c.blk + 8;
-    if (c.mode == 0) { // the first 96 of the row's 128 bytes; decode_row loads the rest
+    if (c.mode() == 0) { // the first 96 of the row's 128 bytes; decode_row loads the rest
         const uint8_t *row = p + size_t(r) * (2 * kD);
 #pragma unroll
         for (int i = 0; i < kRowRegs; ++i) R[i] = ld16(row + 16 * i);
@@ -135,8 +135,8 @@ __device__ __forceinline__ void load_rows(const Cursor &c, int r0, int rows, uin
     const uint8_t *sm = p + kD + size_t(r) * kD;
 #pragma unroll
     for (int i = 0; i < 4; ++i) R[i] = ld16(sm + 16 * i);
-    const uint8_t *codes = p + kD + size_t(c.ntok) * kD;
-    if (c.mode == 4) {
+    const uint8_t *codes = p + kD + size_t(c.ntok()) * kD;
+    if (c.mode() == 4) {
         R[4] = ld16(codes + size_t(r) * (kD / 2));
         R[5] = ld16(codes + size_t(r) * (kD / 2) + 16);
     } else {
@@ -172,7 +172,7 @@ __device__ __forceinline__ uint32_t pair4(uint32_t sw, int lb, uint32_t lo, uint
 __device__ __forceinline__ void decode_row(const Cursor &c, const uint4 (&R)[kRowRegs], const uint32_t *bp,
                                            uint8_t *row, int r0, int rows) {
     uint4 *dst = reinterpret_cast<uint4 *>(row);
-    if (c.mode == 0) {
+    if (c.mode() == 0) {
         const int lane = lane_id();
         if (lane < rows) {
             const uint8_t *src = c.blk + 8 + size_t(r0 + lane) * (2 * kD);
@@ -188,7 +188,7 @@ __device__ __forceinline__ void decode_row(const Cursor &c, const uint4 (&R)[kRo
         const uint32_t s0 = comp(R[dg >> 1], (dg & 1) * 2);
         const uint32_t s1 = comp(R[dg >> 1], (dg & 1) * 2 + 1);
         uint32_t lo, hi;
-        if (c.mode == 4) {
+        if (c.mode() == 4) {
             const uint32_t cw = comp(R[4 + (dg >> 2)], dg & 3);
             lo = cw & 0x0F0F0F0Fu;
             hi = (cw >> 4) & 0x0F0F0F0Fu;
@@ -214,19 +214,20 @@ __device__ __forceinline__ void decode_row(const Cursor &c, const uint4 (&R)[kRo
 // with the block, any further ones (blocks with more than 64) loaded here in
 // windows of 64. Positions ascend within a block.
 __device__ __forceinline__ void patch_escapes(const Cursor &c, int r0, int n, uint8_t *tile) {
-    if (c.nesc == 0) return;
+    const int nesc = c.nesc();
+    if (nesc == 0) return;
     const uint32_t lo = uint32_t(r0 * kD), hi = uint32_t((r0 + n) * kD);
     if (c.epos >= lo && c.epos < hi) {
         const uint32_t row = c.epos / kD - uint32_t(r0), col = c.epos % kD;
         *reinterpret_cast<uint16_t *>(tile + row * kTileStride + col * 2) = uint16_t(c.eval);
     }
-    if (c.nesc <= kWave) return;
+    if (nesc <= kWave) return;
     const int lane = lane_id();
     const uint8_t *esc = esc_words(c);
-    for (int k0 = kWave; k0 < c.nesc; k0 += kWave) {
+    for (int k0 = kWave; k0 < nesc; k0 += kWave) {
         const int k = k0 + lane;
         uint32_t pos = 0xFFFFFFFFu;
-        if (k < c.nesc) pos = *(g_u16 *)(c.escpos + c.eb + k);
+        if (k < nesc) pos = *(g_u16 *)(c.esc + k);
         if (pos >= lo && pos < hi) {
             const uint32_t row = pos / kD - uint32_t(r0), col = pos % kD;
             *reinterpret_cast<uint16_t *>(tile + row * kTileStride + col * 2) = uint16_t(ldu16(esc + 2 * size_t(k)));
@@ -336,12 +337,8 @@ __global__ __launch_bounds__(kWavesPerWg * 64) __attribute__((amdgpu_waves_per_e
     uint4 RK[XKV ? kRowRegs : 8], RV[XKV ? kRowRegs : 8];
     int t = wi.tok_begin;
     if constexpr (XKV) {
-        kc.desc = hd.kdesc;
-        kc.escpos = hd.kescpos;
-        vc.desc = hd.vdesc;
-        vc.escpos = hd.vescpos;
-        open_block(kc, wi.kblk, t);
-        open_block(vc, wi.vblk, t);
+        open_block(kc, hd.kdesc + wi.kblk, t);
+        open_block(vc, hd.vdesc + wi.vblk, t);
         load_rows(kc, 0, min(kChunk, min(kc.t1, wi.tok_end) - t), RK);
         load_rows(vc, 0, min(kChunk, min(vc.t1, wi.tok_end) - t), RV);
     } else {
@@ -366,7 +363,7 @@ __global__ __launch_bounds__(kWavesPerWg * 64) __attribute__((amdgpu_waves_per_e
 
         // 1. K rows -> tile
         if constexpr (XKV) {
-            if (kc.mode != 0) {
+            if (kc.mode() != 0) {
                 base_pairs(kc.blk + 8, S.bp);
                 wave_sync();
             }
@@ -391,7 +388,7 @@ __global__ __launch_bounds__(kWavesPerWg * 64) __attribute__((amdgpu_waves_per_e
         // 3. V rows -> tile; request the next chunk's V and K rows (RK and RV
         // are then not live across the score and decode registers)
         if constexpr (XKV) {
-            if (vc.mode != 0) {
+            if (vc.mode() != 0) {
                 base_pairs(vc.blk + 8, S.bp);
                 wave_sync();
             }
@@ -399,9 +396,9 @@ __global__ __launch_bounds__(kWavesPerWg * 64) __attribute__((amdgpu_waves_per_e
             wave_sync();
             patch_escapes(vc, t - vc.t0, n, S.tile);
             if (tn < wi.tok_end) {
-                if (tn >= vc.t1) open_block(vc, vc.b + 1, vc.t1);
+                if (tn >= vc.t1) open_block(vc, vc.d + 1, vc.t1);
                 load_rows(vc, tn - vc.t0, min(kChunk, min(vc.t1, wi.tok_end) - tn), RV);
-                if (tn >= kc.t1) open_block(kc, kc.b + 1, kc.t1);
+                if (tn >= kc.t1) open_block(kc, kc.d + 1, kc.t1);
                 load_rows(kc, tn - kc.t0, min(kChunk, min(kc.t1, wi.tok_end) - tn), RK);
             }
         } else {
@@ -462,7 +459,7 @@ __global__ __launch_bounds__(kWavesPerWg * 64) __attribute__((amdgpu_waves_per_e
         uint64_t rmask = rmask0;
         int tok = 0;
         while (true) {
-            const int stop = rmask != 0 ? int(__builtin_ctzll(rmask)) : n;
+            const int stop = __builtin_amdgcn_readfirstlane(rmask != 0 ? int(__builtin_ctzll(rmask)) : n);
 #pragma unroll 4
             for (; tok < stop; ++tok) {
                 const float v = __uint_as_float(uint32_t(vt[tok * (kTileStride / 2) + lane]) << 16);

@@ -333,10 +333,10 @@ __global__ __launch_bounds__(kThreads) void encode_write_kernel(const uint16_t *
 
 // -------------------------------------------------- escape-position index --
 // esc0[b] = escape words in blocks before b (raw blocks count 0), one
-// workgroup per tensor. With j.desc set, every block is also checked against
+// workgroup per tensor. With j.first set, every block is also checked against
 // the index (header inside the container, head_dim, n_tokens equal to the
-// index's token count, known mode, payload inside the container) and its
-// descriptor written.
+// index's token count, known mode, payload inside the container); with
+// j.desc set (and j.pos allocated), its descriptor is written.
 __global__ __launch_bounds__(kThreads) void esc_start_kernel(const EscJob *__restrict__ jobs,
                                                             uint32_t *__restrict__ status) {
     __shared__ int scan_tmp[kWaves];
@@ -350,7 +350,7 @@ __global__ __launch_bounds__(kThreads) void esc_start_kernel(const EscJob *__res
         int64_t off = 0;
         if (b < j.n_blocks) {
             off = j.offs[b];
-            if (j.desc != nullptr) {
+            if (j.first != nullptr) {
                 st = check_block(j.blob, j.bytes, off, j.dim, j.first[b + 1] - j.first[b], &h);
             } else if (off >= 0 && uint64_t(off) + 8u <= j.bytes) {
                 h = read_hdr(j.blob + off);
@@ -365,9 +365,9 @@ __global__ __launch_bounds__(kThreads) void esc_start_kernel(const EscJob *__res
         if (b < j.n_blocks) {
             j.esc0[b] = carry + excl;
             if (j.desc != nullptr) {
-                BlockDesc d;
+                BlockDesc d{};
                 d.data = j.blob + off;
-                d.esc0 = carry + excl;
+                d.esc = j.pos + (carry + excl);
                 d.meta = st != 0u ? 0u : uint32_t(h.mode) | (uint32_t(h.n_tokens) << 8) | (uint32_t(ne) << 16);
                 j.desc[b] = d;
             }

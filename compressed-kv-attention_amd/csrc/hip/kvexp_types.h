@@ -37,11 +37,13 @@ struct HeadDev {
 };
 
 // One block of a container as the wave kernel reads it, built and checked
-// against the block index once per plan (esc_start_kernel).
+// against the block index once per plan (esc_start_kernel). 32 bytes, so a
+// scalar load of one descriptor reads exactly one.
 struct BlockDesc {
     const uint8_t *data; // the block's header
-    int32_t esc0;        // index of its first escape in the tensor's escape-position index
+    const uint16_t *esc; // its entries in the tensor's escape-position index
     uint32_t meta;       // mode | n_tokens << 8 | n_escape << 16 (n_escape 0 for raw blocks)
+    uint32_t pad[3];
 };
 
 // One tensor (container + block index) for the plan-time builders.

@@ -278,9 +278,14 @@ void build_escape_index(kvexp_hip_plan &p, const kvexp_hip_head *heads, int n_he
         jobs[i].desc = p.desc.as<kvexp_dev::BlockDesc>() + e0_at[i];
     }
     DevBuf djobs(jobs.size() * sizeof(kvexp_dev::EscJob));
-    HIPX(hipMemcpy(djobs.p, jobs.data(), jobs.size() * sizeof(kvexp_dev::EscJob), hipMemcpyHostToDevice));
     uint32_t *st = p.ctx->status.as<uint32_t>();
+    // pass 1: block checks and escape counts (descriptors need the position array)
+    std::vector<kvexp_dev::EscJob> jobs1 = jobs;
+    for (auto &j : jobs1) j.desc = nullptr;
+    HIPX(hipMemcpy(djobs.p, jobs1.data(), jobs1.size() * sizeof(kvexp_dev::EscJob), hipMemcpyHostToDevice));
     HIPX(kvexp_launch::esc_start(djobs.as<kvexp_dev::EscJob>(), int(jobs.size()), st, nullptr));
+    HIPX(hipDeviceSynchronize());
+    check_status_word(st, nullptr);
     std::vector<int32_t> e0(e0_total);
     HIPX(hipMemcpy(e0.data(), p.esc0.p, e0_total * sizeof(int32_t), hipMemcpyDeviceToHost));
     size_t pos_total = 0;
@@ -294,6 +299,8 @@ void build_escape_index(kvexp_hip_plan &p, const kvexp_hip_head *heads, int n_he
     p.escpos = DevBuf(std::max<size_t>(pos_total, 1) * sizeof(uint16_t));
     for (size_t i = 0; i < jobs.size(); ++i) jobs[i].pos = p.escpos.as<uint16_t>() + pos_at[i];
     HIPX(hipMemcpy(djobs.p, jobs.data(), jobs.size() * sizeof(kvexp_dev::EscJob), hipMemcpyHostToDevice));
+    // pass 2: descriptors (with the escape-position pointers)
+    HIPX(kvexp_launch::esc_start(djobs.as<kvexp_dev::EscJob>(), int(jobs.size()), st, nullptr));
     DevBuf dblocks(std::max<size_t>(blocks.size(), 1) * sizeof(int2));
     HIPX(hipMemcpy(dblocks.p, blocks.data(), blocks.size() * sizeof(int2), hipMemcpyHostToDevice));
     HIPX(kvexp_launch::esc_pos(djobs.as<kvexp_dev::EscJob>(), dblocks.as<int2>(), int(blocks.size()), st, nullptr));
