@@ -433,7 +433,7 @@ __global__ __launch_bounds__(kWavesPerWg * 64) __attribute__((amdgpu_waves_per_e
             nz |= !(d[g] == 0.0f);
         }
 #pragma unroll
-        for (int g = 0; g < 8; ++g) ev[g] = g < G ? kvexp_expf_tab_nb(s[g < G ? g : 0] - mi[g < G ? g : 0], tab) : 0.0f;
+        for (int g = 0; g < 8; ++g) ev[g] = g < G ? kvexp_expf_nonpos_nb(s[g < G ? g : 0] - mi[g < G ? g : 0], tab) : 0.0f;
         *reinterpret_cast<float4 *>(&S.e[lane][0]) = make_float4(ev[0], ev[1], ev[2], ev[3]);
         if (G > 4) *reinterpret_cast<float4 *>(&S.e[lane][4]) = make_float4(ev[4], ev[5], ev[6], ev[7]);
         // tokens (bits) where some row's running maximum moves: alpha != 1;
@@ -442,7 +442,7 @@ __global__ __launch_bounds__(kWavesPerWg * 64) __attribute__((amdgpu_waves_per_e
         float alpha[G];
         if (rmask0 != 0) {
 #pragma unroll
-            for (int g = 0; g < G; ++g) alpha[g] = kvexp_expf_tab_nb(d[g], tab);
+            for (int g = 0; g < G; ++g) alpha[g] = kvexp_expf_nonpos_nb(d[g], tab);
         }
 #pragma unroll
         for (int g = 0; g < G; ++g) {
@@ -555,8 +555,8 @@ __global__ __launch_bounds__(kWavesPerWg * 64) void wave_merge_kernel(
             // lane = split s0 + 64h + lane: running maximum and the two exponentials
             const float mm = fmaxf(wave_scan_max(ms[h]), mf);
             const float mprev = wave_shift_up(mm, mf);
-            const float e1 = kvexp_expf_tab_nb(mprev - mm, tab); // scale of the running state
-            const float e2 = kvexp_expf_tab_nb(ms[h] - mm, tab); // scale of split s0 + 64h + lane
+            const float e1 = kvexp_expf_nonpos_nb(mprev - mm, tab); // scale of the running state
+            const float e2 = kvexp_expf_nonpos_nb(ms[h] - mm, tab); // scale of split s0 + 64h + lane
             mf = readlane_f32(mm, min(64, cnt - 64 * h) - 1);
 #pragma unroll
             for (int jj = 0; jj < 64; ++jj) {

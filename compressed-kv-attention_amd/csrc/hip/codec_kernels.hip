@@ -427,15 +427,22 @@ __global__ __launch_bounds__(kThreads) void esc_pos_kernel(const EscJob *__restr
     if (threadIdx.x == 0 && carry != h.n_escape) atomicOr(status, kStEscape);
 }
 
-// y = expf(x) in the form the attention kernels evaluate it: even threads use
-// the branching special cases with the constant-memory table, odd threads the
-// branch-free form with the table copied to LDS (both must equal glibc).
+// y = expf(x) in the forms the attention kernels evaluate it (all must equal
+// glibc): thread % 3 == 0 the branching special cases with the constant-memory
+// table, 1 the branch-free form with the table copied to LDS, 2 the
+// non-positive form for x <= 0, +0 and NaN (the branch-free form otherwise).
 __global__ __launch_bounds__(256) void expf_kernel(const float *__restrict__ x, float *__restrict__ y, size_t n) {
     __shared__ uint64_t tab[32];
     if (threadIdx.x < 32) tab[threadIdx.x] = kvexp_exp2_32_table[threadIdx.x];
     __syncthreads();
     const size_t i = size_t(blockIdx.x) * 256u + threadIdx.x;
-    if (i < n) y[i] = (threadIdx.x & 1) ? kvexp_expf_tab_nb(x[i], tab) : kvexp_expf(x[i]);
+    if (i >= n) return;
+    const float v = x[i];
+    const uint32_t b = __float_as_uint(v);
+    const int form = int(threadIdx.x % 3u);
+    if (form == 0) y[i] = kvexp_expf(v);
+    else if (form == 2 && ((b >> 31) != 0u || b == 0u || v != v)) y[i] = kvexp_expf_nonpos_nb(v, tab);
+    else y[i] = kvexp_expf_tab_nb(v, tab);
 }
 
 } // namespace kvexp_dev

@@ -140,6 +140,16 @@ KVEXP_HD float kvexp_expf_tab_nb(float x, const uint64_t *tab) {
     return abstop >= 0x42bu ? special : core;
 }
 
+/* kvexp_expf_tab_nb for arguments that are not positive (x <= 0, -0, -inf)
+ * or NaN, as every softmax exponent is (s - m and m_prev - m with m the
+ * running maximum); +0 is also handled. Only two special cases remain:
+ * x < -0x1.9fe368p6 (including -inf) -> +0, NaN -> x + x. */
+KVEXP_HD float kvexp_expf_nonpos_nb(float x, const uint64_t *tab) {
+    const float core = kvexp_expf_core_tab(x, tab);
+    const float r = x < -0x1.9fe368p6f ? 0.0f : core;
+    return x != x ? x + x : r;
+}
+
 /* The reduction and polynomial with the built-in table. */
 KVEXP_HD float kvexp_expf_core(float x) { return kvexp_expf_core_tab(x, kvexp_exp2_32_table); }
 

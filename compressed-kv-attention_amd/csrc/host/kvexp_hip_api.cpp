@@ -484,10 +484,10 @@ int kvexp_hip_decode(kvexp_hip_ctx *ctx, const uint8_t *d_blob, size_t bytes, co
 int kvexp_hip_suggest_splits(kvexp_hip_ctx *ctx, int n_heads, int seq, int split_tokens) {
     if (ctx == nullptr || n_heads <= 0 || seq <= 0 || split_tokens <= 0) return 1;
     const int tiles = (seq + split_tokens - 1) / split_tokens;
-    // about 24 single-wave splits per CU over the whole launch: two to three
-    // rounds of the head_dim-64 kernel's 8-12 resident waves per CU, so the
-    // dispatcher can even out splits that finish at different times
-    const int target = std::max(1, (24 * ctx->cu_count + n_heads - 1) / n_heads);
+    // one round of the head_dim-64 kernel's resident waves: 12 single-wave
+    // splits per CU (three waves per SIMD), so every split starts at once and
+    // no SIMD runs a second, partly filled round
+    const int target = std::max(1, (12 * ctx->cu_count) / n_heads);
     return std::max(1, std::min(tiles, target));
 }
 

@@ -1,6 +1,6 @@
 /* Exhaustive comparison of the device expf restatement (compiled here for the
- * host; both the branching and the branch-free form) with the host libm expf
- * over every float bit pattern in [lo, hi).
+ * host; the branching, the branch-free and, on its domain, the non-positive
+ * form) with the host libm expf over every float bit pattern in [lo, hi).
  * Usage: expf_exhaustive FORM_UNUSED lo hi   (the form is fixed at compile time)
  * Prints: "<mismatches> <first mismatching bits or -1>". */
 #include <math.h>
@@ -24,11 +24,16 @@ int main(int argc, char **argv) {
         float x;
         memcpy(&x, &b, 4);
         float a = expf(x), d = kvexp_expf(x), e = kvexp_expf_tab_nb(x, kvexp_exp2_32_table);
-        uint32_t ua, ud, ue;
+        /* the non-positive form: x <= 0 (sign bit set), +0 and NaN only */
+        const int np = (b >> 31) || b == 0u || isnan(x);
+        float f = np ? kvexp_expf_nonpos_nb(x, kvexp_exp2_32_table) : a;
+        uint32_t ua, ud, ue, uf;
         memcpy(&ua, &a, 4);
         memcpy(&ud, &d, 4);
         memcpy(&ue, &e, 4);
-        if ((ua != ud && !(isnan(a) && isnan(d))) || (ua != ue && !(isnan(a) && isnan(e)))) {
+        memcpy(&uf, &f, 4);
+        if ((ua != ud && !(isnan(a) && isnan(d))) || (ua != ue && !(isnan(a) && isnan(e))) ||
+            (ua != uf && !(isnan(a) && isnan(f)))) {
             ++bad;
 #pragma omp critical
             if (first < 0 || u < first) first = u;
