@@ -73,6 +73,7 @@ __device__ __forceinline__ T load_scalar(const T *p) {
 
 // Constant address space (4): uniform loads from it are scalar loads.
 typedef float f8 __attribute__((ext_vector_type(8)));
+typedef unsigned int u32x8 __attribute__((ext_vector_type(8)));
 typedef const __attribute__((address_space(4))) f8 c_f8;
 
 __device__ __forceinline__ uint4 ld16(const uint8_t *p) {
@@ -83,7 +84,7 @@ __device__ __forceinline__ uint32_t ldu16(const uint8_t *p) { return *(g_u16 *)(
 
 // Position of one tensor inside its XKV container. The scalar fields are
 // wave-uniform; epos / eval hold the current block's first 64 escapes (lane
-// k: element index and word of escape k; epos = ~0 past the last).
+// k < n_escape: element index and word of escape k).
 struct Cursor {
     const BlockDesc *d;  // descriptor of the current block (the next one follows it)
     const uint8_t *blk;  // current block's header
@@ -91,6 +92,7 @@ struct Cursor {
     int t0, t1;          // its token range
     uint32_t meta;       // mode | n_tokens << 8 | n_escape << 16
     uint32_t epos, eval;
+    uint32_t base2;      // lane p < 32: base exponents 2p, 2p + 1 of the block
     __device__ int mode() const { return int(meta & 0xFFu); }
     __device__ int ntok() const { return int((meta >> 8) & 0xFFu); }
     __device__ int nesc() const { return int(meta >> 16); }
@@ -101,61 +103,63 @@ __device__ __forceinline__ const uint8_t *esc_words(const Cursor &c) {
 }
 
 // Enters the block of descriptor d, whose first token is t0: one scalar load
-// of the descriptor (checked against the container when the plan was built),
-// then the positions and words of the block's first 64 escapes.
-__device__ __forceinline__ void open_block(Cursor &c, const BlockDesc *d, int t0) {
-    const BlockDesc bd = load_scalar(d);
+// of the descriptor (checked against the container when the plan was built).
+// Scalar state only; block_vectors loads the per-lane data.
+__device__ __forceinline__ void enter_block(Cursor &c, const BlockDesc *d, int t0) {
+    const u32x8 w = *(const __attribute__((address_space(4))) u32x8 *)(d);
     c.d = d;
-    c.blk = bd.data;
-    c.esc = bd.esc;
-    c.meta = __builtin_amdgcn_readfirstlane(bd.meta);
+    c.blk = reinterpret_cast<const uint8_t *>((uint64_t(w.s1) << 32) | w.s0);
+    c.esc = reinterpret_cast<const uint16_t *>((uint64_t(w.s3) << 32) | w.s2);
+    c.meta = w.s4;
     c.t0 = t0;
     c.t1 = t0 + c.ntok();
-    c.epos = 0xFFFFFFFFu;
-    c.eval = 0u;
+}
+
+// The block's base exponents (lane p < 32: pair p) and its first 64 escape
+// positions and words (lane k < n_escape: escape k). Every lane loads, from a
+// clamped and always valid address, and the call is made on every chunk
+// whether or not the block changed, so the number of loads in flight does
+// not depend on the path taken: a result is then never merged with a default
+// value, and waits for the row loads can leave later loads in flight. Lanes
+// >= n_escape are masked where the values are used.
+__device__ __forceinline__ void block_vectors(Cursor &c) {
     const int lane = lane_id();
-    if (lane < c.nesc()) {
-        c.epos = *(g_u16 *)(c.esc + lane);
-        c.eval = ldu16(esc_words(c) + 2 * lane);
-    }
+    const int nesc = c.nesc();
+    const int k = min(lane, max(nesc - 1, 0));
+    c.base2 = ldu16(c.blk + 8 + 2 * (lane & (kD / 2 - 1)));
+    c.epos = *(g_u16 *)(nesc > 0 ? c.esc + k : reinterpret_cast<const uint16_t *>(c.blk));
+    c.eval = ldu16(nesc > 0 ? esc_words(c) + 2 * k : c.blk);
 }
 
 // Loads rows [r0 + lane] of the cursor's block (lanes < rows) into R.
 __device__ __forceinline__ void load_rows(const Cursor &c, int r0, int rows, uint4 (&R)[kRowRegs]) {
-    const int lane = lane_id();
-    if (lane >= rows) return;
-    const int r = r0 + lane;
-    const uint8_t *p = c.blk + 8;
-    if (c.mode() == 0) { // the first 96 of the row's 128 bytes; decode_row loads the rest
-        const uint8_t *row = p + size_t(r) * (2 * kD);
+    // Lanes past `rows` load row rows - 1 again (their tile rows are not
+    // used): every load is unconditional, with the mode's layout picked by
+    // uniform selects, so the registers need no merge before their use.
+    const int r = r0 + min(lane_id(), rows - 1);
+    const int mode = c.mode();
+    const bool raw = mode == 0;
+    // sign/mantissa bytes (or the first 64 raw bytes) of the row
+    const uint8_t *rowp = c.blk + 8 + (raw ? 0 : kD) + size_t(r) * (raw ? 2 * kD : kD);
+    // codes of the row (or raw bytes 64..95)
+    const uint8_t *tail = raw ? rowp + 64
+                              : c.blk + 8 + kD + size_t(c.ntok()) * kD + size_t(r) * (mode == 4 ? kD / 2 : kD / 4);
 #pragma unroll
-        for (int i = 0; i < kRowRegs; ++i) R[i] = ld16(row + 16 * i);
-        return;
-    }
-    const uint8_t *sm = p + kD + size_t(r) * kD;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) R[i] = ld16(sm + 16 * i);
-    const uint8_t *codes = p + kD + size_t(c.ntok()) * kD;
-    if (c.mode() == 4) {
-        R[4] = ld16(codes + size_t(r) * (kD / 2));
-        R[5] = ld16(codes + size_t(r) * (kD / 2) + 16);
-    } else {
-        R[4] = ld16(codes + size_t(r) * (kD / 4));
-    }
+    for (int i = 0; i < 4; ++i) R[i] = ld16(rowp + 16 * i);
+    R[4] = ld16(tail);
+    R[5] = ld16(tail + (mode == 2 ? 0 : 16));
 }
 
 __device__ __forceinline__ uint32_t comp(const uint4 &v, int i) {
     return i == 0 ? v.x : (i == 1 ? v.y : (i == 2 ? v.z : v.w));
 }
 
-// Base pair words of the block into LDS: word p = base[2p] << 7 | base[2p+1] << 23
-// (lane p < 32 builds word p).
-__device__ __forceinline__ void base_pairs(const uint8_t *base, uint32_t *bp) {
+// Base pair words of the cursor's block into LDS: word p = base[2p] << 7 |
+// base[2p+1] << 23 (lane p < 32 builds word p from the bytes loaded with the
+// block).
+__device__ __forceinline__ void base_pairs(const Cursor &c, uint32_t *bp) {
     const int lane = lane_id();
-    if (lane < kD / 2) {
-        const uint32_t two = ldu16(base + 2 * lane);
-        bp[lane] = ((two & 0xFFu) << 7) | ((two >> 8) << 23);
-    }
+    if (lane < kD / 2) bp[lane] = ((c.base2 & 0xFFu) << 7) | ((c.base2 >> 8) << 23);
 }
 
 // One BF16 pair from two sign/mantissa bytes (positions lb, lb+1 of sw), two
@@ -217,7 +221,7 @@ __device__ __forceinline__ void patch_escapes(const Cursor &c, int r0, int n, ui
     const int nesc = c.nesc();
     if (nesc == 0) return;
     const uint32_t lo = uint32_t(r0 * kD), hi = uint32_t((r0 + n) * kD);
-    if (c.epos >= lo && c.epos < hi) {
+    if (lane_id() < nesc && c.epos >= lo && c.epos < hi) {
         const uint32_t row = c.epos / kD - uint32_t(r0), col = c.epos % kD;
         *reinterpret_cast<uint16_t *>(tile + row * kTileStride + col * 2) = uint16_t(c.eval);
     }
@@ -236,8 +240,12 @@ __device__ __forceinline__ void patch_escapes(const Cursor &c, int r0, int n, ui
     }
 }
 
+// Phase boundary inside one wave. The LDS performs one wave's operations in
+// issue order, so a lane reads what other lanes of its wave wrote before
+// without any wait; this only keeps the compiler from moving LDS accesses
+// across the boundary.
 __device__ __forceinline__ void wave_sync() {
-    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    asm volatile("" ::: "memory");
     __builtin_amdgcn_wave_barrier();
 }
 
@@ -337,20 +345,21 @@ __global__ __launch_bounds__(kWavesPerWg * 64) __attribute__((amdgpu_waves_per_e
     uint4 RK[XKV ? kRowRegs : 8], RV[XKV ? kRowRegs : 8];
     int t = wi.tok_begin;
     if constexpr (XKV) {
-        open_block(kc, hd.kdesc + wi.kblk, t);
-        open_block(vc, hd.vdesc + wi.vblk, t);
+        enter_block(kc, hd.kdesc + wi.kblk, t);
+        enter_block(vc, hd.vdesc + wi.vblk, t);
+        block_vectors(kc);
         load_rows(kc, 0, min(kChunk, min(kc.t1, wi.tok_end) - t), RK);
+        block_vectors(vc);
         load_rows(vc, 0, min(kChunk, min(vc.t1, wi.tok_end) - t), RV);
     } else {
-        const int rows = min(kChunk, wi.tok_end - t);
-        if (lane < rows) {
-            const uint8_t *kr = reinterpret_cast<const uint8_t *>(hd.kraw + size_t(t + lane) * kD);
-            const uint8_t *vr = reinterpret_cast<const uint8_t *>(hd.vraw + size_t(t + lane) * kD);
+        // unconditional loads (lanes past the chunk repeat its last row)
+        const int row = t + min(lane, min(kChunk, wi.tok_end - t) - 1);
+        const uint8_t *kr = reinterpret_cast<const uint8_t *>(hd.kraw + size_t(row) * kD);
+        const uint8_t *vr = reinterpret_cast<const uint8_t *>(hd.vraw + size_t(row) * kD);
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                RK[i] = ld16(kr + 16 * i);
-                RV[i] = ld16(vr + 16 * i);
-            }
+        for (int i = 0; i < 8; ++i) {
+            RK[i] = ld16(kr + 16 * i);
+            RV[i] = ld16(vr + 16 * i);
         }
     }
     uint8_t *my_row = S.tile + lane * kTileStride;
@@ -364,7 +373,7 @@ __global__ __launch_bounds__(kWavesPerWg * 64) __attribute__((amdgpu_waves_per_e
         // 1. K rows -> tile
         if constexpr (XKV) {
             if (kc.mode() != 0) {
-                base_pairs(kc.blk + 8, S.bp);
+                base_pairs(kc, S.bp);
                 wave_sync();
             }
             decode_row(kc, RK, S.bp, my_row, t - kc.t0, n);
@@ -389,30 +398,36 @@ __global__ __launch_bounds__(kWavesPerWg * 64) __attribute__((amdgpu_waves_per_e
         // are then not live across the score and decode registers)
         if constexpr (XKV) {
             if (vc.mode() != 0) {
-                base_pairs(vc.blk + 8, S.bp);
+                base_pairs(vc, S.bp);
                 wave_sync();
             }
             decode_row(vc, RV, S.bp, my_row, t - vc.t0, n);
             wave_sync();
             patch_escapes(vc, t - vc.t0, n, S.tile);
-            if (tn < wi.tok_end) {
-                if (tn >= vc.t1) open_block(vc, vc.d + 1, vc.t1);
-                load_rows(vc, tn - vc.t0, min(kChunk, min(vc.t1, wi.tok_end) - tn), RV);
-                if (tn >= kc.t1) open_block(kc, kc.d + 1, kc.t1);
-                load_rows(kc, tn - kc.t0, min(kChunk, min(kc.t1, wi.tok_end) - tn), RK);
-            }
+            // the loads are issued on every chunk (the last one re-reads its
+            // own final row), K first: the K decode can then wait for its
+            // loads while the V loads stay in flight
+            const int tp = min(tn, wi.tok_end - 1);
+            if (tp >= kc.t1) enter_block(kc, kc.d + 1, kc.t1);
+            block_vectors(kc);
+            load_rows(kc, tp - kc.t0, min(kChunk, min(kc.t1, wi.tok_end) - tp), RK);
+            if (tp >= vc.t1) enter_block(vc, vc.d + 1, vc.t1);
+            block_vectors(vc);
+            load_rows(vc, tp - vc.t0, min(kChunk, min(vc.t1, wi.tok_end) - tp), RV);
         } else {
             uint4 *dst = reinterpret_cast<uint4 *>(my_row);
 #pragma unroll
             for (int i = 0; i < 8; ++i) dst[i] = RV[i];
-            if (tn < wi.tok_end && lane < min(kChunk, wi.tok_end - tn)) {
-                const uint8_t *vr = reinterpret_cast<const uint8_t *>(hd.vraw + size_t(tn + lane) * kD);
-                const uint8_t *kr = reinterpret_cast<const uint8_t *>(hd.kraw + size_t(tn + lane) * kD);
+            {
+                // issued on every chunk (the last one re-reads its final row), K first
+                const int tp = min(tn, wi.tok_end - 1);
+                const int row = tp + min(lane, min(kChunk, wi.tok_end - tp) - 1);
+                const uint8_t *vr = reinterpret_cast<const uint8_t *>(hd.vraw + size_t(row) * kD);
+                const uint8_t *kr = reinterpret_cast<const uint8_t *>(hd.kraw + size_t(row) * kD);
 #pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    RV[i] = ld16(vr + 16 * i);
-                    RK[i] = ld16(kr + 16 * i);
-                }
+                for (int i = 0; i < 8; ++i) RK[i] = ld16(kr + 16 * i);
+#pragma unroll
+                for (int i = 0; i < 8; ++i) RV[i] = ld16(vr + 16 * i);
             }
         }
 
