@@ -10,14 +10,22 @@
 //      escape words are then written over their elements using the plan's
 //      escape-position index, so no sentinel search runs here;
 //   2. computes the G scores of each token (lane = token) in the reference
-//      order: 8 strided FMA chains over the 64 channels, q widened from BF16
-//      scalar registers, then the ((l0+l4)+(l1+l5))+((l2+l6)+(l3+l7)) tree;
-//   3. decodes the V rows into the same tile;
-//   4. turns scores into alpha = exp(m_prev - m), e = exp(s - m) with an
-//      exact DPP prefix maximum and the glibc-identical expf (table in LDS);
-//   5. folds the chunk's tokens in order (lane = channel):
-//      acc = fma(e, v, acc * alpha), l = fma(l, alpha, e); alpha == 1 for a
-//      whole chunk skips the multiply, which is exact.
+//      order: 8 strided FMA chains over the 64 channels, q from scalar
+//      registers, then the ((l0+l4)+(l1+l5))+((l2+l6)+(l3+l7)) tree;
+//   3. decodes the V rows into the same tile (tokens past the chunk's end get
+//      -0, which the fold adds as an exact no-op);
+//   4. turns scores into e = exp(s - m) and, for the query rows where some
+//      token moves the running maximum, alpha = exp(m_prev - m), with an
+//      exact DPP prefix maximum seeded by the maxima held in scalar registers
+//      and the glibc-identical expf; e and alpha go to LDS by query row;
+//   5. folds the chunk's tokens in order (lane = channel), fully unrolled:
+//      acc = fma(e, v, acc), with acc scaled by alpha first only on the
+//      tokens that move a maximum (a uniform branch; alpha == 1 elsewhere, so
+//      skipping the multiply is exact), and l = fma(l, alpha, e) on lane g.
+//      The weights e[g][t] reach all 64 lanes from registers: each quarter of
+//      the chunk is gathered with ds_bpermute so that lane k of every row of
+//      16 holds token 16q + k, and v_fmac_f32 takes it through a DPP
+//      row_newbcast source.
 // A head cut into several splits leaves one partial state (m, l, acc) per
 // split; wave_merge_kernel, launched after the split kernels, folds them left
 // to right (merge_state order) and finalizes out = acc * (1/l).
@@ -34,21 +42,34 @@ namespace wave {
 constexpr int kD = 64;          // head_dim of this kernel
 constexpr int kChunk = 64;      // tokens per chunk (one per lane)
 constexpr int kTileStride = 144; // bytes per tile row: 64 BF16 + 16 (conflict-free 16-byte rows)
+constexpr uint16_t kNegZeroBf16 = 0x8000u; // V of a token past the chunk's end: fma(0, -0, acc) == acc exactly
 constexpr int kWavesPerWg = 4;
 constexpr int kSlotQ = 8;       // partial-state slot: m[8], l[8], acc[8][64]
 constexpr int kSlotFloats = kSlotQ * (kD + 2);
 constexpr int kRowRegs = 6;     // 16-byte registers per prefetched XKV row (coded rows need at most 6)
 constexpr int kMergeBatch = 128; // split slots whose loads are in flight together in the merge
 
-struct WaveLds {
+// Per-wave LDS. The tile holds the chunk's K rows (row t: the 64 BF16 of
+// token t) and then its V transposed (row c: channel c of the 64 tokens).
+// eT / aT hold e and alpha by query row (row g: the chunk's 64 tokens), so a
+// lane reads four tokens of its row in one access. For G <= 7 a wave takes
+// 13,152 bytes and four waves with the shared table 52,864 bytes, which
+// leaves room for three workgroups per CU (the limit lies between 53,760
+// and 54,016 bytes per workgroup).
+constexpr int kRowPad = kChunk + 4; // floats per eT / aT row: 16 spare bytes keep the rows' reads conflict-free
+
+template <int G>
+struct alignas(16) WaveLds {
     uint8_t tile[kChunk * kTileStride];
-    float e[kChunk][8];  // e of token t, row g
-    uint32_t bp[kD / 2]; // base pair words of the block being decoded
+    float eT[G][kRowPad]; // e of token t, row g (0 past the chunk's end)
+    float aT[G][kRowPad]; // alpha of token t, row g (1 where no running maximum moves)
+    uint32_t bp[kD / 2];  // base pair words of the block being decoded
 };
 
-struct WgLds {
+template <int G>
+struct alignas(16) WgLds {
     uint64_t exptab[32];
-    WaveLds w[kWavesPerWg];
+    WaveLds<G> w[kWavesPerWg];
 };
 
 // Global-memory loads (address space 1, so they are issued as global_load_*
@@ -75,6 +96,11 @@ __device__ __forceinline__ T load_scalar(const T *p) {
 typedef float f8 __attribute__((ext_vector_type(8)));
 typedef unsigned int u32x8 __attribute__((ext_vector_type(8)));
 typedef const __attribute__((address_space(4))) f8 c_f8;
+// An LDS float (address space 3), for pointers that pass through inline asm
+// and must still be read with ds_read.
+typedef const __attribute__((address_space(3))) float lds_f32;
+typedef float f4 __attribute__((ext_vector_type(4)));
+typedef const __attribute__((address_space(3))) f4 lds_f4;
 
 __device__ __forceinline__ uint4 ld16(const uint8_t *p) {
     const u32x4 v = *(g_u32x4 *)(p);
@@ -172,45 +198,64 @@ __device__ __forceinline__ uint32_t pair4(uint32_t sw, int lb, uint32_t lo, uint
     return (s & 0x807F807Fu) | (t & ~0x807F807Fu);
 }
 
+// Octet dg (channels 8dg..8dg+7) of a coded row: four BF16 pairs from the
+// row's sign/mantissa bytes in R[0..3], its codes split into lo (byte p: code
+// 2p) and hi (byte p: code 2p+1), and the channel pairs' base words.
+__device__ __forceinline__ uint4 octet(const uint4 (&R)[kRowRegs], int dg, uint32_t lo, uint32_t hi,
+                                       const uint32_t *bp) {
+    const uint32_t s0 = comp(R[dg >> 1], (dg & 1) * 2);
+    const uint32_t s1 = comp(R[dg >> 1], (dg & 1) * 2 + 1);
+    const uint4 b4 = *reinterpret_cast<const uint4 *>(bp + 4 * dg);
+    uint4 o;
+    o.x = pair4(s0, 0, lo, hi, 0, b4.x);
+    o.y = pair4(s0, 2, lo, hi, 1, b4.y);
+    o.z = pair4(s1, 0, lo, hi, 2, b4.z);
+    o.w = pair4(s1, 2, lo, hi, 3, b4.w);
+    return o;
+}
+
+// -0 in every channel of the lane's tile row (a token past the chunk's end).
+__device__ __forceinline__ void fill_negzero(uint8_t *row) {
+    const uint32_t z = uint32_t(kNegZeroBf16) * 0x10001u;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) reinterpret_cast<uint4 *>(row)[i] = make_uint4(z, z, z, z);
+}
+
 // Decodes the lane's row held in R (cursor's block mode) into its tile row.
+// One uniform branch on the mode, then a straight-line body per mode. Lanes
+// >= rows (past the chunk's end) then store -0 in every channel (wanted for
+// V; harmless for K).
 __device__ __forceinline__ void decode_row(const Cursor &c, const uint4 (&R)[kRowRegs], const uint32_t *bp,
                                            uint8_t *row, int r0, int rows) {
     uint4 *dst = reinterpret_cast<uint4 *>(row);
-    if (c.mode() == 0) {
-        const int lane = lane_id();
-        if (lane < rows) {
-            const uint8_t *src = c.blk + 8 + size_t(r0 + lane) * (2 * kD);
+    const int mode = c.mode();
+    const int lane = lane_id();
+    if (mode == 4) {
 #pragma unroll
-            for (int i = 0; i < kRowRegs; ++i) dst[i] = R[i];
-            dst[6] = ld16(src + 96);
-            dst[7] = ld16(src + 112);
-        }
-        return;
-    }
-#pragma unroll
-    for (int dg = 0; dg < 8; ++dg) {
-        const uint32_t s0 = comp(R[dg >> 1], (dg & 1) * 2);
-        const uint32_t s1 = comp(R[dg >> 1], (dg & 1) * 2 + 1);
-        uint32_t lo, hi;
-        if (c.mode() == 4) {
+        for (int dg = 0; dg < 8; ++dg) {
             const uint32_t cw = comp(R[4 + (dg >> 2)], dg & 3);
-            lo = cw & 0x0F0F0F0Fu;
-            hi = (cw >> 4) & 0x0F0F0F0Fu;
-        } else {
-            // 16 two-bit codes per dword; octet dg uses 16 bits.
-            const uint32_t cw = comp(R[4], dg >> 1) >> (16 * (dg & 1));
-            // byte p of lo/hi: codes 2p and 2p+1 of the octet
-            lo = (cw & 3u) | (((cw >> 4) & 3u) << 8) | (((cw >> 8) & 3u) << 16) | (((cw >> 12) & 3u) << 24);
-            hi = ((cw >> 2) & 3u) | (((cw >> 6) & 3u) << 8) | (((cw >> 10) & 3u) << 16) | (((cw >> 14) & 3u) << 24);
+            dst[dg] = octet(R, dg, cw & 0x0F0F0F0Fu, (cw >> 4) & 0x0F0F0F0Fu, bp);
         }
-        const uint4 b4 = *reinterpret_cast<const uint4 *>(bp + 4 * dg);
-        uint4 o;
-        o.x = pair4(s0, 0, lo, hi, 0, b4.x);
-        o.y = pair4(s0, 2, lo, hi, 1, b4.y);
-        o.z = pair4(s1, 0, lo, hi, 2, b4.z);
-        o.w = pair4(s1, 2, lo, hi, 3, b4.w);
-        dst[dg] = o;
+    } else if (mode == 2) {
+#pragma unroll
+        for (int dg = 0; dg < 8; ++dg) {
+            // 16 two-bit codes per dword; octet dg uses 16 bits. Byte p of
+            // lo/hi: codes 2p and 2p+1 of the octet.
+            const uint32_t cw = comp(R[4], dg >> 1) >> (16 * (dg & 1));
+            const uint32_t lo =
+                (cw & 3u) | (((cw >> 4) & 3u) << 8) | (((cw >> 8) & 3u) << 16) | (((cw >> 12) & 3u) << 24);
+            const uint32_t hi = ((cw >> 2) & 3u) | (((cw >> 6) & 3u) << 8) | (((cw >> 10) & 3u) << 16) |
+                                (((cw >> 14) & 3u) << 24);
+            dst[dg] = octet(R, dg, lo, hi, bp);
+        }
+    } else if (lane < rows) {
+        const uint8_t *src = c.blk + 8 + size_t(r0 + lane) * (2 * kD);
+#pragma unroll
+        for (int i = 0; i < kRowRegs; ++i) dst[i] = R[i];
+        dst[6] = ld16(src + 96);
+        dst[7] = ld16(src + 112);
     }
+    if (rows < kChunk && lane >= rows) fill_negzero(row);
 }
 
 // Writes the escape words of rows [r0, r0 + n) of the cursor's block over
@@ -304,6 +349,73 @@ __device__ __forceinline__ void scores(const uint8_t *row, uint64_t qa, float (&
     }
 }
 
+// acc += E[lane of its row of 16 with index K] * v (v_fmac_f32 with a DPP
+// row_newbcast:K source): the weight comes from a register, not from LDS.
+template <int K>
+__device__ __forceinline__ void fmac_rowbcast(float &acc, float e, float v) {
+    asm("v_fmac_f32_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf" : "+v"(acc) : "v"(e), "v"(v), "n"(K));
+}
+
+// Operands of the fold in flight: V of the lane's channel for the next
+// tokens (BF16 in the low half) and e / alpha of four tokens (lane g < G:
+// its row).
+struct FoldIn {
+    uint32_t v[4];
+    f4 e4[2], a4[2];
+};
+
+// Token T of the ordered fold, lane = channel, for a whole chunk (tokens past
+// the chunk's end carry e = 0, alpha = 1 and V = -0, which leave acc and l
+// exactly as they are). A token that moves no running maximum (alpha == 1 for
+// every row, exactly) takes acc = fma(e, v, acc); a token that moves one
+// (rec, a uniform branch) scales by alpha first: acc = fma(e, v, acc * alpha),
+// the multiply done in place (inline asm with tied registers) so the join
+// needs no register copies. Lane g < G carries l of row g through
+// l = fma(l, alpha, e), which is l + e when alpha is 1, so it needs no branch.
+// The weights e[g][T] come from registers: Eq[g] holds, in every row of 16
+// lanes, e[g][16q + k] at lane k (q = T / 16), so row_newbcast:(T % 16) hands
+// every lane e[g][T]. Loads run ahead: V eight tokens and e / alpha four
+// tokens before their use.
+template <int G, int T>
+__device__ __forceinline__ void fold_rb(const WaveLds<G> &S, lds_f32 *eb, lds_f32 *ab, const uint16_t *vb,
+                                        uint64_t amask, const float (&ev)[G], float (&E)[2][G], FoldIn &in,
+                                        float (&acc)[G], float &lvec, int lane) {
+    if constexpr (T < kChunk) {
+        constexpr int q = T / 16;
+        if constexpr (T % 16 == 0 && q + 1 < kChunk / 16) {
+            const int src = ((q + 1) * 16 + (lane & 15)) * 4;
+#pragma unroll
+            for (int g = 0; g < G; ++g)
+                E[(q + 1) & 1][g] = __int_as_float(__builtin_amdgcn_ds_bpermute(src, __float_as_int(ev[g])));
+        }
+        if constexpr (T + 3 < kChunk) in.v[(T + 3) & 3] = vb[(T + 3) * (kTileStride / 2)];
+        if constexpr (T % 4 == 0 && T + 4 < kChunk) {
+            in.e4[((T / 4) + 1) & 1] = *reinterpret_cast<lds_f4 *>(eb + T + 4);
+            in.a4[((T / 4) + 1) & 1] = *reinterpret_cast<lds_f4 *>(ab + T + 4);
+        }
+        const float v = __uint_as_float(in.v[T & 3] << 16);
+        const f4 e4 = in.e4[(T / 4) & 1], a4 = in.a4[(T / 4) & 1];
+        const float el = (T % 4 == 0) ? e4.x : (T % 4 == 1) ? e4.y : (T % 4 == 2) ? e4.z : e4.w;
+        const float al = (T % 4 == 0) ? a4.x : (T % 4 == 1) ? a4.y : (T % 4 == 2) ? a4.z : a4.w;
+        if (((amask >> T) & 1ull) != 0) {
+            // every load first (a volatile asm between them would be a
+            // scheduling barrier and serialise their latencies)
+            float av[G];
+#pragma unroll
+            for (int g = 0; g < G; ++g) av[g] = S.aT[g][T];
+#pragma unroll
+            for (int g = 0; g < G; ++g) asm("v_mul_f32 %0, %0, %1" : "+v"(acc[g]) : "v"(av[g]));
+        }
+        lvec = fmaf(lvec, al, el);
+        // keeps the l chain in token order (otherwise it may be sunk to the
+        // end of the unrolled fold with every token's operands held live)
+        asm volatile("" : "+v"(lvec));
+#pragma unroll
+        for (int g = 0; g < G; ++g) fmac_rowbcast<T % 16>(acc[g], E[q & 1][g], v);
+        fold_rb<G, T + 1>(S, eb, ab, vb, amask, ev, E, in, acc, lvec, lane);
+    }
+}
+
 // q32[h][g][d] = FP32 of query row q_row + g of device head h (rows >= n_q
 // left alone). One workgroup per device head.
 __global__ __launch_bounds__(256) void q_widen_kernel(const HeadDev *__restrict__ heads,
@@ -321,7 +433,7 @@ __global__ __launch_bounds__(kWavesPerWg * 64) __attribute__((amdgpu_waves_per_e
     const HeadDev *__restrict__ heads, const WorkItem *__restrict__ items, int n_items,
     const float *__restrict__ q32_all, float *__restrict__ out_all, float *__restrict__ lse_all,
     float *__restrict__ ws) {
-    __shared__ WgLds L;
+    __shared__ WgLds<G> L;
     if (threadIdx.x < 32) L.exptab[threadIdx.x] = kvexp_exp2_32_table[threadIdx.x];
     __syncthreads();
 
@@ -329,17 +441,20 @@ __global__ __launch_bounds__(kWavesPerWg * 64) __attribute__((amdgpu_waves_per_e
     const int w = int(threadIdx.x) >> 6;
     const int item = __builtin_amdgcn_readfirstlane(int(blockIdx.x) * kWavesPerWg + w);
     if (item >= n_items) return;
-    WaveLds &S = L.w[w];
+    WaveLds<G> &S = L.w[w];
     const uint64_t *tab = L.exptab;
     const WorkItem wi = load_scalar(items + item);
     const HeadDev hd = load_scalar(heads + wi.head);
     const float *q32 = q32_all + size_t(wi.head) * kSlotQ * kD;
 
     float acc[G];
+    float msc[G]; // running maximum of each query row (wave-uniform)
 #pragma unroll
-    for (int g = 0; g < G; ++g) acc[g] = 0.0f;
-    float mvec = -__builtin_inff(); // lane g < G holds m of query row g
-    float lvec = 0.0f;              // lane g < G holds l of query row g
+    for (int g = 0; g < G; ++g) {
+        acc[g] = 0.0f;
+        msc[g] = -__builtin_inff();
+    }
+    float lvec = 0.0f; // lane g < G holds l of query row g
 
     Cursor kc{}, vc{};
     uint4 RK[XKV ? kRowRegs : 8], RV[XKV ? kRowRegs : 8];
@@ -362,7 +477,7 @@ __global__ __launch_bounds__(kWavesPerWg * 64) __attribute__((amdgpu_waves_per_e
             RV[i] = ld16(vr + 16 * i);
         }
     }
-    uint8_t *my_row = S.tile + lane * kTileStride;
+    uint8_t *my_row = S.tile + lane * kTileStride; // the lane's token
 
     while (t < wi.tok_end) {
         int n = min(kChunk, wi.tok_end - t);
@@ -418,6 +533,7 @@ __global__ __launch_bounds__(kWavesPerWg * 64) __attribute__((amdgpu_waves_per_e
             uint4 *dst = reinterpret_cast<uint4 *>(my_row);
 #pragma unroll
             for (int i = 0; i < 8; ++i) dst[i] = RV[i];
+            if (n < kChunk && lane >= n) fill_negzero(my_row);
             {
                 // issued on every chunk (the last one re-reads its final row), K first
                 const int tp = min(tn, wi.tok_end - 1);
@@ -431,85 +547,76 @@ __global__ __launch_bounds__(kWavesPerWg * 64) __attribute__((amdgpu_waves_per_e
             }
         }
 
-        // 4. softmax coefficients, lane = token. All G rows are computed
-        // together without branches (independent chains the scheduler can
-        // interleave); alpha is only computed when some token of the chunk
-        // raises a running maximum.
-        float mi[G], d[G], ev[8];
-        bool nz = false;
+        // 4. softmax coefficients, lane = token: the running maxima by an exact
+        // DPP prefix maximum (seeded with each row's maximum so far, held in
+        // scalar registers), e = exp(s - m) for every token and row, and, for
+        // the rows where some token of the chunk moves the maximum,
+        // alpha = exp(m_prev - m) (rows without such a token keep 1). Tokens
+        // past the chunk's end get e = 0 and alpha = 1.
+        const uint64_t nmask = n >= kChunk ? ~0ull : ((1ull << n) - 1ull);
+        float mi[G], d[G], ev[G];
+        uint64_t rmask[G];
+        uint64_t amask = 0;
 #pragma unroll
         for (int g = 0; g < G; ++g) mi[g] = s[g];
         wave_scan_max_rows<G>(mi);
 #pragma unroll
         for (int g = 0; g < G; ++g) {
-            const float mg = readlane_f32(mvec, g);
-            mi[g] = fmaxf(mi[g], mg);
-            d[g] = wave_shift_up(mi[g], mg) - mi[g];
-            nz |= !(d[g] == 0.0f);
+            mi[g] = fmaxf(mi[g], msc[g]);
+            d[g] = wave_shift_up(mi[g], msc[g]) - mi[g];
+            // alpha != 1 exactly when m_prev - m is not zero (NaN included)
+            rmask[g] = __ballot(!(d[g] == 0.0f)) & nmask;
+            amask |= rmask[g];
+            ev[g] = kvexp_expf_nonpos_nb(s[g] - mi[g], tab);
+            msc[g] = readlane_f32(mi[g], n - 1);
         }
+        if (n < kChunk) {
 #pragma unroll
-        for (int g = 0; g < 8; ++g) ev[g] = g < G ? kvexp_expf_nonpos_nb(s[g < G ? g : 0] - mi[g < G ? g : 0], tab) : 0.0f;
-        *reinterpret_cast<float4 *>(&S.e[lane][0]) = make_float4(ev[0], ev[1], ev[2], ev[3]);
-        if (G > 4) *reinterpret_cast<float4 *>(&S.e[lane][4]) = make_float4(ev[4], ev[5], ev[6], ev[7]);
-        // tokens (bits) where some row's running maximum moves: alpha != 1;
-        // alpha stays in registers (lane = token) for the few tokens that need it
-        const uint64_t rmask0 = __ballot(lane < n && nz);
-        float alpha[G];
-        if (rmask0 != 0) {
-#pragma unroll
-            for (int g = 0; g < G; ++g) alpha[g] = kvexp_expf_nonpos_nb(d[g], tab);
+            for (int g = 0; g < G; ++g) ev[g] = lane < n ? ev[g] : 0.0f;
         }
+        {
+            float al[G];
 #pragma unroll
-        for (int g = 0; g < G; ++g) {
-            const float mn = readlane_f32(mi[g], n - 1);
-            mvec = lane == g ? mn : mvec;
+            for (int g = 0; g < G; ++g) al[g] = 1.0f;
+            if (amask != 0) {
+#pragma unroll
+                for (int g = 0; g < G; ++g)
+                    if (rmask[g] != 0) al[g] = lane < n ? kvexp_expf_nonpos_nb(d[g], tab) : 1.0f;
+            }
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                S.eT[g][lane] = ev[g];
+                S.aT[g][lane] = al[g];
+            }
         }
         wave_sync();
 
-        // 5. ordered fold, lane = channel. Runs of tokens whose alpha is 1 for
-        // every row take acc = fma(e, v, acc), l = l + e (exact: alpha is
-        // exactly 1); a token that moves a running maximum also scales by
-        // alpha: acc = fma(e, v, acc * alpha), l = fma(l, alpha, e).
-        const uint16_t *vt = reinterpret_cast<const uint16_t *>(S.tile);
-        uint64_t rmask = rmask0;
-        int tok = 0;
-        while (true) {
-            const int stop = __builtin_amdgcn_readfirstlane(rmask != 0 ? int(__builtin_ctzll(rmask)) : n);
-#pragma unroll 4
-            for (; tok < stop; ++tok) {
-                const float v = __uint_as_float(uint32_t(vt[tok * (kTileStride / 2) + lane]) << 16);
-                const float4 e0 = *reinterpret_cast<const float4 *>(&S.e[tok][0]);
-                const float4 e1 = *reinterpret_cast<const float4 *>(&S.e[tok][4]);
-                const float ev[8] = {e0.x, e0.y, e0.z, e0.w, e1.x, e1.y, e1.z, e1.w};
+        // 5. ordered fold, lane = channel, fully unrolled over the chunk
+        {
+            float E[2][G];
+            const int src = (lane & 15) * 4;
 #pragma unroll
-                for (int g = 0; g < G; ++g) acc[g] = fmaf(ev[g], v, acc[g]);
-                lvec = lvec + S.e[tok][lane & 7];
-            }
-            if (stop >= n) break;
-            {
-                const float v = __uint_as_float(uint32_t(vt[tok * (kTileStride / 2) + lane]) << 16);
-                const float4 e0 = *reinterpret_cast<const float4 *>(&S.e[tok][0]);
-                const float4 e1 = *reinterpret_cast<const float4 *>(&S.e[tok][4]);
-                const float ev[8] = {e0.x, e0.y, e0.z, e0.w, e1.x, e1.y, e1.z, e1.w};
-                float av[G];
+            for (int g = 0; g < G; ++g)
+                E[0][g] = __int_as_float(__builtin_amdgcn_ds_bpermute(src, __float_as_int(ev[g])));
+            const int gl = min(lane & 7, G - 1); // lanes >= G read a row they do not use
+            lds_f32 *eb = (lds_f32 *)&S.eT[gl][0];
+            lds_f32 *ab = (lds_f32 *)&S.aT[gl][0];
+            FoldIn in;
+            const uint16_t *vb = reinterpret_cast<const uint16_t *>(S.tile) + lane; // channel lane of token 0
 #pragma unroll
-                for (int g = 0; g < G; ++g) av[g] = readlane_f32(alpha[g], tok);
-#pragma unroll
-                for (int g = 0; g < G; ++g) acc[g] = fmaf(ev[g], v, acc[g] * av[g]);
-                float al = av[0]; // lane g < G: alpha of row g
-#pragma unroll
-                for (int g = 1; g < G; ++g) al = lane == g ? av[g] : al;
-                lvec = fmaf(lvec, al, S.e[tok][lane & 7]);
-            }
-            rmask &= rmask - 1;
-            tok = stop + 1;
+            for (int k = 0; k < 3; ++k) in.v[k] = vb[k * (kTileStride / 2)];
+            in.e4[0] = *reinterpret_cast<lds_f4 *>(eb);
+            in.a4[0] = *reinterpret_cast<lds_f4 *>(ab);
+            fold_rb<G, 0>(S, eb, ab, vb, amask, ev, E, in, acc, lvec, lane);
         }
         wave_sync();
         t = tn;
     }
 
     // ---- epilogue --------------------------------------------------------------
-    const float mv = mvec;
+    float mv = msc[0]; // lane g < G: running maximum of row g
+#pragma unroll
+    for (int g = 1; g < G; ++g) mv = lane == g ? msc[g] : mv;
     if (hd.n_splits == 1) {
 #pragma unroll
         for (int g = 0; g < G; ++g) {

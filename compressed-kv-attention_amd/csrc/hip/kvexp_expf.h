@@ -96,8 +96,11 @@ KVEXP_HD float kvexp_expf_core_tab(float x, const uint64_t *tab) {
     kd -= KVEXP_EXP_SHIFT;
     const double r = z - kd;
 #endif
-    const uint64_t t = tab[ki & 31u] + (ki << 47);
-    const double s = kvexp_f64_from(t);
+    /* s = tab[ki % 32] + (ki << 47): the shifted index has no bits in the
+     * low word, so only the high word is added to (one 32-bit add). */
+    const uint64_t tb = tab[ki & 31u];
+    const uint32_t s_hi = (uint32_t)(tb >> 32) + ((uint32_t)ki << 15);
+    const double s = kvexp_f64_from(((uint64_t)s_hi << 32) | (uint32_t)tb);
     const double r2 = r * r;
 #if KVEXP_EXPF_FORM >= 1
     const double p = KVEXP_FMA64(KVEXP_EXP_C0, r, KVEXP_EXP_C1);
@@ -140,14 +143,51 @@ KVEXP_HD float kvexp_expf_tab_nb(float x, const uint64_t *tab) {
     return abstop >= 0x42bu ? special : core;
 }
 
+#if defined(__HIP_DEVICE_COMPILE__) && KVEXP_EXPF_FORM == 2
+/* Device form of kvexp_expf_core_tab (form 2): the same operations in a fixed
+ * instruction sequence. Left to itself the compiler rebuilds the table add
+ * through 32-bit halves and copies constants for two-address forms (21
+ * instructions instead of 16). s = tab[k % 32] + (ki << 47) is a 64-bit
+ * shift and a 64-bit add (v_lshl_add_u64 itself only shifts by 0..4). tab
+ * must point into LDS. */
+__device__ static inline __attribute__((always_inline)) float kvexp_expf_core_fast(float x, const uint64_t *tab) {
+    double xd, kd, r;
+    const double c = KVEXP_EXP_INVLN2N, sh = KVEXP_EXP_SHIFT, nsh = -KVEXP_EXP_SHIFT;
+    asm("v_cvt_f64_f32 %0, %3\n\t"
+        "v_fma_f64 %1, %4, %0, %5\n\t"
+        "v_add_f64 %2, %1, %6\n\t"
+        "v_fma_f64 %2, %4, %0, -%2"
+        : "=&v"(xd), "=&v"(kd), "=&v"(r)
+        : "v"(x), "s"(c), "v"(sh), "s"(nsh));
+    const uint64_t tb = tab[(uint32_t)kvexp_f64_bits(kd) & 31u];
+    const double c0 = KVEXP_EXP_C0, c1 = KVEXP_EXP_C1, c2 = KVEXP_EXP_C2;
+    double s, r2, p, y;
+    float yf;
+    asm("v_lshlrev_b64 %0, 47, %5\n\t"
+        "v_lshl_add_u64 %0, %0, 0, %6\n\t"
+        "v_mul_f64 %1, %7, %7\n\t"
+        "v_fma_f64 %2, %8, %7, %9\n\t"
+        "v_fma_f64 %3, %10, %7, 1.0\n\t"
+        "v_fma_f64 %3, %2, %1, %3\n\t"
+        "v_mul_f64 %3, %3, %0\n\t"
+        "v_cvt_f32_f64 %4, %3"
+        : "=&v"(s), "=&v"(r2), "=&v"(p), "=&v"(y), "=v"(yf)
+        : "v"(kd), "v"(tb), "v"(r), "s"(c0), "v"(c1), "s"(c2));
+    return yf;
+}
+#else
+#define kvexp_expf_core_fast kvexp_expf_core_tab
+#endif
+
 /* kvexp_expf_tab_nb for arguments that are not positive (x <= 0, -0, -inf)
  * or NaN, as every softmax exponent is (s - m and m_prev - m with m the
- * running maximum); +0 is also handled. Only two special cases remain:
- * x < -0x1.9fe368p6 (including -inf) -> +0, NaN -> x + x. */
+ * running maximum); +0 is also handled. One special case remains:
+ * x < -0x1.9fe368p6 (including -inf) -> +0. A NaN argument needs no case of
+ * its own: it makes r NaN, so the polynomial and the result are NaN (the
+ * payload may differ from glibc's x + x; every NaN is treated alike). */
 KVEXP_HD float kvexp_expf_nonpos_nb(float x, const uint64_t *tab) {
-    const float core = kvexp_expf_core_tab(x, tab);
-    const float r = x < -0x1.9fe368p6f ? 0.0f : core;
-    return x != x ? x + x : r;
+    const float core = kvexp_expf_core_fast(x, tab);
+    return x < -0x1.9fe368p6f ? 0.0f : core;
 }
 
 /* The reduction and polynomial with the built-in table. */
