@@ -298,8 +298,8 @@ __device__ __forceinline__ float lo_f32(uint32_t w) { return __uint_as_float(w <
 __device__ __forceinline__ float hi_f32(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
 
 // Scores of the lane's tile row for G query rows (scalar/AVX2 order).
-// qa is the address of the head's query rows widened to FP32 ([8][64],
-// written by q_widen_kernel before this launch). Stage st = dg * G + g
+// qa is the address of the split's query rows widened to FP32 ([8][64],
+// written by this wave before its first chunk). Stage st = dg * G + g
 // multiplies channels 8dg..8dg+7 of row g; its eight q values arrive by one
 // scalar load issued two stages earlier, whose address is tied (through an
 // empty asm) to that earlier stage's FMA results, so at most two stages of q
@@ -416,23 +416,14 @@ __device__ __forceinline__ void fold_rb(const WaveLds<G> &S, lds_f32 *eb, lds_f3
     }
 }
 
-// q32[h][g][d] = FP32 of query row q_row + g of device head h (rows >= n_q
-// left alone). One workgroup per device head.
-__global__ __launch_bounds__(256) void q_widen_kernel(const HeadDev *__restrict__ heads,
-                                                     const uint16_t *__restrict__ q_all, float *__restrict__ q32) {
-    const HeadDev hd = heads[blockIdx.x];
-    for (int i = int(threadIdx.x); i < hd.n_q * kD; i += 256)
-        q32[size_t(blockIdx.x) * kSlotQ * kD + i] = __uint_as_float(uint32_t(q_all[size_t(hd.q_row) * kD + i]) << 16);
-}
-
 // XKV instantiations are held to three waves per SIMD (168 VGPRs; a few
 // loop-invariant lane addresses then live in scratch and are reloaded only
 // on the rare paths that use them); LDS allows three workgroups per CU.
 template <int G, bool XKV>
 __global__ __launch_bounds__(kWavesPerWg * 64) __attribute__((amdgpu_waves_per_eu(XKV ? 3 : 2))) void attn_wave_kernel(
     const HeadDev *__restrict__ heads, const WorkItem *__restrict__ items, int n_items,
-    const float *__restrict__ q32_all, float *__restrict__ out_all, float *__restrict__ lse_all,
-    float *__restrict__ ws) {
+    const uint16_t *__restrict__ q_all, float *__restrict__ q32_all, float *__restrict__ out_all,
+    float *__restrict__ lse_all, float *__restrict__ ws) {
     __shared__ WgLds<G> L;
     if (threadIdx.x < 32) L.exptab[threadIdx.x] = kvexp_exp2_32_table[threadIdx.x];
     __syncthreads();
@@ -445,7 +436,19 @@ __global__ __launch_bounds__(kWavesPerWg * 64) __attribute__((amdgpu_waves_per_e
     const uint64_t *tab = L.exptab;
     const WorkItem wi = load_scalar(items + item);
     const HeadDev hd = load_scalar(heads + wi.head);
-    const float *q32 = q32_all + size_t(wi.head) * kSlotQ * kD;
+    // The head's query rows, widened to FP32 (lane = channel) into the head's
+    // copy, which the chunks then read with scalar loads (one copy per head,
+    // so that the scalar cache serves the head's splits from the same lines).
+    // Every split of the head writes the same values there; each waits for
+    // its own stores to reach L2 before its first scalar load, so whichever
+    // split's load brings a line into the scalar cache finds it complete (the
+    // cache holds no line of this launch's copy before: it starts each launch
+    // empty, and the copy is written before it is read).
+    float *q32 = q32_all + size_t(wi.head) * kSlotQ * kD;
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+        q32[g * kD + lane] = __uint_as_float(uint32_t(q_all[(size_t(hd.q_row) + g) * kD + lane]) << 16);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
     float acc[G];
     float msc[G]; // running maximum of each query row (wave-uniform)
@@ -701,33 +704,28 @@ namespace kvexp_launch {
 using namespace kvexp_dev;
 
 template <int G, bool XKV>
-static hipError_t launch_wave_g(const HeadDev *heads, const WorkItem *items, int n_items, const float *q,
-                                float *out, float *lse, float *ws, hipStream_t s) {
+static hipError_t launch_wave_g(const HeadDev *heads, const WorkItem *items, int n_items, const uint16_t *q,
+                                float *q32, float *out, float *lse, float *ws, hipStream_t s) {
     const int grid = (n_items + wave::kWavesPerWg - 1) / wave::kWavesPerWg;
     hipLaunchKernelGGL((wave::attn_wave_kernel<G, XKV>), dim3(grid), dim3(wave::kWavesPerWg * 64), 0, s, heads,
-                       items, n_items, q, out, lse, ws);
+                       items, n_items, q, q32, out, lse, ws);
     return hipGetLastError();
 }
 
 template <bool XKV>
-static hipError_t launch_wave_x(int G, const HeadDev *heads, const WorkItem *items, int n_items, const float *q,
-                                float *out, float *lse, float *ws, hipStream_t s) {
+static hipError_t launch_wave_x(int G, const HeadDev *heads, const WorkItem *items, int n_items, const uint16_t *q,
+                                float *q32, float *out, float *lse, float *ws, hipStream_t s) {
     switch (G) {
-    case 1: return launch_wave_g<1, XKV>(heads, items, n_items, q, out, lse, ws, s);
-    case 2: return launch_wave_g<2, XKV>(heads, items, n_items, q, out, lse, ws, s);
-    case 3: return launch_wave_g<3, XKV>(heads, items, n_items, q, out, lse, ws, s);
-    case 4: return launch_wave_g<4, XKV>(heads, items, n_items, q, out, lse, ws, s);
-    case 5: return launch_wave_g<5, XKV>(heads, items, n_items, q, out, lse, ws, s);
-    case 6: return launch_wave_g<6, XKV>(heads, items, n_items, q, out, lse, ws, s);
-    case 7: return launch_wave_g<7, XKV>(heads, items, n_items, q, out, lse, ws, s);
-    case 8: return launch_wave_g<8, XKV>(heads, items, n_items, q, out, lse, ws, s);
+    case 1: return launch_wave_g<1, XKV>(heads, items, n_items, q, q32, out, lse, ws, s);
+    case 2: return launch_wave_g<2, XKV>(heads, items, n_items, q, q32, out, lse, ws, s);
+    case 3: return launch_wave_g<3, XKV>(heads, items, n_items, q, q32, out, lse, ws, s);
+    case 4: return launch_wave_g<4, XKV>(heads, items, n_items, q, q32, out, lse, ws, s);
+    case 5: return launch_wave_g<5, XKV>(heads, items, n_items, q, q32, out, lse, ws, s);
+    case 6: return launch_wave_g<6, XKV>(heads, items, n_items, q, q32, out, lse, ws, s);
+    case 7: return launch_wave_g<7, XKV>(heads, items, n_items, q, q32, out, lse, ws, s);
+    case 8: return launch_wave_g<8, XKV>(heads, items, n_items, q, q32, out, lse, ws, s);
     default: return hipErrorInvalidValue;
     }
-}
-
-hipError_t q_widen(const HeadDev *heads, int n_heads, const uint16_t *q, float *q32, hipStream_t s) {
-    hipLaunchKernelGGL(wave::q_widen_kernel, dim3(n_heads), dim3(256), 0, s, heads, q, q32);
-    return hipGetLastError();
 }
 
 hipError_t wave_merge(const HeadDev *heads, const int2 *mitems, int n_mitems, float *out, float *lse, const float *ws,
@@ -739,11 +737,13 @@ hipError_t wave_merge(const HeadDev *heads, const int2 *mitems, int n_mitems, fl
     return hipGetLastError();
 }
 
+// q32 holds [n_heads][8][64] floats: the splits of a head widen its query rows
+// into the head's copy.
 hipError_t attention_wave(bool xkv, int G, const HeadDev *heads, const WorkItem *items, int n_items,
-                          const float *q, float *out, float *lse, float *ws, hipStream_t s) {
+                          const uint16_t *q, float *q32, float *out, float *lse, float *ws, hipStream_t s) {
     if (n_items <= 0) return hipSuccess;
-    return xkv ? launch_wave_x<true>(G, heads, items, n_items, q, out, lse, ws, s)
-               : launch_wave_x<false>(G, heads, items, n_items, q, out, lse, ws, s);
+    return xkv ? launch_wave_x<true>(G, heads, items, n_items, q, q32, out, lse, ws, s)
+               : launch_wave_x<false>(G, heads, items, n_items, q, q32, out, lse, ws, s);
 }
 
 } // namespace kvexp_launch

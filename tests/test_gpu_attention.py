@@ -241,3 +241,33 @@ def test_split_and_argument_errors(ctx, oracle):
     # one thread reads from token 0: any split works
     out = H(0, q, kx=kx, vx=vx, n_q=2, dim=64, seq=300, split=100, threads=1)
     assert bits_equal(out, oracle.attention("scalar", q, k, v, n_q=2, dim=64, seq=300, split=100, threads=1))
+
+
+def test_plan_reused_with_new_queries(ctx, oracle):
+    """One plan run several times with different queries (as a decode loop
+    does): every run must read its own queries, never a previous run's copy."""
+    import torch
+
+    rng = np.random.default_rng(909)
+    dim, n_q, block, seq = 64, 7, 128, 1500
+    heads_np = [dict(k=random_kv(rng, seq, dim, spread_lo=-6, spread_hi=4, outliers=2),
+                     v=random_kv(rng, seq, dim, sigma=0.5), seq=seq, splits=s) for s in (1, 5, 12)]
+    for xkv in (False, True):
+        hs = []
+        for h in heads_np:
+            if xkv:
+                hs.append(dict(kx=ctx.encode(to_dev(h["k"], torch.int16), seq, dim, block),
+                               vx=ctx.encode(to_dev(h["v"], torch.int16), seq, dim, block), seq=seq,
+                               splits=h["splits"]))
+            else:
+                hs.append(dict(k=to_dev(h["k"], torch.int16), v=to_dev(h["v"], torch.int16), seq=seq,
+                               splits=h["splits"]))
+        plan = ctx.plan(hs, n_q, dim, block, 0)
+        for run in range(4):
+            q = random_kv(rng, len(heads_np) * n_q, dim)
+            say("plan reuse", dict(xkv=xkv, run=run))
+            got = plan.run(to_dev(q, torch.int16), check_errors=True).cpu().numpy()
+            want = oracle.attention_heads("scalar", q, [dict(k=h["k"], v=h["v"], seq=seq, threads=h["splits"])
+                                                        for h in heads_np], n_q=n_q, dim=dim, split=block)
+            assert bits_equal(got, want), (xkv, run)
+        plan.close()
