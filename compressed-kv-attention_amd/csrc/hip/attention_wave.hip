@@ -297,63 +297,65 @@ __device__ __forceinline__ void wave_sync() {
 __device__ __forceinline__ float lo_f32(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float hi_f32(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
 
-// Scores of the lane's tile row for G query rows (scalar/AVX2 order).
-// qa is the address of the split's query rows widened to FP32 ([8][64],
-// written by this wave before its first chunk). Stage st = dg * G + g
-// multiplies channels 8dg..8dg+7 of row g; its eight q values arrive by one
-// scalar load issued two stages earlier, whose address is tied (through an
-// empty asm) to that earlier stage's FMA results, so at most two stages of q
-// are live in scalar registers and no load is hoisted out of the chunk loop.
-template <int G>
-__device__ __forceinline__ void scores(const uint8_t *row, uint64_t qa, float (&s)[G]) {
-    constexpr int NS = 8 * G;
-    float c[G][8];
-#pragma unroll
-    for (int g = 0; g < G; ++g)
-#pragma unroll
-        for (int j = 0; j < 8; ++j) c[g][j] = 0.0f;
-    f8 qb[2];
-    qb[0] = *(const c_f8 *)(qa);
-    if (NS > 1) qb[1] = *(const c_f8 *)(qa + ((1 % G) * kD + 8 * (1 / G)) * 4);
-    float k[8];
-#pragma unroll
-    for (int st = 0; st < NS; ++st) {
-        const int dg = st / G, g = st % G;
-        if (g == 0) {
-            const uint4 kb = *reinterpret_cast<const uint4 *>(row + 16 * dg);
-            k[0] = lo_f32(kb.x); k[1] = hi_f32(kb.x); k[2] = lo_f32(kb.y); k[3] = hi_f32(kb.y);
-            k[4] = lo_f32(kb.z); k[5] = hi_f32(kb.z); k[6] = lo_f32(kb.w); k[7] = hi_f32(kb.w);
-        }
-        const f8 q = qb[st & 1];
-        c[g][0] = fmaf(q.s0, k[0], c[g][0]);
-        c[g][1] = fmaf(q.s1, k[1], c[g][1]);
-        c[g][2] = fmaf(q.s2, k[2], c[g][2]);
-        c[g][3] = fmaf(q.s3, k[3], c[g][3]);
-        c[g][4] = fmaf(q.s4, k[4], c[g][4]);
-        c[g][5] = fmaf(q.s5, k[5], c[g][5]);
-        c[g][6] = fmaf(q.s6, k[6], c[g][6]);
-        c[g][7] = fmaf(q.s7, k[7], c[g][7]);
-        if (st + 2 < NS) {
-            const int n2 = st + 2;
-            uint64_t a2 = qa + uint64_t(((n2 % G) * kD + 8 * (n2 / G)) * 4);
-            asm volatile("" : "+s"(a2), "+v"(c[g][0]), "+v"(c[g][1]), "+v"(c[g][2]), "+v"(c[g][3]), "+v"(c[g][4]),
-                         "+v"(c[g][5]), "+v"(c[g][6]), "+v"(c[g][7]));
-            qb[st & 1] = *(const c_f8 *)(a2);
-        }
-    }
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-        const float a = (c[g][0] + c[g][4]) + (c[g][1] + c[g][5]);
-        const float b = (c[g][2] + c[g][6]) + (c[g][3] + c[g][7]);
-        s[g] = a + b;
+// Rank-1 update on the matrix cores: v_mfma_f32_4x4x1_16b_f32 with A taken
+// from block ABID for all 16 blocks (CBSZ 4), so that
+//   D[r] at lane l = A[lane 4 * ABID + r] * B[lane l] + C[r] at lane l.
+// Each element is one IEEE fused multiply-add with round-to-nearest-even and
+// denormals kept, the same bits as fmaf; the query rows (r) go in A and the
+// tokens or channels (l) in B, so one instruction performs four query rows'
+// fmaf of one channel for 64 tokens (scores), or of one token for 64
+// channels (the V fold).
+template <int ABID>
+__device__ __forceinline__ f4 mfma_rank1(float a, float b, f4 c) {
+    return __builtin_amdgcn_mfma_f32_4x4x1f32(a, b, c, 4, ABID, 0);
+}
+
+template <int I, int N, class F>
+__device__ __forceinline__ void static_for(F &&f) {
+    if constexpr (I < N) {
+        f(std::integral_constant<int, I>{});
+        static_for<I + 1, N>(f);
     }
 }
 
-// acc += E[lane of its row of 16 with index K] * v (v_fmac_f32 with a DPP
-// row_newbcast:K source): the weight comes from a register, not from LDS.
-template <int K>
-__device__ __forceinline__ void fmac_rowbcast(float &acc, float e, float v) {
-    asm("v_fmac_f32_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf" : "+v"(acc) : "v"(e), "v"(v), "n"(K));
+// Query rows in 4-row groups (rg): query row g is register g % 4 of group g / 4.
+template <int G>
+constexpr int kGroups = (G + 3) / 4;
+
+// Scores of the lane's tile row (lane = token) for G query rows in the
+// scalar/AVX2 order of attention_scalar.cpp:23-29: chain j (j = 0..7) takes
+// channels j, j + 8, ..., j + 56 in order, lane[j] = fmaf(q, k, lane[j]),
+// then hsum8's ((l0 + l4) + (l1 + l5)) + ((l2 + l6) + (l3 + l7)). Channel d
+// is one rank-1 product per row group into chain d % 8. qa[rg][d / 16] holds
+// q[4 rg + r][d] at lane 4 (d % 16) + r.
+template <int G>
+__device__ __forceinline__ void scores(const uint8_t *row, const float (&qa)[kGroups<G>][4], float (&s)[G]) {
+    constexpr int NG = kGroups<G>;
+    f4 ch[NG][8];
+#pragma unroll
+    for (int rg = 0; rg < NG; ++rg)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) ch[rg][j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    static_for<0, 8>([&](auto DG) {
+        const uint4 kb = *reinterpret_cast<const uint4 *>(row + 16 * DG);
+        const float k[8] = {lo_f32(kb.x), hi_f32(kb.x), lo_f32(kb.y), hi_f32(kb.y),
+                            lo_f32(kb.z), hi_f32(kb.z), lo_f32(kb.w), hi_f32(kb.w)};
+        static_for<0, 8>([&](auto J) {
+            constexpr int d = 8 * decltype(DG)::value + decltype(J)::value;
+#pragma unroll
+            for (int rg = 0; rg < NG; ++rg) ch[rg][J] = mfma_rank1<d % 16>(qa[rg][d / 16], k[J], ch[rg][J]);
+        });
+    });
+#pragma unroll
+    for (int rg = 0; rg < NG; ++rg) {
+        const f4 a = (ch[rg][0] + ch[rg][4]) + (ch[rg][1] + ch[rg][5]);
+        const f4 b = (ch[rg][2] + ch[rg][6]) + (ch[rg][3] + ch[rg][7]);
+        const f4 t = a + b;
+        if (4 * rg + 0 < G) s[(4 * rg + 0) % G] = t.x;
+        if (4 * rg + 1 < G) s[(4 * rg + 1) % G] = t.y;
+        if (4 * rg + 2 < G) s[(4 * rg + 2) % G] = t.z;
+        if (4 * rg + 3 < G) s[(4 * rg + 3) % G] = t.w;
+    }
 }
 
 // Operands of the fold in flight: V of the lane's channel for the next
@@ -364,30 +366,23 @@ struct FoldIn {
     f4 e4[2], a4[2];
 };
 
-// Token T of the ordered fold, lane = channel, for a whole chunk (tokens past
-// the chunk's end carry e = 0, alpha = 1 and V = -0, which leave acc and l
-// exactly as they are). A token that moves no running maximum (alpha == 1 for
-// every row, exactly) takes acc = fma(e, v, acc); a token that moves one
-// (rec, a uniform branch) scales by alpha first: acc = fma(e, v, acc * alpha),
-// the multiply done in place (inline asm with tied registers) so the join
-// needs no register copies. Lane g < G carries l of row g through
-// l = fma(l, alpha, e), which is l + e when alpha is 1, so it needs no branch.
-// The weights e[g][T] come from registers: Eq[g] holds, in every row of 16
-// lanes, e[g][16q + k] at lane k (q = T / 16), so row_newbcast:(T % 16) hands
-// every lane e[g][T]. Loads run ahead: V eight tokens and e / alpha four
-// tokens before their use.
+// Token T of the ordered fold (attention_scalar.cpp:33-40), lane = channel,
+// for a whole chunk (tokens past the chunk's end carry e = 0, alpha = 1 and
+// V = -0, which leave acc and l exactly as they are). A token that moves no
+// running maximum (alpha == 1 for every row, exactly) takes
+// acc = fma(e, v, acc); a token that moves one (a uniform branch) scales by
+// alpha first: acc = fma(e, v, acc * alpha). acc[rg] register r is row
+// 4 rg + r; the fma of every row of a group is one rank-1 product whose A
+// operand is ea[rg][T / 16] (e[4 rg + r][T] at lane 4 (T % 16) + r). Lane
+// g < G carries l of row g through l = fma(l, alpha, e), which is l + e when
+// alpha is 1. Loads run ahead: V three tokens and e / alpha four tokens
+// before their use.
 template <int G, int T>
-__device__ __forceinline__ void fold_rb(const WaveLds<G> &S, lds_f32 *eb, lds_f32 *ab, const uint16_t *vb,
-                                        uint64_t amask, const float (&ev)[G], float (&E)[2][G], FoldIn &in,
-                                        float (&acc)[G], float &lvec, int lane) {
+__device__ __forceinline__ void fold(const WaveLds<G> &S, lds_f32 *eb, lds_f32 *ab, const uint16_t *vb,
+                                     uint64_t amask, const float (&ea)[kGroups<G>][4], FoldIn &in,
+                                     f4 (&acc)[kGroups<G>], float &lvec) {
+    constexpr int NG = kGroups<G>;
     if constexpr (T < kChunk) {
-        constexpr int q = T / 16;
-        if constexpr (T % 16 == 0 && q + 1 < kChunk / 16) {
-            const int src = ((q + 1) * 16 + (lane & 15)) * 4;
-#pragma unroll
-            for (int g = 0; g < G; ++g)
-                E[(q + 1) & 1][g] = __int_as_float(__builtin_amdgcn_ds_bpermute(src, __float_as_int(ev[g])));
-        }
         if constexpr (T + 3 < kChunk) in.v[(T + 3) & 3] = vb[(T + 3) * (kTileStride / 2)];
         if constexpr (T % 4 == 0 && T + 4 < kChunk) {
             in.e4[((T / 4) + 1) & 1] = *reinterpret_cast<lds_f4 *>(eb + T + 4);
@@ -398,21 +393,19 @@ __device__ __forceinline__ void fold_rb(const WaveLds<G> &S, lds_f32 *eb, lds_f3
         const float el = (T % 4 == 0) ? e4.x : (T % 4 == 1) ? e4.y : (T % 4 == 2) ? e4.z : e4.w;
         const float al = (T % 4 == 0) ? a4.x : (T % 4 == 1) ? a4.y : (T % 4 == 2) ? a4.z : a4.w;
         if (((amask >> T) & 1ull) != 0) {
-            // every load first (a volatile asm between them would be a
-            // scheduling barrier and serialise their latencies)
             float av[G];
 #pragma unroll
             for (int g = 0; g < G; ++g) av[g] = S.aT[g][T];
 #pragma unroll
-            for (int g = 0; g < G; ++g) asm("v_mul_f32 %0, %0, %1" : "+v"(acc[g]) : "v"(av[g]));
+            for (int g = 0; g < G; ++g) acc[g / 4][g % 4] *= av[g];
         }
         lvec = fmaf(lvec, al, el);
         // keeps the l chain in token order (otherwise it may be sunk to the
         // end of the unrolled fold with every token's operands held live)
         asm volatile("" : "+v"(lvec));
 #pragma unroll
-        for (int g = 0; g < G; ++g) fmac_rowbcast<T % 16>(acc[g], E[q & 1][g], v);
-        fold_rb<G, T + 1>(S, eb, ab, vb, amask, ev, E, in, acc, lvec, lane);
+        for (int rg = 0; rg < NG; ++rg) acc[rg] = mfma_rank1<T % 16>(ea[rg][T / 16], v, acc[rg]);
+        fold<G, T + 1>(S, eb, ab, vb, amask, ea, in, acc, lvec);
     }
 }
 
@@ -436,27 +429,30 @@ __global__ __launch_bounds__(kWavesPerWg * 64) __attribute__((amdgpu_waves_per_e
     const uint64_t *tab = L.exptab;
     const WorkItem wi = load_scalar(items + item);
     const HeadDev hd = load_scalar(heads + wi.head);
-    // The head's query rows, widened to FP32 (lane = channel) into the head's
-    // copy, which the chunks then read with scalar loads (one copy per head,
-    // so that the scalar cache serves the head's splits from the same lines).
-    // Every split of the head writes the same values there; each waits for
-    // its own stores to reach L2 before its first scalar load, so whichever
-    // split's load brings a line into the scalar cache finds it complete (the
-    // cache holds no line of this launch's copy before: it starts each launch
-    // empty, and the copy is written before it is read).
-    float *q32 = q32_all + size_t(wi.head) * kSlotQ * kD;
+    // The head's query rows widened to FP32 as the A operands of the score
+    // products: qa[rg][j] at lane 4b + r holds q[4 rg + r][16 j + b] (0 for
+    // rows past G).
+    constexpr int NG = kGroups<G>;
+    float qa[NG][4];
+    {
+        const int r = lane & 3, b = lane >> 2;
 #pragma unroll
-    for (int g = 0; g < G; ++g)
-        q32[g * kD + lane] = __uint_as_float(uint32_t(q_all[(size_t(hd.q_row) + g) * kD + lane]) << 16);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        for (int rg = 0; rg < NG; ++rg) {
+            const int g = min(4 * rg + r, G - 1);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float qv = __uint_as_float(uint32_t(q_all[(size_t(hd.q_row) + g) * kD + 16 * j + b]) << 16);
+                qa[rg][j] = 4 * rg + r < G ? qv : 0.0f;
+            }
+        }
+    }
 
-    float acc[G];
+    f4 acc[NG];
+#pragma unroll
+    for (int rg = 0; rg < NG; ++rg) acc[rg] = f4{0.0f, 0.0f, 0.0f, 0.0f};
     float msc[G]; // running maximum of each query row (wave-uniform)
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-        acc[g] = 0.0f;
-        msc[g] = -__builtin_inff();
-    }
+    for (int g = 0; g < G; ++g) msc[g] = -__builtin_inff();
     float lvec = 0.0f; // lane g < G holds l of query row g
 
     Cursor kc{}, vc{};
@@ -504,11 +500,8 @@ __global__ __launch_bounds__(kWavesPerWg * 64) __attribute__((amdgpu_waves_per_e
         }
         wave_sync();
 
-        // 2. scores, lane = token (an opaque copy of the q address per chunk
-        // keeps the q loads inside the loop)
+        // 2. scores, lane = token
         float s[G];
-        uint64_t qa = reinterpret_cast<uint64_t>(q32);
-        asm volatile("" : "+s"(qa));
         scores<G>(my_row, qa, s);
         wave_sync();
 
@@ -596,11 +589,15 @@ __global__ __launch_bounds__(kWavesPerWg * 64) __attribute__((amdgpu_waves_per_e
 
         // 5. ordered fold, lane = channel, fully unrolled over the chunk
         {
-            float E[2][G];
-            const int src = (lane & 15) * 4;
+            // e as the A operands: ea[rg][j] at lane 4b + r holds e[4 rg + r][16 j + b]
+            // (rows past G repeat row G - 1; their results are not used)
+            float ea[NG][4];
 #pragma unroll
-            for (int g = 0; g < G; ++g)
-                E[0][g] = __int_as_float(__builtin_amdgcn_ds_bpermute(src, __float_as_int(ev[g])));
+            for (int rg = 0; rg < NG; ++rg) {
+                const int g = min(4 * rg + (lane & 3), G - 1);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) ea[rg][j] = S.eT[g][16 * j + (lane >> 2)];
+            }
             const int gl = min(lane & 7, G - 1); // lanes >= G read a row they do not use
             lds_f32 *eb = (lds_f32 *)&S.eT[gl][0];
             lds_f32 *ab = (lds_f32 *)&S.aT[gl][0];
@@ -610,7 +607,7 @@ __global__ __launch_bounds__(kWavesPerWg * 64) __attribute__((amdgpu_waves_per_e
             for (int k = 0; k < 3; ++k) in.v[k] = vb[k * (kTileStride / 2)];
             in.e4[0] = *reinterpret_cast<lds_f4 *>(eb);
             in.a4[0] = *reinterpret_cast<lds_f4 *>(ab);
-            fold_rb<G, 0>(S, eb, ab, vb, amask, ev, E, in, acc, lvec, lane);
+            fold<G, 0>(S, eb, ab, vb, amask, ea, in, acc, lvec);
         }
         wave_sync();
         t = tn;
@@ -624,7 +621,7 @@ __global__ __launch_bounds__(kWavesPerWg * 64) __attribute__((amdgpu_waves_per_e
 #pragma unroll
         for (int g = 0; g < G; ++g) {
             const float l = readlane_f32(lvec, g);
-            out_all[(size_t(hd.q_row) + g) * kD + lane] = acc[g] * (1.0f / l);
+            out_all[(size_t(hd.q_row) + g) * kD + lane] = acc[g / 4][g % 4] * (1.0f / l);
         }
         if (lse_all != nullptr && lane < G) lse_all[hd.q_row + lane] = mv + logf(lvec);
         return;
@@ -635,7 +632,7 @@ __global__ __launch_bounds__(kWavesPerWg * 64) __attribute__((amdgpu_waves_per_e
         slot[kSlotQ + lane] = lvec;
     }
 #pragma unroll
-    for (int g = 0; g < G; ++g) slot[2 * kSlotQ + g * kD + lane] = acc[g];
+    for (int g = 0; g < G; ++g) slot[2 * kSlotQ + g * kD + lane] = acc[g / 4][g % 4];
 }
 
 // Ordered merge of a head's split states (softmax.hpp:16-30 merge_state,
