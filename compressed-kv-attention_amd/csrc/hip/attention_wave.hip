@@ -109,14 +109,15 @@ __device__ __forceinline__ uint4 ld16(const uint8_t *p) {
 __device__ __forceinline__ uint32_t ldu16(const uint8_t *p) { return *(g_u16 *)(p); }
 
 // Position of one tensor inside its XKV container. The scalar fields are
-// wave-uniform; epos / eval hold the current block's first 64 escapes (lane
-// k < n_escape: element index and word of escape k).
+// wave-uniform; epos / eval hold the block's next escapes (lane
+// k < n_escape - ecur: element index and word of escape ecur + k).
 struct Cursor {
     const BlockDesc *d;  // descriptor of the current block (the next one follows it)
     const uint8_t *blk;  // current block's header
     const uint16_t *esc; // its escape positions
     int t0, t1;          // its token range
     uint32_t meta;       // mode | n_tokens << 8 | n_escape << 16
+    int ecur;            // first escape of the block not yet written into a tile
     uint32_t epos, eval;
     uint32_t base2;      // lane p < 32: base exponents 2p, 2p + 1 of the block
     __device__ int mode() const { return int(meta & 0xFFu); }
@@ -139,10 +140,11 @@ __device__ __forceinline__ void enter_block(Cursor &c, const BlockDesc *d, int t
     c.meta = w.s4;
     c.t0 = t0;
     c.t1 = t0 + c.ntok();
+    c.ecur = 0;
 }
 
-// The block's base exponents (lane p < 32: pair p) and its first 64 escape
-// positions and words (lane k < n_escape: escape k). Every lane loads, from a
+// The block's base exponents (lane p < 32: pair p) and its next 64 escape
+// positions and words (lane k < n_escape - ecur: escape ecur + k). Every lane loads, from a
 // clamped and always valid address, and the call is made on every chunk
 // whether or not the block changed, so the number of loads in flight does
 // not depend on the path taken: a result is then never merged with a default
@@ -151,7 +153,7 @@ __device__ __forceinline__ void enter_block(Cursor &c, const BlockDesc *d, int t
 __device__ __forceinline__ void block_vectors(Cursor &c) {
     const int lane = lane_id();
     const int nesc = c.nesc();
-    const int k = min(lane, max(nesc - 1, 0));
+    const int k = min(c.ecur + lane, max(nesc - 1, 0));
     c.base2 = ldu16(c.blk + 8 + 2 * (lane & (kD / 2 - 1)));
     c.epos = *(g_u16 *)(nesc > 0 ? c.esc + k : reinterpret_cast<const uint16_t *>(c.blk));
     c.eval = ldu16(nesc > 0 ? esc_words(c) + 2 * k : c.blk);
@@ -259,29 +261,46 @@ __device__ __forceinline__ void decode_row(const Cursor &c, const uint4 (&R)[kRo
 }
 
 // Writes the escape words of rows [r0, r0 + n) of the cursor's block over
-// their elements in the tile: the first 64 escapes from the registers loaded
-// with the block, any further ones (blocks with more than 64) loaded here in
-// windows of 64. Positions ascend within a block.
-__device__ __forceinline__ void patch_escapes(const Cursor &c, int r0, int n, uint8_t *tile) {
+// their elements in the tile and advances the cursor's escape index past
+// them. Positions ascend within a block and every escape before ecur lies in
+// an earlier chunk, so the chunk's escapes are the next ones from ecur whose
+// positions are below (r0 + n) * 64: the 64 loaded with the chunk's rows
+// (block_vectors), and, only for a chunk with more than 64, further windows
+// loaded here, two at a time.
+__device__ __forceinline__ void patch_escapes(Cursor &c, int r0, int n, uint8_t *tile) {
     const int nesc = c.nesc();
-    if (nesc == 0) return;
-    const uint32_t lo = uint32_t(r0 * kD), hi = uint32_t((r0 + n) * kD);
-    if (lane_id() < nesc && c.epos >= lo && c.epos < hi) {
+    if (c.ecur >= nesc) return;
+    const int lane = lane_id();
+    const uint32_t hi = uint32_t((r0 + n) * kD);
+    const bool mine = c.ecur + lane < nesc && c.epos < hi;
+    if (mine) {
         const uint32_t row = c.epos / kD - uint32_t(r0), col = c.epos % kD;
         *reinterpret_cast<uint16_t *>(tile + row * kTileStride + col * 2) = uint16_t(c.eval);
     }
-    if (nesc <= kWave) return;
-    const int lane = lane_id();
-    const uint8_t *esc = esc_words(c);
-    for (int k0 = kWave; k0 < nesc; k0 += kWave) {
-        const int k = k0 + lane;
-        uint32_t pos = 0xFFFFFFFFu;
-        if (k < nesc) pos = *(g_u16 *)(c.esc + k);
-        if (pos >= lo && pos < hi) {
-            const uint32_t row = pos / kD - uint32_t(r0), col = pos % kD;
-            *reinterpret_cast<uint16_t *>(tile + row * kTileStride + col * 2) = uint16_t(ldu16(esc + 2 * size_t(k)));
+    const int got = __popcll(__ballot(mine));
+    c.ecur += got;
+    if (got < kWave || c.ecur >= nesc) return;
+    const uint8_t *words = esc_words(c);
+    for (;;) {
+        uint32_t pos[2], val[2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int k = min(c.ecur + kWave * i + lane, nesc - 1);
+            pos[i] = *(g_u16 *)(c.esc + k);
+            val[i] = ldu16(words + 2 * k);
         }
-        if (uint32_t(__builtin_amdgcn_readfirstlane(int(pos))) >= hi) break; // lane 0 holds the window's first
+        int more = 0;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const bool m = c.ecur + kWave * i + lane < nesc && pos[i] < hi;
+            if (m) {
+                const uint32_t row = pos[i] / kD - uint32_t(r0), col = pos[i] % kD;
+                *reinterpret_cast<uint16_t *>(tile + row * kTileStride + col * 2) = uint16_t(val[i]);
+            }
+            more += __popcll(__ballot(m));
+        }
+        c.ecur += more;
+        if (more < 2 * kWave || c.ecur >= nesc) break;
     }
 }
 
