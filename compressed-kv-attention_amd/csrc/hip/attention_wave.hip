@@ -7,11 +7,16 @@
 //      chunk ahead into a BF16 tile in its own LDS slice: a coded element is
 //      (sm & 0x80) << 8 | (base + code) << 7 | (sm & 0x7F), built two at a
 //      time with v_perm_b32 / v_lshl_add_u32 / v_bfi_b32 on packed pairs;
-//      escape words are then written over their elements using the plan's
-//      escape-position index, so no sentinel search runs here;
-//   2. computes the G scores of each token (lane = token) in the reference
-//      order: 8 strided FMA chains over the 64 channels, q from scalar
-//      registers, then the ((l0+l4)+(l1+l5))+((l2+l6)+(l3+l7)) tree;
+//      escape words are then written over their elements from the plan's
+//      escape-position index (an escape cursor per tensor: the window of 64
+//      loaded with the rows starts at the chunk's first escape);
+//   2. computes the G scores of each token in the reference order: 8 strided
+//      FMA chains over the 64 channels, then the
+//      ((l0+l4)+(l1+l5))+((l2+l6)+(l3+l7)) tree. Every fmaf of the chains is
+//      done on the matrix cores as a rank-1 product
+//      (v_mfma_f32_4x4x1_16b_f32, one IEEE fused multiply-add per element, the
+//      same bits as fmaf): four query rows (A, the block-broadcast operand)
+//      times the lane's token (B), one instruction per channel and row group;
 //   3. decodes the V rows into the same tile (tokens past the chunk's end get
 //      -0, which the fold adds as an exact no-op);
 //   4. turns scores into e = exp(s - m) and, for the query rows where some
@@ -19,13 +24,11 @@
 //      exact DPP prefix maximum seeded by the maxima held in scalar registers
 //      and the glibc-identical expf; e and alpha go to LDS by query row;
 //   5. folds the chunk's tokens in order (lane = channel), fully unrolled:
-//      acc = fma(e, v, acc), with acc scaled by alpha first only on the
-//      tokens that move a maximum (a uniform branch; alpha == 1 elsewhere, so
+//      acc = fma(e, v, acc) as one rank-1 product per token and row group
+//      (e of four rows in A, picked per token by the block broadcast; the
+//      token's V row in B), with acc scaled by alpha first only on the tokens
+//      that move a maximum (a uniform branch; alpha == 1 elsewhere, so
 //      skipping the multiply is exact), and l = fma(l, alpha, e) on lane g.
-//      The weights e[g][t] reach all 64 lanes from registers: each quarter of
-//      the chunk is gathered with ds_bpermute so that lane k of every row of
-//      16 holds token 16q + k, and v_fmac_f32 takes it through a DPP
-//      row_newbcast source.
 // A head cut into several splits leaves one partial state (m, l, acc) per
 // split; wave_merge_kernel, launched after the split kernels, folds them left
 // to right (merge_state order) and finalizes out = acc * (1/l).
