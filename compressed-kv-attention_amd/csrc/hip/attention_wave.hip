@@ -437,8 +437,8 @@ __device__ __forceinline__ void fold(const WaveLds<G> &S, lds_f32 *eb, lds_f32 *
 template <int G, bool XKV>
 __global__ __launch_bounds__(kWavesPerWg * 64) __attribute__((amdgpu_waves_per_eu(XKV ? 3 : 2))) void attn_wave_kernel(
     const HeadDev *__restrict__ heads, const WorkItem *__restrict__ items, int n_items,
-    const uint16_t *__restrict__ q_all, float *__restrict__ q32_all, float *__restrict__ out_all,
-    float *__restrict__ lse_all, float *__restrict__ ws) {
+    const uint16_t *__restrict__ q_all, float *__restrict__ out_all, float *__restrict__ lse_all,
+    float *__restrict__ ws) {
     __shared__ WgLds<G> L;
     if (threadIdx.x < 32) L.exptab[threadIdx.x] = kvexp_exp2_32_table[threadIdx.x];
     __syncthreads();
@@ -724,25 +724,25 @@ using namespace kvexp_dev;
 
 template <int G, bool XKV>
 static hipError_t launch_wave_g(const HeadDev *heads, const WorkItem *items, int n_items, const uint16_t *q,
-                                float *q32, float *out, float *lse, float *ws, hipStream_t s) {
+                                float *out, float *lse, float *ws, hipStream_t s) {
     const int grid = (n_items + wave::kWavesPerWg - 1) / wave::kWavesPerWg;
     hipLaunchKernelGGL((wave::attn_wave_kernel<G, XKV>), dim3(grid), dim3(wave::kWavesPerWg * 64), 0, s, heads,
-                       items, n_items, q, q32, out, lse, ws);
+                       items, n_items, q, out, lse, ws);
     return hipGetLastError();
 }
 
 template <bool XKV>
 static hipError_t launch_wave_x(int G, const HeadDev *heads, const WorkItem *items, int n_items, const uint16_t *q,
-                                float *q32, float *out, float *lse, float *ws, hipStream_t s) {
+                                float *out, float *lse, float *ws, hipStream_t s) {
     switch (G) {
-    case 1: return launch_wave_g<1, XKV>(heads, items, n_items, q, q32, out, lse, ws, s);
-    case 2: return launch_wave_g<2, XKV>(heads, items, n_items, q, q32, out, lse, ws, s);
-    case 3: return launch_wave_g<3, XKV>(heads, items, n_items, q, q32, out, lse, ws, s);
-    case 4: return launch_wave_g<4, XKV>(heads, items, n_items, q, q32, out, lse, ws, s);
-    case 5: return launch_wave_g<5, XKV>(heads, items, n_items, q, q32, out, lse, ws, s);
-    case 6: return launch_wave_g<6, XKV>(heads, items, n_items, q, q32, out, lse, ws, s);
-    case 7: return launch_wave_g<7, XKV>(heads, items, n_items, q, q32, out, lse, ws, s);
-    case 8: return launch_wave_g<8, XKV>(heads, items, n_items, q, q32, out, lse, ws, s);
+    case 1: return launch_wave_g<1, XKV>(heads, items, n_items, q, out, lse, ws, s);
+    case 2: return launch_wave_g<2, XKV>(heads, items, n_items, q, out, lse, ws, s);
+    case 3: return launch_wave_g<3, XKV>(heads, items, n_items, q, out, lse, ws, s);
+    case 4: return launch_wave_g<4, XKV>(heads, items, n_items, q, out, lse, ws, s);
+    case 5: return launch_wave_g<5, XKV>(heads, items, n_items, q, out, lse, ws, s);
+    case 6: return launch_wave_g<6, XKV>(heads, items, n_items, q, out, lse, ws, s);
+    case 7: return launch_wave_g<7, XKV>(heads, items, n_items, q, out, lse, ws, s);
+    case 8: return launch_wave_g<8, XKV>(heads, items, n_items, q, out, lse, ws, s);
     default: return hipErrorInvalidValue;
     }
 }
@@ -756,13 +756,11 @@ hipError_t wave_merge(const HeadDev *heads, const int2 *mitems, int n_mitems, fl
     return hipGetLastError();
 }
 
-// q32 holds [n_heads][8][64] floats: the splits of a head widen its query rows
-// into the head's copy.
 hipError_t attention_wave(bool xkv, int G, const HeadDev *heads, const WorkItem *items, int n_items,
-                          const uint16_t *q, float *q32, float *out, float *lse, float *ws, hipStream_t s) {
+                          const uint16_t *q, float *out, float *lse, float *ws, hipStream_t s) {
     if (n_items <= 0) return hipSuccess;
-    return xkv ? launch_wave_x<true>(G, heads, items, n_items, q, q32, out, lse, ws, s)
-               : launch_wave_x<false>(G, heads, items, n_items, q, q32, out, lse, ws, s);
+    return xkv ? launch_wave_x<true>(G, heads, items, n_items, q, out, lse, ws, s)
+               : launch_wave_x<false>(G, heads, items, n_items, q, out, lse, ws, s);
 }
 
 } // namespace kvexp_launch

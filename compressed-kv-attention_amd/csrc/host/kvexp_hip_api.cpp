@@ -35,7 +35,7 @@ hipError_t expf(const float *x, float *y, size_t n, hipStream_t s);
 hipError_t esc_start(const kvexp_dev::EscJob *jobs, int n_jobs, uint32_t *status, hipStream_t s);
 hipError_t esc_pos(const kvexp_dev::EscJob *jobs, const int2 *blocks, int n_blocks, uint32_t *status, hipStream_t s);
 hipError_t attention_wave(bool xkv, int G, const HeadDev *heads, const WorkItem *items, int n_items,
-                          const uint16_t *q, float *q32, float *out, float *lse, float *ws, hipStream_t s);
+                          const uint16_t *q, float *out, float *lse, float *ws, hipStream_t s);
 hipError_t wave_merge(const HeadDev *heads, const int2 *mitems, int n_mitems, float *out, float *lse, const float *ws,
                       hipStream_t s);
 } // namespace kvexp_launch
@@ -196,8 +196,8 @@ struct kvexp_hip_plan {
     bool xkv = false;
     bool wave = false; // one-wave-per-split kernel (dim 64, scalar order)
     DevBuf heads, items, merge_ids, ws, status;
-    // wave kernel: merge work (head, row), escape-position index, block descriptors, FP32 q
-    DevBuf mitems, esc0, escpos, desc, q32;
+    // wave kernel: merge work (head, row), escape-position index, block descriptors
+    DevBuf mitems, esc0, escpos, desc;
     int n_mitems = 0;
     int n_dev_heads = 0, n_items = 0, n_merge = 0;
     // wave kernel: items sorted by query-row count G; group_start[G] .. group_start[G+1]
@@ -596,8 +596,6 @@ int kvexp_hip_plan_create(kvexp_hip_ctx *ctx, const kvexp_hip_head *heads, int n
                     p->group_start[G + 1] =
                         int(std::count_if(items.begin(), items.end(),
                                           [&](const WorkItem &w) { return hv[size_t(w.head)].n_q <= G; }));
-                // one FP32 copy of the query rows per device head (written by its splits)
-                p->q32 = DevBuf(hv.size() * size_t(kMaxQPerLaunch) * size_t(dim) * sizeof(float));
                 std::vector<int2> mi;
                 for (int32_t dh : merge)
                     for (int g = 0; g < hv[size_t(dh)].n_q; ++g) mi.push_back(make_int2(dh, g));
@@ -656,8 +654,8 @@ int kvexp_hip_attention_run(kvexp_hip_plan *plan, const uint16_t *d_q, float *d_
                 const int b = plan->group_start[G], e = plan->group_start[G + 1];
                 if (e > b)
                     HIPX(kvexp_launch::attention_wave(plan->xkv, G, plan->heads.as<HeadDev>(),
-                                                      plan->items.as<WorkItem>() + b, e - b, d_q,
-                                                      plan->q32.as<float>(), d_out, d_lse, plan->ws.as<float>(), s));
+                                                      plan->items.as<WorkItem>() + b, e - b, d_q, d_out, d_lse,
+                                                      plan->ws.as<float>(), s));
             }
             if (ev1) HIPX(hipEventRecord(ev1, s));
             HIPX(kvexp_launch::wave_merge(plan->heads.as<HeadDev>(), plan->mitems.as<int2>(), plan->n_mitems, d_out,
