@@ -1,5 +1,5 @@
-// gfx950 fused decode attention, head_dim 64, scalar/AVX2 score order:
-// one wave64 per split, no workgroup barriers on the hot path.
+// gfx950 fused decode attention, head_dim 64 or 128, scalar/AVX2 score
+// order: one wave64 per split, no workgroup barriers on the hot path.
 //
 // A split [tok_begin, tok_end) of one KV head is processed in chunks of up to
 // 64 tokens that never cross a K or V block. Per chunk the wave:
@@ -11,7 +11,7 @@
 //      escape-position index (an escape cursor per tensor: the window of 64
 //      loaded with the rows starts at the chunk's first escape);
 //   2. computes the G scores of each token in the reference order: 8 strided
-//      FMA chains over the 64 channels, then the
+//      FMA chains over the head's channels, then the
 //      ((l0+l4)+(l1+l5))+((l2+l6)+(l3+l7)) tree. Every fmaf of the chains is
 //      done on the matrix cores as a rank-1 product
 //      (v_mfma_f32_4x4x1_16b_f32, one IEEE fused multiply-add per element, the
@@ -23,7 +23,8 @@
 //      token moves the running maximum, alpha = exp(m_prev - m), with an
 //      exact DPP prefix maximum seeded by the maxima held in scalar registers
 //      and the glibc-identical expf; e and alpha go to LDS by query row;
-//   5. folds the chunk's tokens in order (lane = channel), fully unrolled:
+//   5. folds the chunk's tokens in order (lane = channel; at head_dim 128
+//      each lane holds channels lane and lane + 64), fully unrolled:
 //      acc = fma(e, v, acc) as one rank-1 product per token and row group
 //      (e of four rows in A, picked per token by the block broadcast; the
 //      token's V row in B), with acc scaled by alpha first only on the tokens
@@ -42,37 +43,46 @@
 namespace kvexp_dev {
 namespace wave {
 
-constexpr int kD = 64;          // head_dim of this kernel
 constexpr int kChunk = 64;      // tokens per chunk (one per lane)
-constexpr int kTileStride = 144; // bytes per tile row: 64 BF16 + 16 (conflict-free 16-byte rows)
 constexpr uint16_t kNegZeroBf16 = 0x8000u; // V of a token past the chunk's end: fma(0, -0, acc) == acc exactly
-constexpr int kWavesPerWg = 4;
-constexpr int kSlotQ = 8;       // partial-state slot: m[8], l[8], acc[8][64]
-constexpr int kSlotFloats = kSlotQ * (kD + 2);
-constexpr int kRowRegs = 6;     // 16-byte registers per prefetched XKV row (coded rows need at most 6)
-constexpr int kMergeBatch = 128; // split slots whose loads are in flight together in the merge
+constexpr int kSlotQ = 8;       // partial-state slot: m[8], l[8], acc[8][head_dim]
 
-// Per-wave LDS. The tile holds the chunk's K rows (row t: the 64 BF16 of
-// token t) and then its V transposed (row c: channel c of the 64 tokens).
-// eT / aT hold e and alpha by query row (row g: the chunk's 64 tokens), so a
-// lane reads four tokens of its row in one access. For G <= 7 a wave takes
-// 13,152 bytes and four waves with the shared table 52,864 bytes, which
-// leaves room for three workgroups per CU (the limit lies between 53,760
-// and 54,016 bytes per workgroup).
-constexpr int kRowPad = kChunk + 4; // floats per eT / aT row: 16 spare bytes keep the rows' reads conflict-free
-
-template <int G>
-struct alignas(16) WaveLds {
-    uint8_t tile[kChunk * kTileStride];
-    float eT[G][kRowPad]; // e of token t, row g (0 past the chunk's end)
-    float aT[G][kRowPad]; // alpha of token t, row g (1 where no running maximum moves)
-    uint32_t bp[kD / 2];  // base pair words of the block being decoded
+// The kernel's sizes for head_dim D (64 or 128).
+template <int D>
+struct Shape {
+    static constexpr int kTileStride = 2 * D + 16;  // bytes per tile row: D BF16 + 16 (conflict-free 16-byte rows)
+    static constexpr int kSlotFloats = kSlotQ * (D + 2);
+    static constexpr int kSmRegs = D / 16;          // 16-byte registers of a row's sign/mantissa bytes
+    static constexpr int kRowRegs = kSmRegs + D / 32; // + its 4-bit codes: what a coded row needs
+    static constexpr int kRawRegs = D / 8;          // 16-byte registers of a raw BF16 row
+    static constexpr int kOctets = D / 8;           // channel octets per row
+    static constexpr int kHalves = D / 64;          // channels per lane in the fold (lane, lane + 64, ...)
+    static constexpr int kWaves = D == 64 ? 4 : 2;  // waves per workgroup (LDS: see WaveLds)
+    static constexpr int kMergeBatch = 128 / kHalves; // split slots whose loads are in flight together in the merge
 };
 
-template <int G>
+// Per-wave LDS. The tile holds the chunk's K rows (row t: the D BF16 of
+// token t) and then its V rows, read by channel in the fold.
+// eT / aT hold e and alpha by query row (row g: the chunk's 64 tokens), so a
+// lane reads four tokens of its row in one access. At D = 64 and G <= 7 a
+// wave takes 13,152 bytes and a workgroup of four waves with the shared table
+// 52,864 bytes, which leaves room for three workgroups per CU (the limit lies
+// between 53,760 and 54,016 bytes per workgroup). At D = 128 and G = 4 a wave
+// takes 19,840 bytes; workgroups of two waves, four per CU.
+constexpr int kRowPad = kChunk + 4; // floats per eT / aT row: 16 spare bytes keep the rows' reads conflict-free
+
+template <int G, int D>
+struct alignas(16) WaveLds {
+    uint8_t tile[kChunk * Shape<D>::kTileStride];
+    float eT[G][kRowPad]; // e of token t, row g (0 past the chunk's end)
+    float aT[G][kRowPad]; // alpha of token t, row g (1 where no running maximum moves)
+    uint32_t bp[D / 2];   // base pair words of the block being decoded
+};
+
+template <int G, int D>
 struct alignas(16) WgLds {
     uint64_t exptab[32];
-    WaveLds<G> w[kWavesPerWg];
+    WaveLds<G, D> w[Shape<D>::kWaves];
 };
 
 // Global-memory loads (address space 1, so they are issued as global_load_*
@@ -122,14 +132,15 @@ struct Cursor {
     uint32_t meta;       // mode | n_tokens << 8 | n_escape << 16
     int ecur;            // first escape of the block not yet written into a tile
     uint32_t epos, eval;
-    uint32_t base2;      // lane p < 32: base exponents 2p, 2p + 1 of the block
+    uint32_t base2;      // lane p < D / 2: base exponents 2p, 2p + 1 of the block
     __device__ int mode() const { return int(meta & 0xFFu); }
     __device__ int ntok() const { return int((meta >> 8) & 0xFFu); }
     __device__ int nesc() const { return int(meta >> 16); }
 };
 
+template <int D>
 __device__ __forceinline__ const uint8_t *esc_words(const Cursor &c) {
-    return c.blk + 8 + kD + size_t(c.ntok()) * kD + exp_payload_bytes(c.ntok(), kD, c.mode());
+    return c.blk + 8 + D + size_t(c.ntok()) * D + exp_payload_bytes(c.ntok(), D, c.mode());
 }
 
 // Enters the block of descriptor d, whose first token is t0: one scalar load
@@ -146,39 +157,45 @@ __device__ __forceinline__ void enter_block(Cursor &c, const BlockDesc *d, int t
     c.ecur = 0;
 }
 
-// The block's base exponents (lane p < 32: pair p) and its next 64 escape
+// The block's base exponents (lane p < D / 2: pair p) and its next 64 escape
 // positions and words (lane k < n_escape - ecur: escape ecur + k). Every lane loads, from a
 // clamped and always valid address, and the call is made on every chunk
 // whether or not the block changed, so the number of loads in flight does
 // not depend on the path taken: a result is then never merged with a default
 // value, and waits for the row loads can leave later loads in flight. Lanes
 // >= n_escape are masked where the values are used.
+template <int D>
 __device__ __forceinline__ void block_vectors(Cursor &c) {
     const int lane = lane_id();
     const int nesc = c.nesc();
     const int k = min(c.ecur + lane, max(nesc - 1, 0));
-    c.base2 = ldu16(c.blk + 8 + 2 * (lane & (kD / 2 - 1)));
+    c.base2 = ldu16(c.blk + 8 + 2 * (lane & (D / 2 - 1)));
     c.epos = *(g_u16 *)(nesc > 0 ? c.esc + k : reinterpret_cast<const uint16_t *>(c.blk));
-    c.eval = ldu16(nesc > 0 ? esc_words(c) + 2 * k : c.blk);
+    c.eval = ldu16(nesc > 0 ? esc_words<D>(c) + 2 * k : c.blk);
 }
 
-// Loads rows [r0 + lane] of the cursor's block (lanes < rows) into R.
-__device__ __forceinline__ void load_rows(const Cursor &c, int r0, int rows, uint4 (&R)[kRowRegs]) {
+// Loads rows [r0 + lane] of the cursor's block (lanes < rows) into R: a
+// coded row's D sign/mantissa bytes and D/2 (4-bit) or D/4 (2-bit, its
+// registers repeated) code bytes; a raw row's first 3D/2 bytes (the rest is
+// read at decode).
+template <int D>
+__device__ __forceinline__ void load_rows(const Cursor &c, int r0, int rows, uint4 (&R)[Shape<D>::kRowRegs]) {
     // Lanes past `rows` load row rows - 1 again (their tile rows are not
     // used): every load is unconditional, with the mode's layout picked by
     // uniform selects, so the registers need no merge before their use.
+    constexpr int SM = Shape<D>::kSmRegs;
     const int r = r0 + min(lane_id(), rows - 1);
     const int mode = c.mode();
     const bool raw = mode == 0;
-    // sign/mantissa bytes (or the first 64 raw bytes) of the row
-    const uint8_t *rowp = c.blk + 8 + (raw ? 0 : kD) + size_t(r) * (raw ? 2 * kD : kD);
-    // codes of the row (or raw bytes 64..95)
-    const uint8_t *tail = raw ? rowp + 64
-                              : c.blk + 8 + kD + size_t(c.ntok()) * kD + size_t(r) * (mode == 4 ? kD / 2 : kD / 4);
+    // sign/mantissa bytes (or the first D raw bytes) of the row
+    const uint8_t *rowp = c.blk + 8 + (raw ? 0 : D) + size_t(r) * (raw ? 2 * D : D);
+    // codes of the row (or raw bytes D .. 3D/2 - 1)
+    const uint8_t *tail = raw ? rowp + D
+                              : c.blk + 8 + D + size_t(c.ntok()) * D + size_t(r) * (mode == 4 ? D / 2 : D / 4);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) R[i] = ld16(rowp + 16 * i);
-    R[4] = ld16(tail);
-    R[5] = ld16(tail + (mode == 2 ? 0 : 16));
+    for (int i = 0; i < SM; ++i) R[i] = ld16(rowp + 16 * i);
+#pragma unroll
+    for (int i = 0; i < D / 32; ++i) R[SM + i] = ld16(tail + 16 * (mode == 2 ? min(i, D / 64 - 1) : i));
 }
 
 __device__ __forceinline__ uint32_t comp(const uint4 &v, int i) {
@@ -186,11 +203,12 @@ __device__ __forceinline__ uint32_t comp(const uint4 &v, int i) {
 }
 
 // Base pair words of the cursor's block into LDS: word p = base[2p] << 7 |
-// base[2p+1] << 23 (lane p < 32 builds word p from the bytes loaded with the
-// block).
+// base[2p+1] << 23 (lane p < D / 2 builds word p from the bytes loaded with
+// the block).
+template <int D>
 __device__ __forceinline__ void base_pairs(const Cursor &c, uint32_t *bp) {
     const int lane = lane_id();
-    if (lane < kD / 2) bp[lane] = ((c.base2 & 0xFFu) << 7) | ((c.base2 >> 8) << 23);
+    if (lane < D / 2) bp[lane] = ((c.base2 & 0xFFu) << 7) | ((c.base2 >> 8) << 23);
 }
 
 // One BF16 pair from two sign/mantissa bytes (positions lb, lb+1 of sw), two
@@ -204,10 +222,10 @@ __device__ __forceinline__ uint32_t pair4(uint32_t sw, int lb, uint32_t lo, uint
 }
 
 // Octet dg (channels 8dg..8dg+7) of a coded row: four BF16 pairs from the
-// row's sign/mantissa bytes in R[0..3], its codes split into lo (byte p: code
-// 2p) and hi (byte p: code 2p+1), and the channel pairs' base words.
-__device__ __forceinline__ uint4 octet(const uint4 (&R)[kRowRegs], int dg, uint32_t lo, uint32_t hi,
-                                       const uint32_t *bp) {
+// row's sign/mantissa bytes in R[0 .. D/16), its codes split into lo (byte p:
+// code 2p) and hi (byte p: code 2p+1), and the channel pairs' base words.
+template <int N>
+__device__ __forceinline__ uint4 octet(const uint4 (&R)[N], int dg, uint32_t lo, uint32_t hi, const uint32_t *bp) {
     const uint32_t s0 = comp(R[dg >> 1], (dg & 1) * 2);
     const uint32_t s1 = comp(R[dg >> 1], (dg & 1) * 2 + 1);
     const uint4 b4 = *reinterpret_cast<const uint4 *>(bp + 4 * dg);
@@ -220,33 +238,36 @@ __device__ __forceinline__ uint4 octet(const uint4 (&R)[kRowRegs], int dg, uint3
 }
 
 // -0 in every channel of the lane's tile row (a token past the chunk's end).
+template <int D>
 __device__ __forceinline__ void fill_negzero(uint8_t *row) {
     const uint32_t z = uint32_t(kNegZeroBf16) * 0x10001u;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) reinterpret_cast<uint4 *>(row)[i] = make_uint4(z, z, z, z);
+    for (int i = 0; i < D / 8; ++i) reinterpret_cast<uint4 *>(row)[i] = make_uint4(z, z, z, z);
 }
 
 // Decodes the lane's row held in R (cursor's block mode) into its tile row.
 // One uniform branch on the mode, then a straight-line body per mode. Lanes
 // >= rows (past the chunk's end) then store -0 in every channel (wanted for
 // V; harmless for K).
-__device__ __forceinline__ void decode_row(const Cursor &c, const uint4 (&R)[kRowRegs], const uint32_t *bp,
+template <int D>
+__device__ __forceinline__ void decode_row(const Cursor &c, const uint4 (&R)[Shape<D>::kRowRegs], const uint32_t *bp,
                                            uint8_t *row, int r0, int rows) {
+    constexpr int SM = Shape<D>::kSmRegs, RR = Shape<D>::kRowRegs;
     uint4 *dst = reinterpret_cast<uint4 *>(row);
     const int mode = c.mode();
     const int lane = lane_id();
     if (mode == 4) {
 #pragma unroll
-        for (int dg = 0; dg < 8; ++dg) {
-            const uint32_t cw = comp(R[4 + (dg >> 2)], dg & 3);
+        for (int dg = 0; dg < D / 8; ++dg) {
+            const uint32_t cw = comp(R[SM + (dg >> 2)], dg & 3);
             dst[dg] = octet(R, dg, cw & 0x0F0F0F0Fu, (cw >> 4) & 0x0F0F0F0Fu, bp);
         }
     } else if (mode == 2) {
 #pragma unroll
-        for (int dg = 0; dg < 8; ++dg) {
+        for (int dg = 0; dg < D / 8; ++dg) {
             // 16 two-bit codes per dword; octet dg uses 16 bits. Byte p of
             // lo/hi: codes 2p and 2p+1 of the octet.
-            const uint32_t cw = comp(R[4], dg >> 1) >> (16 * (dg & 1));
+            const uint32_t cw = comp(R[SM + (dg >> 3)], (dg >> 1) & 3) >> (16 * (dg & 1));
             const uint32_t lo =
                 (cw & 3u) | (((cw >> 4) & 3u) << 8) | (((cw >> 8) & 3u) << 16) | (((cw >> 12) & 3u) << 24);
             const uint32_t hi = ((cw >> 2) & 3u) | (((cw >> 6) & 3u) << 8) | (((cw >> 10) & 3u) << 16) |
@@ -254,36 +275,38 @@ __device__ __forceinline__ void decode_row(const Cursor &c, const uint4 (&R)[kRo
             dst[dg] = octet(R, dg, lo, hi, bp);
         }
     } else if (lane < rows) {
-        const uint8_t *src = c.blk + 8 + size_t(r0 + lane) * (2 * kD);
+        const uint8_t *src = c.blk + 8 + size_t(r0 + lane) * (2 * D);
 #pragma unroll
-        for (int i = 0; i < kRowRegs; ++i) dst[i] = R[i];
-        dst[6] = ld16(src + 96);
-        dst[7] = ld16(src + 112);
+        for (int i = 0; i < RR; ++i) dst[i] = R[i];
+#pragma unroll
+        for (int i = RR; i < D / 8; ++i) dst[i] = ld16(src + 16 * i);
     }
-    if (rows < kChunk && lane >= rows) fill_negzero(row);
+    if (rows < kChunk && lane >= rows) fill_negzero<D>(row);
 }
 
 // Writes the escape words of rows [r0, r0 + n) of the cursor's block over
 // their elements in the tile and advances the cursor's escape index past
 // them. Positions ascend within a block and every escape before ecur lies in
 // an earlier chunk, so the chunk's escapes are the next ones from ecur whose
-// positions are below (r0 + n) * 64: the 64 loaded with the chunk's rows
+// positions are below (r0 + n) * D: the 64 loaded with the chunk's rows
 // (block_vectors), and, only for a chunk with more than 64, further windows
 // loaded here, two at a time.
+template <int D>
 __device__ __forceinline__ void patch_escapes(Cursor &c, int r0, int n, uint8_t *tile) {
+    constexpr int TS = Shape<D>::kTileStride;
     const int nesc = c.nesc();
     if (c.ecur >= nesc) return;
     const int lane = lane_id();
-    const uint32_t hi = uint32_t((r0 + n) * kD);
+    const uint32_t hi = uint32_t((r0 + n) * D);
     const bool mine = c.ecur + lane < nesc && c.epos < hi;
     if (mine) {
-        const uint32_t row = c.epos / kD - uint32_t(r0), col = c.epos % kD;
-        *reinterpret_cast<uint16_t *>(tile + row * kTileStride + col * 2) = uint16_t(c.eval);
+        const uint32_t row = c.epos / D - uint32_t(r0), col = c.epos % D;
+        *reinterpret_cast<uint16_t *>(tile + row * TS + col * 2) = uint16_t(c.eval);
     }
     const int got = __popcll(__ballot(mine));
     c.ecur += got;
     if (got < kWave || c.ecur >= nesc) return;
-    const uint8_t *words = esc_words(c);
+    const uint8_t *words = esc_words<D>(c);
     for (;;) {
         uint32_t pos[2], val[2];
 #pragma unroll
@@ -297,8 +320,8 @@ __device__ __forceinline__ void patch_escapes(Cursor &c, int r0, int n, uint8_t 
         for (int i = 0; i < 2; ++i) {
             const bool m = c.ecur + kWave * i + lane < nesc && pos[i] < hi;
             if (m) {
-                const uint32_t row = pos[i] / kD - uint32_t(r0), col = pos[i] % kD;
-                *reinterpret_cast<uint16_t *>(tile + row * kTileStride + col * 2) = uint16_t(val[i]);
+                const uint32_t row = pos[i] / D - uint32_t(r0), col = pos[i] % D;
+                *reinterpret_cast<uint16_t *>(tile + row * TS + col * 2) = uint16_t(val[i]);
             }
             more += __popcll(__ballot(m));
         }
@@ -346,19 +369,19 @@ constexpr int kGroups = (G + 3) / 4;
 
 // Scores of the lane's tile row (lane = token) for G query rows in the
 // scalar/AVX2 order of attention_scalar.cpp:23-29: chain j (j = 0..7) takes
-// channels j, j + 8, ..., j + 56 in order, lane[j] = fmaf(q, k, lane[j]),
+// channels j, j + 8, ..., j + D - 8 in order, lane[j] = fmaf(q, k, lane[j]),
 // then hsum8's ((l0 + l4) + (l1 + l5)) + ((l2 + l6) + (l3 + l7)). Channel d
 // is one rank-1 product per row group into chain d % 8. qa[rg][d / 16] holds
 // q[4 rg + r][d] at lane 4 (d % 16) + r.
-template <int G>
-__device__ __forceinline__ void scores(const uint8_t *row, const float (&qa)[kGroups<G>][4], float (&s)[G]) {
+template <int G, int D>
+__device__ __forceinline__ void scores(const uint8_t *row, const float (&qa)[kGroups<G>][D / 16], float (&s)[G]) {
     constexpr int NG = kGroups<G>;
     f4 ch[NG][8];
 #pragma unroll
     for (int rg = 0; rg < NG; ++rg)
 #pragma unroll
         for (int j = 0; j < 8; ++j) ch[rg][j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-    static_for<0, 8>([&](auto DG) {
+    static_for<0, D / 8>([&](auto DG) {
         const uint4 kb = *reinterpret_cast<const uint4 *>(row + 16 * DG);
         const float k[8] = {lo_f32(kb.x), hi_f32(kb.x), lo_f32(kb.y), hi_f32(kb.y),
                             lo_f32(kb.z), hi_f32(kb.z), lo_f32(kb.w), hi_f32(kb.w)};
@@ -380,37 +403,45 @@ __device__ __forceinline__ void scores(const uint8_t *row, const float (&qa)[kGr
     }
 }
 
-// Operands of the fold in flight: V of the lane's channel for the next
-// tokens (BF16 in the low half) and e / alpha of four tokens (lane g < G:
-// its row).
+// Operands of the fold in flight: V of the lane's channels (lane + 64 h) for
+// the next tokens (BF16 in the low half) and e / alpha of four tokens (lane
+// g < G: its row).
+template <int H>
 struct FoldIn {
-    uint32_t v[4];
+    uint32_t v[4][H];
     f4 e4[2], a4[2];
 };
 
-// Token T of the ordered fold (attention_scalar.cpp:33-40), lane = channel,
+// Token T of the ordered fold (attention_scalar.cpp:33-40), lane = channel
+// (channels lane + 64 h, h < D / 64),
 // for a whole chunk (tokens past the chunk's end carry e = 0, alpha = 1 and
 // V = -0, which leave acc and l exactly as they are). A token that moves no
 // running maximum (alpha == 1 for every row, exactly) takes
 // acc = fma(e, v, acc); a token that moves one (a uniform branch) scales by
 // alpha first: acc = fma(e, v, acc * alpha). acc[rg] register r is row
-// 4 rg + r; the fma of every row of a group is one rank-1 product whose A
+// 4 rg + r (acc[rg][h]: channel lane + 64 h); the fma of every row of a
+// group is one rank-1 product per h whose A
 // operand is ea[rg][T / 16] (e[4 rg + r][T] at lane 4 (T % 16) + r). Lane
 // g < G carries l of row g through l = fma(l, alpha, e), which is l + e when
 // alpha is 1. Loads run ahead: V three tokens and e / alpha four tokens
 // before their use.
-template <int G, int T>
-__device__ __forceinline__ void fold(const WaveLds<G> &S, lds_f32 *eb, lds_f32 *ab, const uint16_t *vb,
-                                     uint64_t amask, const float (&ea)[kGroups<G>][4], FoldIn &in,
-                                     f4 (&acc)[kGroups<G>], float &lvec) {
-    constexpr int NG = kGroups<G>;
+template <int G, int D, int T>
+__device__ __forceinline__ void fold(const WaveLds<G, D> &S, lds_f32 *eb, lds_f32 *ab, const uint16_t *vb,
+                                     uint64_t amask, const float (&ea)[kGroups<G>][4], FoldIn<D / 64> &in,
+                                     f4 (&acc)[kGroups<G>][D / 64], float &lvec) {
+    constexpr int NG = kGroups<G>, H = D / 64, TS = Shape<D>::kTileStride;
     if constexpr (T < kChunk) {
-        if constexpr (T + 3 < kChunk) in.v[(T + 3) & 3] = vb[(T + 3) * (kTileStride / 2)];
+        if constexpr (T + 3 < kChunk) {
+#pragma unroll
+            for (int h = 0; h < H; ++h) in.v[(T + 3) & 3][h] = vb[(T + 3) * (TS / 2) + 64 * h];
+        }
         if constexpr (T % 4 == 0 && T + 4 < kChunk) {
             in.e4[((T / 4) + 1) & 1] = *reinterpret_cast<lds_f4 *>(eb + T + 4);
             in.a4[((T / 4) + 1) & 1] = *reinterpret_cast<lds_f4 *>(ab + T + 4);
         }
-        const float v = __uint_as_float(in.v[T & 3] << 16);
+        float v[H];
+#pragma unroll
+        for (int h = 0; h < H; ++h) v[h] = __uint_as_float(in.v[T & 3][h] << 16);
         const f4 e4 = in.e4[(T / 4) & 1], a4 = in.a4[(T / 4) & 1];
         const float el = (T % 4 == 0) ? e4.x : (T % 4 == 1) ? e4.y : (T % 4 == 2) ? e4.z : e4.w;
         const float al = (T % 4 == 0) ? a4.x : (T % 4 == 1) ? a4.y : (T % 4 == 2) ? a4.z : a4.w;
@@ -419,35 +450,40 @@ __device__ __forceinline__ void fold(const WaveLds<G> &S, lds_f32 *eb, lds_f32 *
 #pragma unroll
             for (int g = 0; g < G; ++g) av[g] = S.aT[g][T];
 #pragma unroll
-            for (int g = 0; g < G; ++g) acc[g / 4][g % 4] *= av[g];
+            for (int g = 0; g < G; ++g)
+#pragma unroll
+                for (int h = 0; h < H; ++h) acc[g / 4][h][g % 4] *= av[g];
         }
         lvec = fmaf(lvec, al, el);
         // keeps the l chain in token order (otherwise it may be sunk to the
         // end of the unrolled fold with every token's operands held live)
         asm volatile("" : "+v"(lvec));
 #pragma unroll
-        for (int rg = 0; rg < NG; ++rg) acc[rg] = mfma_rank1<T % 16>(ea[rg][T / 16], v, acc[rg]);
-        fold<G, T + 1>(S, eb, ab, vb, amask, ea, in, acc, lvec);
+        for (int rg = 0; rg < NG; ++rg)
+#pragma unroll
+            for (int h = 0; h < H; ++h) acc[rg][h] = mfma_rank1<T % 16>(ea[rg][T / 16], v[h], acc[rg][h]);
+        fold<G, D, T + 1>(S, eb, ab, vb, amask, ea, in, acc, lvec);
     }
 }
 
-// XKV instantiations are held to three waves per SIMD (168 VGPRs; a few
-// loop-invariant lane addresses then live in scratch and are reloaded only
-// on the rare paths that use them); LDS allows three workgroups per CU.
-template <int G, bool XKV>
-__global__ __launch_bounds__(kWavesPerWg * 64) __attribute__((amdgpu_waves_per_eu(XKV ? 3 : 2))) void attn_wave_kernel(
-    const HeadDev *__restrict__ heads, const WorkItem *__restrict__ items, int n_items,
-    const uint16_t *__restrict__ q_all, float *__restrict__ out_all, float *__restrict__ lse_all,
-    float *__restrict__ ws) {
-    __shared__ WgLds<G> L;
+// At D = 64 the XKV instantiations are held to three waves per SIMD (168
+// VGPRs), and LDS allows three workgroups of four waves per CU; at D = 128
+// two waves per SIMD (the rows in flight take twice the registers).
+template <int G, int D, bool XKV>
+__global__ __launch_bounds__(Shape<D>::kWaves * 64) __attribute__((amdgpu_waves_per_eu(D == 64 && XKV ? 3 : 2)))
+void attn_wave_kernel(const HeadDev *__restrict__ heads, const WorkItem *__restrict__ items, int n_items,
+                      const uint16_t *__restrict__ q_all, float *__restrict__ out_all, float *__restrict__ lse_all,
+                      float *__restrict__ ws) {
+    constexpr int TS = Shape<D>::kTileStride, H = D / 64;
+    __shared__ WgLds<G, D> L;
     if (threadIdx.x < 32) L.exptab[threadIdx.x] = kvexp_exp2_32_table[threadIdx.x];
     __syncthreads();
 
     const int lane = lane_id();
     const int w = int(threadIdx.x) >> 6;
-    const int item = __builtin_amdgcn_readfirstlane(int(blockIdx.x) * kWavesPerWg + w);
+    const int item = __builtin_amdgcn_readfirstlane(int(blockIdx.x) * Shape<D>::kWaves + w);
     if (item >= n_items) return;
-    WaveLds<G> &S = L.w[w];
+    WaveLds<G, D> &S = L.w[w];
     const uint64_t *tab = L.exptab;
     const WorkItem wi = load_scalar(items + item);
     const HeadDev hd = load_scalar(heads + wi.head);
@@ -455,50 +491,52 @@ __global__ __launch_bounds__(kWavesPerWg * 64) __attribute__((amdgpu_waves_per_e
     // products: qa[rg][j] at lane 4b + r holds q[4 rg + r][16 j + b] (0 for
     // rows past G).
     constexpr int NG = kGroups<G>;
-    float qa[NG][4];
+    float qa[NG][D / 16];
     {
         const int r = lane & 3, b = lane >> 2;
 #pragma unroll
         for (int rg = 0; rg < NG; ++rg) {
             const int g = min(4 * rg + r, G - 1);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const float qv = __uint_as_float(uint32_t(q_all[(size_t(hd.q_row) + g) * kD + 16 * j + b]) << 16);
+            for (int j = 0; j < D / 16; ++j) {
+                const float qv = __uint_as_float(uint32_t(q_all[(size_t(hd.q_row) + g) * D + 16 * j + b]) << 16);
                 qa[rg][j] = 4 * rg + r < G ? qv : 0.0f;
             }
         }
     }
 
-    f4 acc[NG];
+    f4 acc[NG][H];
 #pragma unroll
-    for (int rg = 0; rg < NG; ++rg) acc[rg] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int rg = 0; rg < NG; ++rg)
+#pragma unroll
+        for (int h = 0; h < H; ++h) acc[rg][h] = f4{0.0f, 0.0f, 0.0f, 0.0f};
     float msc[G]; // running maximum of each query row (wave-uniform)
 #pragma unroll
     for (int g = 0; g < G; ++g) msc[g] = -__builtin_inff();
     float lvec = 0.0f; // lane g < G holds l of query row g
 
     Cursor kc{}, vc{};
-    uint4 RK[XKV ? kRowRegs : 8], RV[XKV ? kRowRegs : 8];
+    uint4 RK[XKV ? Shape<D>::kRowRegs : Shape<D>::kRawRegs], RV[XKV ? Shape<D>::kRowRegs : Shape<D>::kRawRegs];
     int t = wi.tok_begin;
     if constexpr (XKV) {
         enter_block(kc, hd.kdesc + wi.kblk, t);
         enter_block(vc, hd.vdesc + wi.vblk, t);
-        block_vectors(kc);
-        load_rows(kc, 0, min(kChunk, min(kc.t1, wi.tok_end) - t), RK);
-        block_vectors(vc);
-        load_rows(vc, 0, min(kChunk, min(vc.t1, wi.tok_end) - t), RV);
+        block_vectors<D>(kc);
+        load_rows<D>(kc, 0, min(kChunk, min(kc.t1, wi.tok_end) - t), RK);
+        block_vectors<D>(vc);
+        load_rows<D>(vc, 0, min(kChunk, min(vc.t1, wi.tok_end) - t), RV);
     } else {
         // unconditional loads (lanes past the chunk repeat its last row)
         const int row = t + min(lane, min(kChunk, wi.tok_end - t) - 1);
-        const uint8_t *kr = reinterpret_cast<const uint8_t *>(hd.kraw + size_t(row) * kD);
-        const uint8_t *vr = reinterpret_cast<const uint8_t *>(hd.vraw + size_t(row) * kD);
+        const uint8_t *kr = reinterpret_cast<const uint8_t *>(hd.kraw + size_t(row) * D);
+        const uint8_t *vr = reinterpret_cast<const uint8_t *>(hd.vraw + size_t(row) * D);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
+        for (int i = 0; i < D / 8; ++i) {
             RK[i] = ld16(kr + 16 * i);
             RV[i] = ld16(vr + 16 * i);
         }
     }
-    uint8_t *my_row = S.tile + lane * kTileStride; // the lane's token
+    uint8_t *my_row = S.tile + lane * TS; // the lane's token
 
     while (t < wi.tok_end) {
         int n = min(kChunk, wi.tok_end - t);
@@ -509,59 +547,59 @@ __global__ __launch_bounds__(kWavesPerWg * 64) __attribute__((amdgpu_waves_per_e
         // 1. K rows -> tile
         if constexpr (XKV) {
             if (kc.mode() != 0) {
-                base_pairs(kc, S.bp);
+                base_pairs<D>(kc, S.bp);
                 wave_sync();
             }
-            decode_row(kc, RK, S.bp, my_row, t - kc.t0, n);
+            decode_row<D>(kc, RK, S.bp, my_row, t - kc.t0, n);
             wave_sync();
-            patch_escapes(kc, t - kc.t0, n, S.tile);
+            patch_escapes<D>(kc, t - kc.t0, n, S.tile);
         } else {
             uint4 *dst = reinterpret_cast<uint4 *>(my_row);
 #pragma unroll
-            for (int i = 0; i < 8; ++i) dst[i] = RK[i];
+            for (int i = 0; i < D / 8; ++i) dst[i] = RK[i];
         }
         wave_sync();
 
         // 2. scores, lane = token
         float s[G];
-        scores<G>(my_row, qa, s);
+        scores<G, D>(my_row, qa, s);
         wave_sync();
 
         // 3. V rows -> tile; request the next chunk's V and K rows (RK and RV
         // are then not live across the score and decode registers)
         if constexpr (XKV) {
             if (vc.mode() != 0) {
-                base_pairs(vc, S.bp);
+                base_pairs<D>(vc, S.bp);
                 wave_sync();
             }
-            decode_row(vc, RV, S.bp, my_row, t - vc.t0, n);
+            decode_row<D>(vc, RV, S.bp, my_row, t - vc.t0, n);
             wave_sync();
-            patch_escapes(vc, t - vc.t0, n, S.tile);
+            patch_escapes<D>(vc, t - vc.t0, n, S.tile);
             // the loads are issued on every chunk (the last one re-reads its
             // own final row), K first: the K decode can then wait for its
             // loads while the V loads stay in flight
             const int tp = min(tn, wi.tok_end - 1);
             if (tp >= kc.t1) enter_block(kc, kc.d + 1, kc.t1);
-            block_vectors(kc);
-            load_rows(kc, tp - kc.t0, min(kChunk, min(kc.t1, wi.tok_end) - tp), RK);
+            block_vectors<D>(kc);
+            load_rows<D>(kc, tp - kc.t0, min(kChunk, min(kc.t1, wi.tok_end) - tp), RK);
             if (tp >= vc.t1) enter_block(vc, vc.d + 1, vc.t1);
-            block_vectors(vc);
-            load_rows(vc, tp - vc.t0, min(kChunk, min(vc.t1, wi.tok_end) - tp), RV);
+            block_vectors<D>(vc);
+            load_rows<D>(vc, tp - vc.t0, min(kChunk, min(vc.t1, wi.tok_end) - tp), RV);
         } else {
             uint4 *dst = reinterpret_cast<uint4 *>(my_row);
 #pragma unroll
-            for (int i = 0; i < 8; ++i) dst[i] = RV[i];
-            if (n < kChunk && lane >= n) fill_negzero(my_row);
+            for (int i = 0; i < D / 8; ++i) dst[i] = RV[i];
+            if (n < kChunk && lane >= n) fill_negzero<D>(my_row);
             {
                 // issued on every chunk (the last one re-reads its final row), K first
                 const int tp = min(tn, wi.tok_end - 1);
                 const int row = tp + min(lane, min(kChunk, wi.tok_end - tp) - 1);
-                const uint8_t *vr = reinterpret_cast<const uint8_t *>(hd.vraw + size_t(row) * kD);
-                const uint8_t *kr = reinterpret_cast<const uint8_t *>(hd.kraw + size_t(row) * kD);
+                const uint8_t *vr = reinterpret_cast<const uint8_t *>(hd.vraw + size_t(row) * D);
+                const uint8_t *kr = reinterpret_cast<const uint8_t *>(hd.kraw + size_t(row) * D);
 #pragma unroll
-                for (int i = 0; i < 8; ++i) RK[i] = ld16(kr + 16 * i);
+                for (int i = 0; i < D / 8; ++i) RK[i] = ld16(kr + 16 * i);
 #pragma unroll
-                for (int i = 0; i < 8; ++i) RV[i] = ld16(vr + 16 * i);
+                for (int i = 0; i < D / 8; ++i) RV[i] = ld16(vr + 16 * i);
             }
         }
 
@@ -623,13 +661,15 @@ __global__ __launch_bounds__(kWavesPerWg * 64) __attribute__((amdgpu_waves_per_e
             const int gl = min(lane & 7, G - 1); // lanes >= G read a row they do not use
             lds_f32 *eb = (lds_f32 *)&S.eT[gl][0];
             lds_f32 *ab = (lds_f32 *)&S.aT[gl][0];
-            FoldIn in;
+            FoldIn<H> in;
             const uint16_t *vb = reinterpret_cast<const uint16_t *>(S.tile) + lane; // channel lane of token 0
 #pragma unroll
-            for (int k = 0; k < 3; ++k) in.v[k] = vb[k * (kTileStride / 2)];
+            for (int k = 0; k < 3; ++k)
+#pragma unroll
+                for (int h = 0; h < H; ++h) in.v[k][h] = vb[k * (TS / 2) + 64 * h];
             in.e4[0] = *reinterpret_cast<lds_f4 *>(eb);
             in.a4[0] = *reinterpret_cast<lds_f4 *>(ab);
-            fold<G, 0>(S, eb, ab, vb, amask, ea, in, acc, lvec);
+            fold<G, D, 0>(S, eb, ab, vb, amask, ea, in, acc, lvec);
         }
         wave_sync();
         t = tn;
@@ -643,58 +683,69 @@ __global__ __launch_bounds__(kWavesPerWg * 64) __attribute__((amdgpu_waves_per_e
 #pragma unroll
         for (int g = 0; g < G; ++g) {
             const float l = readlane_f32(lvec, g);
-            out_all[(size_t(hd.q_row) + g) * kD + lane] = acc[g / 4][g % 4] * (1.0f / l);
+#pragma unroll
+            for (int h = 0; h < H; ++h)
+                out_all[(size_t(hd.q_row) + g) * D + 64 * h + lane] = acc[g / 4][h][g % 4] * (1.0f / l);
         }
         if (lse_all != nullptr && lane < G) lse_all[hd.q_row + lane] = mv + logf(lvec);
         return;
     }
-    float *slot = ws + size_t(hd.ws_base + wi.split) * kSlotFloats;
+    float *slot = ws + size_t(hd.ws_base + wi.split) * Shape<D>::kSlotFloats;
     if (lane < G) {
         slot[lane] = mv;
         slot[kSlotQ + lane] = lvec;
     }
 #pragma unroll
-    for (int g = 0; g < G; ++g) slot[2 * kSlotQ + g * kD + lane] = acc[g / 4][g % 4];
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int h = 0; h < H; ++h) slot[2 * kSlotQ + g * D + 64 * h + lane] = acc[g / 4][h][g % 4];
 }
 
 // Ordered merge of a head's split states (softmax.hpp:16-30 merge_state,
 // left to right in split order), then out = acc * (1/l) and lse = m + log l.
-// One wave per (device head, query row): lane = channel. A separate launch,
-// so the slots written by the split kernel are visible without fences.
-__global__ __launch_bounds__(kWavesPerWg * 64) void wave_merge_kernel(
+// One wave per (device head, query row): lane = channel (channels lane +
+// 64 h). A separate launch, so the slots written by the split kernel are
+// visible without fences.
+template <int D>
+__global__ __launch_bounds__(4 * 64) void wave_merge_kernel(
     const HeadDev *__restrict__ heads, const int2 *__restrict__ mitems, int n_mitems, float *__restrict__ out_all,
     float *__restrict__ lse_all, const float *__restrict__ ws) {
+    constexpr int H = D / 64, B = Shape<D>::kMergeBatch, SF = Shape<D>::kSlotFloats;
     __shared__ uint64_t tab[32];
     if (threadIdx.x < 32) tab[threadIdx.x] = kvexp_exp2_32_table[threadIdx.x];
     __syncthreads();
     const int lane = lane_id();
-    const int mi = __builtin_amdgcn_readfirstlane(int(blockIdx.x) * kWavesPerWg + (int(threadIdx.x) >> 6));
+    const int mi = __builtin_amdgcn_readfirstlane(int(blockIdx.x) * 4 + (int(threadIdx.x) >> 6));
     if (mi >= n_mitems) return;
     const int2 it = mitems[mi];
     const HeadDev hd = heads[it.x];
     const int g = it.y;
-    const float *slots = ws + size_t(hd.ws_base) * kSlotFloats;
+    const float *slots = ws + size_t(hd.ws_base) * SF;
     const int n = hd.n_splits;
-    float a = slots[2 * kSlotQ + g * kD + lane];
+    float a[H];
+#pragma unroll
+    for (int c = 0; c < H; ++c) a[c] = slots[2 * kSlotQ + g * D + 64 * c + lane];
     float mf = slots[g];
     float lf = slots[kSlotQ + g];
-    for (int s0 = 1; s0 < n; s0 += kMergeBatch) {
-        const int cnt = min(kMergeBatch, n - s0);
+    for (int s0 = 1; s0 < n; s0 += B) {
+        const int cnt = min(B, n - s0);
         // every load of the batch is issued before any use (indices clamped)
-        float ab[kMergeBatch];
+        float ab[B][H];
 #pragma unroll
-        for (int j = 0; j < kMergeBatch; ++j)
-            ab[j] = slots[size_t(s0 + min(j, cnt - 1)) * kSlotFloats + 2 * kSlotQ + g * kD + lane];
-        float ms[kMergeBatch / 64], lb[kMergeBatch / 64];
+        for (int j = 0; j < B; ++j)
 #pragma unroll
-        for (int h = 0; h < kMergeBatch / 64; ++h) {
+            for (int c = 0; c < H; ++c)
+                ab[j][c] = slots[size_t(s0 + min(j, cnt - 1)) * SF + 2 * kSlotQ + g * D + 64 * c + lane];
+        float ms[(B + 63) / 64], lb[(B + 63) / 64];
+#pragma unroll
+        for (int h = 0; h < (B + 63) / 64; ++h) {
             const int j = 64 * h + lane;
-            const float *ls = slots + size_t(s0 + min(j, cnt - 1)) * kSlotFloats;
+            const float *ls = slots + size_t(s0 + min(j, cnt - 1)) * SF;
             ms[h] = j < cnt ? ls[g] : -__builtin_inff();
             lb[h] = ls[kSlotQ + g];
         }
 #pragma unroll
-        for (int h = 0; h < kMergeBatch / 64; ++h) {
+        for (int h = 0; h < (B + 63) / 64; ++h) {
             if (64 * h >= cnt) break;
             // lane = split s0 + 64h + lane: running maximum and the two exponentials
             const float mm = fmaxf(wave_scan_max(ms[h]), mf);
@@ -706,13 +757,15 @@ __global__ __launch_bounds__(kWavesPerWg * 64) void wave_merge_kernel(
             for (int jj = 0; jj < 64; ++jj) {
                 if (64 * h + jj < cnt) {
                     const float x1 = readlane_f32(e1, jj), x2 = readlane_f32(e2, jj);
-                    a = fmaf(a, x1, ab[64 * h + jj] * x2);
+#pragma unroll
+                    for (int c = 0; c < H; ++c) a[c] = fmaf(a[c], x1, ab[64 * h + jj][c] * x2);
                     lf = fmaf(lf, x1, readlane_f32(lb[h], jj) * x2);
                 }
             }
         }
     }
-    out_all[(size_t(hd.q_row) + g) * kD + lane] = a * (1.0f / lf);
+#pragma unroll
+    for (int c = 0; c < H; ++c) out_all[(size_t(hd.q_row) + g) * D + 64 * c + lane] = a[c] * (1.0f / lf);
     if (lse_all != nullptr && lane == 0) lse_all[hd.q_row + g] = mf + logf(lf);
 }
 
@@ -722,45 +775,60 @@ __global__ __launch_bounds__(kWavesPerWg * 64) void wave_merge_kernel(
 namespace kvexp_launch {
 using namespace kvexp_dev;
 
-template <int G, bool XKV>
+template <int G, int D, bool XKV>
 static hipError_t launch_wave_g(const HeadDev *heads, const WorkItem *items, int n_items, const uint16_t *q,
                                 float *out, float *lse, float *ws, hipStream_t s) {
-    const int grid = (n_items + wave::kWavesPerWg - 1) / wave::kWavesPerWg;
-    hipLaunchKernelGGL((wave::attn_wave_kernel<G, XKV>), dim3(grid), dim3(wave::kWavesPerWg * 64), 0, s, heads,
-                       items, n_items, q, out, lse, ws);
-    return hipGetLastError();
-}
-
-template <bool XKV>
-static hipError_t launch_wave_x(int G, const HeadDev *heads, const WorkItem *items, int n_items, const uint16_t *q,
-                                float *out, float *lse, float *ws, hipStream_t s) {
-    switch (G) {
-    case 1: return launch_wave_g<1, XKV>(heads, items, n_items, q, out, lse, ws, s);
-    case 2: return launch_wave_g<2, XKV>(heads, items, n_items, q, out, lse, ws, s);
-    case 3: return launch_wave_g<3, XKV>(heads, items, n_items, q, out, lse, ws, s);
-    case 4: return launch_wave_g<4, XKV>(heads, items, n_items, q, out, lse, ws, s);
-    case 5: return launch_wave_g<5, XKV>(heads, items, n_items, q, out, lse, ws, s);
-    case 6: return launch_wave_g<6, XKV>(heads, items, n_items, q, out, lse, ws, s);
-    case 7: return launch_wave_g<7, XKV>(heads, items, n_items, q, out, lse, ws, s);
-    case 8: return launch_wave_g<8, XKV>(heads, items, n_items, q, out, lse, ws, s);
-    default: return hipErrorInvalidValue;
-    }
-}
-
-hipError_t wave_merge(const HeadDev *heads, const int2 *mitems, int n_mitems, float *out, float *lse, const float *ws,
-                      hipStream_t s) {
-    if (n_mitems <= 0) return hipSuccess;
-    const int grid = (n_mitems + wave::kWavesPerWg - 1) / wave::kWavesPerWg;
-    hipLaunchKernelGGL(wave::wave_merge_kernel, dim3(grid), dim3(wave::kWavesPerWg * 64), 0, s, heads, mitems, n_mitems,
+    constexpr int W = wave::Shape<D>::kWaves;
+    const int grid = (n_items + W - 1) / W;
+    hipLaunchKernelGGL((wave::attn_wave_kernel<G, D, XKV>), dim3(grid), dim3(W * 64), 0, s, heads, items, n_items, q,
                        out, lse, ws);
     return hipGetLastError();
 }
 
-hipError_t attention_wave(bool xkv, int G, const HeadDev *heads, const WorkItem *items, int n_items,
+template <int D, bool XKV>
+static hipError_t launch_wave_x(int G, const HeadDev *heads, const WorkItem *items, int n_items, const uint16_t *q,
+                                float *out, float *lse, float *ws, hipStream_t s) {
+    switch (G) {
+    case 1: return launch_wave_g<1, D, XKV>(heads, items, n_items, q, out, lse, ws, s);
+    case 2: return launch_wave_g<2, D, XKV>(heads, items, n_items, q, out, lse, ws, s);
+    case 3: return launch_wave_g<3, D, XKV>(heads, items, n_items, q, out, lse, ws, s);
+    case 4: return launch_wave_g<4, D, XKV>(heads, items, n_items, q, out, lse, ws, s);
+    case 5: return launch_wave_g<5, D, XKV>(heads, items, n_items, q, out, lse, ws, s);
+    case 6: return launch_wave_g<6, D, XKV>(heads, items, n_items, q, out, lse, ws, s);
+    case 7: return launch_wave_g<7, D, XKV>(heads, items, n_items, q, out, lse, ws, s);
+    case 8: return launch_wave_g<8, D, XKV>(heads, items, n_items, q, out, lse, ws, s);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+// head_dim 64 and 128 (the host sends other sizes to the general kernel).
+bool wave_supports(int dim) { return dim == 64 || dim == 128; }
+
+hipError_t wave_merge(int dim, const HeadDev *heads, const int2 *mitems, int n_mitems, float *out, float *lse,
+                      const float *ws, hipStream_t s) {
+    if (n_mitems <= 0) return hipSuccess;
+    const int grid = (n_mitems + 3) / 4;
+    if (dim == 64)
+        hipLaunchKernelGGL(wave::wave_merge_kernel<64>, dim3(grid), dim3(4 * 64), 0, s, heads, mitems, n_mitems, out,
+                           lse, ws);
+    else if (dim == 128)
+        hipLaunchKernelGGL(wave::wave_merge_kernel<128>, dim3(grid), dim3(4 * 64), 0, s, heads, mitems, n_mitems, out,
+                           lse, ws);
+    else
+        return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+hipError_t attention_wave(bool xkv, int G, int dim, const HeadDev *heads, const WorkItem *items, int n_items,
                           const uint16_t *q, float *out, float *lse, float *ws, hipStream_t s) {
     if (n_items <= 0) return hipSuccess;
-    return xkv ? launch_wave_x<true>(G, heads, items, n_items, q, out, lse, ws, s)
-               : launch_wave_x<false>(G, heads, items, n_items, q, out, lse, ws, s);
+    if (dim == 64)
+        return xkv ? launch_wave_x<64, true>(G, heads, items, n_items, q, out, lse, ws, s)
+                   : launch_wave_x<64, false>(G, heads, items, n_items, q, out, lse, ws, s);
+    if (dim == 128)
+        return xkv ? launch_wave_x<128, true>(G, heads, items, n_items, q, out, lse, ws, s)
+                   : launch_wave_x<128, false>(G, heads, items, n_items, q, out, lse, ws, s);
+    return hipErrorInvalidValue;
 }
 
 } // namespace kvexp_launch

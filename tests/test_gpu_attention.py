@@ -163,14 +163,14 @@ def _max_block_escapes(oracle, blob, dim, seq):
     return int(esc[coded].max()) if coded.any() else 0
 
 
-def test_wave_kernel_groups_and_escapes(ctx, oracle):
-    """The head_dim-64 one-wave kernel for every query-row count G it is
-    instantiated for, on containers whose blocks carry from 0 to several
-    hundred escapes (blocks with more than 64 read the escape index in
-    windows), block sizes that do and do not split into 64-token chunks,
+@pytest.mark.parametrize("dim", [64, 128])
+def test_wave_kernel_groups_and_escapes(ctx, oracle, dim):
+    """The one-wave kernel (head_dim 64 and 128) for every query-row count G
+    it is instantiated for, on containers whose blocks carry from 0 to
+    several hundred escapes (blocks with more than 64 read the escape index
+    in windows), block sizes that do and do not split into 64-token chunks,
     ragged lengths and several splits per head."""
-    rng = np.random.default_rng(4242)
-    dim = 64
+    rng = np.random.default_rng(4242 + dim)
     seen_big = False
     cases = [(1, 128, 0.05, False), (2, 255, 0.02, False), (3, 100, 0.0, False), (7, 128, 0.3, False),
              (8, 64, 0.01, False), (5, 128, 0.002, True), (7, 255, 0.1, True), (11, 128, 0.05, False),
