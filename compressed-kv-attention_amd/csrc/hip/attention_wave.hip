@@ -108,6 +108,7 @@ __device__ __forceinline__ T load_scalar(const T *p) {
 // Constant address space (4): uniform loads from it are scalar loads.
 typedef float f8 __attribute__((ext_vector_type(8)));
 typedef unsigned int u32x8 __attribute__((ext_vector_type(8)));
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 typedef const __attribute__((address_space(4))) f8 c_f8;
 // An LDS float (address space 3), for pointers that pass through inline asm
 // and must still be read with ds_read.
@@ -284,18 +285,43 @@ __device__ __forceinline__ void decode_row(const Cursor &c, const uint4 (&R)[Sha
     if (rows < kChunk && lane >= rows) fill_negzero<D>(row);
 }
 
+// ---- AVX-512 BF16 order ------------------------------------------------------
+// VDPBF16PS (attention_avx512.cpp:21-30) reads denormal inputs as zero and
+// flushes denormal results. The matrix-core products keep denormals, so the
+// fast score path runs only on chunks where no flush can happen: every
+// product k * q of nonzero BF16 values (8-bit significands) is an integer
+// multiple of 2^(e_k + e_q - 14) (unbiased exponents), every partial sum of
+// such products rounded to FP32 stays a multiple of the smallest of these
+// powers, and a nonzero multiple of 2^-126 is a normal number. So with
+// biased exponents E_k + E_q >= 142 for every nonzero K element and query
+// element of the head (denormal queries read as zero beforehand), no input,
+// chain value or sum is denormal, and the flushes are the identity. A chunk
+// with a smaller K exponent (or a raw block, which is not checked element by
+// element) takes the vector path that applies the flushes.
+
+// Whether BF16 x is nonzero with exponent field below T, for
+// low = (T << 7) - 1 (T >= 1): (x & 0x7FFF) - 1 wraps to 2^32 - 1 for a zero.
+__device__ __forceinline__ bool low_bf16(uint32_t x, uint32_t low) { return (x & 0x7FFFu) - 1u < low; }
+
+// Denormal to signed zero (VDPBF16PS's DAZ on inputs and FTZ on results).
+__device__ __forceinline__ float flush_tiny(float x) {
+    return fabsf(x) < 1.17549435e-38f ? copysignf(0.0f, x) : x;
+}
+
 // Writes the escape words of rows [r0, r0 + n) of the cursor's block over
 // their elements in the tile and advances the cursor's escape index past
 // them. Positions ascend within a block and every escape before ecur lies in
 // an earlier chunk, so the chunk's escapes are the next ones from ecur whose
 // positions are below (r0 + n) * D: the 64 loaded with the chunk's rows
 // (block_vectors), and, only for a chunk with more than 64, further windows
-// loaded here, two at a time.
-template <int D>
-__device__ __forceinline__ void patch_escapes(Cursor &c, int r0, int n, uint8_t *tile) {
+// loaded here, two at a time. With CHK, returns whether any of the words
+// written is a nonzero value whose exponent field lies below the threshold
+// that `low` encodes (see low_bf16).
+template <int D, bool CHK = false>
+__device__ __forceinline__ bool patch_escapes(Cursor &c, int r0, int n, uint8_t *tile, uint32_t low = 0) {
     constexpr int TS = Shape<D>::kTileStride;
     const int nesc = c.nesc();
-    if (c.ecur >= nesc) return;
+    if (c.ecur >= nesc) return false;
     const int lane = lane_id();
     const uint32_t hi = uint32_t((r0 + n) * D);
     const bool mine = c.ecur + lane < nesc && c.epos < hi;
@@ -303,9 +329,10 @@ __device__ __forceinline__ void patch_escapes(Cursor &c, int r0, int n, uint8_t 
         const uint32_t row = c.epos / D - uint32_t(r0), col = c.epos % D;
         *reinterpret_cast<uint16_t *>(tile + row * TS + col * 2) = uint16_t(c.eval);
     }
+    bool bad = CHK && __ballot(mine && low_bf16(c.eval, low)) != 0;
     const int got = __popcll(__ballot(mine));
     c.ecur += got;
-    if (got < kWave || c.ecur >= nesc) return;
+    if (got < kWave || c.ecur >= nesc) return bad;
     const uint8_t *words = esc_words<D>(c);
     for (;;) {
         uint32_t pos[2], val[2];
@@ -323,11 +350,13 @@ __device__ __forceinline__ void patch_escapes(Cursor &c, int r0, int n, uint8_t 
                 const uint32_t row = pos[i] / D - uint32_t(r0), col = pos[i] % D;
                 *reinterpret_cast<uint16_t *>(tile + row * TS + col * 2) = uint16_t(val[i]);
             }
+            if (CHK) bad |= __ballot(m && low_bf16(val[i], low)) != 0;
             more += __popcll(__ballot(m));
         }
         c.ecur += more;
         if (more < 2 * kWave || c.ecur >= nesc) break;
     }
+    return bad;
 }
 
 // Phase boundary inside one wave. The LDS performs one wave's operations in
@@ -403,6 +432,117 @@ __device__ __forceinline__ void scores(const uint8_t *row, const float (&qa)[kGr
     }
 }
 
+// Scores in the AVX-512 BF16 order (attention_avx512.cpp:21-30,116-124) for a
+// chunk where no flush can happen (see low_bf16): 16 chains; per 32-channel
+// step c, chain j takes k[c + 2j + 1] * q[c + 2j + 1] and then
+// k[c + 2j] * q[c + 2j] (VDPBF16PS's order, one rounding each); then the
+// pairwise tree over the 16 chains, ((a0 + a1) + (a2 + a3)) with
+// a_i = (t_4i + t_4i+1) + (t_4i+2 + t_4i+3). The chains run in quads
+// (chains 4Q .. 4Q + 3 read octets Q, Q + 4, ...), R quads at a time: two
+// for one row group (eight independent products between dependent ones),
+// one for two row groups (the same, and fewer registers live); each run is
+// reduced to its a_i before the next starts.
+template <int G, int D>
+__device__ __forceinline__ void scores_dp(const uint8_t *row, const float (&qa)[kGroups<G>][D / 16], float (&s)[G]) {
+    constexpr int NG = kGroups<G>, R = NG == 1 ? 2 : 1;
+    f4 a01[NG], a2[NG];
+    static_for<0, 4 / R>([&](auto RUN) {
+        constexpr int Q0 = R * decltype(RUN)::value;
+        f4 ch[NG][4 * R];
+#pragma unroll
+        for (int rg = 0; rg < NG; ++rg)
+#pragma unroll
+            for (int j = 0; j < 4 * R; ++j) ch[rg][j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+        static_for<0, D / 32>([&](auto S) {
+            constexpr int DG0 = 4 * decltype(S)::value + Q0; // octets DG0 .. DG0 + R - 1
+            uint32_t w[4 * R];
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const uint4 kb = *reinterpret_cast<const uint4 *>(row + 16 * (DG0 + r));
+                w[4 * r + 0] = kb.x;
+                w[4 * r + 1] = kb.y;
+                w[4 * r + 2] = kb.z;
+                w[4 * r + 3] = kb.w;
+            }
+            static_for<0, 4 * R>([&](auto J) { // odd channel of pair J first
+                constexpr int d = 8 * DG0 + 2 * decltype(J)::value + 1;
+#pragma unroll
+                for (int rg = 0; rg < NG; ++rg)
+                    ch[rg][J] = mfma_rank1<d % 16>(qa[rg][d / 16], hi_f32(w[J]), ch[rg][J]);
+            });
+            static_for<0, 4 * R>([&](auto J) {
+                constexpr int d = 8 * DG0 + 2 * decltype(J)::value;
+#pragma unroll
+                for (int rg = 0; rg < NG; ++rg)
+                    ch[rg][J] = mfma_rank1<d % 16>(qa[rg][d / 16], lo_f32(w[J]), ch[rg][J]);
+            });
+        });
+#pragma unroll
+        for (int rg = 0; rg < NG; ++rg) {
+            f4 a = (ch[rg][0] + ch[rg][1]) + (ch[rg][2] + ch[rg][3]); // a_Q0
+            if constexpr (R == 2) a = a + ((ch[rg][4] + ch[rg][5]) + (ch[rg][6] + ch[rg][7])); // a_Q0 + a_Q0+1
+            f4 t;
+            if constexpr (R == 2 && Q0 == 0) {
+                a01[rg] = a;
+                continue;
+            } else if constexpr (R == 2) {
+                t = a01[rg] + a;
+            } else if constexpr (Q0 == 0) {
+                a01[rg] = a;
+                continue;
+            } else if constexpr (Q0 == 1) {
+                a01[rg] = a01[rg] + a;
+                continue;
+            } else if constexpr (Q0 == 2) {
+                a2[rg] = a;
+                continue;
+            } else {
+                t = a01[rg] + (a2[rg] + a);
+            }
+            if (4 * rg + 0 < G) s[(4 * rg + 0) % G] = t.x;
+            if (4 * rg + 1 < G) s[(4 * rg + 1) % G] = t.y;
+            if (4 * rg + 2 < G) s[(4 * rg + 2) % G] = t.z;
+            if (4 * rg + 3 < G) s[(4 * rg + 3) % G] = t.w;
+        }
+    });
+}
+
+// The same order on the vector ALU with every flush applied, for chunks the
+// fast path cannot take: q from the head's BF16 rows in global memory, one
+// query row and one quad of chains at a time (few registers live; the chains
+// are independent, and each keeps its order), the score staged in `st`
+// (row g at st + g * kRowPad).
+template <int G, int D>
+__device__ __forceinline__ void scores_dp_flush(const uint8_t *row, const uint16_t *q, float *st) {
+    const int lane = lane_id();
+#pragma unroll 1
+    for (int g = 0; g < G; ++g) {
+        float a01 = 0.0f, a2 = 0.0f, res = 0.0f;
+#pragma unroll 1
+        for (int Q = 0; Q < 4; ++Q) {
+            float t[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int c = 0; c < D; c += 32) {
+                // pairs 4Q .. 4Q + 3 of the step: elements c + 8Q .. c + 8Q + 7
+                const uint4 kb = *reinterpret_cast<const uint4 *>(row + 2 * (c + 8 * Q));
+                const uint4 qb = *reinterpret_cast<const uint4 *>(q + size_t(g) * D + c + 8 * Q);
+                const uint32_t kw[4] = {kb.x, kb.y, kb.z, kb.w}, qw[4] = {qb.x, qb.y, qb.z, qb.w};
+#pragma unroll
+                for (int p = 0; p < 4; ++p) {
+                    t[p] = flush_tiny(fmaf(flush_tiny(hi_f32(kw[p])), flush_tiny(hi_f32(qw[p])), t[p]));
+                    t[p] = flush_tiny(fmaf(flush_tiny(lo_f32(kw[p])), flush_tiny(lo_f32(qw[p])), t[p]));
+                }
+            }
+            const float a = (t[0] + t[1]) + (t[2] + t[3]);
+            if (Q == 0) a01 = a;
+            else if (Q == 1) a01 = a01 + a;
+            else if (Q == 2) a2 = a;
+            else res = a01 + (a2 + a);
+        }
+        st[g * kRowPad + lane] = res;
+    }
+}
+
 // Operands of the fold in flight: V of the lane's channels (lane + 64 h) for
 // the next tokens (BF16 in the low half) and e / alpha of four tokens (lane
 // g < G: its row).
@@ -468,9 +608,15 @@ __device__ __forceinline__ void fold(const WaveLds<G, D> &S, lds_f32 *eb, lds_f3
 
 // At D = 64 the XKV instantiations are held to three waves per SIMD (168
 // VGPRs), and LDS allows three workgroups of four waves per CU; at D = 128
-// two waves per SIMD (the rows in flight take twice the registers).
-template <int G, int D, bool XKV>
-__global__ __launch_bounds__(Shape<D>::kWaves * 64) __attribute__((amdgpu_waves_per_eu(D == 64 && XKV ? 3 : 2)))
+// two waves per SIMD (the rows in flight take twice the registers), and
+// also for the AVX-512 order at D = 64 with six or more query rows (its
+// flush checks do not fit in 168 VGPRs there without spilling in the loop).
+// ORDER 0: scalar/AVX2 score order; ORDER 1: AVX-512 BF16 order.
+template <int G, int D, bool XKV, int ORDER>
+constexpr int kWaveOcc = D == 64 && XKV && !(ORDER == 1 && G >= 6) ? 3 : 2;
+
+template <int G, int D, bool XKV, int ORDER>
+__global__ __launch_bounds__(Shape<D>::kWaves * 64) __attribute__((amdgpu_waves_per_eu(kWaveOcc<G, D, XKV, ORDER>)))
 void attn_wave_kernel(const HeadDev *__restrict__ heads, const WorkItem *__restrict__ items, int n_items,
                       const uint16_t *__restrict__ q_all, float *__restrict__ out_all, float *__restrict__ lse_all,
                       float *__restrict__ ws) {
@@ -499,10 +645,29 @@ void attn_wave_kernel(const HeadDev *__restrict__ heads, const WorkItem *__restr
             const int g = min(4 * rg + r, G - 1);
 #pragma unroll
             for (int j = 0; j < D / 16; ++j) {
-                const float qv = __uint_as_float(uint32_t(q_all[(size_t(hd.q_row) + g) * D + 16 * j + b]) << 16);
+                float qv = __uint_as_float(uint32_t(q_all[(size_t(hd.q_row) + g) * D + 16 * j + b]) << 16);
+                if constexpr (ORDER == 1) qv = flush_tiny(qv);
                 qa[rg][j] = 4 * rg + r < G ? qv : 0.0f;
             }
         }
+    }
+    // ORDER 1: the K exponent bound of the fast score path, as low_bf16's
+    // argument (T = 142 - the smallest exponent field of a nonzero query
+    // element, at least 1), and T itself.
+    uint32_t klow = 0, kmin = 0;
+    if constexpr (ORDER == 1) {
+        int qe = 255;
+#pragma unroll
+        for (int rg = 0; rg < NG; ++rg)
+#pragma unroll
+            for (int j = 0; j < D / 16; ++j) {
+                const uint32_t b = __float_as_uint(qa[rg][j]);
+                if ((b & 0x7FFFFFFFu) != 0) qe = min(qe, int((b >> 23) & 0xFFu));
+            }
+#pragma unroll
+        for (int m = 1; m < kWave; m *= 2) qe = min(qe, __shfl_xor(qe, m));
+        kmin = uint32_t(max(1, 142 - __builtin_amdgcn_readfirstlane(qe)));
+        klow = (kmin << 7) - 1u;
     }
 
     f4 acc[NG][H];
@@ -544,25 +709,57 @@ void attn_wave_kernel(const HeadDev *__restrict__ heads, const WorkItem *__restr
         if (n <= 0) break; // unreachable with plan-checked descriptors (n_tokens > 0)
         const int tn = t + n;
 
-        // 1. K rows -> tile
+        // 1. K rows -> tile (ORDER 1: and whether the chunk needs the flushing
+        // score path)
+        bool flush = false;
         if constexpr (XKV) {
             if (kc.mode() != 0) {
+                if constexpr (ORDER == 1) {
+                    // coded exponents are base + code with code <= 15 (4-bit) or 3
+                    // (2-bit): all >= kmin when no base is below it or wraps
+                    const uint32_t b0 = kc.base2 & 0xFFu, b1 = (kc.base2 >> 8) & 0xFFu;
+                    const uint32_t top = kc.mode() == 4 ? 240u : 252u;
+                    flush = __ballot(lane < D / 2 && (min(b0, b1) < kmin || max(b0, b1) > top)) != 0;
+                }
                 base_pairs<D>(kc, S.bp);
                 wave_sync();
+            } else {
+                flush = ORDER == 1;
             }
             decode_row<D>(kc, RK, S.bp, my_row, t - kc.t0, n);
             wave_sync();
-            patch_escapes<D>(kc, t - kc.t0, n, S.tile);
+            flush |= patch_escapes<D, ORDER == 1>(kc, t - kc.t0, n, S.tile, klow);
         } else {
             uint4 *dst = reinterpret_cast<uint4 *>(my_row);
 #pragma unroll
             for (int i = 0; i < D / 8; ++i) dst[i] = RK[i];
+            if constexpr (ORDER == 1) {
+                u16x2 lo = {0xFFFFu, 0xFFFFu};
+#pragma unroll
+                for (int i = 0; i < D / 8; ++i) {
+                    const uint32_t c4[4] = {RK[i].x, RK[i].y, RK[i].z, RK[i].w};
+#pragma unroll
+                    for (int k = 0; k < 4; ++k)
+                        lo = __builtin_elementwise_min(lo, (__builtin_bit_cast(u16x2, c4[k]) & uint16_t(0x7FFF)) -
+                                                               uint16_t(1));
+                }
+                flush = __ballot(lane < n && uint32_t(min(lo.x, lo.y)) < klow) != 0;
+            }
         }
         wave_sync();
 
         // 2. scores, lane = token
         float s[G];
-        scores<G, D>(my_row, qa, s);
+        if constexpr (ORDER == 0) {
+            scores<G, D>(my_row, qa, s);
+        } else if (!flush) {
+            scores_dp<G, D>(my_row, qa, s);
+        } else {
+            scores_dp_flush<G, D>(my_row, q_all + size_t(hd.q_row) * D, &S.eT[0][0]);
+            wave_sync();
+#pragma unroll
+            for (int g = 0; g < G; ++g) s[g] = S.eT[g][lane];
+        }
         wave_sync();
 
         // 3. V rows -> tile; request the next chunk's V and K rows (RK and RV
@@ -775,33 +972,46 @@ __global__ __launch_bounds__(4 * 64) void wave_merge_kernel(
 namespace kvexp_launch {
 using namespace kvexp_dev;
 
-template <int G, int D, bool XKV>
+template <int G, int D, bool XKV, int ORDER>
 static hipError_t launch_wave_g(const HeadDev *heads, const WorkItem *items, int n_items, const uint16_t *q,
                                 float *out, float *lse, float *ws, hipStream_t s) {
     constexpr int W = wave::Shape<D>::kWaves;
     const int grid = (n_items + W - 1) / W;
-    hipLaunchKernelGGL((wave::attn_wave_kernel<G, D, XKV>), dim3(grid), dim3(W * 64), 0, s, heads, items, n_items, q,
-                       out, lse, ws);
+    hipLaunchKernelGGL((wave::attn_wave_kernel<G, D, XKV, ORDER>), dim3(grid), dim3(W * 64), 0, s, heads, items,
+                       n_items, q, out, lse, ws);
     return hipGetLastError();
 }
 
-template <int D, bool XKV>
+template <int D, bool XKV, int ORDER>
 static hipError_t launch_wave_x(int G, const HeadDev *heads, const WorkItem *items, int n_items, const uint16_t *q,
                                 float *out, float *lse, float *ws, hipStream_t s) {
     switch (G) {
-    case 1: return launch_wave_g<1, D, XKV>(heads, items, n_items, q, out, lse, ws, s);
-    case 2: return launch_wave_g<2, D, XKV>(heads, items, n_items, q, out, lse, ws, s);
-    case 3: return launch_wave_g<3, D, XKV>(heads, items, n_items, q, out, lse, ws, s);
-    case 4: return launch_wave_g<4, D, XKV>(heads, items, n_items, q, out, lse, ws, s);
-    case 5: return launch_wave_g<5, D, XKV>(heads, items, n_items, q, out, lse, ws, s);
-    case 6: return launch_wave_g<6, D, XKV>(heads, items, n_items, q, out, lse, ws, s);
-    case 7: return launch_wave_g<7, D, XKV>(heads, items, n_items, q, out, lse, ws, s);
-    case 8: return launch_wave_g<8, D, XKV>(heads, items, n_items, q, out, lse, ws, s);
+    case 1: return launch_wave_g<1, D, XKV, ORDER>(heads, items, n_items, q, out, lse, ws, s);
+    case 2: return launch_wave_g<2, D, XKV, ORDER>(heads, items, n_items, q, out, lse, ws, s);
+    case 3: return launch_wave_g<3, D, XKV, ORDER>(heads, items, n_items, q, out, lse, ws, s);
+    case 4: return launch_wave_g<4, D, XKV, ORDER>(heads, items, n_items, q, out, lse, ws, s);
+    case 5: return launch_wave_g<5, D, XKV, ORDER>(heads, items, n_items, q, out, lse, ws, s);
+    case 6: return launch_wave_g<6, D, XKV, ORDER>(heads, items, n_items, q, out, lse, ws, s);
+    case 7: return launch_wave_g<7, D, XKV, ORDER>(heads, items, n_items, q, out, lse, ws, s);
+    case 8: return launch_wave_g<8, D, XKV, ORDER>(heads, items, n_items, q, out, lse, ws, s);
     default: return hipErrorInvalidValue;
     }
 }
 
-// head_dim 64 and 128 (the host sends other sizes to the general kernel).
+template <int D>
+static hipError_t launch_wave_d(bool xkv, int order, int G, const HeadDev *heads, const WorkItem *items, int n_items,
+                                const uint16_t *q, float *out, float *lse, float *ws, hipStream_t s) {
+    if (order == 0)
+        return xkv ? launch_wave_x<D, true, 0>(G, heads, items, n_items, q, out, lse, ws, s)
+                   : launch_wave_x<D, false, 0>(G, heads, items, n_items, q, out, lse, ws, s);
+    if (order == 1)
+        return xkv ? launch_wave_x<D, true, 1>(G, heads, items, n_items, q, out, lse, ws, s)
+                   : launch_wave_x<D, false, 1>(G, heads, items, n_items, q, out, lse, ws, s);
+    return hipErrorInvalidValue;
+}
+
+// head_dim 64 and 128, both score orders (the host sends other sizes to the
+// general kernel).
 bool wave_supports(int dim) { return dim == 64 || dim == 128; }
 
 hipError_t wave_merge(int dim, const HeadDev *heads, const int2 *mitems, int n_mitems, float *out, float *lse,
@@ -819,15 +1029,11 @@ hipError_t wave_merge(int dim, const HeadDev *heads, const int2 *mitems, int n_m
     return hipGetLastError();
 }
 
-hipError_t attention_wave(bool xkv, int G, int dim, const HeadDev *heads, const WorkItem *items, int n_items,
-                          const uint16_t *q, float *out, float *lse, float *ws, hipStream_t s) {
+hipError_t attention_wave(bool xkv, int order, int G, int dim, const HeadDev *heads, const WorkItem *items,
+                          int n_items, const uint16_t *q, float *out, float *lse, float *ws, hipStream_t s) {
     if (n_items <= 0) return hipSuccess;
-    if (dim == 64)
-        return xkv ? launch_wave_x<64, true>(G, heads, items, n_items, q, out, lse, ws, s)
-                   : launch_wave_x<64, false>(G, heads, items, n_items, q, out, lse, ws, s);
-    if (dim == 128)
-        return xkv ? launch_wave_x<128, true>(G, heads, items, n_items, q, out, lse, ws, s)
-                   : launch_wave_x<128, false>(G, heads, items, n_items, q, out, lse, ws, s);
+    if (dim == 64) return launch_wave_d<64>(xkv, order, G, heads, items, n_items, q, out, lse, ws, s);
+    if (dim == 128) return launch_wave_d<128>(xkv, order, G, heads, items, n_items, q, out, lse, ws, s);
     return hipErrorInvalidValue;
 }
 

@@ -35,8 +35,8 @@ hipError_t expf(const float *x, float *y, size_t n, hipStream_t s);
 hipError_t esc_start(const kvexp_dev::EscJob *jobs, int n_jobs, uint32_t *status, hipStream_t s);
 hipError_t esc_pos(const kvexp_dev::EscJob *jobs, const int2 *blocks, int n_blocks, uint32_t *status, hipStream_t s);
 bool wave_supports(int dim);
-hipError_t attention_wave(bool xkv, int G, int dim, const HeadDev *heads, const WorkItem *items, int n_items,
-                          const uint16_t *q, float *out, float *lse, float *ws, hipStream_t s);
+hipError_t attention_wave(bool xkv, int order, int G, int dim, const HeadDev *heads, const WorkItem *items,
+                          int n_items, const uint16_t *q, float *out, float *lse, float *ws, hipStream_t s);
 hipError_t wave_merge(int dim, const HeadDev *heads, const int2 *mitems, int n_mitems, float *out, float *lse,
                       const float *ws, hipStream_t s);
 } // namespace kvexp_launch
@@ -195,7 +195,7 @@ struct kvexp_hip_plan {
     kvexp_hip_ctx *ctx = nullptr;
     int n_heads = 0, n_q = 0, dim = 0, order = 0;
     bool xkv = false;
-    bool wave = false; // one-wave-per-split kernel (dim 64 or 128, scalar order)
+    bool wave = false; // one-wave-per-split kernel (dim 64 or 128)
     DevBuf heads, items, merge_ids, ws, status;
     // wave kernel: merge work (head, row), escape-position index, block descriptors
     DevBuf mitems, esc0, escpos, desc;
@@ -584,7 +584,7 @@ int kvexp_hip_plan_create(kvexp_hip_ctx *ctx, const kvexp_hip_head *heads, int n
             p->dim = dim;
             p->order = order;
             p->xkv = xkv;
-            p->wave = kvexp_launch::wave_supports(dim) && order == KVEXP_HIP_ORDER_SCALAR;
+            p->wave = kvexp_launch::wave_supports(dim);
             p->n_dev_heads = int(hv.size());
             p->n_items = int(items.size());
             p->n_merge = int(merge.size());
@@ -654,7 +654,7 @@ int kvexp_hip_attention_run(kvexp_hip_plan *plan, const uint16_t *d_q, float *d_
             for (int G = 1; G <= 8; ++G) {
                 const int b = plan->group_start[G], e = plan->group_start[G + 1];
                 if (e > b)
-                    HIPX(kvexp_launch::attention_wave(plan->xkv, G, plan->dim, plan->heads.as<HeadDev>(),
+                    HIPX(kvexp_launch::attention_wave(plan->xkv, plan->order, G, plan->dim, plan->heads.as<HeadDev>(),
                                                       plan->items.as<WorkItem>() + b, e - b, d_q, d_out, d_lse,
                                                       plan->ws.as<float>(), s));
             }

@@ -163,13 +163,14 @@ def _max_block_escapes(oracle, blob, dim, seq):
     return int(esc[coded].max()) if coded.any() else 0
 
 
+@pytest.mark.parametrize("backend", ["scalar", "avx512"])
 @pytest.mark.parametrize("dim", [64, 128])
-def test_wave_kernel_groups_and_escapes(ctx, oracle, dim):
-    """The one-wave kernel (head_dim 64 and 128) for every query-row count G
-    it is instantiated for, on containers whose blocks carry from 0 to
-    several hundred escapes (blocks with more than 64 read the escape index
-    in windows), block sizes that do and do not split into 64-token chunks,
-    ragged lengths and several splits per head."""
+def test_wave_kernel_groups_and_escapes(ctx, oracle, dim, backend):
+    """The one-wave kernel (head_dim 64 and 128, both score orders) for every
+    query-row count G it is instantiated for, on containers whose blocks
+    carry from 0 to several hundred escapes (blocks with more than 64 read
+    the escape index in windows), block sizes that do and do not split into
+    64-token chunks, ragged lengths and several splits per head."""
     rng = np.random.default_rng(4242 + dim)
     seen_big = False
     cases = [(1, 128, 0.05, False), (2, 255, 0.02, False), (3, 100, 0.0, False), (7, 128, 0.3, False),
@@ -185,14 +186,62 @@ def test_wave_kernel_groups_and_escapes(ctx, oracle, dim):
             if frac:
                 seen_big |= _max_block_escapes(oracle, oracle.encode(k, seq, dim, block), dim, seq) > 64
         q = random_kv(rng, len(heads) * n_q, dim, spread_lo=-1, spread_hi=1)
-        say("wave kernel", trial, dict(n_q=n_q, block=block, frac=frac, narrow=narrow, seqs=[h["seq"] for h in heads]))
-        want = oracle.attention_heads("scalar", q, [dict(k=h["k"], v=h["v"], seq=h["seq"], threads=h["splits"])
-                                                    for h in heads], n_q=n_q, dim=dim, split=block)
-        raw = run_gpu(ctx, 0, q, heads, n_q, dim, block, False)
-        xkv = run_gpu(ctx, 0, q, heads, n_q, dim, block, True)
+        say("wave kernel", backend, dim, trial,
+            dict(n_q=n_q, block=block, frac=frac, narrow=narrow, seqs=[h["seq"] for h in heads]))
+        want = oracle.attention_heads(backend, q, [dict(k=h["k"], v=h["v"], seq=h["seq"], threads=h["splits"])
+                                                   for h in heads], n_q=n_q, dim=dim, split=block)
+        raw = run_gpu(ctx, ORDER[backend], q, heads, n_q, dim, block, False)
+        xkv = run_gpu(ctx, ORDER[backend], q, heads, n_q, dim, block, True)
         assert bits_equal(raw, xkv), trial
         assert bits_equal(raw, want), (trial, max_rel_err(raw, want))
     assert seen_big
+
+
+def _scaled_blocks(rng, x, block, shifts, special_blocks=0.3):
+    """x [seq, dim] float32 with each block of `block` rows scaled by 2^s, s
+    drawn from `shifts` per block; a fraction `special_blocks` of the blocks
+    also gets a few zeros and BF16 denormals."""
+    seq, dim = x.shape
+    nb = (seq + block - 1) // block
+    s = np.repeat(rng.choice(shifts, size=nb), block)[:seq]
+    b = bf16_from_f32((x * np.exp2(s)[:, None]).astype(np.float32).reshape(-1)).reshape(seq, dim)
+    pool = np.array([0x0000, 0x8000, 0x0001, 0x8003, 0x0050], np.uint16)
+    for i in np.flatnonzero(rng.random(nb) < special_blocks):
+        rows = b[i * block:(i + 1) * block].reshape(-1)
+        idx = rng.choice(rows.size, max(1, rows.size // 1000), replace=False)
+        rows[idx] = rng.choice(pool, idx.size)
+        b[i * block:(i + 1) * block] = rows.reshape(-1, dim)
+    return b.reshape(-1)
+
+
+@pytest.mark.parametrize("dim", [64, 128])
+def test_wave_dpbf16_flush_guard(ctx, oracle, dim):
+    """AVX-512 BF16 order on the one-wave kernel where VDPBF16PS's flushes
+    matter: K blocks scaled by 2^0 .. 2^-90 and query rows by 2^0 .. 2^-50,
+    so that some chunks meet the exponent bound of the matrix-core path
+    (E_k + E_q >= 142) and others take the flushing path, with products
+    below 2^-126 (flushed to zero), denormal K and q elements (read as zero)
+    and escapes among them; XKV and raw inputs, every G class."""
+    rng = np.random.default_rng(777 + dim)
+    block = 128
+    for trial, n_q in enumerate([1, 4, 5, 7, 8]):
+        heads = []
+        for h in range(3):
+            seq = int(rng.integers(1, 1200))
+            kx = (random_kv(rng, seq, dim, spread_lo=-3, spread_hi=3).astype(np.uint32) << 16).view(np.float32)
+            vx = (random_kv(rng, seq, dim, sigma=0.5).astype(np.uint32) << 16).view(np.float32)
+            k = _scaled_blocks(rng, kx.reshape(seq, dim), block, [0, -40, -60, -75, -90])
+            v = _scaled_blocks(rng, vx.reshape(seq, dim), block, [0, 0, -20])
+            heads.append(dict(k=k, v=v, seq=seq, splits=int(rng.integers(1, 6)), block=block))
+        qx = (random_kv(rng, len(heads) * n_q, dim, spread_lo=-1, spread_hi=1).astype(np.uint32) << 16)
+        q = _scaled_blocks(rng, qx.view(np.float32).reshape(-1, dim), 1, [0, -30, -50])
+        say("dpbf16 flush guard", dim, trial, dict(n_q=n_q, seqs=[h["seq"] for h in heads]))
+        want = oracle.attention_heads("avx512", q, [dict(k=h["k"], v=h["v"], seq=h["seq"], threads=h["splits"])
+                                                    for h in heads], n_q=n_q, dim=dim, split=block)
+        raw = run_gpu(ctx, 1, q, heads, n_q, dim, block, False)
+        xkv = run_gpu(ctx, 1, q, heads, n_q, dim, block, True)
+        assert bits_equal(raw, xkv), trial
+        assert bits_equal(raw, want), (trial, max_rel_err(raw, want))
 
 
 def test_host_entry_backend_hip(ctx, oracle, golden):
