@@ -197,17 +197,19 @@ __global__ __launch_bounds__(kThreads) void encode_stats_kernel(const uint16_t *
 }
 
 // ------------------------------------------------------------- encode: scan --
-// offs[i] = sum of block sizes before block i (n_blocks + 1 entries);
-// first[i] = i * bt, first[n_blocks] = seq.
+// offs[i] = base + sum of block sizes before block i (n_blocks + 1 entries);
+// first[i] = tok0 + i * bt, first[n_blocks] = tok0 + seq. base is offs[0] as
+// found on entry when `rebase` is set (an append continues the container at
+// its trailing block), else 0.
 __global__ __launch_bounds__(1024) void encode_scan_kernel(const EncBlockMeta *__restrict__ meta, int n_blocks,
                                                           int bt, int seq, int64_t *__restrict__ offs,
-                                                          int32_t *__restrict__ first) {
+                                                          int32_t *__restrict__ first, int rebase, int tok0) {
     __shared__ long long wave_tot[16];
     __shared__ long long carry_s;
     const int tid = int(threadIdx.x);
     const int lane = lane_id();
     const int w = tid >> 6;
-    if (tid == 0) carry_s = 0;
+    if (tid == 0) carry_s = rebase ? offs[0] : 0;
     __syncthreads();
     for (int r = 0; r < n_blocks; r += 1024) {
         const int i = r + tid;
@@ -227,7 +229,7 @@ __global__ __launch_bounds__(1024) void encode_scan_kernel(const EncBlockMeta *_
         }
         if (i < n_blocks) {
             offs[i] = base + incl - v;
-            first[i] = i * bt;
+            first[i] = tok0 + i * bt;
         }
         __syncthreads();
         if (tid == 0) carry_s += tot;
@@ -235,7 +237,7 @@ __global__ __launch_bounds__(1024) void encode_scan_kernel(const EncBlockMeta *_
     }
     if (tid == 0) {
         offs[n_blocks] = carry_s;
-        first[n_blocks] = seq;
+        first[n_blocks] = tok0 + seq;
     }
 }
 
@@ -460,9 +462,11 @@ hipError_t decode(const uint8_t *blob, uint64_t bytes, const int64_t *offs, cons
 }
 
 hipError_t encode(const uint16_t *kv, int seq, int dim, int bt, int n_blocks, EncBlockMeta *meta, uint8_t *bases,
-                  int64_t *offs, int32_t *first, uint8_t *out, uint32_t *status, hipStream_t s) {
+                  int64_t *offs, int32_t *first, uint8_t *out, uint32_t *status, hipStream_t s, bool rebase,
+                  int tok0) {
     hipLaunchKernelGGL(encode_stats_kernel, dim3(n_blocks), dim3(kThreads), 0, s, kv, seq, dim, bt, meta, bases);
-    hipLaunchKernelGGL(encode_scan_kernel, dim3(1), dim3(1024), 0, s, meta, n_blocks, bt, seq, offs, first);
+    hipLaunchKernelGGL(encode_scan_kernel, dim3(1), dim3(1024), 0, s, meta, n_blocks, bt, seq, offs, first,
+                       rebase ? 1 : 0, tok0);
     hipLaunchKernelGGL(encode_write_kernel, dim3(n_blocks), dim3(kThreads), 0, s, kv, seq, dim, bt, meta, bases,
                        offs, out, status);
     return hipGetLastError();

@@ -26,7 +26,8 @@ namespace kvexp_launch {
 hipError_t decode(const uint8_t *blob, uint64_t bytes, const int64_t *offs, const int32_t *first, int n_blocks,
                   int seq, int dim, uint16_t *out, uint32_t *status, hipStream_t s);
 hipError_t encode(const uint16_t *kv, int seq, int dim, int bt, int n_blocks, EncBlockMeta *meta, uint8_t *bases,
-                  int64_t *offs, int32_t *first, uint8_t *out, uint32_t *status, hipStream_t s);
+                  int64_t *offs, int32_t *first, uint8_t *out, uint32_t *status, hipStream_t s, bool rebase = false,
+                  int tok0 = 0);
 hipError_t attention(bool xkv, int order, const HeadDev *heads, const WorkItem *items, int n_items,
                      const int32_t *merge_ids, int n_merge, const uint16_t *q, float *out, float *lse, float *ws,
                      int dim, uint32_t *status, hipStream_t s);
@@ -186,8 +187,8 @@ struct kvexp_hip_ctx {
     int device = 0;
     DevBuf status; // uint32 status word
     // encoder scratch, grown on demand
-    DevBuf enc_meta, enc_bases, enc_off, enc_first;
-    size_t enc_meta_cap = 0, enc_bases_cap = 0, enc_index_cap = 0;
+    DevBuf enc_meta, enc_bases, enc_off, enc_first, enc_stage;
+    size_t enc_meta_cap = 0, enc_bases_cap = 0, enc_index_cap = 0, enc_stage_cap = 0;
     int cu_count = 0;
 };
 
@@ -451,6 +452,79 @@ int kvexp_hip_encode(kvexp_hip_ctx *ctx, const uint16_t *d_kv, int seq, int dim,
                 fail(KVEXP_HIP_LOGIC_ERROR, "escape count drifted from the size model");
             }
             *bytes_out = size_t(total);
+        }
+    });
+}
+
+// Blocks are encoded independently (codec.cpp:54-160 walks t0 = 0, bt, 2bt,
+// ... and each block's bytes depend only on its own tokens), so appending
+// tokens changes only the trailing partial block and adds blocks after it:
+// the tail's raw tokens and the new ones are staged contiguously and encoded
+// at the tail block's offset (offsets[n_tokens / bt], which is the
+// container's size when there is no partial block), and the index is
+// rewritten from that block on.
+int kvexp_hip_append(kvexp_hip_ctx *ctx, const uint16_t *d_new, int n_new, int n_tokens, int dim, int bt,
+                     uint16_t *d_tail, uint8_t *d_blob, size_t capacity, int64_t *d_offsets,
+                     int32_t *d_first_token, int index_capacity, size_t *bytes_out, void *stream) {
+    return guarded([&] {
+        if (ctx == nullptr) fail(KVEXP_HIP_INVALID_ARGUMENT, "kvexp_hip_append: null context");
+        if (n_new < 0 || n_tokens < 0 || dim <= 0 || bt <= 0)
+            fail(KVEXP_HIP_INVALID_ARGUMENT, "kvexp_hip_append: bad shape");
+        if (dim % 4 != 0 || dim > kMaxDim)
+            fail(KVEXP_HIP_INVALID_ARGUMENT, "encode_bf16: head_dim must be a multiple of 4 and at most 256");
+        if (bt > 255) fail(KVEXP_HIP_INVALID_ARGUMENT, "encode_bf16: block_tokens must fit in a byte");
+        if (int64_t(bt) * dim > 65535)
+            fail(KVEXP_HIP_INVALID_ARGUMENT, "encode_bf16: block escape count would not fit in u16");
+        if (d_tail == nullptr || d_blob == nullptr || d_offsets == nullptr || d_first_token == nullptr ||
+            (n_new > 0 && d_new == nullptr))
+            fail(KVEXP_HIP_INVALID_ARGUMENT, "kvexp_hip_append: null argument");
+        const int64_t total = int64_t(n_tokens) + n_new;
+        if (total > INT32_MAX) fail(KVEXP_HIP_INVALID_ARGUMENT, "kvexp_hip_append: too many tokens");
+        if (int64_t(capacity) < kvexp_hip_encode_bound(int(total), dim, bt))
+            fail(KVEXP_HIP_CAPACITY, "kvexp_hip_append: capacity below kvexp_hip_encode_bound");
+        if (index_capacity < kvexp_hip_block_count(int(total), bt) + 1)
+            fail(KVEXP_HIP_CAPACITY, "kvexp_hip_append: index capacity below n_blocks + 1");
+        DeviceGuard g(ctx->device);
+        hipStream_t s = static_cast<hipStream_t>(stream);
+        const int tail = n_tokens % bt, tail_blk = n_tokens / bt;
+        const int seq = tail + n_new; // tokens re-encoded from the tail block on
+        if (n_new > 0) {
+            const int nb = kvexp_hip_block_count(seq, bt);
+            const size_t row = size_t(dim) * sizeof(uint16_t);
+            grow(ctx->enc_stage, ctx->enc_stage_cap, size_t(seq) * row);
+            grow(ctx->enc_meta, ctx->enc_meta_cap, size_t(nb) * sizeof(EncBlockMeta));
+            grow(ctx->enc_bases, ctx->enc_bases_cap, size_t(nb) * 2u * size_t(dim));
+            uint8_t *stage = ctx->enc_stage.as<uint8_t>();
+            if (tail > 0) HIPX(hipMemcpyAsync(stage, d_tail, size_t(tail) * row, hipMemcpyDeviceToDevice, s));
+            HIPX(hipMemcpyAsync(stage + size_t(tail) * row, d_new, size_t(n_new) * row, hipMemcpyDeviceToDevice, s));
+            HIPX(kvexp_launch::encode(reinterpret_cast<const uint16_t *>(stage), seq, dim, bt, nb,
+                                      ctx->enc_meta.as<EncBlockMeta>(), ctx->enc_bases.as<uint8_t>(),
+                                      d_offsets + tail_blk, d_first_token + tail_blk, d_blob,
+                                      ctx->status.as<uint32_t>(), s, n_tokens > 0, tail_blk * bt));
+            const int rest = int(total % bt); // raw tokens of the new trailing partial block
+            if (rest > 0)
+                HIPX(hipMemcpyAsync(d_tail, stage + size_t(nb - 1) * bt * row, size_t(rest) * row,
+                                    hipMemcpyDeviceToDevice, s));
+        } else if (n_tokens == 0) {
+            // an empty container: the index is its terminal entry
+            const int64_t z64 = 0;
+            const int32_t z32 = 0;
+            HIPX(hipMemcpyAsync(d_offsets, &z64, sizeof z64, hipMemcpyHostToDevice, s));
+            HIPX(hipMemcpyAsync(d_first_token, &z32, sizeof z32, hipMemcpyHostToDevice, s));
+            HIPX(hipStreamSynchronize(s));
+        }
+        if (bytes_out != nullptr) {
+            const int nb_all = kvexp_hip_block_count(int(total), bt);
+            int64_t bytes = 0;
+            uint32_t st = 0;
+            HIPX(hipMemcpyAsync(&bytes, d_offsets + nb_all, sizeof bytes, hipMemcpyDeviceToHost, s));
+            HIPX(hipMemcpyAsync(&st, ctx->status.p, sizeof st, hipMemcpyDeviceToHost, s));
+            HIPX(hipStreamSynchronize(s));
+            if (st != 0u) {
+                HIPX(hipMemset(ctx->status.p, 0, sizeof(uint32_t)));
+                fail(KVEXP_HIP_LOGIC_ERROR, "escape count drifted from the size model");
+            }
+            *bytes_out = size_t(bytes);
         }
     });
 }

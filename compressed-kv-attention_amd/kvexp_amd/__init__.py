@@ -84,6 +84,7 @@ def lib() -> C.CDLL:
     L.kvexp_hip_build_index.argtypes = [vp, sz, i32, i32, vp, vp, i32, C.POINTER(i32)]
     L.kvexp_hip_encode.argtypes = [vp, vp, i32, i32, i32, vp, sz, vp, vp, C.POINTER(sz), vp]
     L.kvexp_hip_decode.argtypes = [vp, vp, sz, vp, vp, i32, i32, i32, vp, i32, vp]
+    L.kvexp_hip_append.argtypes = [vp, vp, i32, i32, i32, i32, vp, vp, sz, vp, vp, i32, C.POINTER(sz), vp]
     L.kvexp_hip_plan_create.argtypes = [vp, C.POINTER(_Head), i32, i32, i32, i32, i32, C.POINTER(vp)]
     L.kvexp_hip_plan_destroy.argtypes = [vp]
     L.kvexp_hip_suggest_splits.argtypes = [vp, i32, i32, i32]
@@ -153,6 +154,42 @@ class Encoded:
         return int(self.offsets.numel()) - 1
 
 
+class Cache:
+    """A device container grown by appends (kvexp_hip_append): the buffers for
+    max_tokens tokens, the block index and the raw trailing partial block."""
+
+    def __init__(self, ctx: "Context", dim: int, max_tokens: int, block: int = 128):
+        import torch
+
+        dev = torch.device("cuda", ctx.device)
+        self.ctx, self.dim, self.block, self.max_tokens = ctx, dim, block, max_tokens
+        self.capacity = max(encode_bound(max_tokens, dim, block), 1)
+        self.index_capacity = max(lib().kvexp_hip_block_count(max_tokens, block), 0) + 1
+        self.blob = torch.empty(self.capacity, dtype=torch.uint8, device=dev)
+        self.offsets = torch.empty(self.index_capacity, dtype=torch.int64, device=dev)
+        self.first = torch.empty(self.index_capacity, dtype=torch.int32, device=dev)
+        self.tail = torch.empty(block * dim, dtype=torch.int16, device=dev)
+        self.seq = 0
+        self.nbytes = 0
+        self.append(None, 0)
+
+    def append(self, tokens, n: int | None = None, stream=None, sync_size: bool = True) -> None:
+        """tokens: device tensor holding [n, dim] BF16 bits (or None with n = 0)."""
+        n = int(tokens.numel() // self.dim) if n is None else int(n)
+        out = C.c_size_t(0)
+        check(lib().kvexp_hip_append(self.ctx.h, _ptr(tokens), n, self.seq, self.dim, self.block, _ptr(self.tail),
+                                     _ptr(self.blob), self.capacity, _ptr(self.offsets), _ptr(self.first),
+                                     self.index_capacity, C.byref(out) if sync_size else None, _stream(stream)))
+        self.seq += n
+        self.nbytes = int(out.value) if sync_size else -1
+
+    def view(self) -> Encoded:
+        """The container as an Encoded (shares this cache's memory)."""
+        nb = max(lib().kvexp_hip_block_count(self.seq, self.block), 0)
+        return Encoded(self.blob, self.nbytes, self.offsets[: nb + 1], self.first[: nb + 1], self.seq, self.dim,
+                       self.block)
+
+
 class Context:
     """One device context (workspace + status word)."""
 
@@ -192,6 +229,10 @@ class Context:
         check(lib().kvexp_hip_encode(self.h, _ptr(kv), seq, dim, block, _ptr(blob), cap, _ptr(offs), _ptr(first),
                                      C.byref(n) if sync_size else None, _stream(stream)))
         return Encoded(blob, int(n.value) if sync_size else -1, offs, first, seq, dim, block)
+
+    def cache(self, dim: int, max_tokens: int, block: int = 128) -> "Cache":
+        """An empty appendable container for up to max_tokens tokens."""
+        return Cache(self, dim, max_tokens, block)
 
     def upload(self, blob_np, dim: int, seq: int, block: int = 128) -> Encoded:
         """A host container (numpy uint8) to the device, with its host-built index."""

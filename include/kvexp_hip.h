@@ -21,6 +21,8 @@
  *                                    (src/softmax.hpp:16-41), batched over heads
  *   kvexp_hip_encode                 kvexp::encode_bf16 (include/kvexp/codec.hpp:45-46,
  *                                    src/codec.cpp:39-164)
+ *   kvexp_hip_append                 kvexp::encode_bf16 of the grown sequence
+ *                                    (src/codec.cpp:39-164), done incrementally
  *   kvexp_hip_decode                 kvexp::decode_bf16 (include/kvexp/codec.hpp:48,
  *                                    src/codec.cpp:166-174)
  *   kvexp_hip_build_index            the header walk of XkvReader::seek / open_xkv
@@ -91,6 +93,26 @@ int kvexp_hip_build_index(const uint8_t *blob, size_t bytes, int dim, int seq, i
 int kvexp_hip_encode(kvexp_hip_ctx *ctx, const uint16_t *d_kv, int seq, int dim, int block_tokens,
                      uint8_t *d_out, size_t capacity, int64_t *d_offsets, int32_t *d_first_token,
                      size_t *bytes_out, void *stream);
+
+/* Appends n_new tokens (d_new [n_new, dim] BF16) to a device container that
+ * holds the first n_tokens tokens of a sequence, so that afterwards it is
+ * byte-identical to encode_bf16 of all n_tokens + n_new tokens (blocks are
+ * encoded independently, so only the trailing partial block is encoded
+ * again, followed by the new blocks). d_blob (capacity bytes, at least
+ * kvexp_hip_encode_bound(n_tokens + n_new, ...)) and its block index
+ * d_offsets / d_first_token (index_capacity entries, at least
+ * kvexp_hip_block_count(n_tokens + n_new, ...) + 1) are updated in place.
+ * d_tail [block_tokens, dim] BF16 holds the raw tokens of the trailing
+ * partial block (the last n_tokens % block_tokens tokens) and is updated;
+ * a caller starting from a container made by kvexp_hip_encode fills it with
+ * those tokens. n_tokens = 0 starts a new container (n_new = 0 then writes
+ * the empty index). The new container size goes to *bytes_out after a
+ * synchronisation of `stream` when bytes_out is non-NULL. Staging memory
+ * comes from the context (grown on demand, like kvexp_hip_encode's
+ * scratch), so calls on one context must not overlap. */
+int kvexp_hip_append(kvexp_hip_ctx *ctx, const uint16_t *d_new, int n_new, int n_tokens, int dim,
+                     int block_tokens, uint16_t *d_tail, uint8_t *d_blob, size_t capacity, int64_t *d_offsets,
+                     int32_t *d_first_token, int index_capacity, size_t *bytes_out, void *stream);
 
 /* Decodes seq tokens of a device container into d_out [seq, dim] BF16,
  * bit-identical to decode_bf16. d_offsets / d_first_token is the block index

@@ -99,3 +99,6 @@ def test_null_arguments_rejected():
     p = C.c_void_p()
     assert L.kvexp_hip_plan_create(None, None, 0, 1, 64, 128, 0, C.byref(p)) == 1
     assert b"bad argument" in L.kvexp_hip_last_error()
+    n = C.c_size_t(0)
+    assert L.kvexp_hip_append(None, None, 1, 0, 64, 128, None, None, 0, None, None, 0, C.byref(n), None) == 1
+    assert b"null context" in L.kvexp_hip_last_error()

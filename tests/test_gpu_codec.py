@@ -2,7 +2,9 @@
 oracle and the reference's golden containers: containers byte-identical to
 encode_bf16 (codec.cpp:39-164), decode bit-identical to decode_bf16
 (codec.cpp:166-174), block index equal to the header walk, and the reference's
-format errors reported for damaged containers."""
+format errors reported for damaged containers. Appends (kvexp_hip_append)
+must leave the container byte-identical to encode_bf16 of the whole sequence
+after every call."""
 import numpy as np
 import pytest
 
@@ -159,3 +161,82 @@ def test_encode_argument_errors(ctx, reference):
         with pytest.raises(KvexpError) as er:
             reference.encode(np.zeros(64 * 256, np.uint16), seq, dim, block)
         assert (ei.value.kind, ei.value.msg) == (er.value.kind, er.value.msg)
+
+
+@pytest.mark.parametrize("dim,block", [(64, 128), (128, 128), (256, 255), (36, 100), (8, 1)])
+def test_append_equals_whole_encode(ctx, oracle, dim, block):
+    """A container grown by appends of assorted sizes (single tokens,
+    partial blocks, exact blocks, several blocks at once, none) equals
+    encode_bf16 of the tokens so far after every append: bytes, block index,
+    decode; data with raw, 2-bit and 4-bit blocks, escapes and specials."""
+    import torch
+
+    rng = np.random.default_rng(dim * 1000 + block)
+    total = 3 * block + 37 if block > 1 else 300
+    kv = np.concatenate([_kinds(rng, total, dim, kind)[: (total // 4) * dim] for kind in (0, 1, 2, 3)])
+    total = kv.size // dim
+    cache = ctx.cache(dim, total + 5, block)
+    sizes = [1, 0, 2, block - 1 if block > 1 else 1, block, 1, 2 * block + 3, 5]
+    pos = 0
+    step = 0
+    while pos < total:
+        n = min(sizes[step % len(sizes)], total - pos)
+        step += 1
+        cache.append(to_dev(kv[pos * dim:(pos + n) * dim], torch.int16), n)
+        pos += n
+        if n == 0:
+            continue
+        want = oracle.encode(kv[: pos * dim], pos, dim, block)
+        enc = cache.view()
+        say("append", dim, block, step, dict(n=n, tokens=pos, bytes=enc.nbytes))
+        assert enc.nbytes == want.size
+        assert np.array_equal(enc.blob[: enc.nbytes].cpu().numpy(), want), (step, pos)
+        off, first = oracle.block_index(want, dim, pos)
+        assert np.array_equal(enc.offsets.cpu().numpy(), off), (step, pos)
+        assert np.array_equal(enc.first.cpu().numpy(), first), (step, pos)
+        if step % 3 == 0 or pos == total:
+            dec = ctx.decode(enc).cpu().numpy().view(np.uint16)
+            assert np.array_equal(dec, kv[: pos * dim]), (step, pos)
+    from kvexp_amd import KvexpHipError
+
+    with pytest.raises(KvexpHipError) as e:
+        cache.append(to_dev(kv[: 6 * dim], torch.int16), 6)
+    assert e.value.kind == "capacity"
+
+
+def test_append_attention_after_encode(ctx, oracle):
+    """A container made by kvexp_hip_encode and continued by appends (the tail
+    filled from the caller's tokens) gives the same attention bits as a
+    container encoded whole."""
+    import torch
+
+    rng = np.random.default_rng(99)
+    dim, block, n_q = 64, 128, 7
+    seq0, seq = 1000, 1300
+    k = random_kv(rng, seq, dim, spread_lo=-6, spread_hi=4, outliers=2)
+    v = random_kv(rng, seq, dim, sigma=0.5)
+    q = random_kv(rng, n_q, dim)
+    caches = []
+    for x in (k, v):
+        c = ctx.cache(dim, seq, block)
+        enc0 = ctx.encode(to_dev(x[: seq0 * dim], torch.int16), seq0, dim, block)
+        c.blob[: enc0.nbytes] = enc0.blob[: enc0.nbytes]
+        c.offsets[: enc0.n_blocks + 1] = enc0.offsets
+        c.first[: enc0.n_blocks + 1] = enc0.first
+        tail = seq0 % block
+        c.tail[: tail * dim] = to_dev(x[(seq0 - tail) * dim: seq0 * dim], torch.int16)
+        c.seq, c.nbytes = seq0, enc0.nbytes
+        for t in range(seq0, seq, 60):
+            n = min(60, seq - t)
+            c.append(to_dev(x[t * dim:(t + n) * dim], torch.int16), n)
+        caches.append(c)
+    splits = 3
+    kx, vx = caches[0].view(), caches[1].view()
+    assert np.array_equal(kx.blob[: kx.nbytes].cpu().numpy(), oracle.encode(k, seq, dim, block))
+    plan = ctx.plan([dict(kx=kx, vx=vx, seq=seq, splits=splits)], n_q, dim, block)
+    out = torch.empty(n_q * dim, dtype=torch.float32, device=torch.device("cuda", ctx.device))
+    plan.run(to_dev(q, torch.int16), out)
+    want = oracle.attention_heads("scalar", q, [dict(k=k, v=v, seq=seq, threads=splits)], n_q=n_q, dim=dim,
+                                  split=block)
+    got = out.cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), np.asarray(want, np.float32).view(np.uint32))
