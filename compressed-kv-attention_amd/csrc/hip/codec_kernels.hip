@@ -14,6 +14,10 @@
 //   2. one workgroup: prefix sum of block sizes -> block byte offsets and
 //      first tokens (the block index the attention kernels read);
 //   3. per block: header, base, sign/mantissa bytes, packed codes, escapes.
+// Appends run the same three steps over a batch of containers (one job per
+// container: its trailing partial block and the new blocks), reading each
+// block's rows from the job's raw tail and new tokens in place, then store
+// the new trailing partial block's raw tokens for the next append.
 #include "kvexp_device.h"
 #include "kvexp_types.h"
 
@@ -101,26 +105,64 @@ __global__ __launch_bounds__(kThreads) void decode_blocks_kernel(const uint8_t *
     if (bad) atomicOr(status, bad);
 }
 
+// The elements of one block to encode, token-major: elements [0, split) at
+// a, the rest at b (an append's first block starts with the raw tokens of
+// the container's trailing partial block, then the new tokens).
+struct EncRows {
+    const uint16_t *a, *b;
+    int split;
+    __device__ __forceinline__ uint32_t at(int i) const { return i < split ? a[i] : b[i - split]; }
+};
+
+// The job holding launch block g (jobs sorted by blk0; wave-uniform).
+__device__ __forceinline__ int find_job(const AppendJobDev *jobs, int n_jobs, int g) {
+    int lo = 0, hi = n_jobs - 1;
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (jobs[mid].blk0 <= g) lo = mid;
+        else hi = mid - 1;
+    }
+    return lo;
+}
+
+// Rows of local block b of an append job: block 0 starts with the job's raw
+// tail (tail_n rows), every block then reads new tokens.
+__device__ __forceinline__ EncRows job_rows(const AppendJobDev &j, int b, int bt, int dim) {
+    const int t0 = b * bt;
+    const int na = b == 0 ? j.tail_n : 0;
+    EncRows r;
+    r.a = j.tail;
+    r.b = j.src + size_t(t0 + na - j.tail_n) * size_t(dim);
+    r.split = na * dim;
+    return r;
+}
+
 // ------------------------------------------------------------ encode: stats --
 // bases: [n_blocks][2][dim] (2-bit window base, 4-bit window base).
-__global__ __launch_bounds__(kThreads) void encode_stats_kernel(const uint16_t *__restrict__ kv, int seq, int dim,
-                                                               int bt, EncBlockMeta *__restrict__ meta,
-                                                               uint8_t *__restrict__ bases) {
-    __shared__ uint32_t hist[kWaves][256];
-    __shared__ uint32_t pre[kWaves][257];
-    __shared__ int esc_part[kWaves][2];
-    const int b = int(blockIdx.x);
-    const int t0 = b * bt;
-    const int n = min(bt, seq - t0);
+struct StatsLds {
+    uint32_t hist[kWaves][256];
+    uint32_t pre[kWaves][257];
+    int esc_part[kWaves][2];
+};
+
+__device__ __forceinline__ void encode_stats_block(StatsLds &L, const EncRows src, int n, int dim,
+                                                   EncBlockMeta *__restrict__ meta, uint8_t *__restrict__ bases) {
+    auto &hist = L.hist;
+    auto &pre = L.pre;
+    auto &esc_part = L.esc_part;
     const int lane = lane_id();
     const int w = int(threadIdx.x) >> 6;
-    const uint16_t *src = kv + size_t(t0) * size_t(dim);
     int esc2 = 0, esc4 = 0;
     for (int d = w; d < dim; d += kWaves) { // dim % 4 == 0: every wave runs dim/4 rounds
 #pragma unroll
         for (int i = 0; i < 4; ++i) hist[w][4 * lane + i] = 0u;
         __syncthreads();
-        for (int t = lane; t < n; t += kWave) atomicAdd(&hist[w][(src[size_t(t) * dim + d] >> 7) & 0xFFu], 1u);
+        // rows from each source in a loop of its own (the counts do not
+        // depend on the order)
+        const int na = min(n, src.split / dim);
+        for (int t = lane; t < na; t += kWave) atomicAdd(&hist[w][(src.a[t * dim + d] >> 7) & 0xFFu], 1u);
+        for (int t = na + lane; t < n; t += kWave)
+            atomicAdd(&hist[w][(src.b[(t - na) * dim + d] >> 7) & 0xFFu], 1u);
         __syncthreads();
         uint32_t h4[4], run = 0;
 #pragma unroll
@@ -149,7 +191,7 @@ __global__ __launch_bounds__(kThreads) void encode_stats_kernel(const uint16_t *
             const int cov = key >> 9;
             const int base = 511 - (key & 511);
             if (lane == 0) {
-                bases[(size_t(b) * 2 + size_t(bi)) * size_t(dim) + size_t(d)] = uint8_t(base);
+                bases[size_t(bi) * size_t(dim) + size_t(d)] = uint8_t(base);
                 if (bi == 0)
                     esc2 += n - cov;
                 else
@@ -192,8 +234,29 @@ __global__ __launch_bounds__(kThreads) void encode_stats_kernel(const uint16_t *
         m.bytes = best_bytes;
         m.mode = best_mode;
         m.n_escape = best_esc;
-        meta[b] = m;
+        *meta = m;
     }
+}
+
+__global__ __launch_bounds__(kThreads) void encode_stats_kernel(const uint16_t *__restrict__ kv, int seq, int dim,
+                                                               int bt, EncBlockMeta *__restrict__ meta,
+                                                               uint8_t *__restrict__ bases) {
+    const int b = int(blockIdx.x);
+    const int t0 = b * bt;
+    const EncRows src{kv + size_t(t0) * size_t(dim), kv + size_t(t0) * size_t(dim), 0};
+    __shared__ StatsLds L;
+    encode_stats_block(L, src, min(bt, seq - t0), dim, meta + b, bases + size_t(b) * 2 * size_t(dim));
+}
+
+__global__ __launch_bounds__(kThreads) void append_stats_kernel(const AppendJobDev *__restrict__ jobs, int n_jobs,
+                                                               int dim, int bt, EncBlockMeta *__restrict__ meta,
+                                                               uint8_t *__restrict__ bases) {
+    const int g = int(blockIdx.x);
+    const AppendJobDev j = jobs[find_job(jobs, n_jobs, g)];
+    const int b = g - j.blk0;
+    __shared__ StatsLds L;
+    encode_stats_block(L, job_rows(j, b, bt, dim), min(bt, j.seq - b * bt), dim, meta + g,
+                       bases + size_t(g) * 2 * size_t(dim));
 }
 
 // ------------------------------------------------------------- encode: scan --
@@ -201,11 +264,16 @@ __global__ __launch_bounds__(kThreads) void encode_stats_kernel(const uint16_t *
 // first[i] = tok0 + i * bt, first[n_blocks] = tok0 + seq. base is offs[0] as
 // found on entry when `rebase` is set (an append continues the container at
 // its trailing block), else 0.
-__global__ __launch_bounds__(1024) void encode_scan_kernel(const EncBlockMeta *__restrict__ meta, int n_blocks,
-                                                          int bt, int seq, int64_t *__restrict__ offs,
-                                                          int32_t *__restrict__ first, int rebase, int tok0) {
-    __shared__ long long wave_tot[16];
-    __shared__ long long carry_s;
+struct ScanLds {
+    long long wave_tot[16];
+    long long carry;
+};
+
+__device__ __forceinline__ void encode_scan_body(ScanLds &L, const EncBlockMeta *__restrict__ meta, int n_blocks,
+                                                 int bt, int seq, int64_t *__restrict__ offs,
+                                                 int32_t *__restrict__ first, int rebase, int tok0) {
+    auto &wave_tot = L.wave_tot;
+    auto &carry_s = L.carry;
     const int tid = int(threadIdx.x);
     const int lane = lane_id();
     const int w = tid >> 6;
@@ -241,20 +309,27 @@ __global__ __launch_bounds__(1024) void encode_scan_kernel(const EncBlockMeta *_
     }
 }
 
+__global__ __launch_bounds__(1024) void encode_scan_kernel(const EncBlockMeta *__restrict__ meta, int n_blocks,
+                                                          int bt, int seq, int64_t *__restrict__ offs,
+                                                          int32_t *__restrict__ first, int rebase, int tok0) {
+    __shared__ ScanLds L;
+    encode_scan_body(L, meta, n_blocks, bt, seq, offs, first, rebase, tok0);
+}
+
+// One workgroup per append job.
+__global__ __launch_bounds__(1024) void append_scan_kernel(const AppendJobDev *__restrict__ jobs,
+                                                          const EncBlockMeta *__restrict__ meta, int bt) {
+    const AppendJobDev j = jobs[blockIdx.x];
+    __shared__ ScanLds L;
+    encode_scan_body(L, meta + j.blk0, j.nb, bt, j.seq, j.offs, j.first, j.rebase, j.tok0);
+}
+
 // ------------------------------------------------------------ encode: write --
-__global__ __launch_bounds__(kThreads) void encode_write_kernel(const uint16_t *__restrict__ kv, int seq, int dim,
-                                                               int bt, const EncBlockMeta *__restrict__ meta,
-                                                               const uint8_t *__restrict__ bases,
-                                                               const int64_t *__restrict__ offs,
-                                                               uint8_t *__restrict__ out,
-                                                               uint32_t *__restrict__ status) {
-    __shared__ int scan_tmp[kWaves];
-    const int b = int(blockIdx.x);
-    const int t0 = b * bt;
-    const int n = min(bt, seq - t0);
-    const EncBlockMeta m = meta[b];
-    uint8_t *p = out + offs[b];
-    const uint16_t *src = kv + size_t(t0) * size_t(dim);
+// One block: `p` is its place in the container, `bases2` its two window
+// bases [2][dim].
+__device__ __forceinline__ void encode_write_block(int *scan_tmp, const EncRows src, int n, int dim,
+                                                   const EncBlockMeta m, const uint8_t *__restrict__ bases2,
+                                                   uint8_t *__restrict__ p, uint32_t *__restrict__ status) {
     const int total = n * dim;
     if (threadIdx.x == 0) {
         p[0] = uint8_t(m.mode);
@@ -270,7 +345,7 @@ __global__ __launch_bounds__(kThreads) void encode_write_kernel(const uint16_t *
     p += 8;
     if (m.mode == 0) {
         for (int i = int(threadIdx.x); i < total; i += kThreads) {
-            const uint16_t h = src[i];
+            const uint32_t h = src.at(i);
             p[2 * i] = uint8_t(h & 0xFF);
             p[2 * i + 1] = uint8_t(h >> 8);
         }
@@ -278,7 +353,7 @@ __global__ __launch_bounds__(kThreads) void encode_write_kernel(const uint16_t *
     }
     const bool four = m.mode == 4;
     const int width = four ? 15 : 3;
-    const uint8_t *bsrc = bases + (size_t(b) * 2 + (four ? 1 : 0)) * size_t(dim);
+    const uint8_t *bsrc = bases2 + (four ? size_t(dim) : 0);
     for (int d = int(threadIdx.x); d < dim; d += kThreads) p[d] = bsrc[d];
     uint8_t *sm = p + dim;
     uint8_t *codes = sm + size_t(total);
@@ -296,7 +371,7 @@ __global__ __launch_bounds__(kThreads) void encode_write_kernel(const uint16_t *
             const int d0 = e0 % dim;
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
-                const uint32_t h = src[e0 + k];
+                const uint32_t h = src.at(e0 + k);
                 hv[k] = h;
                 sm[e0 + k] = uint8_t(((h >> 8) & 0x80u) | (h & 0x7Fu));
                 const int delta = int((h >> 7) & 0xFFu) - int(bsrc[d0 + k]);
@@ -331,6 +406,42 @@ __global__ __launch_bounds__(kThreads) void encode_write_kernel(const uint16_t *
         }
     }
     if (threadIdx.x == 0 && carry != m.n_escape) atomicOr(status, kStEscape);
+}
+
+__global__ __launch_bounds__(kThreads) void encode_write_kernel(const uint16_t *__restrict__ kv, int seq, int dim,
+                                                               int bt, const EncBlockMeta *__restrict__ meta,
+                                                               const uint8_t *__restrict__ bases,
+                                                               const int64_t *__restrict__ offs,
+                                                               uint8_t *__restrict__ out,
+                                                               uint32_t *__restrict__ status) {
+    const int b = int(blockIdx.x);
+    const int t0 = b * bt;
+    const EncRows src{kv + size_t(t0) * size_t(dim), kv + size_t(t0) * size_t(dim), 0};
+    __shared__ int scan_tmp[kWaves];
+    encode_write_block(scan_tmp, src, min(bt, seq - t0), dim, meta[b], bases + size_t(b) * 2 * size_t(dim),
+                       out + offs[b], status);
+}
+
+__global__ __launch_bounds__(kThreads) void append_write_kernel(const AppendJobDev *__restrict__ jobs, int n_jobs,
+                                                               int dim, int bt, const EncBlockMeta *__restrict__ meta,
+                                                               const uint8_t *__restrict__ bases,
+                                                               uint32_t *__restrict__ status) {
+    const int g = int(blockIdx.x);
+    const AppendJobDev j = jobs[find_job(jobs, n_jobs, g)];
+    const int b = g - j.blk0;
+    __shared__ int scan_tmp[kWaves];
+    encode_write_block(scan_tmp, job_rows(j, b, bt, dim), min(bt, j.seq - b * bt), dim, meta[g],
+                       bases + size_t(g) * 2 * size_t(dim), j.out + j.offs[b], status);
+}
+
+// The raw rows of each job's new trailing partial block that are not in
+// its tail buffer yet, copied there (after the write kernel has read it).
+__global__ __launch_bounds__(kThreads) void append_tail_kernel(const AppendJobDev *__restrict__ jobs, int dim) {
+    const AppendJobDev j = jobs[blockIdx.x];
+    const int total = j.copy_rows * dim;
+    const uint16_t *from = j.src + size_t(j.copy_from) * size_t(dim);
+    uint16_t *to = j.tail + size_t(j.copy_to) * size_t(dim);
+    for (int i = int(threadIdx.x); i < total; i += kThreads) to[i] = from[i];
 }
 
 // -------------------------------------------------- escape-position index --
@@ -469,6 +580,20 @@ hipError_t encode(const uint16_t *kv, int seq, int dim, int bt, int n_blocks, En
                        rebase ? 1 : 0, tok0);
     hipLaunchKernelGGL(encode_write_kernel, dim3(n_blocks), dim3(kThreads), 0, s, kv, seq, dim, bt, meta, bases,
                        offs, out, status);
+    return hipGetLastError();
+}
+
+hipError_t append(const AppendJobDev *jobs, int n_jobs, int total_blocks, int dim, int bt, EncBlockMeta *meta,
+                  uint8_t *bases, uint32_t *status, hipStream_t s) {
+    if (n_jobs <= 0) return hipSuccess;
+    if (total_blocks > 0)
+        hipLaunchKernelGGL(append_stats_kernel, dim3(total_blocks), dim3(kThreads), 0, s, jobs, n_jobs, dim, bt, meta,
+                           bases);
+    hipLaunchKernelGGL(append_scan_kernel, dim3(n_jobs), dim3(1024), 0, s, jobs, meta, bt);
+    if (total_blocks > 0)
+        hipLaunchKernelGGL(append_write_kernel, dim3(total_blocks), dim3(kThreads), 0, s, jobs, n_jobs, dim, bt, meta,
+                           bases, status);
+    hipLaunchKernelGGL(append_tail_kernel, dim3(n_jobs), dim3(kThreads), 0, s, jobs, dim);
     return hipGetLastError();
 }
 

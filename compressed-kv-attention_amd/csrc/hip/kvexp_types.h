@@ -75,4 +75,23 @@ struct EncBlockMeta {
     int32_t n_escape;
 };
 
+// Job of a batched append, as the kernels read it (built by the host API).
+struct AppendJobDev {
+    uint16_t *tail;        // raw trailing partial block [bt, dim] (read, then rewritten)
+    const uint16_t *src;   // new tokens [n_new, dim]
+    int64_t *offs;         // the container's index from its trailing block on
+    int32_t *first;
+    uint8_t *out;          // the container
+    int32_t tail_n;        // raw tokens in `tail` (n_tokens % bt)
+    int32_t seq;           // tokens encoded: tail_n + n_new
+    int32_t tok0;          // first token of the trailing block
+    int32_t blk0;          // first block of this job in the launch
+    int32_t nb;            // blocks encoded
+    int32_t rebase;        // the container is not empty (its trailing block starts at offs[0])
+    int32_t copy_from;     // new-token row that starts the raw rows kept for the next append
+    int32_t copy_to;       // their first row in `tail`
+    int32_t copy_rows;
+    int32_t pad;
+};
+
 } // namespace kvexp_dev

@@ -10,6 +10,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <climits>
 #include <cstring>
 #include <mutex>
 #include <new>
@@ -18,6 +19,7 @@
 
 #include "../hip/kvexp_types.h"
 
+using kvexp_dev::AppendJobDev;
 using kvexp_dev::EncBlockMeta;
 using kvexp_dev::HeadDev;
 using kvexp_dev::WorkItem;
@@ -28,6 +30,8 @@ hipError_t decode(const uint8_t *blob, uint64_t bytes, const int64_t *offs, cons
 hipError_t encode(const uint16_t *kv, int seq, int dim, int bt, int n_blocks, EncBlockMeta *meta, uint8_t *bases,
                   int64_t *offs, int32_t *first, uint8_t *out, uint32_t *status, hipStream_t s, bool rebase = false,
                   int tok0 = 0);
+hipError_t append(const kvexp_dev::AppendJobDev *jobs, int n_jobs, int total_blocks, int dim, int bt,
+                  EncBlockMeta *meta, uint8_t *bases, uint32_t *status, hipStream_t s);
 hipError_t attention(bool xkv, int order, const HeadDev *heads, const WorkItem *items, int n_items,
                      const int32_t *merge_ids, int n_merge, const uint16_t *q, float *out, float *lse, float *ws,
                      int dim, uint32_t *status, hipStream_t s);
@@ -187,8 +191,8 @@ struct kvexp_hip_ctx {
     int device = 0;
     DevBuf status; // uint32 status word
     // encoder scratch, grown on demand
-    DevBuf enc_meta, enc_bases, enc_off, enc_first, enc_stage;
-    size_t enc_meta_cap = 0, enc_bases_cap = 0, enc_index_cap = 0, enc_stage_cap = 0;
+    DevBuf enc_meta, enc_bases, enc_off, enc_first, app_jobs;
+    size_t enc_meta_cap = 0, enc_bases_cap = 0, enc_index_cap = 0, app_jobs_cap = 0;
     int cu_count = 0;
 };
 
@@ -459,73 +463,128 @@ int kvexp_hip_encode(kvexp_hip_ctx *ctx, const uint16_t *d_kv, int seq, int dim,
 // Blocks are encoded independently (codec.cpp:54-160 walks t0 = 0, bt, 2bt,
 // ... and each block's bytes depend only on its own tokens), so appending
 // tokens changes only the trailing partial block and adds blocks after it:
-// the tail's raw tokens and the new ones are staged contiguously and encoded
-// at the tail block's offset (offsets[n_tokens / bt], which is the
-// container's size when there is no partial block), and the index is
-// rewritten from that block on.
+// each job encodes its container's raw tail followed by the new tokens at
+// the tail block's offset (offsets[n_tokens / bt], which is the container's
+// size when there is no partial block) and rewrites the index from that
+// block on; then the raw rows of the new partial block go to the tail.
+namespace {
+
+void check_append_shape(int dim, int bt) {
+    if (dim <= 0 || bt <= 0) fail(KVEXP_HIP_INVALID_ARGUMENT, "kvexp_hip_append: bad shape");
+    if (dim % 4 != 0 || dim > kMaxDim)
+        fail(KVEXP_HIP_INVALID_ARGUMENT, "encode_bf16: head_dim must be a multiple of 4 and at most 256");
+    if (bt > 255) fail(KVEXP_HIP_INVALID_ARGUMENT, "encode_bf16: block_tokens must fit in a byte");
+    if (int64_t(bt) * dim > 65535)
+        fail(KVEXP_HIP_INVALID_ARGUMENT, "encode_bf16: block escape count would not fit in u16");
+}
+
+// Validates one job and appends its device form (none for a no-op);
+// returns the blocks it encodes.
+int add_append_job(const kvexp_hip_append_job &a, int dim, int bt, int blk0, std::vector<AppendJobDev> &out) {
+    if (a.n_new < 0 || a.n_tokens < 0) fail(KVEXP_HIP_INVALID_ARGUMENT, "kvexp_hip_append: bad shape");
+    if (a.d_tail == nullptr || a.d_blob == nullptr || a.d_offsets == nullptr || a.d_first_token == nullptr ||
+        (a.n_new > 0 && a.d_new == nullptr))
+        fail(KVEXP_HIP_INVALID_ARGUMENT, "kvexp_hip_append: null argument");
+    const int64_t total = int64_t(a.n_tokens) + a.n_new;
+    if (total > INT32_MAX) fail(KVEXP_HIP_INVALID_ARGUMENT, "kvexp_hip_append: too many tokens");
+    if (int64_t(a.capacity) < kvexp_hip_encode_bound(int(total), dim, bt))
+        fail(KVEXP_HIP_CAPACITY, "kvexp_hip_append: capacity below kvexp_hip_encode_bound");
+    if (a.index_capacity < kvexp_hip_block_count(int(total), bt) + 1)
+        fail(KVEXP_HIP_CAPACITY, "kvexp_hip_append: index capacity below n_blocks + 1");
+    if (a.n_new == 0 && a.n_tokens > 0) return 0;
+    const int tail_n = a.n_tokens % bt, tail_blk = a.n_tokens / bt;
+    AppendJobDev j{};
+    j.tail = a.d_tail;
+    j.src = a.d_new;
+    j.offs = a.d_offsets + tail_blk;
+    j.first = a.d_first_token + tail_blk;
+    j.out = a.d_blob;
+    j.tail_n = tail_n;
+    j.seq = tail_n + a.n_new;
+    j.tok0 = tail_blk * bt;
+    j.blk0 = blk0;
+    j.nb = kvexp_hip_block_count(j.seq, bt);
+    j.rebase = a.n_tokens > 0 ? 1 : 0;
+    const int rest = int(total % bt);
+    if (rest > 0) {
+        const int start = int(total - rest) - j.tok0; // first local row of the new partial block
+        const int from = std::max(start, tail_n);      // rows before tail_n are in the tail already
+        j.copy_from = from - tail_n;
+        j.copy_to = from - start;
+        j.copy_rows = start + rest - from;
+    }
+    out.push_back(j);
+    return j.nb;
+}
+
+void run_append(kvexp_hip_ctx *ctx, const kvexp_hip_append_job *jobs, int n_jobs, int dim, int bt, hipStream_t s) {
+    std::vector<AppendJobDev> dj;
+    dj.reserve(size_t(n_jobs));
+    int blocks = 0;
+    for (int i = 0; i < n_jobs; ++i) blocks += add_append_job(jobs[i], dim, bt, blocks, dj);
+    if (dj.empty()) return;
+    grow(ctx->enc_meta, ctx->enc_meta_cap, size_t(std::max(blocks, 1)) * sizeof(EncBlockMeta));
+    grow(ctx->enc_bases, ctx->enc_bases_cap, size_t(std::max(blocks, 1)) * 2u * size_t(dim));
+    grow(ctx->app_jobs, ctx->app_jobs_cap, dj.size() * sizeof(AppendJobDev));
+    // pageable source: the runtime has consumed it when the call returns
+    HIPX(hipMemcpyAsync(ctx->app_jobs.p, dj.data(), dj.size() * sizeof(AppendJobDev), hipMemcpyHostToDevice, s));
+    HIPX(kvexp_launch::append(ctx->app_jobs.as<AppendJobDev>(), int(dj.size()), blocks, dim, bt,
+                              ctx->enc_meta.as<EncBlockMeta>(), ctx->enc_bases.as<uint8_t>(),
+                              ctx->status.as<uint32_t>(), s));
+}
+
+void check_encoder_status(kvexp_hip_ctx *ctx, hipStream_t s) {
+    uint32_t st = 0;
+    HIPX(hipMemcpyAsync(&st, ctx->status.p, sizeof st, hipMemcpyDeviceToHost, s));
+    HIPX(hipStreamSynchronize(s));
+    if (st != 0u) {
+        HIPX(hipMemset(ctx->status.p, 0, sizeof(uint32_t)));
+        fail(KVEXP_HIP_LOGIC_ERROR, "escape count drifted from the size model");
+    }
+}
+
+} // namespace
+
 int kvexp_hip_append(kvexp_hip_ctx *ctx, const uint16_t *d_new, int n_new, int n_tokens, int dim, int bt,
                      uint16_t *d_tail, uint8_t *d_blob, size_t capacity, int64_t *d_offsets,
                      int32_t *d_first_token, int index_capacity, size_t *bytes_out, void *stream) {
     return guarded([&] {
         if (ctx == nullptr) fail(KVEXP_HIP_INVALID_ARGUMENT, "kvexp_hip_append: null context");
-        if (n_new < 0 || n_tokens < 0 || dim <= 0 || bt <= 0)
-            fail(KVEXP_HIP_INVALID_ARGUMENT, "kvexp_hip_append: bad shape");
-        if (dim % 4 != 0 || dim > kMaxDim)
-            fail(KVEXP_HIP_INVALID_ARGUMENT, "encode_bf16: head_dim must be a multiple of 4 and at most 256");
-        if (bt > 255) fail(KVEXP_HIP_INVALID_ARGUMENT, "encode_bf16: block_tokens must fit in a byte");
-        if (int64_t(bt) * dim > 65535)
-            fail(KVEXP_HIP_INVALID_ARGUMENT, "encode_bf16: block escape count would not fit in u16");
-        if (d_tail == nullptr || d_blob == nullptr || d_offsets == nullptr || d_first_token == nullptr ||
-            (n_new > 0 && d_new == nullptr))
-            fail(KVEXP_HIP_INVALID_ARGUMENT, "kvexp_hip_append: null argument");
-        const int64_t total = int64_t(n_tokens) + n_new;
-        if (total > INT32_MAX) fail(KVEXP_HIP_INVALID_ARGUMENT, "kvexp_hip_append: too many tokens");
-        if (int64_t(capacity) < kvexp_hip_encode_bound(int(total), dim, bt))
-            fail(KVEXP_HIP_CAPACITY, "kvexp_hip_append: capacity below kvexp_hip_encode_bound");
-        if (index_capacity < kvexp_hip_block_count(int(total), bt) + 1)
-            fail(KVEXP_HIP_CAPACITY, "kvexp_hip_append: index capacity below n_blocks + 1");
+        check_append_shape(dim, bt);
+        kvexp_hip_append_job a{};
+        a.d_new = d_new;
+        a.n_new = n_new;
+        a.n_tokens = n_tokens;
+        a.d_tail = d_tail;
+        a.d_blob = d_blob;
+        a.capacity = capacity;
+        a.d_offsets = d_offsets;
+        a.d_first_token = d_first_token;
+        a.index_capacity = index_capacity;
         DeviceGuard g(ctx->device);
         hipStream_t s = static_cast<hipStream_t>(stream);
-        const int tail = n_tokens % bt, tail_blk = n_tokens / bt;
-        const int seq = tail + n_new; // tokens re-encoded from the tail block on
-        if (n_new > 0) {
-            const int nb = kvexp_hip_block_count(seq, bt);
-            const size_t row = size_t(dim) * sizeof(uint16_t);
-            grow(ctx->enc_stage, ctx->enc_stage_cap, size_t(seq) * row);
-            grow(ctx->enc_meta, ctx->enc_meta_cap, size_t(nb) * sizeof(EncBlockMeta));
-            grow(ctx->enc_bases, ctx->enc_bases_cap, size_t(nb) * 2u * size_t(dim));
-            uint8_t *stage = ctx->enc_stage.as<uint8_t>();
-            if (tail > 0) HIPX(hipMemcpyAsync(stage, d_tail, size_t(tail) * row, hipMemcpyDeviceToDevice, s));
-            HIPX(hipMemcpyAsync(stage + size_t(tail) * row, d_new, size_t(n_new) * row, hipMemcpyDeviceToDevice, s));
-            HIPX(kvexp_launch::encode(reinterpret_cast<const uint16_t *>(stage), seq, dim, bt, nb,
-                                      ctx->enc_meta.as<EncBlockMeta>(), ctx->enc_bases.as<uint8_t>(),
-                                      d_offsets + tail_blk, d_first_token + tail_blk, d_blob,
-                                      ctx->status.as<uint32_t>(), s, n_tokens > 0, tail_blk * bt));
-            const int rest = int(total % bt); // raw tokens of the new trailing partial block
-            if (rest > 0)
-                HIPX(hipMemcpyAsync(d_tail, stage + size_t(nb - 1) * bt * row, size_t(rest) * row,
-                                    hipMemcpyDeviceToDevice, s));
-        } else if (n_tokens == 0) {
-            // an empty container: the index is its terminal entry
-            const int64_t z64 = 0;
-            const int32_t z32 = 0;
-            HIPX(hipMemcpyAsync(d_offsets, &z64, sizeof z64, hipMemcpyHostToDevice, s));
-            HIPX(hipMemcpyAsync(d_first_token, &z32, sizeof z32, hipMemcpyHostToDevice, s));
-            HIPX(hipStreamSynchronize(s));
-        }
+        run_append(ctx, &a, 1, dim, bt, s);
         if (bytes_out != nullptr) {
-            const int nb_all = kvexp_hip_block_count(int(total), bt);
+            const int nb_all = kvexp_hip_block_count(n_tokens + n_new, bt);
             int64_t bytes = 0;
-            uint32_t st = 0;
             HIPX(hipMemcpyAsync(&bytes, d_offsets + nb_all, sizeof bytes, hipMemcpyDeviceToHost, s));
-            HIPX(hipMemcpyAsync(&st, ctx->status.p, sizeof st, hipMemcpyDeviceToHost, s));
-            HIPX(hipStreamSynchronize(s));
-            if (st != 0u) {
-                HIPX(hipMemset(ctx->status.p, 0, sizeof(uint32_t)));
-                fail(KVEXP_HIP_LOGIC_ERROR, "escape count drifted from the size model");
-            }
+            check_encoder_status(ctx, s);
             *bytes_out = size_t(bytes);
         }
+    });
+}
+
+int kvexp_hip_append_batch(kvexp_hip_ctx *ctx, const kvexp_hip_append_job *jobs, int n_jobs, int dim, int bt,
+                           int check, void *stream) {
+    return guarded([&] {
+        if (ctx == nullptr) fail(KVEXP_HIP_INVALID_ARGUMENT, "kvexp_hip_append: null context");
+        if (n_jobs < 0 || (n_jobs > 0 && jobs == nullptr))
+            fail(KVEXP_HIP_INVALID_ARGUMENT, "kvexp_hip_append: null argument");
+        check_append_shape(dim, bt);
+        DeviceGuard g(ctx->device);
+        hipStream_t s = static_cast<hipStream_t>(stream);
+        run_append(ctx, jobs, n_jobs, dim, bt, s);
+        if (check) check_encoder_status(ctx, s);
     });
 }
 

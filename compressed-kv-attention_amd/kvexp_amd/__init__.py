@@ -38,6 +38,15 @@ class KvexpHipError(RuntimeError):
         self.msg = msg
 
 
+class _AppendJob(C.Structure):
+    _fields_ = [
+        ("d_new", C.c_void_p), ("n_new", C.c_int32), ("n_tokens", C.c_int32),
+        ("d_tail", C.c_void_p), ("d_blob", C.c_void_p), ("capacity", C.c_uint64),
+        ("d_offsets", C.c_void_p), ("d_first_token", C.c_void_p),
+        ("index_capacity", C.c_int32), ("reserved", C.c_int32),
+    ]
+
+
 class _Head(C.Structure):
     _fields_ = [
         ("k_xkv", C.c_void_p), ("v_xkv", C.c_void_p),
@@ -85,6 +94,7 @@ def lib() -> C.CDLL:
     L.kvexp_hip_encode.argtypes = [vp, vp, i32, i32, i32, vp, sz, vp, vp, C.POINTER(sz), vp]
     L.kvexp_hip_decode.argtypes = [vp, vp, sz, vp, vp, i32, i32, i32, vp, i32, vp]
     L.kvexp_hip_append.argtypes = [vp, vp, i32, i32, i32, i32, vp, vp, sz, vp, vp, i32, C.POINTER(sz), vp]
+    L.kvexp_hip_append_batch.argtypes = [vp, C.POINTER(_AppendJob), i32, i32, i32, i32, vp]
     L.kvexp_hip_plan_create.argtypes = [vp, C.POINTER(_Head), i32, i32, i32, i32, i32, C.POINTER(vp)]
     L.kvexp_hip_plan_destroy.argtypes = [vp]
     L.kvexp_hip_suggest_splits.argtypes = [vp, i32, i32, i32]
@@ -183,6 +193,19 @@ class Cache:
         self.seq += n
         self.nbytes = int(out.value) if sync_size else -1
 
+    def _job(self, tokens, n: int) -> _AppendJob:
+        j = _AppendJob()
+        j.d_new, j.n_new, j.n_tokens = _ptr(tokens), n, self.seq
+        j.d_tail, j.d_blob, j.capacity = _ptr(self.tail), _ptr(self.blob), self.capacity
+        j.d_offsets, j.d_first_token, j.index_capacity = _ptr(self.offsets), _ptr(self.first), self.index_capacity
+        return j
+
+    def size(self, stream=None) -> int:
+        """Container bytes (reads the index's terminal entry; synchronises)."""
+        nb = max(lib().kvexp_hip_block_count(self.seq, self.block), 0)
+        self.nbytes = int(self.offsets[nb].item())
+        return self.nbytes
+
     def view(self) -> Encoded:
         """The container as an Encoded (shares this cache's memory)."""
         nb = max(lib().kvexp_hip_block_count(self.seq, self.block), 0)
@@ -233,6 +256,22 @@ class Context:
     def cache(self, dim: int, max_tokens: int, block: int = 128) -> "Cache":
         """An empty appendable container for up to max_tokens tokens."""
         return Cache(self, dim, max_tokens, block)
+
+    def append_batch(self, caches: list, tokens: list, n: int | list, check_errors: bool = False,
+                     stream=None) -> None:
+        """Appends tokens[i] ([n_i, dim] BF16 device tensors) to caches[i] in one
+        kvexp_hip_append_batch call (all caches of one dim and block size).
+        Container sizes are not read back (Cache.size() does that)."""
+        ns = [int(n)] * len(caches) if isinstance(n, int) else [int(x) for x in n]
+        arr = (_AppendJob * len(caches))()
+        for i, (c, t) in enumerate(zip(caches, tokens)):
+            arr[i] = c._job(t, ns[i])
+        c0 = caches[0]
+        check(lib().kvexp_hip_append_batch(self.h, arr, len(caches), c0.dim, c0.block, 1 if check_errors else 0,
+                                           _stream(stream)))
+        for c, k in zip(caches, ns):
+            c.seq += k
+            c.nbytes = -1
 
     def upload(self, blob_np, dim: int, seq: int, block: int = 128) -> Encoded:
         """A host container (numpy uint8) to the device, with its host-built index."""

@@ -21,7 +21,7 @@
  *                                    (src/softmax.hpp:16-41), batched over heads
  *   kvexp_hip_encode                 kvexp::encode_bf16 (include/kvexp/codec.hpp:45-46,
  *                                    src/codec.cpp:39-164)
- *   kvexp_hip_append                 kvexp::encode_bf16 of the grown sequence
+ *   kvexp_hip_append(_batch)         kvexp::encode_bf16 of the grown sequence
  *                                    (src/codec.cpp:39-164), done incrementally
  *   kvexp_hip_decode                 kvexp::decode_bf16 (include/kvexp/codec.hpp:48,
  *                                    src/codec.cpp:166-174)
@@ -107,12 +107,33 @@ int kvexp_hip_encode(kvexp_hip_ctx *ctx, const uint16_t *d_kv, int seq, int dim,
  * a caller starting from a container made by kvexp_hip_encode fills it with
  * those tokens. n_tokens = 0 starts a new container (n_new = 0 then writes
  * the empty index). The new container size goes to *bytes_out after a
- * synchronisation of `stream` when bytes_out is non-NULL. Staging memory
- * comes from the context (grown on demand, like kvexp_hip_encode's
- * scratch), so calls on one context must not overlap. */
+ * synchronisation of `stream` when bytes_out is non-NULL. Scratch memory
+ * comes from the context (grown on demand, like kvexp_hip_encode's), so
+ * calls on one context must not overlap. */
 int kvexp_hip_append(kvexp_hip_ctx *ctx, const uint16_t *d_new, int n_new, int n_tokens, int dim,
                      int block_tokens, uint16_t *d_tail, uint8_t *d_blob, size_t capacity, int64_t *d_offsets,
                      int32_t *d_first_token, int index_capacity, size_t *bytes_out, void *stream);
+
+/* One container of a batched append: the arguments of kvexp_hip_append. */
+typedef struct kvexp_hip_append_job {
+    const uint16_t *d_new;      /* [n_new, dim] BF16 */
+    int32_t n_new;
+    int32_t n_tokens;           /* tokens already in the container */
+    uint16_t *d_tail;           /* [block_tokens, dim] BF16, raw trailing partial block */
+    uint8_t *d_blob;
+    uint64_t capacity;
+    int64_t *d_offsets;
+    int32_t *d_first_token;
+    int32_t index_capacity;
+    int32_t reserved;
+} kvexp_hip_append_job;
+
+/* kvexp_hip_append for n_jobs containers of one shape in one set of
+ * launches (a decode step appends one token to every K and V tensor). No
+ * synchronisation unless `check` is non-zero, which then reports an encoder
+ * size-model error. */
+int kvexp_hip_append_batch(kvexp_hip_ctx *ctx, const kvexp_hip_append_job *jobs, int n_jobs, int dim,
+                           int block_tokens, int check, void *stream);
 
 /* Decodes seq tokens of a device container into d_out [seq, dim] BF16,
  * bit-identical to decode_bf16. d_offsets / d_first_token is the block index

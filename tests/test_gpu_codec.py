@@ -240,3 +240,39 @@ def test_append_attention_after_encode(ctx, oracle):
                                   split=block)
     got = out.cpu().numpy()
     assert np.array_equal(got.view(np.uint32), np.asarray(want, np.float32).view(np.uint32))
+
+
+def test_append_batch(ctx, oracle):
+    """kvexp_hip_append_batch over containers in different states (empty,
+    partial trailing block, block-aligned) with different append sizes (0, 1,
+    a partial block, several blocks) in one call; repeated rounds, each
+    container equal to encode_bf16 of its tokens so far after every round."""
+    import torch
+
+    rng = np.random.default_rng(2024)
+    dim, block, n_c = 64, 128, 12
+    total = 1200
+    data = [_kinds(rng, total, dim, i % 4) for i in range(n_c)]
+    caches = [ctx.cache(dim, total, block) for _ in range(n_c)]
+    start = [0, 1, 127, 128, 129, 300, 0, 5, 256, 511, 64, 1000]
+    for c, d, st in zip(caches, data, start):  # bring each container to its starting length
+        if st:
+            c.append(to_dev(d[: st * dim], torch.int16), st)
+    pos = list(start)
+    for rnd, sizes in enumerate([[1] * n_c, [0, 3, 1, 127, 128, 129, 0, 250, 1, 1, 64, 2],
+                                 [1] * n_c, [5, 0, 300, 2, 1, 77, 128, 1, 0, 130, 7, 100]]):
+        ns = [min(k, total - p) for k, p in zip(sizes, pos)]
+        toks = [to_dev(d[p * dim:(p + k) * dim] if k else d[:dim], torch.int16) for d, p, k in zip(data, pos, ns)]
+        ctx.append_batch(caches, toks, ns, check_errors=True)
+        for i, (c, d) in enumerate(zip(caches, data)):
+            pos[i] += ns[i]
+            if pos[i] == 0:
+                continue
+            want = oracle.encode(d[: pos[i] * dim], pos[i], dim, block)
+            n = c.size()
+            say("append batch", rnd, i, dict(tokens=pos[i], bytes=n))
+            assert n == want.size, (rnd, i)
+            assert np.array_equal(c.blob[:n].cpu().numpy(), want), (rnd, i)
+            off, first = oracle.block_index(want, dim, pos[i])
+            assert np.array_equal(c.view().offsets.cpu().numpy(), off), (rnd, i)
+            assert np.array_equal(c.view().first.cpu().numpy(), first), (rnd, i)
