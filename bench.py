@@ -1,6 +1,7 @@
 """Benchmark of the fused compressed-KV decode step on one MI355X.
 
     python bench.py [--steps K] [--warmup W] [--config c2] [--gpus 1]
+    python bench.py --workload append [--steps K] [--warmup W]
 
 Workload ("c2"): a full Qwen2.5-0.5B decode step at a
 32K context: 24 layers x 2 KV heads, 7 queries per KV head (GQA), head_dim 64,
@@ -25,6 +26,14 @@ profiles/attn_wave_c2_traffic.md (null when absent). cpu_baseline = the
 reference library (oracle/_ref, compiled from the reference sources) running
 its model_heads scope (OpenMP over KV heads, AVX-512 BF16 when the host has
 it, else AVX2) on a bounded sample of the same step.
+
+--workload append measures the producer side on the same c2 shape: the
+96 K/V containers (48 KV heads) grown on the device by kvexp_hip_append_batch.
+value = decode-step append time (one new token per container, one batched
+call) in µs; the line also carries the prefill rate (32768 tokens into every
+container in one call, GB/s of BF16 input) with its HBM roofline, and the
+reference's encode_bf16 on the host as the CPU baseline. Containers are
+checked byte for byte against kvexp_hip_encode of the same tokens.
 """
 from __future__ import annotations
 
@@ -71,6 +80,129 @@ def copy_probe(torch, dev):
     log(f"copy probe: 3 copies of {n} bytes")
 
 
+def bench_append(a, torch, np, kvexp_amd, synth) -> int:
+    cfg = synth.CONFIGS["c2"]
+    L, KV, D, S, BT = cfg["layers"], cfg["kv_heads"], cfg["dim"], cfg["seq"], cfg["block"]
+    T = 2 * L * KV  # K and V containers
+    dev = torch.device("cuda:0")
+    ctx = kvexp_amd.Context(0)
+    steps, warmup = a.steps, a.warmup
+    extra = steps + warmup + 1
+    t0 = time.time()
+    src, host = [], []
+    for l in range(L):
+        for h in range(KV):
+            k, v = synth.head_kv("c2", S + extra, 0, l, h)
+            for x in (k, v):
+                src.append(torch.from_numpy(x.view(np.int16)).to(dev))
+                if len(host) < 16:
+                    host.append(x)
+    caches = [ctx.cache(D, S + extra, BT) for _ in range(T)]
+    torch.cuda.synchronize()
+    log(f"append inputs ready in {time.time() - t0:.1f}s: {T} containers")
+
+    # prefill: every container from empty to S tokens in one call (the
+    # calls rewrite the same buffers: each starts from n_tokens = 0)
+    pre = [t[: S * D] for t in src]
+
+    def prefill():
+        for c in caches:
+            c.seq = 0
+        ctx.append_batch(caches, pre, S)
+
+    for _ in range(2):
+        prefill()
+    torch.cuda.synchronize()
+    n_pre = max(3, min(20, steps // 10))
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(n_pre):
+        prefill()
+    e1.record()
+    torch.cuda.synchronize()
+    pre_ms = e0.elapsed_time(e1) / n_pre
+    container = sum(c.size() for c in caches)
+    raw_bytes = 2 * S * D * T
+    pre_gbps = raw_bytes / (pre_ms * 1e-3) / 1e9
+    algo = raw_bytes + container  # read the tokens once, write the containers
+    log(f"prefill {pre_ms * 1e3:.1f} us for {T} x {S} tokens: {pre_gbps:.1f} GB/s of input, "
+        f"containers {container} B")
+
+    # decode steps: one token per container per call, the step's tokens as
+    # one [containers, 1, dim] tensor (as a model's K/V projections give them)
+    one = torch.stack([t.view(-1, D)[S:S + extra] for t in src], dim=1).contiguous()  # [extra, T, D]
+    aset = ctx.append_set(caches)
+    for i in range(warmup):
+        aset.append(one[i], 1)
+    torch.cuda.synchronize()
+    t_start = time.perf_counter()
+    e0.record()
+    for i in range(warmup, warmup + steps):
+        aset.append(one[i], 1)
+    e1.record()
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t_start) * 1e3 / steps
+    step_ms = e0.elapsed_time(e1) / steps
+    n_tok = S + warmup + steps
+    # parity: every container equals the GPU encoder's output for the same tokens
+    same = True
+    for c, t in zip(caches, src):
+        enc = ctx.encode(t[: n_tok * D], n_tok, D, BT)
+        n = c.size()
+        same &= n == enc.nbytes and bool(torch.equal(c.blob[:n], enc.blob[:n]))
+    log(f"decode-step append {step_ms * 1e3:.1f} us (wall {wall_ms * 1e3:.1f}), containers equal encode: {same}")
+
+    cpu = None
+    if not a.no_cpu_baseline:
+        try:
+            sys.path.insert(0, os.path.join(ROOT, "oracle"))
+            from oracle import Reference
+
+            R = Reference()
+            times = []
+            budget = time.perf_counter()
+            while len(times) < 2 or (time.perf_counter() - budget < 15.0 and len(times) < 10):
+                t1 = time.perf_counter()
+                for x in host:
+                    R.encode(x[: S * D], S, D, BT)
+                times.append(time.perf_counter() - t1)
+            med = float(np.median(times))
+            cpu = {"value": round(len(host) * 2 * S * D / med / 1e9, 4), "unit": "GB/s", "cores": 1,
+                   "kind": "reference",
+                   "sample": f"encode_bf16 of {len(host)} of the {T} c2 tensors ({S} tokens each), one thread, "
+                             f"median of {len(times)} runs ({med * 1e3:.1f} ms)"}
+            log("cpu baseline", cpu)
+        except FileNotFoundError:
+            cpu = {"value": None, "unit": "GB/s", "cores": 0, "kind": "reference",
+                   "sample": "oracle/_ref/libkvexp_ref.so not present on this host"}
+    line = {
+        "metric": "decode-step append µs (one token into each of 96 K/V containers), Qwen2.5-0.5B shape, 32K ctx",
+        "value": round(step_ms * 1e3, 2),
+        "unit": "us",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": round(step_ms, 5),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "u8",
+        "data": "synthetic (seeded, kvexp_amd/synth.py config c2)",
+        "config": {"workload": "append: 48 KV heads x (K, V), head_dim 64, 128-token blocks, containers at 32K "
+                               "tokens", "containers": T, "dim": D, "block": BT, "seq": S},
+        "wall_us_per_step": round(wall_ms * 1e3, 2),
+        "prefill": {"us": round(pre_ms * 1e3, 2), "tokens_per_container": S, "input_GBps": round(pre_gbps, 2)},
+        "containers_equal_encode": same,
+        "roofline": {"bound": "hbm", "achieved": round(algo / (pre_ms * 1e-3) / 1e9, 2), "peak": HBM_PEAK_GBPS,
+                     "unit": "GB/s", "frac": round(algo / (pre_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+                     "traffic": None, "kernel": "prefill append (stats + scan + write + tail launches)",
+                     "algorithmic_bytes": algo},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -81,6 +213,7 @@ def main() -> int:
     ap.add_argument("--splits", type=int, default=0, help="splits per KV head (0 = library suggestion)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=0)
+    ap.add_argument("--workload", default="attention", choices=["attention", "append"])
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run a 256 MiB device copy (counter calibration under rocprofv3 --pmc)")
     a = ap.parse_args()
@@ -95,6 +228,8 @@ def main() -> int:
     import kvexp_amd
     from kvexp_amd import synth
 
+    if a.workload == "append":
+        return bench_append(a, torch, np, kvexp_amd, synth)
     if a.config != "c2":
         raise SystemExit("the bench line is quoted on c2 (BASELINE.json configs[1]); other configs are test cases")
     cfg = synth.CONFIGS["c2"]

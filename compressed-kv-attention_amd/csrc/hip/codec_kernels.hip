@@ -139,77 +139,83 @@ __device__ __forceinline__ EncRows job_rows(const AppendJobDev &j, int b, int bt
 
 // ------------------------------------------------------------ encode: stats --
 // bases: [n_blocks][2][dim] (2-bit window base, 4-bit window base).
-struct StatsLds {
-    uint32_t hist[kWaves][256];
-    uint32_t pre[kWaves][257];
-    int esc_part[kWaves][2];
-};
+// Thread i of the workgroup (at most 128 threads) owns channels i, i + 128:
+// it counts a channel's exponents in a private column of LDS byte counters
+// (four bins per dword; a block has at most 255 tokens, so a byte cannot
+// overflow into its neighbour) with fire-and-forget LDS adds, then slides
+// each code window over the bins between its smallest and largest exponent
+// (windows outside them cover nothing) to find best_base: the most covered
+// exponents, then the smallest base (codec.cpp:18-35).
+constexpr int kHistStride = 65; // dwords per channel column (64 + 1: columns start on different banks)
 
-__device__ __forceinline__ void encode_stats_block(StatsLds &L, const EncRows src, int n, int dim,
+__device__ __forceinline__ void encode_stats_block(uint32_t *hist, int *esc_part, const EncRows src, int n, int dim,
                                                    EncBlockMeta *__restrict__ meta, uint8_t *__restrict__ bases) {
-    auto &hist = L.hist;
-    auto &pre = L.pre;
-    auto &esc_part = L.esc_part;
-    const int lane = lane_id();
-    const int w = int(threadIdx.x) >> 6;
+    const int tid = int(threadIdx.x);
+    uint32_t *h = hist + tid * kHistStride;
     int esc2 = 0, esc4 = 0;
-    for (int d = w; d < dim; d += kWaves) { // dim % 4 == 0: every wave runs dim/4 rounds
-#pragma unroll
-        for (int i = 0; i < 4; ++i) hist[w][4 * lane + i] = 0u;
-        __syncthreads();
+    for (int d = tid; d < dim; d += int(blockDim.x)) {
+        int e_lo = 255, e_hi = 0;
+#pragma unroll 16
+        for (int k = 0; k < 64; ++k) h[k] = 0u;
         // rows from each source in a loop of its own (the counts do not
-        // depend on the order)
+        // depend on the order), 32 loads in flight before their adds
         const int na = min(n, src.split / dim);
-        for (int t = lane; t < na; t += kWave) atomicAdd(&hist[w][(src.a[t * dim + d] >> 7) & 0xFFu], 1u);
-        for (int t = na + lane; t < n; t += kWave)
-            atomicAdd(&hist[w][(src.b[(t - na) * dim + d] >> 7) & 0xFFu], 1u);
-        __syncthreads();
-        uint32_t h4[4], run = 0;
+        auto count_rows = [&](const uint16_t *p, int rows) {
+            for (int t0 = 0; t0 < rows; t0 += 32) {
+                uint32_t x[32];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            run += hist[w][4 * lane + i];
-            h4[i] = run;
-        }
-        const int excl = wave_scan_add(int(run)) - int(run);
-        if (lane == 0) pre[w][0] = 0u;
+                for (int k = 0; k < 32; ++k) x[k] = t0 + k < rows ? uint32_t(p[(t0 + k) * dim + d]) : 0xFFFFFFFFu;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) pre[w][4 * lane + i + 1] = uint32_t(excl) + h4[i];
-        __syncthreads();
+                for (int k = 0; k < 32; ++k) {
+                    if (x[k] == 0xFFFFFFFFu) break;
+                    const uint32_t e = (x[k] >> 7) & 0xFFu;
+                    atomicAdd(&h[e >> 2], 1u << (8 * (e & 3u)));
+                    e_lo = min(e_lo, int(e));
+                    e_hi = max(e_hi, int(e));
+                }
+            }
+        };
+        count_rows(src.a, na);
+        count_rows(src.b, n - na);
+        auto count = [&](int b) { return int((h[b >> 2] >> (8 * (b & 3))) & 0xFFu); };
 #pragma unroll
         for (int bi = 0; bi < 2; ++bi) {
             const int width = bi == 0 ? 3 : 15; // codes 0..2^bits-2
-            int key = -1;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int base = 4 * lane + i;
-                if (base <= 256 - width) {
-                    const int cov = int(pre[w][base + width] - pre[w][base]);
-                    key = max(key, (cov << 9) | (511 - base)); // most covered, then smallest base
+            const int lo = min(max(0, e_lo - width + 1), 256 - width);
+            const int hi = min(e_hi, 256 - width);
+            int cov = 0;
+            for (int b = lo; b < lo + width; ++b) cov += count(b);
+            int best = cov, best_base = lo;
+            for (int b = lo + 1; b <= hi; ++b) {
+                cov += count(b + width - 1) - count(b - 1);
+                if (cov > best) {
+                    best = cov;
+                    best_base = b;
                 }
             }
-            for (int o = 32; o > 0; o >>= 1) key = max(key, __shfl_xor(key, o));
-            const int cov = key >> 9;
-            const int base = 511 - (key & 511);
-            if (lane == 0) {
-                bases[size_t(bi) * size_t(dim) + size_t(d)] = uint8_t(base);
-                if (bi == 0)
-                    esc2 += n - cov;
-                else
-                    esc4 += n - cov;
-            }
+            bases[size_t(bi) * size_t(dim) + size_t(d)] = uint8_t(best_base);
+            if (bi == 0)
+                esc2 += n - best;
+            else
+                esc4 += n - best;
         }
-        __syncthreads();
     }
-    if (lane == 0) {
-        esc_part[w][0] = esc2;
-        esc_part[w][1] = esc4;
+    // escape counts of the whole block
+    for (int o = 32; o > 0; o >>= 1) {
+        esc2 += __shfl_xor(esc2, o);
+        esc4 += __shfl_xor(esc4, o);
+    }
+    const int w = tid >> 6, nw = int(blockDim.x) >> 6;
+    if ((tid & 63) == 0) {
+        esc_part[2 * w] = esc2;
+        esc_part[2 * w + 1] = esc4;
     }
     __syncthreads();
-    if (threadIdx.x == 0) {
+    if (tid == 0) {
         int e2 = 0, e4 = 0;
-        for (int i = 0; i < kWaves; ++i) {
-            e2 += esc_part[i][0];
-            e4 += esc_part[i][1];
+        for (int i = 0; i < nw; ++i) {
+            e2 += esc_part[2 * i];
+            e4 += esc_part[2 * i + 1];
         }
         // codec.cpp:94-103: raw, then 2-bit, then 4-bit; replace when smaller,
         // or on a tie when the best is not raw and has more escapes (or equal
@@ -238,24 +244,33 @@ __device__ __forceinline__ void encode_stats_block(StatsLds &L, const EncRows sr
     }
 }
 
-__global__ __launch_bounds__(kThreads) void encode_stats_kernel(const uint16_t *__restrict__ kv, int seq, int dim,
+// Threads and LDS of the stats kernels: one channel column per thread, then
+// the per-wave escape sums.
+__host__ __device__ constexpr int stats_threads(int dim) { return dim > 64 ? 128 : 64; }
+__host__ __device__ constexpr size_t stats_lds_bytes(int dim) {
+    return size_t(stats_threads(dim)) * kHistStride * sizeof(uint32_t) + 4 * sizeof(int);
+}
+
+__global__ __launch_bounds__(128) void encode_stats_kernel(const uint16_t *__restrict__ kv, int seq, int dim,
                                                                int bt, EncBlockMeta *__restrict__ meta,
                                                                uint8_t *__restrict__ bases) {
     const int b = int(blockIdx.x);
     const int t0 = b * bt;
     const EncRows src{kv + size_t(t0) * size_t(dim), kv + size_t(t0) * size_t(dim), 0};
-    __shared__ StatsLds L;
-    encode_stats_block(L, src, min(bt, seq - t0), dim, meta + b, bases + size_t(b) * 2 * size_t(dim));
+    extern __shared__ uint32_t stats_lds[];
+    encode_stats_block(stats_lds, reinterpret_cast<int *>(stats_lds + blockDim.x * kHistStride), src,
+                       min(bt, seq - t0), dim, meta + b, bases + size_t(b) * 2 * size_t(dim));
 }
 
-__global__ __launch_bounds__(kThreads) void append_stats_kernel(const AppendJobDev *__restrict__ jobs, int n_jobs,
+__global__ __launch_bounds__(128) void append_stats_kernel(const AppendJobDev *__restrict__ jobs, int n_jobs,
                                                                int dim, int bt, EncBlockMeta *__restrict__ meta,
                                                                uint8_t *__restrict__ bases) {
     const int g = int(blockIdx.x);
     const AppendJobDev j = jobs[find_job(jobs, n_jobs, g)];
     const int b = g - j.blk0;
-    __shared__ StatsLds L;
-    encode_stats_block(L, job_rows(j, b, bt, dim), min(bt, j.seq - b * bt), dim, meta + g,
+    extern __shared__ uint32_t stats_lds[];
+    encode_stats_block(stats_lds, reinterpret_cast<int *>(stats_lds + blockDim.x * kHistStride),
+                       job_rows(j, b, bt, dim), min(bt, j.seq - b * bt), dim, meta + g,
                        bases + size_t(g) * 2 * size_t(dim));
 }
 
@@ -575,7 +590,8 @@ hipError_t decode(const uint8_t *blob, uint64_t bytes, const int64_t *offs, cons
 hipError_t encode(const uint16_t *kv, int seq, int dim, int bt, int n_blocks, EncBlockMeta *meta, uint8_t *bases,
                   int64_t *offs, int32_t *first, uint8_t *out, uint32_t *status, hipStream_t s, bool rebase,
                   int tok0) {
-    hipLaunchKernelGGL(encode_stats_kernel, dim3(n_blocks), dim3(kThreads), 0, s, kv, seq, dim, bt, meta, bases);
+    hipLaunchKernelGGL(encode_stats_kernel, dim3(n_blocks), dim3(stats_threads(dim)), stats_lds_bytes(dim), s, kv, seq,
+                       dim, bt, meta, bases);
     hipLaunchKernelGGL(encode_scan_kernel, dim3(1), dim3(1024), 0, s, meta, n_blocks, bt, seq, offs, first,
                        rebase ? 1 : 0, tok0);
     hipLaunchKernelGGL(encode_write_kernel, dim3(n_blocks), dim3(kThreads), 0, s, kv, seq, dim, bt, meta, bases,
@@ -587,8 +603,8 @@ hipError_t append(const AppendJobDev *jobs, int n_jobs, int total_blocks, int di
                   uint8_t *bases, uint32_t *status, hipStream_t s) {
     if (n_jobs <= 0) return hipSuccess;
     if (total_blocks > 0)
-        hipLaunchKernelGGL(append_stats_kernel, dim3(total_blocks), dim3(kThreads), 0, s, jobs, n_jobs, dim, bt, meta,
-                           bases);
+        hipLaunchKernelGGL(append_stats_kernel, dim3(total_blocks), dim3(stats_threads(dim)), stats_lds_bytes(dim), s,
+                           jobs, n_jobs, dim, bt, meta, bases);
     hipLaunchKernelGGL(append_scan_kernel, dim3(n_jobs), dim3(1024), 0, s, jobs, meta, bt);
     if (total_blocks > 0)
         hipLaunchKernelGGL(append_write_kernel, dim3(total_blocks), dim3(kThreads), 0, s, jobs, n_jobs, dim, bt, meta,

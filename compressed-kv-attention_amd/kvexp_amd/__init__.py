@@ -46,6 +46,10 @@ class _AppendJob(C.Structure):
         ("index_capacity", C.c_int32), ("reserved", C.c_int32),
     ]
 
+    @classmethod
+    def _fields_offsets(cls):
+        return [(name, getattr(cls, name).offset) for name, _ in cls._fields_]
+
 
 class _Head(C.Structure):
     _fields_ = [
@@ -213,6 +217,47 @@ class Cache:
                        self.block)
 
 
+class AppendSet:
+    """A fixed list of caches (one dim and block size) appended together each
+    step, as a decode loop does: the kvexp_hip_append_job table is kept as a
+    numpy structured array with the C layout and updated in place, and the
+    new tokens come as one [n_caches, n, dim] BF16 device tensor."""
+
+    def __init__(self, ctx: "Context", caches: list):
+        import numpy as np
+
+        self.ctx, self.caches = ctx, list(caches)
+        c0 = self.caches[0]
+        self.dim, self.block = c0.dim, c0.block
+        dt = np.dtype({"names": ["d_new", "n_new", "n_tokens", "d_tail", "d_blob", "capacity", "d_offsets",
+                                 "d_first_token", "index_capacity", "reserved"],
+                       "formats": ["<u8", "<i4", "<i4", "<u8", "<u8", "<u8", "<u8", "<u8", "<i4", "<i4"],
+                       "offsets": [o for _, o in _AppendJob._fields_offsets()],
+                       "itemsize": C.sizeof(_AppendJob)})
+        j = np.zeros(len(self.caches), dtype=dt)
+        for i, c in enumerate(self.caches):
+            if c.dim != self.dim or c.block != self.block:
+                raise ValueError("AppendSet: caches of one dim and block size")
+            j[i] = (0, 0, c.seq, _ptr(c.tail), _ptr(c.blob), c.capacity, _ptr(c.offsets), _ptr(c.first),
+                    c.index_capacity, 0)
+        self.jobs = j
+        self._stride = np.arange(len(self.caches), dtype=np.uint64)
+
+    def append(self, tokens, n: int, check_errors: bool = False, stream=None) -> None:
+        """tokens: contiguous device tensor [n_caches, n, dim] of BF16 bits."""
+        import numpy as np
+
+        j = self.jobs
+        j["d_new"] = np.uint64(_ptr(tokens)) + self._stride * np.uint64(n * self.dim * 2)
+        j["n_new"] = n
+        check(lib().kvexp_hip_append_batch(self.ctx.h, C.cast(j.ctypes.data, C.POINTER(_AppendJob)), len(j),
+                                           self.dim, self.block, 1 if check_errors else 0, _stream(stream)))
+        j["n_tokens"] += n
+        for c in self.caches:
+            c.seq += n
+            c.nbytes = -1
+
+
 class Context:
     """One device context (workspace + status word)."""
 
@@ -256,6 +301,9 @@ class Context:
     def cache(self, dim: int, max_tokens: int, block: int = 128) -> "Cache":
         """An empty appendable container for up to max_tokens tokens."""
         return Cache(self, dim, max_tokens, block)
+
+    def append_set(self, caches: list) -> "AppendSet":
+        return AppendSet(self, caches)
 
     def append_batch(self, caches: list, tokens: list, n: int | list, check_errors: bool = False,
                      stream=None) -> None:

@@ -276,3 +276,29 @@ def test_append_batch(ctx, oracle):
             off, first = oracle.block_index(want, dim, pos[i])
             assert np.array_equal(c.view().offsets.cpu().numpy(), off), (rnd, i)
             assert np.array_equal(c.view().first.cpu().numpy(), first), (rnd, i)
+
+
+def test_append_set_steps(ctx, oracle):
+    """AppendSet (the job table kept between steps) over 24 decode steps of
+    one token per container plus one multi-token step, against encode_bf16."""
+    import torch
+
+    rng = np.random.default_rng(5)
+    dim, block, n_c, seq0, steps = 64, 128, 6, 250, 24
+    data = [_kinds(rng, seq0 + steps + 40, dim, i % 4).reshape(-1, dim) for i in range(n_c)]
+    caches = [ctx.cache(dim, seq0 + steps + 40, block) for _ in range(n_c)]
+    for c, d in zip(caches, data):
+        c.append(to_dev(d[:seq0].reshape(-1), torch.int16), seq0)
+    aset = ctx.append_set(caches)
+    pos = seq0
+    for step in list(range(steps)) + [-1]:
+        n = 1 if step >= 0 else 40
+        toks = to_dev(np.stack([d[pos:pos + n] for d in data]).reshape(-1), torch.int16)
+        aset.append(toks, n, check_errors=(step % 8 == 0))
+        pos += n
+    for i, (c, d) in enumerate(zip(caches, data)):
+        want = oracle.encode(d[:pos].reshape(-1), pos, dim, block)
+        nb = c.size()
+        say("append set", i, dict(tokens=pos, bytes=nb))
+        assert c.seq == pos and nb == want.size
+        assert np.array_equal(c.blob[:nb].cpu().numpy(), want), i
