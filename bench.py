@@ -151,6 +151,27 @@ def bench_append(a, torch, np, kvexp_amd, synth) -> int:
         n = c.size()
         same &= n == enc.nbytes and bool(torch.equal(c.blob[:n], enc.blob[:n]))
     log(f"decode-step append {step_ms * 1e3:.1f} us (wall {wall_ms * 1e3:.1f}), containers equal encode: {same}")
+    # attention over the grown containers: a plan is built per step in a
+    # decode loop; its creation time, and the output against a plan over
+    # freshly encoded copies of the same tokens
+    G = cfg["group"]
+    H = L * KV
+    q = torch.from_numpy(synth.queries("c2", H).view(np.int16)).to(dev)
+    splits = ctx.suggest_splits(H, n_tok, BT)
+    views = [c.view() for c in caches]
+    torch.cuda.synchronize()
+    t_plan = time.perf_counter()
+    plan = ctx.plan([dict(kx=views[2 * i], vx=views[2 * i + 1], seq=n_tok, splits=splits) for i in range(H)], G, D,
+                    BT)
+    plan_ms = (time.perf_counter() - t_plan) * 1e3
+    encs = [ctx.encode(t[: n_tok * D], n_tok, D, BT) for t in src]
+    plan2 = ctx.plan([dict(kx=encs[2 * i], vx=encs[2 * i + 1], seq=n_tok, splits=splits) for i in range(H)], G, D,
+                     BT)
+    o1 = plan.run(q, check_errors=True)
+    o2 = plan2.run(q, check_errors=True)
+    torch.cuda.synchronize()
+    attn_same = bool(torch.equal(o1.view(torch.int32), o2.view(torch.int32)))
+    log(f"plan over appended containers: created in {plan_ms:.2f} ms; attention equals fresh encode: {attn_same}")
 
     cpu = None
     if not a.no_cpu_baseline:
@@ -193,6 +214,8 @@ def bench_append(a, torch, np, kvexp_amd, synth) -> int:
         "wall_us_per_step": round(wall_ms * 1e3, 2),
         "prefill": {"us": round(pre_ms * 1e3, 2), "tokens_per_container": S, "input_GBps": round(pre_gbps, 2)},
         "containers_equal_encode": same,
+        "plan_create_ms": round(plan_ms, 3),
+        "attention_equal_fresh_encode": attn_same,
         "roofline": {"bound": "hbm", "achieved": round(algo / (pre_ms * 1e-3) / 1e9, 2), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(algo / (pre_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
                      "traffic": None, "kernel": "prefill append (stats + scan + write + tail launches)",
