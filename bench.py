@@ -87,7 +87,7 @@ def bench_append(a, torch, np, kvexp_amd, synth) -> int:
     dev = torch.device("cuda:0")
     ctx = kvexp_amd.Context(0)
     steps, warmup = a.steps, a.warmup
-    extra = steps + warmup + 1
+    extra = 2 * steps + warmup + 1  # warmup + timed append steps, then the decode-loop steps
     t0 = time.time()
     src, host = [], []
     for l in range(L):
@@ -173,6 +173,43 @@ def bench_append(a, torch, np, kvexp_amd, synth) -> int:
     attn_same = bool(torch.equal(o1.view(torch.int32), o2.view(torch.int32)))
     log(f"plan over appended containers: created in {plan_ms:.2f} ms; attention equals fresh encode: {attn_same}")
 
+    # decode loop: append one token to every container, re-target the plan,
+    # run the attention (the plan update is the fast path inside a block and
+    # a rebuild when a block starts)
+    def heads_at(seq):
+        out = []
+        for i in range(H):
+            kx, vx = caches[2 * i].view(), caches[2 * i + 1].view()
+            kx.nbytes = vx.nbytes = -1  # capacity stands in for the size
+            out.append(dict(kx=kx, vx=vx, seq=seq, splits=splits))
+        return out
+
+    loop_steps = min(steps, extra - warmup - steps - 1)
+    out = torch.empty(H * G * D, dtype=torch.float32, device=dev)
+    base = warmup + steps
+    plan.update(heads_at(S + base))  # byte counts become the capacities; then lengths only
+    torch.cuda.synchronize()
+    t_loop = time.perf_counter()
+    e0.record()
+    for i in range(base, base + loop_steps):
+        aset.append(one[i], 1)
+        plan.update_lengths(S + i + 1, BT)
+        plan.run(q, out)
+    e1.record()
+    torch.cuda.synchronize()
+    loop_ms = e0.elapsed_time(e1) / max(1, loop_steps)
+    loop_wall = (time.perf_counter() - t_loop) * 1e3 / max(1, loop_steps)
+    n_end = S + base + loop_steps
+    fresh = [ctx.encode(t[: n_end * D], n_end, D, BT) for t in src]
+    plan3 = ctx.plan([dict(kx=fresh[2 * i], vx=fresh[2 * i + 1], seq=n_end, splits=splits) for i in range(H)], G, D,
+                     BT)
+    o3 = plan3.run(q, check_errors=True)
+    plan.status()
+    torch.cuda.synchronize()
+    loop_same = bool(torch.equal(out.view(torch.int32), o3.view(torch.int32)))
+    log(f"decode loop (append + plan update + attention): {loop_ms * 1e3:.1f} us per step (wall "
+        f"{loop_wall * 1e3:.1f}) over {loop_steps} steps; last output equals fresh plan: {loop_same}")
+
     cpu = None
     if not a.no_cpu_baseline:
         try:
@@ -215,6 +252,9 @@ def bench_append(a, torch, np, kvexp_amd, synth) -> int:
         "prefill": {"us": round(pre_ms * 1e3, 2), "tokens_per_container": S, "input_GBps": round(pre_gbps, 2)},
         "containers_equal_encode": same,
         "plan_create_ms": round(plan_ms, 3),
+        "decode_loop_us_per_step": round(loop_ms * 1e3, 2),
+        "decode_loop_wall_us_per_step": round(loop_wall * 1e3, 2),
+        "decode_loop_equal_fresh_plan": loop_same,
         "attention_equal_fresh_encode": attn_same,
         "roofline": {"bound": "hbm", "achieved": round(algo / (pre_ms * 1e-3) / 1e9, 2), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(algo / (pre_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),

@@ -185,7 +185,8 @@ __device__ __forceinline__ void load_rows(const Cursor &c, int r0, int rows, uin
     // used): every load is unconditional, with the mode's layout picked by
     // uniform selects, so the registers need no merge before their use.
     constexpr int SM = Shape<D>::kSmRegs;
-    const int r = r0 + min(lane_id(), rows - 1);
+    // (rows <= 0 only past a plan's zero-token sentinel block: row r0 then)
+    const int r = r0 + max(0, min(lane_id(), rows - 1));
     const int mode = c.mode();
     const bool raw = mode == 0;
     // sign/mantissa bytes (or the first D raw bytes) of the row

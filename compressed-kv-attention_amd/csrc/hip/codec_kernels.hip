@@ -19,6 +19,7 @@
 // block's rows from the job's raw tail and new tokens in place, then store
 // the new trailing partial block's raw tokens for the next append.
 #include "kvexp_device.h"
+#include <algorithm>
 #include "kvexp_types.h"
 
 namespace kvexp_dev {
@@ -555,6 +556,94 @@ __global__ __launch_bounds__(kThreads) void esc_pos_kernel(const EscJob *__restr
     if (threadIdx.x == 0 && carry != h.n_escape) atomicOr(status, kStEscape);
 }
 
+// Plan update after appends. Workgroups [0, n_jobs), one per tensor: the
+// last block is checked against the index again and its descriptor and
+// escape positions are rewritten (blocks before it are unchanged by an
+// append); the entry after it becomes a zero-token sentinel (a split kernel
+// that reached it would stop there), and an index that ends before the
+// attended tokens raises kStIndex. The workgroups after them set each device
+// head's length and byte counts and the end of each head's last split from
+// the jobs (tensors 2h and 2h + 1 are the K and V of head h, which owns
+// device heads [h * per_head, (h + 1) * per_head)).
+__global__ __launch_bounds__(kThreads) void plan_refresh_kernel(const EscJob *__restrict__ jobs, int n_jobs,
+                                                               HeadDev *__restrict__ heads, int n_dev_heads,
+                                                               WorkItem *__restrict__ items, int n_items,
+                                                               int per_head, uint32_t *__restrict__ status) {
+    __shared__ int scan_tmp[kWaves];
+    __shared__ int ok_s;
+    if (int(blockIdx.x) >= n_jobs) {
+        const int i = (int(blockIdx.x) - n_jobs) * kThreads + int(threadIdx.x);
+        if (i < n_dev_heads) {
+            const int h = i / per_head;
+            heads[i].seq = jobs[2 * h].seq;
+            heads[i].kbytes = jobs[2 * h].bytes;
+            heads[i].vbytes = jobs[2 * h + 1].bytes;
+        }
+        if (i < n_items) {
+            WorkItem &w = items[i];
+            const int h = w.head / per_head;
+            if (w.split == heads[w.head].n_splits - 1) w.tok_end = jobs[2 * h].seq;
+        }
+        return;
+    }
+    const EscJob j = jobs[blockIdx.x];
+    const int b = j.n_blocks - 1;
+    const int dim = j.dim;
+    const int64_t off = j.offs[b];
+    const int e0 = j.esc0[b];
+    if (threadIdx.x == 0) {
+        BlockHdr h{};
+        uint32_t st = check_block(j.blob, j.bytes, off, dim, j.first[b + 1] - j.first[b], &h);
+        const int ne = st != 0u || h.mode == 0 ? 0 : h.n_escape;
+        if (st == 0u && e0 + ne > j.pos_cap) st = kStEscape;
+        if (j.first[j.n_blocks] < j.seq) st |= kStIndex;
+        BlockDesc d{};
+        d.data = j.blob + off;
+        d.esc = j.pos + e0;
+        d.meta = st != 0u ? 0u : uint32_t(h.mode) | (uint32_t(h.n_tokens) << 8) | (uint32_t(ne) << 16);
+        j.desc[b] = d;
+        BlockDesc z{};
+        z.data = j.blob;
+        z.esc = j.pos;
+        j.desc[b + 1] = z;
+        j.esc0[b + 1] = e0 + ne;
+        if (st != 0u) atomicOr(status, st);
+        ok_s = st == 0u && ne > 0;
+    }
+    __syncthreads();
+    if (!ok_s) return;
+    const BlockHdr h = read_hdr(j.blob + off);
+    const bool four = h.mode == 4;
+    const uint8_t *codes = j.blob + off + 8 + dim + size_t(h.n_tokens) * size_t(dim);
+    uint16_t *pos = j.pos + e0;
+    const int units = (h.n_tokens * dim) / 4;
+    int carry = 0;
+    for (int r = 0; r < units; r += kThreads) {
+        const int u = r + int(threadIdx.x);
+        const bool act = u < units;
+        uint32_t cw = 0;
+        int cnt = 0;
+        if (act) {
+            cw = four ? load_u16_any(codes + 2 * size_t(u)) : uint32_t(codes[u]);
+            cnt = four ? sentinels4(cw) : sentinels2(cw);
+        }
+        int tot = 0;
+        int rank = carry + block_excl_scan<kWaves>(cnt, scan_tmp, &tot);
+        carry += tot;
+        if (act && cnt) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const uint32_t code = four ? (cw >> (4 * k)) & 15u : (cw >> (2 * k)) & 3u;
+                if (code == (four ? 15u : 3u)) {
+                    if (rank < h.n_escape) pos[rank] = uint16_t(4 * u + k);
+                    ++rank;
+                }
+            }
+        }
+    }
+    if (threadIdx.x == 0 && carry != h.n_escape) atomicOr(status, kStEscape);
+}
+
 // y = expf(x) in the forms the attention kernels evaluate it (all must equal
 // glibc): thread % 3 == 0 the branching special cases with the constant-memory
 // table, 1 the branch-free form with the table copied to LDS, 2 the
@@ -616,6 +705,15 @@ hipError_t append(const AppendJobDev *jobs, int n_jobs, int total_blocks, int di
 hipError_t esc_start(const EscJob *jobs, int n_jobs, uint32_t *status, hipStream_t s) {
     if (n_jobs <= 0) return hipSuccess;
     hipLaunchKernelGGL(esc_start_kernel, dim3(n_jobs), dim3(kThreads), 0, s, jobs, status);
+    return hipGetLastError();
+}
+
+hipError_t plan_refresh(const EscJob *jobs, int n_jobs, HeadDev *heads, int n_dev_heads, WorkItem *items,
+                        int n_items, int per_head, uint32_t *status, hipStream_t s) {
+    const int extra = (std::max(n_dev_heads, n_items) + kThreads - 1) / kThreads;
+    if (n_jobs + extra <= 0) return hipSuccess;
+    hipLaunchKernelGGL(plan_refresh_kernel, dim3(n_jobs + extra), dim3(kThreads), 0, s, jobs, n_jobs, heads,
+                       n_dev_heads, items, n_items, per_head, status);
     return hipGetLastError();
 }
 

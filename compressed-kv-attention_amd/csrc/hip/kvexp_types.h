@@ -57,6 +57,8 @@ struct EscJob {
     BlockDesc *desc;      // out: n_blocks entries (nullable)
     int32_t n_blocks;
     int32_t dim;
+    int32_t pos_cap;      // entries of `pos` (the tensor's escapes plus room for its last block to grow)
+    int32_t seq;          // tokens a plan update attends (esc_tail_kernel checks the index covers them)
 };
 
 // One split: tokens [tok_begin, tok_end) of a head; for XKV the blocks that

@@ -39,6 +39,8 @@ size_t attention_lds_bytes(int dim);
 hipError_t expf(const float *x, float *y, size_t n, hipStream_t s);
 hipError_t esc_start(const kvexp_dev::EscJob *jobs, int n_jobs, uint32_t *status, hipStream_t s);
 hipError_t esc_pos(const kvexp_dev::EscJob *jobs, const int2 *blocks, int n_blocks, uint32_t *status, hipStream_t s);
+hipError_t plan_refresh(const kvexp_dev::EscJob *jobs, int n_jobs, HeadDev *heads, int n_dev_heads, WorkItem *items,
+                        int n_items, int per_head, uint32_t *status, hipStream_t s);
 bool wave_supports(int dim);
 hipError_t attention_wave(bool xkv, int order, int G, int dim, const HeadDev *heads, const WorkItem *items,
                           int n_items, const uint16_t *q, float *out, float *lse, float *ws, hipStream_t s);
@@ -194,12 +196,24 @@ struct kvexp_hip_ctx {
     DevBuf enc_meta, enc_bases, enc_off, enc_first, app_jobs;
     size_t enc_meta_cap = 0, enc_bases_cap = 0, enc_index_cap = 0, app_jobs_cap = 0;
     int cu_count = 0;
+    // pinned host staging for the plan builder's reads of block indexes
+    std::mutex pinned_mu;
+    void *pinned = nullptr;
+    size_t pinned_cap = 0;
+    ~kvexp_hip_ctx() {
+        if (pinned) (void)hipHostFree(pinned);
+    }
 };
 
 struct kvexp_hip_plan {
     kvexp_hip_ctx *ctx = nullptr;
-    int n_heads = 0, n_q = 0, dim = 0, order = 0;
+    int n_heads = 0, n_q = 0, dim = 0, order = 0, split_tokens = 0;
     bool xkv = false;
+    // what kvexp_hip_plan_update needs: the heads as given and the per-tensor
+    // escape-index jobs (host copy and device copy)
+    std::vector<kvexp_hip_head> src;
+    std::vector<kvexp_dev::EscJob> jobs;
+    DevBuf djobs;
     bool wave = false; // one-wave-per-split kernel (dim 64 or 128)
     DevBuf heads, items, merge_ids, ws, status;
     // wave kernel: merge work (head, row), escape-position index, block descriptors
@@ -278,6 +292,9 @@ void build_escape_index(kvexp_hip_plan &p, const kvexp_hip_head *heads, int n_he
     }
     p.esc0 = DevBuf(e0_total * sizeof(int32_t));
     p.desc = DevBuf(e0_total * sizeof(kvexp_dev::BlockDesc));
+    // HIP memory is not zeroed: the entry after each tensor's last block is
+    // the zero-token sentinel until a plan update writes it again
+    HIPX(hipMemset(p.desc.p, 0, e0_total * sizeof(kvexp_dev::BlockDesc)));
     for (size_t i = 0; i < jobs.size(); ++i) {
         jobs[i].esc0 = p.esc0.as<int32_t>() + e0_at[i];
         jobs[i].desc = p.desc.as<kvexp_dev::BlockDesc>() + e0_at[i];
@@ -293,12 +310,16 @@ void build_escape_index(kvexp_hip_plan &p, const kvexp_hip_head *heads, int n_he
     check_status_word(st, nullptr);
     std::vector<int32_t> e0(e0_total);
     HIPX(hipMemcpy(e0.data(), p.esc0.p, e0_total * sizeof(int32_t), hipMemcpyDeviceToHost));
+    // each tensor's positions, then room for its last block to grow to the
+    // largest block the format allows (255 tokens) after appends
     size_t pos_total = 0;
     std::vector<size_t> pos_at;
     std::vector<int2> blocks;
     for (size_t i = 0; i < jobs.size(); ++i) {
         pos_at.push_back(pos_total);
-        pos_total += size_t(e0[e0_at[i] + size_t(jobs[i].n_blocks)]);
+        const size_t own = size_t(e0[e0_at[i] + size_t(jobs[i].n_blocks)]);
+        jobs[i].pos_cap = int32_t(own + size_t(255) * size_t(dim));
+        pos_total += size_t(jobs[i].pos_cap);
         for (int b = 0; b < jobs[i].n_blocks; ++b) blocks.push_back(make_int2(int(i), b));
     }
     p.escpos = DevBuf(std::max<size_t>(pos_total, 1) * sizeof(uint16_t));
@@ -311,6 +332,8 @@ void build_escape_index(kvexp_hip_plan &p, const kvexp_hip_head *heads, int n_he
     HIPX(kvexp_launch::esc_pos(djobs.as<kvexp_dev::EscJob>(), dblocks.as<int2>(), int(blocks.size()), st, nullptr));
     HIPX(hipDeviceSynchronize());
     check_status_word(st, nullptr);
+    p.jobs = jobs;
+    p.djobs = std::move(djobs);
     const int per_head = (n_q + kMaxQPerLaunch - 1) / kMaxQPerLaunch;
     for (int h = 0; h < n_heads; ++h) {
         for (int c = 0; c < per_head; ++c) {
@@ -624,6 +647,159 @@ int kvexp_hip_suggest_splits(kvexp_hip_ctx *ctx, int n_heads, int seq, int split
     return std::max(1, std::min(tiles, target));
 }
 
+namespace {
+
+// Builds (or rebuilds) every device-side part of a plan from its heads: work
+// items (token_bounds splits, split starts checked against the block index),
+// device heads, merge work, and for the one-wave kernel the block descriptors
+// and escape-position index.
+void plan_build(kvexp_hip_plan *p, const kvexp_hip_head *heads, int n_heads) {
+    kvexp_hip_ctx *ctx = p->ctx;
+    const int n_q = p->n_q, dim = p->dim, split_tokens = p->split_tokens;
+    const bool xkv = heads[0].k_xkv != nullptr;
+    std::vector<HeadDev> hv;
+    std::vector<WorkItem> items;
+    std::vector<int32_t> merge;
+    int ws_slots = 0;
+    // every XKV head's block first tokens, read with one synchronisation
+    std::vector<size_t> first_at(size_t(n_heads) * 2, 0);
+    std::vector<int32_t> firsts;
+    const int32_t *first_all = nullptr;
+    if (xkv) {
+        std::lock_guard<std::mutex> lock(ctx->pinned_mu);
+        size_t total = 0;
+        for (int h = 0; h < n_heads; ++h) {
+            const kvexp_hip_head &H = heads[h];
+            if (H.k_xkv == nullptr || H.k_offsets == nullptr || H.v_offsets == nullptr ||
+                H.k_first_token == nullptr || H.v_first_token == nullptr || H.k_n_blocks <= 0 || H.v_n_blocks <= 0)
+                break; // reported below, head by head
+            first_at[size_t(2 * h)] = total;
+            total += size_t(H.k_n_blocks) + 1;
+            first_at[size_t(2 * h + 1)] = total;
+            total += size_t(H.v_n_blocks) + 1;
+        }
+        if (total * 4 > ctx->pinned_cap) {
+            if (ctx->pinned) HIPX(hipHostFree(ctx->pinned));
+            ctx->pinned = nullptr;
+            ctx->pinned_cap = 0;
+            HIPX(hipHostMalloc(&ctx->pinned, total * 4, hipHostMallocDefault));
+            ctx->pinned_cap = total * 4;
+        }
+        int32_t *host = static_cast<int32_t *>(ctx->pinned);
+        for (int h = 0; h < n_heads; ++h) {
+            const kvexp_hip_head &H = heads[h];
+            if (H.k_xkv == nullptr || H.k_offsets == nullptr || H.v_offsets == nullptr ||
+                H.k_first_token == nullptr || H.v_first_token == nullptr || H.k_n_blocks <= 0 || H.v_n_blocks <= 0)
+                break;
+            HIPX(hipMemcpyAsync(host + first_at[size_t(2 * h)], H.k_first_token, (size_t(H.k_n_blocks) + 1) * 4,
+                                hipMemcpyDeviceToHost, nullptr));
+            HIPX(hipMemcpyAsync(host + first_at[size_t(2 * h + 1)], H.v_first_token, (size_t(H.v_n_blocks) + 1) * 4,
+                                hipMemcpyDeviceToHost, nullptr));
+        }
+        HIPX(hipStreamSynchronize(nullptr));
+        firsts.assign(host, host + total);
+        first_all = firsts.data();
+    }
+    for (int h = 0; h < n_heads; ++h) {
+        const kvexp_hip_head &H = heads[h];
+        const bool raw = H.k_raw != nullptr, x = H.k_xkv != nullptr;
+        if (H.seq <= 0) fail(KVEXP_HIP_INVALID_ARGUMENT, "attention_decode: bad argument");
+        if (raw == x || (H.v_raw != nullptr) != raw || (H.v_xkv != nullptr) != x)
+            fail(KVEXP_HIP_INVALID_ARGUMENT, "attention_decode: pass raw K and V or xkv K and V, not both");
+        if (x != xkv) fail(KVEXP_HIP_UNSUPPORTED, "kvexp_hip_plan_create: one plan holds raw or XKV heads, not both");
+        const int ntiles = (H.seq + split_tokens - 1) / split_tokens;
+        const int n_splits = std::min(std::max(1, H.n_splits), ntiles);
+        if (x) {
+            if (H.k_offsets == nullptr || H.v_offsets == nullptr || H.k_first_token == nullptr ||
+                H.v_first_token == nullptr || H.k_n_blocks <= 0 || H.v_n_blocks <= 0)
+                fail(KVEXP_HIP_INVALID_ARGUMENT, "kvexp_hip_plan_create: XKV head without a block index");
+        }
+        const int32_t *kf0 = x ? first_all + first_at[size_t(2 * h)] : nullptr;
+        const int32_t *vf0 = x ? first_all + first_at[size_t(2 * h + 1)] : nullptr;
+        const int32_t *kf1 = x ? kf0 + H.k_n_blocks : nullptr; // last entry: tokens covered
+        const int32_t *vf1 = x ? vf0 + H.v_n_blocks : nullptr;
+        if (x && (*kf1 < H.seq || *vf1 < H.seq)) fail(KVEXP_HIP_FORMAT_ERROR, "xkv ran out of tokens");
+        // query rows in groups of <= 8 per device head, same splits
+        for (int q0 = 0; q0 < n_q; q0 += kMaxQPerLaunch) {
+            HeadDev d{};
+            d.kx = H.k_xkv;
+            d.vx = H.v_xkv;
+            d.kbytes = H.k_bytes;
+            d.vbytes = H.v_bytes;
+            d.koff = H.k_offsets;
+            d.voff = H.v_offsets;
+            d.kfirst = H.k_first_token;
+            d.vfirst = H.v_first_token;
+            d.kraw = H.k_raw;
+            d.vraw = H.v_raw;
+            d.seq = H.seq;
+            d.n_splits = n_splits;
+            d.ws_base = ws_slots;
+            d.q_row = h * n_q + q0;
+            d.n_q = std::min(kMaxQPerLaunch, n_q - q0);
+            const int dh = int(hv.size());
+            for (int sp = 0; sp < n_splits; ++sp) {
+                WorkItem wi{};
+                wi.head = dh;
+                wi.split = sp;
+                token_bounds(H.seq, split_tokens, sp, n_splits, wi.tok_begin, wi.tok_end);
+                wi.kblk = wi.vblk = -1;
+                if (x) {
+                    const int32_t *kit = std::lower_bound(kf0, kf1, wi.tok_begin);
+                    const int32_t *vit = std::lower_bound(vf0, vf1, wi.tok_begin);
+                    if (kit == kf1 || *kit != wi.tok_begin || vit == vf1 || *vit != wi.tok_begin)
+                        fail(KVEXP_HIP_FORMAT_ERROR, "token split is not aligned to an encoded block");
+                    wi.kblk = int(kit - kf0);
+                    wi.vblk = int(vit - vf0);
+                }
+                items.push_back(wi);
+            }
+            if (n_splits > 1) {
+                merge.push_back(dh);
+                ws_slots += n_splits;
+            }
+            hv.push_back(d);
+        }
+    }
+    p->xkv = xkv;
+    p->wave = kvexp_launch::wave_supports(dim);
+    p->n_dev_heads = int(hv.size());
+    p->n_items = int(items.size());
+    p->n_merge = int(merge.size());
+    if (p->wave) {
+        // items grouped by G (one launch per distinct G)
+        std::stable_sort(items.begin(), items.end(), [&](const WorkItem &a, const WorkItem &b) {
+            return hv[size_t(a.head)].n_q < hv[size_t(b.head)].n_q;
+        });
+        for (int G = 0; G <= 8; ++G)
+            p->group_start[G + 1] =
+                int(std::count_if(items.begin(), items.end(),
+                                  [&](const WorkItem &w) { return hv[size_t(w.head)].n_q <= G; }));
+        std::vector<int2> mi;
+        for (int32_t dh : merge)
+            for (int g = 0; g < hv[size_t(dh)].n_q; ++g) mi.push_back(make_int2(dh, g));
+        p->n_mitems = int(mi.size());
+        p->mitems = DevBuf(std::max<size_t>(1, mi.size()) * sizeof(int2));
+        if (!mi.empty())
+            HIPX(hipMemcpy(p->mitems.p, mi.data(), mi.size() * sizeof(int2), hipMemcpyHostToDevice));
+        if (xkv) build_escape_index(*p, heads, n_heads, n_q, dim, hv);
+    }
+    p->heads = DevBuf(hv.size() * sizeof(HeadDev));
+    p->items = DevBuf(items.size() * sizeof(WorkItem));
+    p->merge_ids = DevBuf(std::max<size_t>(1, merge.size()) * sizeof(int32_t));
+    const size_t slot_floats = size_t(kMaxQPerLaunch) * size_t(dim + 2);
+    p->ws = DevBuf(std::max<size_t>(1, size_t(ws_slots)) * slot_floats * sizeof(float));
+    p->status = DevBuf(sizeof(uint32_t));
+    HIPX(hipMemcpy(p->heads.p, hv.data(), hv.size() * sizeof(HeadDev), hipMemcpyHostToDevice));
+    HIPX(hipMemcpy(p->items.p, items.data(), items.size() * sizeof(WorkItem), hipMemcpyHostToDevice));
+    if (!merge.empty())
+        HIPX(hipMemcpy(p->merge_ids.p, merge.data(), merge.size() * sizeof(int32_t), hipMemcpyHostToDevice));
+    HIPX(hipMemset(p->status.p, 0, sizeof(uint32_t)));
+    p->src.assign(heads, heads + n_heads);
+}
+
+} // namespace
+
 int kvexp_hip_plan_create(kvexp_hip_ctx *ctx, const kvexp_hip_head *heads, int n_heads, int n_q, int dim,
                           int split_tokens, int order, kvexp_hip_plan **out) {
     return guarded([&] {
@@ -639,76 +815,6 @@ int kvexp_hip_plan_create(kvexp_hip_ctx *ctx, const kvexp_hip_head *heads, int n
         if (order == KVEXP_HIP_ORDER_DPBF16 && (dim % 32 != 0 || dim > kMaxDim))
             fail(KVEXP_HIP_INVALID_ARGUMENT, "avx512 attention: head_dim must be a multiple of 32");
         DeviceGuard g(ctx->device);
-
-        const bool xkv = heads[0].k_xkv != nullptr;
-        std::vector<HeadDev> hv;
-        std::vector<WorkItem> items;
-        std::vector<int32_t> merge;
-        int ws_slots = 0;
-        std::vector<int32_t> kfirst, vfirst;
-        for (int h = 0; h < n_heads; ++h) {
-            const kvexp_hip_head &H = heads[h];
-            const bool raw = H.k_raw != nullptr, x = H.k_xkv != nullptr;
-            if (H.seq <= 0) fail(KVEXP_HIP_INVALID_ARGUMENT, "attention_decode: bad argument");
-            if (raw == x || (H.v_raw != nullptr) != raw || (H.v_xkv != nullptr) != x)
-                fail(KVEXP_HIP_INVALID_ARGUMENT, "attention_decode: pass raw K and V or xkv K and V, not both");
-            if (x != xkv) fail(KVEXP_HIP_UNSUPPORTED, "kvexp_hip_plan_create: one plan holds raw or XKV heads, not both");
-            const int ntiles = (H.seq + split_tokens - 1) / split_tokens;
-            const int n_splits = std::min(std::max(1, H.n_splits), ntiles);
-            if (x) {
-                if (H.k_offsets == nullptr || H.v_offsets == nullptr || H.k_first_token == nullptr ||
-                    H.v_first_token == nullptr || H.k_n_blocks <= 0 || H.v_n_blocks <= 0)
-                    fail(KVEXP_HIP_INVALID_ARGUMENT, "kvexp_hip_plan_create: XKV head without a block index");
-                kfirst.resize(size_t(H.k_n_blocks) + 1);
-                vfirst.resize(size_t(H.v_n_blocks) + 1);
-                HIPX(hipMemcpy(kfirst.data(), H.k_first_token, kfirst.size() * 4, hipMemcpyDeviceToHost));
-                HIPX(hipMemcpy(vfirst.data(), H.v_first_token, vfirst.size() * 4, hipMemcpyDeviceToHost));
-                if (kfirst.back() < H.seq || vfirst.back() < H.seq)
-                    fail(KVEXP_HIP_FORMAT_ERROR, "xkv ran out of tokens");
-            }
-            // query rows in groups of <= 8 per device head, same splits
-            for (int q0 = 0; q0 < n_q; q0 += kMaxQPerLaunch) {
-                HeadDev d{};
-                d.kx = H.k_xkv;
-                d.vx = H.v_xkv;
-                d.kbytes = H.k_bytes;
-                d.vbytes = H.v_bytes;
-                d.koff = H.k_offsets;
-                d.voff = H.v_offsets;
-                d.kfirst = H.k_first_token;
-                d.vfirst = H.v_first_token;
-                d.kraw = H.k_raw;
-                d.vraw = H.v_raw;
-                d.seq = H.seq;
-                d.n_splits = n_splits;
-                d.ws_base = ws_slots;
-                d.q_row = h * n_q + q0;
-                d.n_q = std::min(kMaxQPerLaunch, n_q - q0);
-                const int dh = int(hv.size());
-                for (int sp = 0; sp < n_splits; ++sp) {
-                    WorkItem wi{};
-                    wi.head = dh;
-                    wi.split = sp;
-                    token_bounds(H.seq, split_tokens, sp, n_splits, wi.tok_begin, wi.tok_end);
-                    wi.kblk = wi.vblk = -1;
-                    if (x) {
-                        auto kit = std::lower_bound(kfirst.begin(), kfirst.end() - 1, wi.tok_begin);
-                        auto vit = std::lower_bound(vfirst.begin(), vfirst.end() - 1, wi.tok_begin);
-                        if (kit == kfirst.end() - 1 || *kit != wi.tok_begin || vit == vfirst.end() - 1 ||
-                            *vit != wi.tok_begin)
-                            fail(KVEXP_HIP_FORMAT_ERROR, "token split is not aligned to an encoded block");
-                        wi.kblk = int(kit - kfirst.begin());
-                        wi.vblk = int(vit - vfirst.begin());
-                    }
-                    items.push_back(wi);
-                }
-                if (n_splits > 1) {
-                    merge.push_back(dh);
-                    ws_slots += n_splits;
-                }
-                hv.push_back(d);
-            }
-        }
         auto *p = new kvexp_hip_plan();
         try {
             p->ctx = ctx;
@@ -716,45 +822,67 @@ int kvexp_hip_plan_create(kvexp_hip_ctx *ctx, const kvexp_hip_head *heads, int n
             p->n_q = n_q;
             p->dim = dim;
             p->order = order;
-            p->xkv = xkv;
-            p->wave = kvexp_launch::wave_supports(dim);
-            p->n_dev_heads = int(hv.size());
-            p->n_items = int(items.size());
-            p->n_merge = int(merge.size());
-            if (p->wave) {
-                // items grouped by G (one launch per distinct G)
-                std::stable_sort(items.begin(), items.end(), [&](const WorkItem &a, const WorkItem &b) {
-                    return hv[size_t(a.head)].n_q < hv[size_t(b.head)].n_q;
-                });
-                for (int G = 0; G <= 8; ++G)
-                    p->group_start[G + 1] =
-                        int(std::count_if(items.begin(), items.end(),
-                                          [&](const WorkItem &w) { return hv[size_t(w.head)].n_q <= G; }));
-                std::vector<int2> mi;
-                for (int32_t dh : merge)
-                    for (int g = 0; g < hv[size_t(dh)].n_q; ++g) mi.push_back(make_int2(dh, g));
-                p->n_mitems = int(mi.size());
-                p->mitems = DevBuf(std::max<size_t>(1, mi.size()) * sizeof(int2));
-                if (!mi.empty())
-                    HIPX(hipMemcpy(p->mitems.p, mi.data(), mi.size() * sizeof(int2), hipMemcpyHostToDevice));
-                if (xkv) build_escape_index(*p, heads, n_heads, n_q, dim, hv);
-            }
-            p->heads = DevBuf(hv.size() * sizeof(HeadDev));
-            p->items = DevBuf(items.size() * sizeof(WorkItem));
-            p->merge_ids = DevBuf(std::max<size_t>(1, merge.size()) * sizeof(int32_t));
-            const size_t slot_floats = size_t(kMaxQPerLaunch) * size_t(dim + 2);
-            p->ws = DevBuf(std::max<size_t>(1, size_t(ws_slots)) * slot_floats * sizeof(float));
-            p->status = DevBuf(sizeof(uint32_t));
-            HIPX(hipMemcpy(p->heads.p, hv.data(), hv.size() * sizeof(HeadDev), hipMemcpyHostToDevice));
-            HIPX(hipMemcpy(p->items.p, items.data(), items.size() * sizeof(WorkItem), hipMemcpyHostToDevice));
-            if (!merge.empty())
-                HIPX(hipMemcpy(p->merge_ids.p, merge.data(), merge.size() * sizeof(int32_t), hipMemcpyHostToDevice));
-            HIPX(hipMemset(p->status.p, 0, sizeof(uint32_t)));
+            p->split_tokens = split_tokens;
+            plan_build(p, heads, n_heads);
         } catch (...) {
             delete p;
             throw;
         }
         *out = p;
+    });
+}
+
+// After appends: the same heads with new lengths. The split partition is
+// unchanged unless a head gains a split tile or a block; then (every
+// block_tokens tokens of a decode loop) the plan is built again. Otherwise
+// only the last split of each head ends later, and only the last block of
+// each container changed (kvexp_hip_append rewrites nothing before it): its
+// descriptor and escape positions are rewritten on the GPU, the device heads
+// and work items are uploaded again, all on `stream`.
+int kvexp_hip_plan_update(kvexp_hip_plan *plan, const kvexp_hip_head *heads, int n_heads, void *stream) {
+    return guarded([&] {
+        if (plan == nullptr || heads == nullptr) fail(KVEXP_HIP_INVALID_ARGUMENT, "attention_decode: bad argument");
+        if (n_heads != plan->n_heads)
+            fail(KVEXP_HIP_INVALID_ARGUMENT, "kvexp_hip_plan_update: the heads of the plan, with new lengths");
+        DeviceGuard g(plan->ctx->device);
+        hipStream_t s = static_cast<hipStream_t>(stream);
+        const int st = plan->split_tokens;
+        bool fast = plan->wave || !plan->xkv;
+        for (int h = 0; h < n_heads; ++h) {
+            const kvexp_hip_head &a = heads[h], &b = plan->src[size_t(h)];
+            if (a.k_xkv != b.k_xkv || a.v_xkv != b.v_xkv || a.k_raw != b.k_raw || a.v_raw != b.v_raw ||
+                a.k_offsets != b.k_offsets || a.v_offsets != b.v_offsets || a.k_first_token != b.k_first_token ||
+                a.v_first_token != b.v_first_token || a.n_splits != b.n_splits)
+                fail(KVEXP_HIP_INVALID_ARGUMENT, "kvexp_hip_plan_update: the heads of the plan, with new lengths");
+            if (a.seq <= 0) fail(KVEXP_HIP_INVALID_ARGUMENT, "attention_decode: bad argument");
+            if ((a.seq + st - 1) / st != (b.seq + st - 1) / st || a.k_n_blocks != b.k_n_blocks ||
+                a.v_n_blocks != b.v_n_blocks)
+                fast = false;
+        }
+        if (!fast) {
+            HIPX(hipStreamSynchronize(s)); // runs in flight still read the old buffers
+            plan_build(plan, heads, n_heads);
+            return;
+        }
+        // the device heads' lengths and byte counts and the last splits' ends
+        // are set on the GPU from the jobs, with the last blocks' descriptors
+        const int per_head = (plan->n_q + kMaxQPerLaunch - 1) / kMaxQPerLaunch;
+        if (plan->jobs.size() != size_t(2 * n_heads)) {
+            plan->jobs.assign(size_t(2 * n_heads), kvexp_dev::EscJob{});
+            plan->djobs = DevBuf(plan->jobs.size() * sizeof(kvexp_dev::EscJob));
+        }
+        for (int h = 0; h < n_heads; ++h)
+            for (int kv = 0; kv < 2; ++kv) {
+                kvexp_dev::EscJob &j = plan->jobs[size_t(2 * h + kv)];
+                j.bytes = kv ? heads[h].v_bytes : heads[h].k_bytes;
+                j.seq = heads[h].seq;
+            }
+        HIPX(hipMemcpyAsync(plan->djobs.p, plan->jobs.data(), plan->jobs.size() * sizeof(kvexp_dev::EscJob),
+                            hipMemcpyHostToDevice, s));
+        HIPX(kvexp_launch::plan_refresh(plan->djobs.as<kvexp_dev::EscJob>(), plan->xkv ? int(plan->jobs.size()) : 0,
+                                        plan->heads.as<HeadDev>(), plan->n_dev_heads, plan->items.as<WorkItem>(),
+                                        plan->n_items, per_head, plan->status.as<uint32_t>(), s));
+        plan->src.assign(heads, heads + n_heads);
     });
 }
 

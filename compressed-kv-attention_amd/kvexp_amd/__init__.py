@@ -101,6 +101,7 @@ def lib() -> C.CDLL:
     L.kvexp_hip_append_batch.argtypes = [vp, C.POINTER(_AppendJob), i32, i32, i32, i32, vp]
     L.kvexp_hip_plan_create.argtypes = [vp, C.POINTER(_Head), i32, i32, i32, i32, i32, C.POINTER(vp)]
     L.kvexp_hip_plan_destroy.argtypes = [vp]
+    L.kvexp_hip_plan_update.argtypes = [vp, C.POINTER(_Head), i32, vp]
     L.kvexp_hip_suggest_splits.argtypes = [vp, i32, i32, i32]
     L.kvexp_hip_attention_run.argtypes = [vp, vp, vp, vp, i32, vp]
     L.kvexp_hip_plan_status.argtypes = [vp, vp]
@@ -345,27 +346,15 @@ class Context:
     # attention --------------------------------------------------------------
     def plan(self, heads: list, n_q: int, dim: int, split: int = 128, order: int = ORDER_SCALAR) -> "Plan":
         """heads: dicts with 'seq', 'splits' and either 'k'/'v' (raw device tensors) or
-        'kx'/'vx' (Encoded)."""
-        arr = (_Head * len(heads))()
-        keep = []
-        for i, h in enumerate(heads):
-            H = arr[i]
-            H.seq = int(h["seq"])
-            H.n_splits = int(h.get("splits", 1))
-            if "kx" in h:
-                kx, vx = h["kx"], h["vx"]
-                keep += [kx, vx]
-                H.k_xkv, H.v_xkv = _ptr(kx.blob), _ptr(vx.blob)
-                H.k_bytes, H.v_bytes = kx.nbytes, vx.nbytes
-                H.k_offsets, H.v_offsets = _ptr(kx.offsets), _ptr(vx.offsets)
-                H.k_first_token, H.v_first_token = _ptr(kx.first), _ptr(vx.first)
-                H.k_n_blocks, H.v_n_blocks = kx.n_blocks, vx.n_blocks
-            else:
-                keep += [h["k"], h["v"]]
-                H.k_raw, H.v_raw = _ptr(h["k"]), _ptr(h["v"])
+        'kx'/'vx' (Encoded; a Cache.view() whose size was not read back passes
+        its capacity as the byte count)."""
+        arr, keep = _heads_array(heads)
         p = C.c_void_p()
         check(lib().kvexp_hip_plan_create(self.h, arr, len(heads), n_q, dim, split, order, C.byref(p)))
-        return Plan(self, p, len(heads), n_q, dim, keep)
+        plan = Plan(self, p, len(heads), n_q, dim, keep)
+        plan._arr = arr
+        plan._caps = [(h["kx"].blob.numel(), h["vx"].blob.numel()) if "kx" in h else (0, 0) for h in heads]
+        return plan
 
     def expf(self, x, out=None, stream=None):
         import torch
@@ -398,9 +387,63 @@ class Context:
         return out[: n_q * dim]
 
 
+def _heads_array(heads: list):
+    arr = (_Head * len(heads))()
+    keep = []
+    for i, h in enumerate(heads):
+        H = arr[i]
+        H.seq = int(h["seq"])
+        H.n_splits = int(h.get("splits", 1))
+        if "kx" in h:
+            kx, vx = h["kx"], h["vx"]
+            keep += [kx, vx]
+            H.k_xkv, H.v_xkv = _ptr(kx.blob), _ptr(vx.blob)
+            H.k_bytes = kx.nbytes if kx.nbytes >= 0 else kx.blob.numel()
+            H.v_bytes = vx.nbytes if vx.nbytes >= 0 else vx.blob.numel()
+            H.k_offsets, H.v_offsets = _ptr(kx.offsets), _ptr(vx.offsets)
+            H.k_first_token, H.v_first_token = _ptr(kx.first), _ptr(vx.first)
+            H.k_n_blocks, H.v_n_blocks = kx.n_blocks, vx.n_blocks
+        else:
+            keep += [h["k"], h["v"]]
+            H.k_raw, H.v_raw = _ptr(h["k"]), _ptr(h["v"])
+    return arr, keep
+
+
 class Plan:
     def __init__(self, ctx: Context, h, n_heads: int, n_q: int, dim: int, keep):
         self.ctx, self.h, self.n_heads, self.n_q, self.dim, self._keep = ctx, h, n_heads, n_q, dim, keep
+
+    def update(self, heads: list, stream=None) -> None:
+        """kvexp_hip_plan_update: the plan's heads (same dicts as for Context.plan)
+        with new lengths after appends."""
+        arr, keep = _heads_array(heads)
+        check(lib().kvexp_hip_plan_update(self.h, arr, len(heads), _stream(stream)))
+        self._keep, self._arr = keep, arr
+        self._caps = [(h["kx"].blob.numel(), h["vx"].blob.numel()) if "kx" in h else (0, 0) for h in heads]
+
+    def update_lengths(self, seq, block: int = 128, stream=None) -> None:
+        """kvexp_hip_plan_update for regular containers grown by appends: every
+        head (or head i, for a list) now holds `seq` tokens in `block`-token
+        blocks; the head table of the last create/update is edited in place
+        (byte counts become the buffers' capacities)."""
+        import numpy as np
+
+        n = self.n_heads
+        if not hasattr(self, "_view"):
+            dt = np.dtype({"names": [f for f, _ in _Head._fields_],
+                           "formats": ["<u8" if t in (C.c_void_p, C.c_uint64) else "<i4" for _, t in _Head._fields_],
+                           "offsets": [getattr(_Head, f).offset for f, _ in _Head._fields_],
+                           "itemsize": C.sizeof(_Head)})
+            self._view_dt = dt
+        v = np.frombuffer(self._arr, dtype=self._view_dt, count=n)
+        seqs = np.full(n, int(seq), np.int64) if np.isscalar(seq) else np.asarray(seq, np.int64)
+        nb = (seqs + block - 1) // block
+        v["seq"] = seqs
+        if self._caps and self._caps[0][0]:
+            caps = np.asarray(self._caps, dtype=np.uint64)
+            v["k_bytes"], v["v_bytes"] = caps[:, 0], caps[:, 1]
+            v["k_n_blocks"], v["v_n_blocks"] = nb, nb
+        check(lib().kvexp_hip_plan_update(self.h, self._arr, n, _stream(stream)))
 
     def run(self, q, out=None, lse=None, check_errors: bool = False, stream=None):
         import torch

@@ -178,6 +178,18 @@ typedef struct kvexp_hip_plan kvexp_hip_plan;
 int kvexp_hip_plan_create(kvexp_hip_ctx *ctx, const kvexp_hip_head *heads, int n_heads, int n_q, int dim,
                           int split_tokens, int order, kvexp_hip_plan **out);
 int kvexp_hip_plan_destroy(kvexp_hip_plan *plan);
+/* Re-targets a plan at its heads after their containers grew
+ * (kvexp_hip_append): `heads` as at creation (same buffers, n_splits and
+ * order of heads) with the new seq, bytes (the buffer capacity will do) and
+ * n_blocks. While no head gains a block or a split tile, only the last
+ * block of each container is read again (its descriptor and escape
+ * positions are rewritten on the GPU) and the device heads and work items
+ * are uploaded: stream-ordered on `stream` (the stream the plan runs on), no
+ * synchronisation, no allocation; an index that does not cover seq is then
+ * reported by the next checked run. Otherwise the plan is built again as by
+ * kvexp_hip_plan_create (synchronising `stream` first). No counterpart in
+ * the reference, which has no plans. */
+int kvexp_hip_plan_update(kvexp_hip_plan *plan, const kvexp_hip_head *heads, int n_heads, void *stream);
 /* Suggested n_splits for a head of `seq` tokens so that a plan over
  * `n_heads` such heads fills the device (one wave group per split). */
 int kvexp_hip_suggest_splits(kvexp_hip_ctx *ctx, int n_heads, int seq, int split_tokens);

@@ -8,7 +8,7 @@ after every call."""
 import numpy as np
 import pytest
 
-from conftest import say, to_dev
+from conftest import bits_equal, say, to_dev
 from kvdata import bf16_from_f32, random_kv
 
 pytestmark = pytest.mark.gpu
@@ -302,3 +302,61 @@ def test_append_set_steps(ctx, oracle):
         say("append set", i, dict(tokens=pos, bytes=nb))
         assert c.seq == pos and nb == want.size
         assert np.array_equal(c.blob[:nb].cpu().numpy(), want), i
+
+
+@pytest.mark.parametrize("dim,n_q,order", [(64, 7, 0), (128, 4, 1), (64, 9, 0)])
+def test_decode_loop_plan_update(ctx, oracle, dim, n_q, order):
+    """A decode loop: every step appends one token to each K/V container
+    (AppendSet), re-targets one plan with kvexp_hip_plan_update (fast path
+    inside a block, full rebuild when a block starts) and runs it; every
+    step's output is bit-equal to a new plan over fresh encodes of the same
+    tokens, and to the oracle at the first and last steps."""
+    import torch
+
+    rng = np.random.default_rng(dim + n_q)
+    block, heads_n, splits = 128, 3, 3
+    seq0, steps = 250, 12  # crosses the block boundary at 256
+    ks = [random_kv(rng, seq0 + steps, dim, spread_lo=-6, spread_hi=4, outliers=2).reshape(-1, dim)
+          for _ in range(heads_n)]
+    vs = [random_kv(rng, seq0 + steps, dim, sigma=0.5).reshape(-1, dim) for _ in range(heads_n)]
+    q = to_dev(random_kv(rng, heads_n * n_q, dim), torch.int16)
+    caches = []
+    for h in range(heads_n):
+        for x in (ks[h], vs[h]):
+            c = ctx.cache(dim, seq0 + steps, block)
+            c.append(to_dev(x[:seq0].reshape(-1), torch.int16), seq0)
+            caches.append(c)
+    aset = ctx.append_set(caches)
+
+    def heads_of(seq, views):
+        return [dict(kx=views[2 * h], vx=views[2 * h + 1], seq=seq, splits=splits) for h in range(heads_n)]
+
+    def views():
+        out = []
+        for c in caches:
+            e = c.view()
+            e.nbytes = -1  # the capacity stands in for the size
+            out.append(e)
+        return out
+
+    plan = ctx.plan(heads_of(seq0, views()), n_q, dim, block, order)
+    backend = "scalar" if order == 0 else "avx512"
+    for step in range(steps):
+        seq = seq0 + step + 1
+        toks = torch.stack([to_dev(x[seq - 1:seq].reshape(-1), torch.int16)
+                            for h in range(heads_n) for x in (ks[h], vs[h])]).contiguous()
+        aset.append(toks, 1)
+        plan.update(heads_of(seq, views()))
+        got = plan.run(q, check_errors=True).cpu().numpy()
+        fresh = [ctx.encode(to_dev(x[:seq].reshape(-1), torch.int16), seq, dim, block)
+                 for h in range(heads_n) for x in (ks[h], vs[h])]
+        ref_plan = ctx.plan(heads_of(seq, fresh), n_q, dim, block, order)
+        want = ref_plan.run(q).cpu().numpy()
+        say("decode loop", dim, n_q, order, step, dict(seq=seq))
+        assert bits_equal(got, want), step
+        if step in (0, steps - 1):
+            ref = oracle.attention_heads(backend, q.cpu().numpy().view(np.uint16),
+                                         [dict(k=ks[h][:seq].reshape(-1), v=vs[h][:seq].reshape(-1), seq=seq,
+                                               threads=splits) for h in range(heads_n)],
+                                         n_q=n_q, dim=dim, split=block)
+            assert bits_equal(got, ref), step
