@@ -466,7 +466,7 @@ def main() -> int:
         "block_modes": stats,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
-                     "kernel": "attn_wave_kernel<7, true>", "kernel_us": round(kern_avg_ms * 1e3, 2),
+                     "kernel": "attn_wave_kernel<7, 64, true, 0>", "kernel_us": round(kern_avg_ms * 1e3, 2),
                      "algorithmic_bytes": algo_bytes},
         "cpu_baseline": cpu,
     }
