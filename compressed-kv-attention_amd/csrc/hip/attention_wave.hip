@@ -1015,6 +1015,10 @@ static hipError_t launch_wave_d(bool xkv, int order, int G, const HeadDev *heads
 // general kernel).
 bool wave_supports(int dim) { return dim == 64 || dim == 128; }
 
+// Waves per workgroup of the split kernel (consecutive work items share a
+// workgroup).
+int wave_waves_per_wg(int dim) { return dim == 64 ? wave::Shape<64>::kWaves : wave::Shape<128>::kWaves; }
+
 hipError_t wave_merge(int dim, const HeadDev *heads, const int2 *mitems, int n_mitems, float *out, float *lse,
                       const float *ws, hipStream_t s) {
     if (n_mitems <= 0) return hipSuccess;

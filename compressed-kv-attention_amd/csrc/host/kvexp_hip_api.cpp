@@ -46,6 +46,7 @@ hipError_t attention_wave(bool xkv, int order, int G, int dim, const HeadDev *he
                           int n_items, const uint16_t *q, float *out, float *lse, float *ws, hipStream_t s);
 hipError_t wave_merge(int dim, const HeadDev *heads, const int2 *mitems, int n_mitems, float *out, float *lse,
                       const float *ws, hipStream_t s);
+int wave_waves_per_wg(int dim);
 } // namespace kvexp_launch
 
 namespace {
@@ -213,6 +214,8 @@ struct kvexp_hip_plan {
     // escape-index jobs (host copy and device copy)
     std::vector<kvexp_hip_head> src;
     std::vector<kvexp_dev::EscJob> jobs;
+    std::vector<int32_t> esc_prefix; // per tensor (jobs order): escapes before each block, n_blocks + 1 entries
+    std::vector<size_t> esc_prefix_at;
     DevBuf djobs;
     bool wave = false; // one-wave-per-split kernel (dim 64 or 128)
     DevBuf heads, items, merge_ids, ws, status;
@@ -310,6 +313,8 @@ void build_escape_index(kvexp_hip_plan &p, const kvexp_hip_head *heads, int n_he
     check_status_word(st, nullptr);
     std::vector<int32_t> e0(e0_total);
     HIPX(hipMemcpy(e0.data(), p.esc0.p, e0_total * sizeof(int32_t), hipMemcpyDeviceToHost));
+    p.esc_prefix = e0;
+    p.esc_prefix_at = e0_at;
     // each tensor's positions, then room for its last block to grow to the
     // largest block the format allows (255 tokens) after appends
     size_t pos_total = 0;
@@ -649,6 +654,62 @@ int kvexp_hip_suggest_splits(kvexp_hip_ctx *ctx, int n_heads, int seq, int split
 
 namespace {
 
+// Orders each query-row group's work items so that the waves sharing a SIMD
+// carry similar work. The dispatcher places workgroup g on XCD g % 8 and the
+// workgroups g, g + C, g + 2C, ... (C = CU count) on the same CU, one wave
+// of each on every SIMD, and a SIMD issues its oldest wave first, so a SIMD
+// is busy for the sum of its waves' work and the launch ends with the
+// busiest SIMD. Cost of a split: its tokens plus its K and V escape words
+// (about 1/15 token each, measured on c2: an escape costs ~5.7 SIMD cycles,
+// a token ~85). Items are sorted by cost, cut into workgroup-sized groups,
+// and the groups are dealt to the workgroup slots tier by tier, in forward
+// order on even tiers and reversed on odd ones, so that each CU receives a
+// mix of heavy and light groups. The merge follows split numbers, not item
+// order, so the results do not depend on it.
+void balance_items(kvexp_hip_plan &p, std::vector<WorkItem> &items, const int32_t *first_all,
+                   const std::vector<size_t> &first_at, int n_q, int dim) {
+    const int per_head = (n_q + kMaxQPerLaunch - 1) / kMaxQPerLaunch;
+    const int wpw = kvexp_launch::wave_waves_per_wg(dim);
+    const int C = std::max(1, p.ctx->cu_count);
+    auto cost = [&](const WorkItem &w) {
+        const int h = w.head / per_head;
+        double c = double(w.tok_end - w.tok_begin);
+        for (int kv = 0; kv < 2; ++kv) {
+            const size_t t = size_t(2 * h + kv);
+            const int32_t *f0 = first_all + first_at[t];
+            const int nb = p.jobs[t].n_blocks;
+            const int b0 = kv ? w.vblk : w.kblk;
+            const int b1 = int(std::lower_bound(f0, f0 + nb, w.tok_end) - f0);
+            const int32_t *e = p.esc_prefix.data() + p.esc_prefix_at[t];
+            c += double(e[b1] - e[b0]) / 15.0;
+        }
+        return c;
+    };
+    for (int G = 1; G <= 8; ++G) {
+        const int b = p.group_start[G], e = p.group_start[G + 1];
+        const int n = e - b;
+        if (n <= wpw || n % wpw != 0) continue; // whole workgroups only
+        std::vector<std::pair<double, int>> order(static_cast<size_t>(n));
+        for (int i = 0; i < n; ++i) order[size_t(i)] = {cost(items[size_t(b + i)]), i};
+        std::stable_sort(order.begin(), order.end(), [](const auto &x, const auto &y) { return x.first > y.first; });
+        const int n_groups = (n + wpw - 1) / wpw;
+        std::vector<int> slot_of_group(static_cast<size_t>(n_groups));
+        for (int t0 = 0; t0 < n_groups; t0 += C) {
+            const int cnt = std::min(C, n_groups - t0);
+            const bool rev = (t0 / C) % 2 == 1;
+            for (int k = 0; k < cnt; ++k) slot_of_group[size_t(t0 + k)] = t0 + (rev ? cnt - 1 - k : k);
+        }
+        std::vector<WorkItem> out(static_cast<size_t>(n));
+        std::vector<int> fill(size_t(n_groups), 0);
+        for (int r = 0; r < n; ++r) {
+            const int gq = r / wpw;
+            const int slot = slot_of_group[size_t(gq)];
+            out[size_t(slot * wpw + fill[size_t(slot)]++)] = items[size_t(b + order[size_t(r)].second)];
+        }
+        std::copy(out.begin(), out.end(), items.begin() + b);
+    }
+}
+
 // Builds (or rebuilds) every device-side part of a plan from its heads: work
 // items (token_bounds splits, split starts checked against the block index),
 // device heads, merge work, and for the one-wave kernel the block descriptors
@@ -782,7 +843,10 @@ void plan_build(kvexp_hip_plan *p, const kvexp_hip_head *heads, int n_heads) {
         p->mitems = DevBuf(std::max<size_t>(1, mi.size()) * sizeof(int2));
         if (!mi.empty())
             HIPX(hipMemcpy(p->mitems.p, mi.data(), mi.size() * sizeof(int2), hipMemcpyHostToDevice));
-        if (xkv) build_escape_index(*p, heads, n_heads, n_q, dim, hv);
+        if (xkv) {
+            build_escape_index(*p, heads, n_heads, n_q, dim, hv);
+            balance_items(*p, items, first_all, first_at, n_q, dim);
+        }
     }
     p->heads = DevBuf(hv.size() * sizeof(HeadDev));
     p->items = DevBuf(items.size() * sizeof(WorkItem));
