@@ -2,6 +2,7 @@
 
     python bench.py [--steps K] [--warmup W] [--config c2] [--gpus 1]
     python bench.py --workload append [--steps K] [--warmup W]
+    python bench.py --workload dump --kvd FILE.kvd --qsnap FILE.qsnap [--lengths 4096,32768]
 
 Workload ("c2"): a full Qwen2.5-0.5B decode step at a
 32K context: 24 layers x 2 KV heads, 7 queries per KV head (GQA), head_dim 64,
@@ -34,6 +35,11 @@ call) in µs; the line also carries the prefill rate (32768 tokens into every
 container in one call, GB/s of BF16 input) with its HBM roofline, and the
 reference's encode_bf16 on the host as the CPU baseline. Containers are
 checked byte for byte against kvexp_hip_encode of the same tokens.
+
+--workload dump runs the reference bench's model scope on a real KV dump
+(KVD1 + QSN1 files written by the reference's python/dump_kv.py): every
+layer and KV head at each snapshot length, XKV checked bit for bit against
+raw BF16 before timing; one JSON line with a row per length.
 """
 from __future__ import annotations
 
@@ -266,6 +272,50 @@ def bench_append(a, torch, np, kvexp_amd, synth) -> int:
     return 0
 
 
+def bench_dump(a, torch, np, kvexp_amd) -> int:
+    from kvexp_amd import dumps
+
+    if not a.kvd or not a.qsnap:
+        raise SystemExit("--workload dump needs --kvd and --qsnap (files written by the reference's dump_kv.py)")
+    d, qs = dumps.parse_dump(a.kvd), dumps.load_qsnap(a.qsnap)
+    lengths = [int(x) for x in a.lengths.split(",")] if a.lengths else [p for p in qs.pos if p <= d.seq]
+    ctx = kvexp_amd.Context(0)
+    rows = []
+    for L in lengths:
+        plan, dq, keep = dumps.model_scope(ctx, d, qs, L, splits=a.splits)
+        plan_r, dq_r, keep_r = dumps.model_scope(ctx, d, qs, L, splits=a.splits, raw=True)
+        ox, orw = plan.run(dq, check_errors=True), plan_r.run(dq_r, check_errors=True)
+        torch.cuda.synchronize()
+        same = bool(torch.equal(ox.view(torch.int32), orw.view(torch.int32)))
+        container = sum(h["kx"].nbytes + h["vx"].nbytes for h in keep[0])
+        tight = 4 * L * d.dim * d.layers * d.kv
+        res = []
+        for p, q in ((plan, dq), (plan_r, dq_r)):
+            for _ in range(a.warmup):
+                p.run(q, ox)
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(a.steps):
+                p.run(q, ox)
+            e1.record()
+            torch.cuda.synchronize()
+            res.append(e0.elapsed_time(e1) / a.steps)
+        row = {"seq": L, "xkv_us": round(res[0] * 1e3, 2), "raw_us": round(res[1] * 1e3, 2),
+               "container_bytes": container, "tight_bytes": tight, "kv_ratio": round(container / tight, 6),
+               "xkv_GBps_container": round(container / (res[0] * 1e-3) / 1e9, 2),
+               "xkv_bit_equal_raw": same}
+        log("dump", row)
+        rows.append(row)
+    print(json.dumps({"metric": "model-scope decode step µs on a real KV dump", "unit": "us",
+                      "value": rows[-1]["xkv_us"] if rows else None, "n_gpus": 1, "steps": a.steps,
+                      "warmup": a.warmup, "higher_is_better": False, "data": os.path.basename(a.kvd),
+                      "config": {"workload": "dump model scope", "layers": d.layers, "kv_heads": d.kv,
+                                 "q_heads": d.nq, "dim": d.dim, "dump_seq": d.seq},
+                      "rows": rows}), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -276,7 +326,10 @@ def main() -> int:
     ap.add_argument("--splits", type=int, default=0, help="splits per KV head (0 = library suggestion)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=0)
-    ap.add_argument("--workload", default="attention", choices=["attention", "append"])
+    ap.add_argument("--workload", default="attention", choices=["attention", "append", "dump"])
+    ap.add_argument("--kvd", default="", help="KVD1 dump (--workload dump)")
+    ap.add_argument("--qsnap", default="", help="QSN1 query snapshots (--workload dump)")
+    ap.add_argument("--lengths", default="", help="comma-separated snapshot lengths (--workload dump)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run a 256 MiB device copy (counter calibration under rocprofv3 --pmc)")
     a = ap.parse_args()
@@ -293,6 +346,8 @@ def main() -> int:
 
     if a.workload == "append":
         return bench_append(a, torch, np, kvexp_amd, synth)
+    if a.workload == "dump":
+        return bench_dump(a, torch, np, kvexp_amd)
     if a.config != "c2":
         raise SystemExit("the bench line is quoted on c2 (BASELINE.json configs[1]); other configs are test cases")
     cfg = synth.CONFIGS["c2"]
