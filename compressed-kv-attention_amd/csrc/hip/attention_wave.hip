@@ -904,6 +904,48 @@ void attn_wave_kernel(const HeadDev *__restrict__ heads, const WorkItem *__restr
 // One wave per (device head, query row): lane = channel (channels lane +
 // 64 h). A separate launch, so the slots written by the split kernel are
 // visible without fences.
+// One batch of the merge: splits [s0, s0 + cnt) (cnt <= B), every load
+// issued before any use (indices clamped), then folded in split order.
+template <int D, int B>
+__device__ __forceinline__ void merge_batch(const float *slots, int g, int s0, int cnt, const uint64_t *tab,
+                                            float (&a)[D / 64], float &mf, float &lf) {
+    constexpr int H = D / 64, SF = Shape<D>::kSlotFloats;
+    const int lane = lane_id();
+    float ab[B][H];
+#pragma unroll
+    for (int j = 0; j < B; ++j)
+#pragma unroll
+        for (int c = 0; c < H; ++c)
+            ab[j][c] = slots[size_t(s0 + min(j, cnt - 1)) * SF + 2 * kSlotQ + g * D + 64 * c + lane];
+    float ms[(B + 63) / 64], lb[(B + 63) / 64];
+#pragma unroll
+    for (int h = 0; h < (B + 63) / 64; ++h) {
+        const int j = 64 * h + lane;
+        const float *ls = slots + size_t(s0 + min(j, cnt - 1)) * SF;
+        ms[h] = j < cnt ? ls[g] : -__builtin_inff();
+        lb[h] = ls[kSlotQ + g];
+    }
+#pragma unroll
+    for (int h = 0; h < (B + 63) / 64; ++h) {
+        if (64 * h >= cnt) break;
+        // lane = split s0 + 64h + lane: running maximum and the two exponentials
+        const float mm = fmaxf(wave_scan_max(ms[h]), mf);
+        const float mprev = wave_shift_up(mm, mf);
+        const float e1 = kvexp_expf_nonpos_nb(mprev - mm, tab); // scale of the running state
+        const float e2 = kvexp_expf_nonpos_nb(ms[h] - mm, tab); // scale of split s0 + 64h + lane
+        mf = readlane_f32(mm, min(64, cnt - 64 * h) - 1);
+#pragma unroll
+        for (int jj = 0; jj < 64; ++jj) {
+            if (64 * h + jj < cnt) {
+                const float x1 = readlane_f32(e1, jj), x2 = readlane_f32(e2, jj);
+#pragma unroll
+                for (int c = 0; c < H; ++c) a[c] = fmaf(a[c], x1, ab[64 * h + jj][c] * x2);
+                lf = fmaf(lf, x1, readlane_f32(lb[h], jj) * x2);
+            }
+        }
+    }
+}
+
 template <int D>
 __global__ __launch_bounds__(4 * 64) void wave_merge_kernel(
     const HeadDev *__restrict__ heads, const int2 *__restrict__ mitems, int n_mitems, float *__restrict__ out_all,
@@ -927,40 +969,11 @@ __global__ __launch_bounds__(4 * 64) void wave_merge_kernel(
     float lf = slots[kSlotQ + g];
     for (int s0 = 1; s0 < n; s0 += B) {
         const int cnt = min(B, n - s0);
-        // every load of the batch is issued before any use (indices clamped)
-        float ab[B][H];
-#pragma unroll
-        for (int j = 0; j < B; ++j)
-#pragma unroll
-            for (int c = 0; c < H; ++c)
-                ab[j][c] = slots[size_t(s0 + min(j, cnt - 1)) * SF + 2 * kSlotQ + g * D + 64 * c + lane];
-        float ms[(B + 63) / 64], lb[(B + 63) / 64];
-#pragma unroll
-        for (int h = 0; h < (B + 63) / 64; ++h) {
-            const int j = 64 * h + lane;
-            const float *ls = slots + size_t(s0 + min(j, cnt - 1)) * SF;
-            ms[h] = j < cnt ? ls[g] : -__builtin_inff();
-            lb[h] = ls[kSlotQ + g];
-        }
-#pragma unroll
-        for (int h = 0; h < (B + 63) / 64; ++h) {
-            if (64 * h >= cnt) break;
-            // lane = split s0 + 64h + lane: running maximum and the two exponentials
-            const float mm = fmaxf(wave_scan_max(ms[h]), mf);
-            const float mprev = wave_shift_up(mm, mf);
-            const float e1 = kvexp_expf_nonpos_nb(mprev - mm, tab); // scale of the running state
-            const float e2 = kvexp_expf_nonpos_nb(ms[h] - mm, tab); // scale of split s0 + 64h + lane
-            mf = readlane_f32(mm, min(64, cnt - 64 * h) - 1);
-#pragma unroll
-            for (int jj = 0; jj < 64; ++jj) {
-                if (64 * h + jj < cnt) {
-                    const float x1 = readlane_f32(e1, jj), x2 = readlane_f32(e2, jj);
-#pragma unroll
-                    for (int c = 0; c < H; ++c) a[c] = fmaf(a[c], x1, ab[64 * h + jj][c] * x2);
-                    lf = fmaf(lf, x1, readlane_f32(lb[h], jj) * x2);
-                }
-            }
-        }
+        // a half-size batch when it covers the rest (fewer clamped loads)
+        if (cnt <= B / 2)
+            merge_batch<D, B / 2>(slots, g, s0, cnt, tab, a, mf, lf);
+        else
+            merge_batch<D, B>(slots, g, s0, cnt, tab, a, mf, lf);
     }
 #pragma unroll
     for (int c = 0; c < H; ++c) out_all[(size_t(hd.q_row) + g) * D + 64 * c + lane] = a[c] * (1.0f / lf);
