@@ -154,7 +154,8 @@ __device__ __forceinline__ void encode_stats_block(uint32_t *hist, int *esc_part
     const int tid = int(threadIdx.x);
     uint32_t *h = hist + tid * kHistStride;
     int esc2 = 0, esc4 = 0;
-    for (int d = tid; d < dim; d += int(blockDim.x)) {
+    const int nthr = min(int(blockDim.x), 128); // threads owning channel columns
+    for (int d = tid; tid < nthr && d < dim; d += nthr) {
         int e_lo = 255, e_hi = 0;
 #pragma unroll 16
         for (int k = 0; k < 64; ++k) h[k] = 0u;
@@ -249,7 +250,7 @@ __device__ __forceinline__ void encode_stats_block(uint32_t *hist, int *esc_part
 // the per-wave escape sums.
 __host__ __device__ constexpr int stats_threads(int dim) { return dim > 64 ? 128 : 64; }
 __host__ __device__ constexpr size_t stats_lds_bytes(int dim) {
-    return size_t(stats_threads(dim)) * kHistStride * sizeof(uint32_t) + 4 * sizeof(int);
+    return size_t(stats_threads(dim)) * kHistStride * sizeof(uint32_t) + 2 * kWaves * sizeof(int);
 }
 
 __global__ __launch_bounds__(128) void encode_stats_kernel(const uint16_t *__restrict__ kv, int seq, int dim,
@@ -454,6 +455,46 @@ __global__ __launch_bounds__(kThreads) void append_write_kernel(const AppendJobD
 // its tail buffer yet, copied there (after the write kernel has read it).
 __global__ __launch_bounds__(kThreads) void append_tail_kernel(const AppendJobDev *__restrict__ jobs, int dim) {
     const AppendJobDev j = jobs[blockIdx.x];
+    const int total = j.copy_rows * dim;
+    const uint16_t *from = j.src + size_t(j.copy_from) * size_t(dim);
+    uint16_t *to = j.tail + size_t(j.copy_to) * size_t(dim);
+    for (int i = int(threadIdx.x); i < total; i += kThreads) to[i] = from[i];
+}
+
+// Append jobs that encode one block each (a decode step: the trailing block
+// plus one token never exceeds a block), fused in one launch: one workgroup
+// (kThreads) per job computes the block's statistics, its place (the
+// container's trailing-block offset, which no other job touches), writes it
+// and the index entries around it, then stores the raw rows kept for the
+// next append (rows the block did not read from the tail).
+__global__ __launch_bounds__(kThreads) void append_one_kernel(const AppendJobDev *__restrict__ jobs, int dim,
+                                                             int bt, uint32_t *__restrict__ status) {
+    extern __shared__ uint32_t one_lds[]; // stats columns, escape sums, then the two window bases
+    __shared__ EncBlockMeta meta_s;
+    __shared__ int scan_tmp[kWaves];
+    const AppendJobDev j = jobs[blockIdx.x];
+    int *esc_part = reinterpret_cast<int *>(one_lds + stats_threads(dim) * kHistStride);
+    uint8_t *bases_s = reinterpret_cast<uint8_t *>(esc_part + 2 * kWaves);
+    const int64_t base = j.rebase ? j.offs[0] : 0;
+    if (j.nb == 0) { // an empty container: its terminal index entry
+        if (threadIdx.x == 0) {
+            j.offs[0] = base;
+            j.first[0] = j.tok0;
+        }
+        return;
+    }
+    const EncRows rows = job_rows(j, 0, bt, dim);
+    encode_stats_block(one_lds, esc_part, rows, j.seq, dim, &meta_s, bases_s);
+    __syncthreads();
+    const EncBlockMeta m = meta_s;
+    if (threadIdx.x == 0) {
+        j.offs[0] = base;
+        j.offs[1] = base + m.bytes;
+        j.first[0] = j.tok0;
+        j.first[1] = j.tok0 + j.seq;
+    }
+    encode_write_block(scan_tmp, rows, j.seq, dim, m, bases_s, j.out + base, status);
+    __syncthreads();
     const int total = j.copy_rows * dim;
     const uint16_t *from = j.src + size_t(j.copy_from) * size_t(dim);
     uint16_t *to = j.tail + size_t(j.copy_to) * size_t(dim);
@@ -689,8 +730,13 @@ hipError_t encode(const uint16_t *kv, int seq, int dim, int bt, int n_blocks, En
 }
 
 hipError_t append(const AppendJobDev *jobs, int n_jobs, int total_blocks, int dim, int bt, EncBlockMeta *meta,
-                  uint8_t *bases, uint32_t *status, hipStream_t s) {
+                  uint8_t *bases, uint32_t *status, hipStream_t s, bool one_block) {
     if (n_jobs <= 0) return hipSuccess;
+    if (one_block) {
+        const size_t lds = stats_lds_bytes(dim) + 2 * size_t(dim);
+        hipLaunchKernelGGL(append_one_kernel, dim3(n_jobs), dim3(kThreads), lds, s, jobs, dim, bt, status);
+        return hipGetLastError();
+    }
     if (total_blocks > 0)
         hipLaunchKernelGGL(append_stats_kernel, dim3(total_blocks), dim3(stats_threads(dim)), stats_lds_bytes(dim), s,
                            jobs, n_jobs, dim, bt, meta, bases);

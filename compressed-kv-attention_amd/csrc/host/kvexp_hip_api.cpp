@@ -31,7 +31,7 @@ hipError_t encode(const uint16_t *kv, int seq, int dim, int bt, int n_blocks, En
                   int64_t *offs, int32_t *first, uint8_t *out, uint32_t *status, hipStream_t s, bool rebase = false,
                   int tok0 = 0);
 hipError_t append(const kvexp_dev::AppendJobDev *jobs, int n_jobs, int total_blocks, int dim, int bt,
-                  EncBlockMeta *meta, uint8_t *bases, uint32_t *status, hipStream_t s);
+                  EncBlockMeta *meta, uint8_t *bases, uint32_t *status, hipStream_t s, bool one_block);
 hipError_t attention(bool xkv, int order, const HeadDev *heads, const WorkItem *items, int n_items,
                      const int32_t *merge_ids, int n_merge, const uint16_t *q, float *out, float *lse, float *ws,
                      int dim, uint32_t *status, hipStream_t s);
@@ -551,6 +551,8 @@ void run_append(kvexp_hip_ctx *ctx, const kvexp_hip_append_job *jobs, int n_jobs
     int blocks = 0;
     for (int i = 0; i < n_jobs; ++i) blocks += add_append_job(jobs[i], dim, bt, blocks, dj);
     if (dj.empty()) return;
+    // every job encodes at most one block (a decode step): one fused launch
+    const bool one_block = std::all_of(dj.begin(), dj.end(), [](const AppendJobDev &j) { return j.nb <= 1; });
     grow(ctx->enc_meta, ctx->enc_meta_cap, size_t(std::max(blocks, 1)) * sizeof(EncBlockMeta));
     grow(ctx->enc_bases, ctx->enc_bases_cap, size_t(std::max(blocks, 1)) * 2u * size_t(dim));
     grow(ctx->app_jobs, ctx->app_jobs_cap, dj.size() * sizeof(AppendJobDev));
@@ -558,7 +560,7 @@ void run_append(kvexp_hip_ctx *ctx, const kvexp_hip_append_job *jobs, int n_jobs
     HIPX(hipMemcpyAsync(ctx->app_jobs.p, dj.data(), dj.size() * sizeof(AppendJobDev), hipMemcpyHostToDevice, s));
     HIPX(kvexp_launch::append(ctx->app_jobs.as<AppendJobDev>(), int(dj.size()), blocks, dim, bt,
                               ctx->enc_meta.as<EncBlockMeta>(), ctx->enc_bases.as<uint8_t>(),
-                              ctx->status.as<uint32_t>(), s));
+                              ctx->status.as<uint32_t>(), s, one_block));
 }
 
 void check_encoder_status(kvexp_hip_ctx *ctx, hipStream_t s) {
