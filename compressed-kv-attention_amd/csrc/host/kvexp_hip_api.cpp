@@ -861,6 +861,10 @@ void plan_build(kvexp_hip_plan *p, const kvexp_hip_head *heads, int n_heads) {
     if (!merge.empty())
         HIPX(hipMemcpy(p->merge_ids.p, merge.data(), merge.size() * sizeof(int32_t), hipMemcpyHostToDevice));
     HIPX(hipMemset(p->status.p, 0, sizeof(uint32_t)));
+    if (!xkv) { // the job table kvexp_hip_plan_update sends lengths through
+        p->jobs.assign(size_t(2 * n_heads), kvexp_dev::EscJob{});
+        p->djobs = DevBuf(p->jobs.size() * sizeof(kvexp_dev::EscJob));
+    }
     p->src.assign(heads, heads + n_heads);
 }
 
@@ -933,10 +937,6 @@ int kvexp_hip_plan_update(kvexp_hip_plan *plan, const kvexp_hip_head *heads, int
         // the device heads' lengths and byte counts and the last splits' ends
         // are set on the GPU from the jobs, with the last blocks' descriptors
         const int per_head = (plan->n_q + kMaxQPerLaunch - 1) / kMaxQPerLaunch;
-        if (plan->jobs.size() != size_t(2 * n_heads)) {
-            plan->jobs.assign(size_t(2 * n_heads), kvexp_dev::EscJob{});
-            plan->djobs = DevBuf(plan->jobs.size() * sizeof(kvexp_dev::EscJob));
-        }
         for (int h = 0; h < n_heads; ++h)
             for (int kv = 0; kv < 2; ++kv) {
                 kvexp_dev::EscJob &j = plan->jobs[size_t(2 * h + kv)];

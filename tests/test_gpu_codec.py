@@ -360,3 +360,29 @@ def test_decode_loop_plan_update(ctx, oracle, dim, n_q, order):
                                                threads=splits) for h in range(heads_n)],
                                          n_q=n_q, dim=dim, split=block)
             assert bits_equal(got, ref), step
+
+
+def test_plan_update_raw_heads(ctx, oracle):
+    """kvexp_hip_plan_update on a plan over raw BF16 heads (buffers sized for
+    the final length): each step's output equals a new plan's, inside a split
+    tile and across one."""
+    import torch
+
+    rng = np.random.default_rng(8)
+    dim, n_q, block, heads_n, splits = 64, 7, 128, 2, 3
+    seq0, steps = 380, 8  # crosses the tile boundary at 384
+    ks = [to_dev(random_kv(rng, seq0 + steps, dim), torch.int16) for _ in range(heads_n)]
+    vs = [to_dev(random_kv(rng, seq0 + steps, dim, sigma=0.5), torch.int16) for _ in range(heads_n)]
+    q = to_dev(random_kv(rng, heads_n * n_q, dim), torch.int16)
+
+    def heads_at(seq):
+        return [dict(k=ks[h], v=vs[h], seq=seq, splits=splits) for h in range(heads_n)]
+
+    plan = ctx.plan(heads_at(seq0), n_q, dim, block)
+    for step in range(steps):
+        seq = seq0 + step + 1
+        plan.update(heads_at(seq))
+        got = plan.run(q, check_errors=True).cpu().numpy()
+        want = ctx.plan(heads_at(seq), n_q, dim, block).run(q).cpu().numpy()
+        say("raw plan update", step, dict(seq=seq))
+        assert bits_equal(got, want), step
