@@ -320,7 +320,8 @@ def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=200,
+                    help="untimed steps first (the GPU clock takes a few ms to ramp up after the setup)")
     ap.add_argument("--config", default="c2")
     ap.add_argument("--copies", type=int, default=4)
     ap.add_argument("--splits", type=int, default=0, help="splits per KV head (0 = library suggestion)")
