@@ -645,12 +645,21 @@ int kvexp_hip_decode(kvexp_hip_ctx *ctx, const uint8_t *d_blob, size_t bytes, co
 
 // ============================================================= attention ==
 int kvexp_hip_suggest_splits(kvexp_hip_ctx *ctx, int n_heads, int seq, int split_tokens) {
+    return kvexp_hip_suggest_splits_for(ctx, n_heads, seq, split_tokens, 64, 7, KVEXP_HIP_ORDER_SCALAR);
+}
+
+// One round of the split kernel's resident waves, so every split starts at
+// once and no SIMD runs a second, partly filled round: three single-wave
+// splits per SIMD at head_dim 64 (two for 8 query rows, and for the AVX-512
+// order with 6 or more), two at head_dim 128.
+int kvexp_hip_suggest_splits_for(kvexp_hip_ctx *ctx, int n_heads, int seq, int split_tokens, int dim, int n_q,
+                                 int order) {
     if (ctx == nullptr || n_heads <= 0 || seq <= 0 || split_tokens <= 0) return 1;
     const int tiles = (seq + split_tokens - 1) / split_tokens;
-    // one round of the head_dim-64 kernel's resident waves: 12 single-wave
-    // splits per CU (three waves per SIMD), so every split starts at once and
-    // no SIMD runs a second, partly filled round
-    const int target = std::max(1, (12 * ctx->cu_count) / n_heads);
+    const int g = std::min(std::max(1, n_q), kMaxQPerLaunch);
+    const int per_simd = dim == 64 && g < 8 && !(order == KVEXP_HIP_ORDER_DPBF16 && g >= 6) ? 3 : 2;
+    const int groups = (std::max(1, n_q) + kMaxQPerLaunch - 1) / kMaxQPerLaunch; // device heads per head
+    const int target = std::max(1, (4 * per_simd * ctx->cu_count) / (n_heads * groups));
     return std::max(1, std::min(tiles, target));
 }
 

@@ -103,6 +103,7 @@ def lib() -> C.CDLL:
     L.kvexp_hip_plan_destroy.argtypes = [vp]
     L.kvexp_hip_plan_update.argtypes = [vp, C.POINTER(_Head), i32, vp]
     L.kvexp_hip_suggest_splits.argtypes = [vp, i32, i32, i32]
+    L.kvexp_hip_suggest_splits_for.argtypes = [vp, i32, i32, i32, i32, i32, i32]
     L.kvexp_hip_attention_run.argtypes = [vp, vp, vp, vp, i32, vp]
     L.kvexp_hip_plan_status.argtypes = [vp, vp]
     L.kvexp_hip_plan_timing.argtypes = [vp, i32]
@@ -364,8 +365,11 @@ class Context:
         check(lib().kvexp_hip_expf(self.h, _ptr(x), _ptr(out), x.numel(), _stream(stream)))
         return out
 
-    def suggest_splits(self, n_heads: int, seq: int, split: int = 128) -> int:
-        return int(lib().kvexp_hip_suggest_splits(self.h, n_heads, seq, split))
+    def suggest_splits(self, n_heads: int, seq: int, split: int = 128, dim: int | None = None, n_q: int = 7,
+                       order: int = ORDER_SCALAR) -> int:
+        if dim is None:
+            return int(lib().kvexp_hip_suggest_splits(self.h, n_heads, seq, split))
+        return int(lib().kvexp_hip_suggest_splits_for(self.h, n_heads, seq, split, dim, n_q, order))
 
     def attention_decode_host(self, order, q, k=None, v=None, kx=None, vx=None, *, n_q, dim, seq, threads=1,
                               split=128):

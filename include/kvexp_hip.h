@@ -193,6 +193,11 @@ int kvexp_hip_plan_update(kvexp_hip_plan *plan, const kvexp_hip_head *heads, int
 /* Suggested n_splits for a head of `seq` tokens so that a plan over
  * `n_heads` such heads fills the device (one wave group per split). */
 int kvexp_hip_suggest_splits(kvexp_hip_ctx *ctx, int n_heads, int seq, int split_tokens);
+/* The same for a given head_dim, query rows per head and score order (the
+ * resident waves per SIMD depend on them); kvexp_hip_suggest_splits is this
+ * at head_dim 64, 7 query rows, scalar order. */
+int kvexp_hip_suggest_splits_for(kvexp_hip_ctx *ctx, int n_heads, int seq, int split_tokens, int dim, int n_q,
+                                 int order);
 
 /* Runs a plan: d_q is [n_heads, n_q, dim] BF16; d_out [n_heads, n_q, dim]
  * FP32 is fully overwritten; d_lse (nullable) [n_heads, n_q] receives

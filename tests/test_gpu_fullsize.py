@@ -60,9 +60,12 @@ def test_c4_full_step(ctx):
     H, S, D, G, BT = 256, 131072, 128, 4, 128
     heads = [_kv(torch, g, dev, S, D, BT, 0.0, (-5, 3), 0) for _ in range(H)]
     q = torch.randn(H * G * D, generator=g, device=dev).to(torch.bfloat16).view(torch.int16)
+    splits = ctx.suggest_splits(H, S, BT, dim=D, n_q=G)
+    assert splits == 8  # one round of resident waves at head_dim 128 (two per SIMD)
+    assert ctx.suggest_splits(48, 32768, 128, dim=64, n_q=7) == 64 == ctx.suggest_splits(48, 32768, 128)
     for order in (0, 1):
-        say("c4 full step", dict(heads=H, seq=S, order=order))
-        same, container = _step(ctx, heads, [S] * H, G, D, BT, [8] * H, order, q)
+        say("c4 full step", dict(heads=H, seq=S, order=order, splits=splits))
+        same, container = _step(ctx, heads, [S] * H, G, D, BT, [splits] * H, order, q)
         assert same, order
         assert 0.70 < container / (4 * S * D * H) < 0.80
 
