@@ -648,19 +648,47 @@ int kvexp_hip_suggest_splits(kvexp_hip_ctx *ctx, int n_heads, int seq, int split
     return kvexp_hip_suggest_splits_for(ctx, n_heads, seq, split_tokens, 64, 7, KVEXP_HIP_ORDER_SCALAR);
 }
 
-// One round of the split kernel's resident waves, so every split starts at
-// once and no SIMD runs a second, partly filled round: three single-wave
-// splits per SIMD at head_dim 64 (two for 8 query rows, and for the AVX-512
-// order with 6 or more), two at head_dim 128.
-int kvexp_hip_suggest_splits_for(kvexp_hip_ctx *ctx, int n_heads, int seq, int split_tokens, int dim, int n_q,
-                                 int order) {
-    if (ctx == nullptr || n_heads <= 0 || seq <= 0 || split_tokens <= 0) return 1;
-    const int tiles = (seq + split_tokens - 1) / split_tokens;
+namespace {
+
+// One round of the split kernel's resident waves: three single-wave splits
+// per SIMD at head_dim 64 (two for 8 query rows, and for the AVX-512 order
+// with 6 or more), two at head_dim 128. The uniform count is the largest one
+// whose longest split is no longer than the mean split of one round
+// (total tokens / resident waves): for equal lengths that is one full round,
+// with no second, partly filled one; for ragged lengths the long heads are
+// cut finer, and the shorter splits that come with it are dealt out by the
+// dispatcher as waves retire.
+int suggest_core(const kvexp_hip_ctx *ctx, int64_t total_tokens, int max_seq, int split_tokens, int dim, int n_q,
+                 int order) {
+    if (ctx == nullptr || total_tokens <= 0 || max_seq <= 0 || split_tokens <= 0) return 1;
+    const int tiles = (max_seq + split_tokens - 1) / split_tokens;
     const int g = std::min(std::max(1, n_q), kMaxQPerLaunch);
     const int per_simd = dim == 64 && g < 8 && !(order == KVEXP_HIP_ORDER_DPBF16 && g >= 6) ? 3 : 2;
-    const int groups = (std::max(1, n_q) + kMaxQPerLaunch - 1) / kMaxQPerLaunch; // device heads per head
-    const int target = std::max(1, (4 * per_simd * ctx->cu_count) / (n_heads * groups));
-    return std::max(1, std::min(tiles, target));
+    const int64_t groups = (std::max(1, n_q) + kMaxQPerLaunch - 1) / kMaxQPerLaunch; // device heads per head
+    const int64_t slots = int64_t(4) * per_simd * std::max(1, ctx->cu_count);
+    const int64_t target = std::max<int64_t>(1, int64_t(max_seq) * slots / (total_tokens * groups));
+    return int(std::max<int64_t>(1, std::min<int64_t>(tiles, target)));
+}
+
+} // namespace
+
+int kvexp_hip_suggest_splits_for(kvexp_hip_ctx *ctx, int n_heads, int seq, int split_tokens, int dim, int n_q,
+                                 int order) {
+    if (n_heads <= 0 || seq <= 0) return 1;
+    return suggest_core(ctx, int64_t(n_heads) * seq, seq, split_tokens, dim, n_q, order);
+}
+
+int kvexp_hip_suggest_splits_batch(kvexp_hip_ctx *ctx, int n_heads, const int *seqs, int split_tokens, int dim,
+                                   int n_q, int order) {
+    if (n_heads <= 0 || seqs == nullptr) return 1;
+    int64_t total = 0;
+    int max_seq = 0;
+    for (int i = 0; i < n_heads; ++i) {
+        if (seqs[i] <= 0) continue;
+        total += seqs[i];
+        max_seq = std::max(max_seq, seqs[i]);
+    }
+    return suggest_core(ctx, total, max_seq, split_tokens, dim, n_q, order);
 }
 
 namespace {

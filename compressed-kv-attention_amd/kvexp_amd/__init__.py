@@ -104,6 +104,7 @@ def lib() -> C.CDLL:
     L.kvexp_hip_plan_update.argtypes = [vp, C.POINTER(_Head), i32, vp]
     L.kvexp_hip_suggest_splits.argtypes = [vp, i32, i32, i32]
     L.kvexp_hip_suggest_splits_for.argtypes = [vp, i32, i32, i32, i32, i32, i32]
+    L.kvexp_hip_suggest_splits_batch.argtypes = [vp, i32, vp, i32, i32, i32, i32]
     L.kvexp_hip_attention_run.argtypes = [vp, vp, vp, vp, i32, vp]
     L.kvexp_hip_plan_status.argtypes = [vp, vp]
     L.kvexp_hip_plan_timing.argtypes = [vp, i32]
@@ -370,6 +371,14 @@ class Context:
         if dim is None:
             return int(lib().kvexp_hip_suggest_splits(self.h, n_heads, seq, split))
         return int(lib().kvexp_hip_suggest_splits_for(self.h, n_heads, seq, split, dim, n_q, order))
+
+    def suggest_splits_batch(self, seqs, split: int = 128, dim: int = 64, n_q: int = 7,
+                             order: int = ORDER_SCALAR) -> int:
+        """One split count for heads of the given (ragged) lengths."""
+        import numpy as np
+
+        arr = np.ascontiguousarray(np.asarray(seqs, dtype=np.int32))
+        return int(lib().kvexp_hip_suggest_splits_batch(self.h, len(arr), arr.ctypes.data, split, dim, n_q, order))
 
     def attention_decode_host(self, order, q, k=None, v=None, kx=None, vx=None, *, n_q, dim, seq, threads=1,
                               split=128):

@@ -198,6 +198,13 @@ int kvexp_hip_suggest_splits(kvexp_hip_ctx *ctx, int n_heads, int seq, int split
  * at head_dim 64, 7 query rows, scalar order. */
 int kvexp_hip_suggest_splits_for(kvexp_hip_ctx *ctx, int n_heads, int seq, int split_tokens, int dim, int n_q,
                                  int order);
+/* One n_splits for a batch of heads of different lengths (seqs[n_heads];
+ * heads of length 0 are skipped): the largest count whose longest split is
+ * no longer than the mean split of one round of resident waves. Equal
+ * lengths give kvexp_hip_suggest_splits_for's count. No counterpart in the
+ * reference, where n_threads is the caller's choice. */
+int kvexp_hip_suggest_splits_batch(kvexp_hip_ctx *ctx, int n_heads, const int *seqs, int split_tokens, int dim,
+                                   int n_q, int order);
 
 /* Runs a plan: d_q is [n_heads, n_q, dim] BF16; d_out [n_heads, n_q, dim]
  * FP32 is fully overwritten; d_lse (nullable) [n_heads, n_q] receives

@@ -85,6 +85,12 @@ def test_c3_full_batch(ctx):
         for _ in range(c["layers"] * c["kv_heads"]):
             heads.append(_kv(torch, g, dev, seq, c["dim"], c["block"], 0.06, (-6, 4), 2))
             seqs.append(seq)
+    # longest split of the uniform count no longer than the mean split of one
+    # round of resident waves (3 per SIMD at head_dim 64, 7 query rows)
+    uniform = ctx.suggest_splits_batch(seqs, c["block"], c["dim"], c["group"])
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    assert uniform == max(seqs) * 12 * cus // sum(seqs)
+    assert ctx.suggest_splits_batch([32768] * 48, 128) == ctx.suggest_splits(48, 32768, 128)
     splits = [max(1, min(64, s // 512)) for s in seqs]
     q = torch.randn(len(heads) * c["group"] * c["dim"], generator=g, device=dev).to(torch.bfloat16).view(torch.int16)
     say("c3 full batch", dict(heads=len(heads), tokens=sum(seqs)))
