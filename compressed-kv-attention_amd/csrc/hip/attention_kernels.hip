@@ -72,7 +72,8 @@ __device__ __forceinline__ void xkv_rows_to_lds(const uint8_t *blk, const BlockH
         }
         return;
     }
-    const bool four = h.mode == 4;
+    const int mode = h.mode; // 2, 3 or 4 code bits
+    const uint32_t sentinel = (1u << mode) - 1u;
     const uint8_t *base = p;
     const uint8_t *sm = p + dim;
     const uint8_t *codes = sm + size_t(h.n_tokens) * size_t(dim);
@@ -88,8 +89,10 @@ __device__ __forceinline__ void xkv_rows_to_lds(const uint8_t *blk, const BlockH
         if (act) {
             s0 = load_u32_any(sm + e);
             s1 = load_u32_any(sm + e + 4);
-            cw = four ? load_u32_any(codes + (e >> 1)) : load_u16_any(codes + (e >> 2));
-            cnt = four ? sentinels4(cw) : sentinels2(cw);
+            // the octet's codes: 4, 3 or 2 bytes
+            cw = mode == 4 ? load_u32_any(codes + (e >> 1))
+                           : (mode == 2 ? load_u16_any(codes + (e >> 2)) : load_codes(codes, 3, int(e >> 3)));
+            cnt = mode == 4 ? sentinels4(cw) : (mode == 2 ? sentinels2(cw) : sentinels3(cw));
         }
         int rank = carry;
         if (h.n_escape > 0) {
@@ -104,11 +107,11 @@ __device__ __forceinline__ void xkv_rows_to_lds(const uint8_t *blk, const BlockH
             float f[8];
 #pragma unroll
             for (int k = 0; k < 8; ++k) {
-                const uint32_t code = four ? (cw >> (4 * k)) & 15u : (cw >> (2 * k)) & 3u;
+                const uint32_t code = unit_code(cw, mode, k);
                 const uint32_t smk = ((k < 4 ? s0 : s1) >> (8 * (k & 3))) & 0xFFu;
                 const uint32_t bk = ((k < 4 ? b0 : b1) >> (8 * (k & 3))) & 0xFFu;
                 uint32_t bf;
-                if (code == (four ? 15u : 3u)) {
+                if (code == sentinel) {
                     if (rank < h.n_escape) {
                         bf = load_u16_any(escp + 2 * size_t(rank));
                     } else {

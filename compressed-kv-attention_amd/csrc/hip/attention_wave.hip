@@ -176,9 +176,10 @@ __device__ __forceinline__ void block_vectors(Cursor &c) {
 }
 
 // Loads rows [r0 + lane] of the cursor's block (lanes < rows) into R: a
-// coded row's D sign/mantissa bytes and D/2 (4-bit) or D/4 (2-bit, its
-// registers repeated) code bytes; a raw row's first 3D/2 bytes (the rest is
-// read at decode).
+// coded row's D sign/mantissa bytes and D/2 (4-bit), 3D/8 (3-bit: at D = 64
+// the second register holds bytes 8..23, at D = 128 the fourth repeats the
+// third) or D/4 (2-bit, its registers repeated) code bytes; a raw row's
+// first 3D/2 bytes (the rest is read at decode).
 template <int D>
 __device__ __forceinline__ void load_rows(const Cursor &c, int r0, int rows, uint4 (&R)[Shape<D>::kRowRegs]) {
     // Lanes past `rows` load row rows - 1 again (their tile rows are not
@@ -192,12 +193,12 @@ __device__ __forceinline__ void load_rows(const Cursor &c, int r0, int rows, uin
     // sign/mantissa bytes (or the first D raw bytes) of the row
     const uint8_t *rowp = c.blk + 8 + (raw ? 0 : D) + size_t(r) * (raw ? 2 * D : D);
     // codes of the row (or raw bytes D .. 3D/2 - 1)
-    const uint8_t *tail = raw ? rowp + D
-                              : c.blk + 8 + D + size_t(c.ntok()) * D + size_t(r) * (mode == 4 ? D / 2 : D / 4);
+    const int cbytes = mode * (D / 8); // code bytes per coded row
+    const uint8_t *tail = raw ? rowp + D : c.blk + 8 + D + size_t(c.ntok()) * D + size_t(r) * cbytes;
 #pragma unroll
     for (int i = 0; i < SM; ++i) R[i] = ld16(rowp + 16 * i);
 #pragma unroll
-    for (int i = 0; i < D / 32; ++i) R[SM + i] = ld16(tail + 16 * (mode == 2 ? min(i, D / 64 - 1) : i));
+    for (int i = 0; i < D / 32; ++i) R[SM + i] = ld16(tail + (raw ? 16 * i : min(16 * i, cbytes - 16)));
 }
 
 __device__ __forceinline__ uint32_t comp(const uint4 &v, int i) {
@@ -239,6 +240,14 @@ __device__ __forceinline__ uint4 octet(const uint4 (&R)[N], int dg, uint32_t lo,
     return o;
 }
 
+// Dword i of a 3-bit coded row's code bytes as load_rows placed them in R.
+template <int D, int N>
+__device__ __forceinline__ uint32_t code_dword3(const uint4 (&R)[N], int i) {
+    constexpr int SM = Shape<D>::kSmRegs;
+    if (D == 64 && i >= 4) return comp(R[SM + 1], i - 2); // bytes 16..23 are dwords 2, 3 of the register at byte 8
+    return comp(R[SM + (i >> 2)], i & 3);
+}
+
 // -0 in every channel of the lane's tile row (a token past the chunk's end).
 template <int D>
 __device__ __forceinline__ void fill_negzero(uint8_t *row) {
@@ -275,6 +284,17 @@ __device__ __forceinline__ void decode_row(const Cursor &c, const uint4 (&R)[Sha
             const uint32_t hi = ((cw >> 2) & 3u) | (((cw >> 6) & 3u) << 8) | (((cw >> 10) & 3u) << 16) |
                                 (((cw >> 14) & 3u) << 24);
             dst[dg] = octet(R, dg, lo, hi, bp);
+        }
+    } else if (mode == 3) {
+        // 3-bit codes: octet dg's 24 bits are bytes [3dg, 3dg + 3) of the
+        // row's codes; groups of two codes (6 bits) are spread to bytes first
+#pragma unroll
+        for (int dg = 0; dg < D / 8; ++dg) {
+            const int q = (3 * dg) >> 2, b = (3 * dg) & 3;
+            const uint32_t w = __builtin_amdgcn_alignbyte(code_dword3<D>(R, q + (b > 1 ? 1 : 0)),
+                                                          code_dword3<D>(R, q), uint32_t(b));
+            const uint32_t x = (w & 0x3Fu) | ((w << 2) & 0x3F00u) | ((w << 4) & 0x3F0000u) | ((w << 6) & 0x3F000000u);
+            dst[dg] = octet(R, dg, x & 0x07070707u, (x >> 3) & 0x07070707u, bp);
         }
     } else if (lane < rows) {
         const uint8_t *src = c.blk + 8 + size_t(r0 + lane) * (2 * D);
@@ -716,10 +736,10 @@ void attn_wave_kernel(const HeadDev *__restrict__ heads, const WorkItem *__restr
         if constexpr (XKV) {
             if (kc.mode() != 0) {
                 if constexpr (ORDER == 1) {
-                    // coded exponents are base + code with code <= 15 (4-bit) or 3
-                    // (2-bit): all >= kmin when no base is below it or wraps
+                    // coded exponents are base + code with code < 2^bits: all
+                    // >= kmin when no base is below it or wraps
                     const uint32_t b0 = kc.base2 & 0xFFu, b1 = (kc.base2 >> 8) & 0xFFu;
-                    const uint32_t top = kc.mode() == 4 ? 240u : 252u;
+                    const uint32_t top = 256u - (1u << kc.mode());
                     flush = __ballot(lane < D / 2 && (min(b0, b1) < kmin || max(b0, b1) > top)) != 0;
                 }
                 base_pairs<D>(kc, S.bp);

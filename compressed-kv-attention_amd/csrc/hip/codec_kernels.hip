@@ -53,23 +53,24 @@ __global__ __launch_bounds__(kThreads) void decode_blocks_kernel(const uint8_t *
         for (int i = int(threadIdx.x); i < total; i += kThreads) o[i] = uint16_t(load_u16_any(p + 2 * i));
         return;
     }
-    const bool four = h.mode == 4;
+    const int mode = h.mode;
+    const int U = code_unit(mode);
+    const uint32_t sentinel = (1u << mode) - 1u;
     const uint8_t *base = p;
     const uint8_t *sm = p + dim;
     const uint8_t *codes = sm + size_t(h.n_tokens) * size_t(dim);
-    const uint8_t *esc = codes + exp_payload_bytes(h.n_tokens, dim, h.mode);
-    const int units = total / 4; // dim % 4 == 0
+    const uint8_t *esc = codes + exp_payload_bytes(h.n_tokens, dim, mode);
+    const int units = total / U; // dim % 4 == 0 (dim % 8 == 0 for 3-bit codes)
     int carry = 0;
     uint32_t bad = 0;
     for (int r = 0; r < units; r += kThreads) {
         const int u = r + int(threadIdx.x);
         const bool act = u < units;
-        uint32_t smw = 0, cw = 0;
+        uint32_t cw = 0;
         int cnt = 0;
         if (act) {
-            smw = load_u32_any(sm + 4 * size_t(u));
-            cw = four ? load_u16_any(codes + 2 * size_t(u)) : uint32_t(codes[u]);
-            cnt = four ? sentinels4(cw) : sentinels2(cw);
+            cw = load_codes(codes, mode, u);
+            cnt = unit_sentinels(cw, mode);
         }
         int rank = carry;
         if (h.n_escape > 0) {
@@ -78,13 +79,13 @@ __global__ __launch_bounds__(kThreads) void decode_blocks_kernel(const uint8_t *
             carry += tot;
         }
         if (act) {
-            const int e0 = 4 * u;
+            const int e0 = U * u;
             const int d0 = e0 % dim;
-            uint32_t v[4];
+            uint32_t v[8];
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const uint32_t code = four ? (cw >> (4 * k)) & 15u : (cw >> (2 * k)) & 3u;
-                const uint32_t sentinel = four ? 15u : 3u;
+            for (int k = 0; k < 8; ++k) {
+                if (k >= U) break;
+                const uint32_t code = unit_code(cw, mode, k);
                 if (code == sentinel) {
                     if (rank < h.n_escape) {
                         v[k] = load_u16_any(esc + 2 * size_t(rank));
@@ -94,13 +95,15 @@ __global__ __launch_bounds__(kThreads) void decode_blocks_kernel(const uint8_t *
                     }
                     ++rank;
                 } else {
-                    v[k] = bf16_join(uint32_t(base[d0 + k]) + code, (smw >> (8 * k)) & 0xFFu);
+                    v[k] = bf16_join(uint32_t(base[d0 + k]) + code, load_u8(sm + e0 + k));
                 }
             }
-            uint2 w;
-            w.x = v[0] | (v[1] << 16);
-            w.y = v[2] | (v[3] << 16);
-            *reinterpret_cast<uint2 *>(o + e0) = w;
+            for (int k = 0; k < U; k += 4) {
+                uint2 w;
+                w.x = v[k] | (v[k + 1] << 16);
+                w.y = v[k + 2] | (v[k + 3] << 16);
+                *reinterpret_cast<uint2 *>(o + e0 + k) = w;
+            }
         }
     }
     if (bad) atomicOr(status, bad);
@@ -139,7 +142,10 @@ __device__ __forceinline__ EncRows job_rows(const AppendJobDev &j, int b, int bt
 }
 
 // ------------------------------------------------------------ encode: stats --
-// bases: [n_blocks][2][dim] (2-bit window base, 4-bit window base).
+// bases: [n_blocks][3][dim] (2-, 3- and 4-bit window bases). `modes` has bit
+// m set for each coded mode m that may be chosen (raw always may): bits 2
+// and 4 give the reference's encoder; bit 3 adds the 3-bit extension, taken
+// only when dim % 8 == 0.
 // Thread i of the workgroup (at most 128 threads) owns channels i, i + 128:
 // it counts a channel's exponents in a private column of LDS byte counters
 // (four bins per dword; a block has at most 255 tokens, so a byte cannot
@@ -150,10 +156,12 @@ __device__ __forceinline__ EncRows job_rows(const AppendJobDev &j, int b, int bt
 constexpr int kHistStride = 65; // dwords per channel column (64 + 1: columns start on different banks)
 
 __device__ __forceinline__ void encode_stats_block(uint32_t *hist, int *esc_part, const EncRows src, int n, int dim,
-                                                   EncBlockMeta *__restrict__ meta, uint8_t *__restrict__ bases) {
+                                                   EncBlockMeta *__restrict__ meta, uint8_t *__restrict__ bases,
+                                                   int modes) {
     const int tid = int(threadIdx.x);
     uint32_t *h = hist + tid * kHistStride;
-    int esc2 = 0, esc4 = 0;
+    int esc[3] = {0, 0, 0}; // escapes of the 2-, 3- and 4-bit codes
+    const int nwin = (modes & 8) && dim % 8 == 0 ? 3 : 2; // windows computed (the 3-bit one only when allowed)
     const int nthr = min(int(blockDim.x), 128); // threads owning channel columns
     for (int d = tid; tid < nthr && d < dim; d += nthr) {
         int e_lo = 255, e_hi = 0;
@@ -180,9 +188,9 @@ __device__ __forceinline__ void encode_stats_block(uint32_t *hist, int *esc_part
         count_rows(src.a, na);
         count_rows(src.b, n - na);
         auto count = [&](int b) { return int((h[b >> 2] >> (8 * (b & 3))) & 0xFFu); };
-#pragma unroll
-        for (int bi = 0; bi < 2; ++bi) {
-            const int width = bi == 0 ? 3 : 15; // codes 0..2^bits-2
+        for (int wi = 0; wi < nwin; ++wi) {
+            const int bi = wi == 0 ? 0 : (wi == 1 && nwin == 2 ? 2 : wi); // 2-, (3-,) 4-bit
+            const int width = (4 << bi) - 1; // codes 0..2^bits-2
             const int lo = min(max(0, e_lo - width + 1), 256 - width);
             const int hi = min(e_hi, 256 - width);
             int cov = 0;
@@ -196,38 +204,37 @@ __device__ __forceinline__ void encode_stats_block(uint32_t *hist, int *esc_part
                 }
             }
             bases[size_t(bi) * size_t(dim) + size_t(d)] = uint8_t(best_base);
-            if (bi == 0)
-                esc2 += n - best;
-            else
-                esc4 += n - best;
+            esc[bi] += n - best;
         }
     }
     // escape counts of the whole block
     for (int o = 32; o > 0; o >>= 1) {
-        esc2 += __shfl_xor(esc2, o);
-        esc4 += __shfl_xor(esc4, o);
+#pragma unroll
+        for (int bi = 0; bi < 3; ++bi) esc[bi] += __shfl_xor(esc[bi], o);
     }
     const int w = tid >> 6, nw = int(blockDim.x) >> 6;
     if ((tid & 63) == 0) {
-        esc_part[2 * w] = esc2;
-        esc_part[2 * w + 1] = esc4;
+#pragma unroll
+        for (int bi = 0; bi < 3; ++bi) esc_part[3 * w + bi] = esc[bi];
     }
     __syncthreads();
     if (tid == 0) {
-        int e2 = 0, e4 = 0;
+        int cand_esc[3] = {0, 0, 0};
         for (int i = 0; i < nw; ++i) {
-            e2 += esc_part[2 * i];
-            e4 += esc_part[2 * i + 1];
+#pragma unroll
+            for (int bi = 0; bi < 3; ++bi) cand_esc[bi] += esc_part[3 * i + bi];
         }
-        // codec.cpp:94-103: raw, then 2-bit, then 4-bit; replace when smaller,
-        // or on a tie when the best is not raw and has more escapes (or equal
-        // escapes and more bits).
+        // codec.cpp:94-103: raw, then the coded modes by width; replace when
+        // smaller, or on a tie when the best is not raw and has more escapes
+        // (or equal escapes and more bits). With the 3-bit mode this is the
+        // order of the reference's sizer (analyze_exponents.py:142-143:
+        // smaller, then raw, then fewer escapes, then narrower codes).
         int best_mode = 0, best_esc = 0;
         int64_t best_bytes = block_bytes(0, n, 0, dim);
-        const int cand_esc[2] = {e2, e4};
 #pragma unroll
-        for (int bi = 0; bi < 2; ++bi) {
-            const int mode = bi == 0 ? 2 : 4;
+        for (int bi = 0; bi < 3; ++bi) {
+            const int mode = bi + 2;
+            if (!(modes & (1 << mode)) || (mode == 3 && nwin < 3)) continue;
             const int64_t by = block_bytes(mode, n, cand_esc[bi], dim);
             const bool smaller = by < best_bytes;
             const bool tie_win = by == best_bytes && best_mode != 0 &&
@@ -250,30 +257,30 @@ __device__ __forceinline__ void encode_stats_block(uint32_t *hist, int *esc_part
 // the per-wave escape sums.
 __host__ __device__ constexpr int stats_threads(int dim) { return dim > 64 ? 128 : 64; }
 __host__ __device__ constexpr size_t stats_lds_bytes(int dim) {
-    return size_t(stats_threads(dim)) * kHistStride * sizeof(uint32_t) + 2 * kWaves * sizeof(int);
+    return size_t(stats_threads(dim)) * kHistStride * sizeof(uint32_t) + 3 * kWaves * sizeof(int);
 }
 
 __global__ __launch_bounds__(128) void encode_stats_kernel(const uint16_t *__restrict__ kv, int seq, int dim,
                                                                int bt, EncBlockMeta *__restrict__ meta,
-                                                               uint8_t *__restrict__ bases) {
+                                                               uint8_t *__restrict__ bases, int modes) {
     const int b = int(blockIdx.x);
     const int t0 = b * bt;
     const EncRows src{kv + size_t(t0) * size_t(dim), kv + size_t(t0) * size_t(dim), 0};
     extern __shared__ uint32_t stats_lds[];
     encode_stats_block(stats_lds, reinterpret_cast<int *>(stats_lds + blockDim.x * kHistStride), src,
-                       min(bt, seq - t0), dim, meta + b, bases + size_t(b) * 2 * size_t(dim));
+                       min(bt, seq - t0), dim, meta + b, bases + size_t(b) * 3 * size_t(dim), modes);
 }
 
 __global__ __launch_bounds__(128) void append_stats_kernel(const AppendJobDev *__restrict__ jobs, int n_jobs,
                                                                int dim, int bt, EncBlockMeta *__restrict__ meta,
-                                                               uint8_t *__restrict__ bases) {
+                                                               uint8_t *__restrict__ bases, int modes) {
     const int g = int(blockIdx.x);
     const AppendJobDev j = jobs[find_job(jobs, n_jobs, g)];
     const int b = g - j.blk0;
     extern __shared__ uint32_t stats_lds[];
     encode_stats_block(stats_lds, reinterpret_cast<int *>(stats_lds + blockDim.x * kHistStride),
                        job_rows(j, b, bt, dim), min(bt, j.seq - b * bt), dim, meta + g,
-                       bases + size_t(g) * 2 * size_t(dim));
+                       bases + size_t(g) * 3 * size_t(dim), modes);
 }
 
 // ------------------------------------------------------------- encode: scan --
@@ -342,10 +349,10 @@ __global__ __launch_bounds__(1024) void append_scan_kernel(const AppendJobDev *_
 }
 
 // ------------------------------------------------------------ encode: write --
-// One block: `p` is its place in the container, `bases2` its two window
-// bases [2][dim].
+// One block: `p` is its place in the container, `bases3` its window bases
+// [3][dim] (2-, 3-, 4-bit).
 __device__ __forceinline__ void encode_write_block(int *scan_tmp, const EncRows src, int n, int dim,
-                                                   const EncBlockMeta m, const uint8_t *__restrict__ bases2,
+                                                   const EncBlockMeta m, const uint8_t *__restrict__ bases3,
                                                    uint8_t *__restrict__ p, uint32_t *__restrict__ status) {
     const int total = n * dim;
     if (threadIdx.x == 0) {
@@ -368,54 +375,59 @@ __device__ __forceinline__ void encode_write_block(int *scan_tmp, const EncRows 
         }
         return;
     }
-    const bool four = m.mode == 4;
-    const int width = four ? 15 : 3;
-    const uint8_t *bsrc = bases2 + (four ? size_t(dim) : 0);
+    const int mode = m.mode;
+    const int U = code_unit(mode); // elements per thread and step: 4, or 8 for 3-bit codes (3 bytes)
+    const int width = (1 << mode) - 1;
+    const uint8_t *bsrc = bases3 + size_t(mode - 2) * size_t(dim);
     for (int d = int(threadIdx.x); d < dim; d += kThreads) p[d] = bsrc[d];
     uint8_t *sm = p + dim;
     uint8_t *codes = sm + size_t(total);
-    uint8_t *esc = codes + exp_payload_bytes(n, dim, m.mode);
-    const int units = total / 4;
+    uint8_t *esc = codes + exp_payload_bytes(n, dim, mode);
+    const int units = total / U;
     int carry = 0;
     for (int r = 0; r < units; r += kThreads) {
         const int u = r + int(threadIdx.x);
         const bool act = u < units;
-        uint32_t c[4] = {0, 0, 0, 0};
-        uint32_t hv[4] = {0, 0, 0, 0};
+        uint32_t cw = 0;
         int cnt = 0;
         if (act) {
-            const int e0 = 4 * u;
+            const int e0 = U * u;
             const int d0 = e0 % dim;
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
+            for (int k = 0; k < 8; ++k) {
+                if (k >= U) break;
                 const uint32_t h = src.at(e0 + k);
-                hv[k] = h;
                 sm[e0 + k] = uint8_t(((h >> 8) & 0x80u) | (h & 0x7Fu));
                 const int delta = int((h >> 7) & 0xFFu) - int(bsrc[d0 + k]);
-                if (delta >= 0 && delta < width) {
-                    c[k] = uint32_t(delta);
-                } else {
-                    c[k] = uint32_t(width);
-                    ++cnt;
-                }
+                uint32_t c = uint32_t(width);
+                if (delta >= 0 && delta < width) c = uint32_t(delta);
+                else ++cnt;
+                cw |= c << (mode * k);
             }
-            if (four) {
-                codes[2 * u] = uint8_t(c[0] | (c[1] << 4));
-                codes[2 * u + 1] = uint8_t(c[2] | (c[3] << 4));
+            if (mode == 4) {
+                codes[2 * u] = uint8_t(cw);
+                codes[2 * u + 1] = uint8_t(cw >> 8);
+            } else if (mode == 2) {
+                codes[u] = uint8_t(cw);
             } else {
-                codes[u] = uint8_t(c[0] | (c[1] << 2) | (c[2] << 4) | (c[3] << 6));
+                codes[3 * u] = uint8_t(cw);
+                codes[3 * u + 1] = uint8_t(cw >> 8);
+                codes[3 * u + 2] = uint8_t(cw >> 16);
             }
         }
         int tot = 0;
         int rank = carry + block_excl_scan<kWaves>(cnt, scan_tmp, &tot);
         carry += tot;
         if (act && cnt) {
+            const int e0 = U * u;
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                if (c[k] == uint32_t(width)) {
+            for (int k = 0; k < 8; ++k) {
+                if (k >= U) break;
+                if (unit_code(cw, mode, k) == uint32_t(width)) {
+                    const uint32_t h = src.at(e0 + k);
                     if (rank < m.n_escape) {
-                        esc[2 * rank] = uint8_t(hv[k] & 0xFF);
-                        esc[2 * rank + 1] = uint8_t(hv[k] >> 8);
+                        esc[2 * rank] = uint8_t(h & 0xFF);
+                        esc[2 * rank + 1] = uint8_t(h >> 8);
                     }
                     ++rank;
                 }
@@ -435,7 +447,7 @@ __global__ __launch_bounds__(kThreads) void encode_write_kernel(const uint16_t *
     const int t0 = b * bt;
     const EncRows src{kv + size_t(t0) * size_t(dim), kv + size_t(t0) * size_t(dim), 0};
     __shared__ int scan_tmp[kWaves];
-    encode_write_block(scan_tmp, src, min(bt, seq - t0), dim, meta[b], bases + size_t(b) * 2 * size_t(dim),
+    encode_write_block(scan_tmp, src, min(bt, seq - t0), dim, meta[b], bases + size_t(b) * 3 * size_t(dim),
                        out + offs[b], status);
 }
 
@@ -448,7 +460,7 @@ __global__ __launch_bounds__(kThreads) void append_write_kernel(const AppendJobD
     const int b = g - j.blk0;
     __shared__ int scan_tmp[kWaves];
     encode_write_block(scan_tmp, job_rows(j, b, bt, dim), min(bt, j.seq - b * bt), dim, meta[g],
-                       bases + size_t(g) * 2 * size_t(dim), j.out + j.offs[b], status);
+                       bases + size_t(g) * 3 * size_t(dim), j.out + j.offs[b], status);
 }
 
 // The raw rows of each job's new trailing partial block that are not in
@@ -468,13 +480,13 @@ __global__ __launch_bounds__(kThreads) void append_tail_kernel(const AppendJobDe
 // and the index entries around it, then stores the raw rows kept for the
 // next append (rows the block did not read from the tail).
 __global__ __launch_bounds__(kThreads) void append_one_kernel(const AppendJobDev *__restrict__ jobs, int dim,
-                                                             int bt, uint32_t *__restrict__ status) {
-    extern __shared__ uint32_t one_lds[]; // stats columns, escape sums, then the two window bases
+                                                             int bt, uint32_t *__restrict__ status, int modes) {
+    extern __shared__ uint32_t one_lds[]; // stats columns, escape sums, then the three window bases
     __shared__ EncBlockMeta meta_s;
     __shared__ int scan_tmp[kWaves];
     const AppendJobDev j = jobs[blockIdx.x];
     int *esc_part = reinterpret_cast<int *>(one_lds + stats_threads(dim) * kHistStride);
-    uint8_t *bases_s = reinterpret_cast<uint8_t *>(esc_part + 2 * kWaves);
+    uint8_t *bases_s = reinterpret_cast<uint8_t *>(esc_part + 3 * kWaves);
     const int64_t base = j.rebase ? j.offs[0] : 0;
     if (j.nb == 0) { // an empty container: its terminal index entry
         if (threadIdx.x == 0) {
@@ -484,7 +496,7 @@ __global__ __launch_bounds__(kThreads) void append_one_kernel(const AppendJobDev
         return;
     }
     const EncRows rows = job_rows(j, 0, bt, dim);
-    encode_stats_block(one_lds, esc_part, rows, j.seq, dim, &meta_s, bases_s);
+    encode_stats_block(one_lds, esc_part, rows, j.seq, dim, &meta_s, bases_s, modes);
     __syncthreads();
     const EncBlockMeta m = meta_s;
     if (threadIdx.x == 0) {
@@ -502,6 +514,43 @@ __global__ __launch_bounds__(kThreads) void append_one_kernel(const AppendJobDev
 }
 
 // -------------------------------------------------- escape-position index --
+// Element index of every escape of a coded block (mode 2, 3 or 4) whose
+// `total` codes start at `codes`, written to pos[0 .. n_escape); a sentinel
+// count other than n_escape raises kStEscape. All threads of the workgroup
+// call it.
+__device__ __forceinline__ void escape_positions(const uint8_t *codes, int mode, int total, int n_escape,
+                                                 uint16_t *__restrict__ pos, int *scan_tmp,
+                                                 uint32_t *__restrict__ status) {
+    const int U = code_unit(mode);
+    const uint32_t sentinel = (1u << mode) - 1u;
+    const int units = total / U;
+    int carry = 0;
+    for (int r = 0; r < units; r += kThreads) {
+        const int u = r + int(threadIdx.x);
+        const bool act = u < units;
+        uint32_t cw = 0;
+        int cnt = 0;
+        if (act) {
+            cw = load_codes(codes, mode, u);
+            cnt = unit_sentinels(cw, mode);
+        }
+        int tot = 0;
+        int rank = carry + block_excl_scan<kWaves>(cnt, scan_tmp, &tot);
+        carry += tot;
+        if (act && cnt) {
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                if (k >= U) break;
+                if (unit_code(cw, mode, k) == sentinel) {
+                    if (rank < n_escape) pos[rank] = uint16_t(U * u + k);
+                    ++rank;
+                }
+            }
+        }
+    }
+    if (threadIdx.x == 0 && carry != n_escape) atomicOr(status, kStEscape);
+}
+
 // esc0[b] = escape words in blocks before b (raw blocks count 0), one
 // workgroup per tensor. With j.first set, every block is also checked against
 // the index (header inside the container, head_dim, n_tokens equal to the
@@ -566,35 +615,8 @@ __global__ __launch_bounds__(kThreads) void esc_pos_kernel(const EscJob *__restr
         if (threadIdx.x == 0) atomicOr(status, kStTruncated);
         return;
     }
-    const bool four = h.mode == 4;
     const uint8_t *codes = j.blob + off + 8 + dim + size_t(h.n_tokens) * size_t(dim);
-    uint16_t *pos = j.pos + j.esc0[b];
-    const int units = (h.n_tokens * dim) / 4;
-    int carry = 0;
-    for (int r = 0; r < units; r += kThreads) {
-        const int u = r + int(threadIdx.x);
-        const bool act = u < units;
-        uint32_t cw = 0;
-        int cnt = 0;
-        if (act) {
-            cw = four ? load_u16_any(codes + 2 * size_t(u)) : uint32_t(codes[u]);
-            cnt = four ? sentinels4(cw) : sentinels2(cw);
-        }
-        int tot = 0;
-        int rank = carry + block_excl_scan<kWaves>(cnt, scan_tmp, &tot);
-        carry += tot;
-        if (act && cnt) {
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const uint32_t code = four ? (cw >> (4 * k)) & 15u : (cw >> (2 * k)) & 3u;
-                if (code == (four ? 15u : 3u)) {
-                    if (rank < h.n_escape) pos[rank] = uint16_t(4 * u + k);
-                    ++rank;
-                }
-            }
-        }
-    }
-    if (threadIdx.x == 0 && carry != h.n_escape) atomicOr(status, kStEscape);
+    escape_positions(codes, h.mode, h.n_tokens * dim, h.n_escape, j.pos + j.esc0[b], scan_tmp, status);
 }
 
 // Plan update after appends. Workgroups [0, n_jobs), one per tensor: the
@@ -654,35 +676,8 @@ __global__ __launch_bounds__(kThreads) void plan_refresh_kernel(const EscJob *__
     __syncthreads();
     if (!ok_s) return;
     const BlockHdr h = read_hdr(j.blob + off);
-    const bool four = h.mode == 4;
     const uint8_t *codes = j.blob + off + 8 + dim + size_t(h.n_tokens) * size_t(dim);
-    uint16_t *pos = j.pos + e0;
-    const int units = (h.n_tokens * dim) / 4;
-    int carry = 0;
-    for (int r = 0; r < units; r += kThreads) {
-        const int u = r + int(threadIdx.x);
-        const bool act = u < units;
-        uint32_t cw = 0;
-        int cnt = 0;
-        if (act) {
-            cw = four ? load_u16_any(codes + 2 * size_t(u)) : uint32_t(codes[u]);
-            cnt = four ? sentinels4(cw) : sentinels2(cw);
-        }
-        int tot = 0;
-        int rank = carry + block_excl_scan<kWaves>(cnt, scan_tmp, &tot);
-        carry += tot;
-        if (act && cnt) {
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const uint32_t code = four ? (cw >> (4 * k)) & 15u : (cw >> (2 * k)) & 3u;
-                if (code == (four ? 15u : 3u)) {
-                    if (rank < h.n_escape) pos[rank] = uint16_t(4 * u + k);
-                    ++rank;
-                }
-            }
-        }
-    }
-    if (threadIdx.x == 0 && carry != h.n_escape) atomicOr(status, kStEscape);
+    escape_positions(codes, h.mode, h.n_tokens * dim, h.n_escape, j.pos + e0, scan_tmp, status);
 }
 
 // y = expf(x) in the forms the attention kernels evaluate it (all must equal
@@ -719,9 +714,9 @@ hipError_t decode(const uint8_t *blob, uint64_t bytes, const int64_t *offs, cons
 
 hipError_t encode(const uint16_t *kv, int seq, int dim, int bt, int n_blocks, EncBlockMeta *meta, uint8_t *bases,
                   int64_t *offs, int32_t *first, uint8_t *out, uint32_t *status, hipStream_t s, bool rebase,
-                  int tok0) {
+                  int tok0, int modes) {
     hipLaunchKernelGGL(encode_stats_kernel, dim3(n_blocks), dim3(stats_threads(dim)), stats_lds_bytes(dim), s, kv, seq,
-                       dim, bt, meta, bases);
+                       dim, bt, meta, bases, modes);
     hipLaunchKernelGGL(encode_scan_kernel, dim3(1), dim3(1024), 0, s, meta, n_blocks, bt, seq, offs, first,
                        rebase ? 1 : 0, tok0);
     hipLaunchKernelGGL(encode_write_kernel, dim3(n_blocks), dim3(kThreads), 0, s, kv, seq, dim, bt, meta, bases,
@@ -730,16 +725,16 @@ hipError_t encode(const uint16_t *kv, int seq, int dim, int bt, int n_blocks, En
 }
 
 hipError_t append(const AppendJobDev *jobs, int n_jobs, int total_blocks, int dim, int bt, EncBlockMeta *meta,
-                  uint8_t *bases, uint32_t *status, hipStream_t s, bool one_block) {
+                  uint8_t *bases, uint32_t *status, hipStream_t s, bool one_block, int modes) {
     if (n_jobs <= 0) return hipSuccess;
     if (one_block) {
-        const size_t lds = stats_lds_bytes(dim) + 2 * size_t(dim);
-        hipLaunchKernelGGL(append_one_kernel, dim3(n_jobs), dim3(kThreads), lds, s, jobs, dim, bt, status);
+        const size_t lds = stats_lds_bytes(dim) + 3 * size_t(dim);
+        hipLaunchKernelGGL(append_one_kernel, dim3(n_jobs), dim3(kThreads), lds, s, jobs, dim, bt, status, modes);
         return hipGetLastError();
     }
     if (total_blocks > 0)
         hipLaunchKernelGGL(append_stats_kernel, dim3(total_blocks), dim3(stats_threads(dim)), stats_lds_bytes(dim), s,
-                           jobs, n_jobs, dim, bt, meta, bases);
+                           jobs, n_jobs, dim, bt, meta, bases, modes);
     hipLaunchKernelGGL(append_scan_kernel, dim3(n_jobs), dim3(1024), 0, s, jobs, meta, bt);
     if (total_blocks > 0)
         hipLaunchKernelGGL(append_write_kernel, dim3(total_blocks), dim3(kThreads), 0, s, jobs, n_jobs, dim, bt, meta,

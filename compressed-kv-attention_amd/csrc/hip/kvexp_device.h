@@ -4,6 +4,10 @@
 // Container format (reference include/kvexp/codec.hpp:12-36): blocks of
 //   u8 mode (0 raw, 2, 4) | u8 n_tokens | u16 n_escape | u16 head_dim | u16 0
 // then raw BF16 rows, or base[dim], sm[n*dim], packed codes, u16 escapes.
+// Mode 3 is this library's format extension (3-bit codes, sentinel 7,
+// element i in bits [3i, 3i + 3) of the little-endian code bytes, head_dim a
+// multiple of 8 so that rows start on a byte); the reference's readers
+// reject it, and the encoders write it only when asked to.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -65,7 +69,7 @@ __host__ __device__ __forceinline__ int exp_payload_bytes(int n, int dim, int bi
 // Byte size of a block from its header, or -1 when the mode is unknown.
 __host__ __device__ __forceinline__ int64_t block_bytes(int mode, int n, int n_escape, int dim) {
     if (mode == 0) return 8 + 2 * int64_t(n) * dim;
-    if (mode != 2 && mode != 4) return -1;
+    if (mode != 2 && mode != 4 && !(mode == 3 && dim % 8 == 0)) return -1;
     return 8 + int64_t(dim) + int64_t(n) * dim + exp_payload_bytes(n, dim, mode) + 2 * int64_t(n_escape);
 }
 
@@ -227,6 +231,27 @@ __device__ __forceinline__ int sentinels4(uint32_t x) {
 // Number of 2-bit codes equal to 3 (sentinels) in a dword of 16 codes.
 __device__ __forceinline__ int sentinels2(uint32_t x) {
     return __builtin_popcount(x & (x >> 1) & 0x55555555u);
+}
+// Number of 3-bit codes equal to 7 (sentinels) in the low 24 bits (8 codes).
+__device__ __forceinline__ int sentinels3(uint32_t x) {
+    return __builtin_popcount(x & (x >> 1) & (x >> 2) & 0x249249u);
+}
+
+// Code units of a coded block: the codes of elements [U u, U u + U), with
+// U = 4 for 2- and 4-bit codes (one byte or two) and 8 for 3-bit codes
+// (three bytes); code k of a unit is bits [mode k, mode k + mode).
+__device__ __forceinline__ int code_unit(int mode) { return mode == 3 ? 8 : 4; }
+__device__ __forceinline__ uint32_t load_codes(const uint8_t *codes, int mode, int u) {
+    if (mode == 4) return load_u16_any(codes + 2 * size_t(u));
+    if (mode == 2) return codes[u];
+    const uint8_t *p = codes + 3 * size_t(u);
+    return uint32_t(p[0]) | (uint32_t(p[1]) << 8) | (uint32_t(p[2]) << 16);
+}
+__device__ __forceinline__ int unit_sentinels(uint32_t cw, int mode) {
+    return mode == 4 ? sentinels4(cw) : (mode == 2 ? sentinels2(cw) : sentinels3(cw));
+}
+__device__ __forceinline__ uint32_t unit_code(uint32_t cw, int mode, int k) {
+    return (cw >> (mode * k)) & ((1u << mode) - 1u);
 }
 
 } // namespace kvexp_dev

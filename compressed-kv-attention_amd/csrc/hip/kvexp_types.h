@@ -8,7 +8,7 @@ namespace kvexp_dev {
 // Status bits a kernel raises in the context's status word.
 enum : uint32_t {
     kStHeader = 1u << 0,    // header past the end, dim mismatch or n_tokens == 0
-    kStMode = 1u << 1,      // mode not in {0, 2, 4}
+    kStMode = 1u << 1,      // mode not in {0, 2, 4} (nor 3 with head_dim % 8 == 0)
     kStTruncated = 1u << 2, // payload past the end of the container
     kStEscape = 1u << 3,    // more sentinels than n_escape
     kStIndex = 1u << 4,     // block index disagrees with the headers

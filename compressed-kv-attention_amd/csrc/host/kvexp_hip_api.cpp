@@ -28,10 +28,10 @@ namespace kvexp_launch {
 hipError_t decode(const uint8_t *blob, uint64_t bytes, const int64_t *offs, const int32_t *first, int n_blocks,
                   int seq, int dim, uint16_t *out, uint32_t *status, hipStream_t s);
 hipError_t encode(const uint16_t *kv, int seq, int dim, int bt, int n_blocks, EncBlockMeta *meta, uint8_t *bases,
-                  int64_t *offs, int32_t *first, uint8_t *out, uint32_t *status, hipStream_t s, bool rebase = false,
-                  int tok0 = 0);
+                  int64_t *offs, int32_t *first, uint8_t *out, uint32_t *status, hipStream_t s, bool rebase,
+                  int tok0, int modes);
 hipError_t append(const kvexp_dev::AppendJobDev *jobs, int n_jobs, int total_blocks, int dim, int bt,
-                  EncBlockMeta *meta, uint8_t *bases, uint32_t *status, hipStream_t s, bool one_block);
+                  EncBlockMeta *meta, uint8_t *bases, uint32_t *status, hipStream_t s, bool one_block, int modes);
 hipError_t attention(bool xkv, int order, const HeadDev *heads, const WorkItem *items, int n_items,
                      const int32_t *merge_ids, int n_merge, const uint16_t *q, float *out, float *lse, float *ws,
                      int dim, uint32_t *status, hipStream_t s);
@@ -126,7 +126,8 @@ struct HostBlock {
 
 inline unsigned rd16(const uint8_t *p) { return unsigned(p[0]) | (unsigned(p[1]) << 8); }
 
-// parse_block (scan.hpp:28-66): validation order and messages.
+// parse_block (scan.hpp:28-66): validation order and messages. Mode 3
+// (3-bit codes, head_dim a multiple of 8) is this library's extension.
 HostBlock parse_block_host(const uint8_t *blob, size_t bytes, size_t at, int dim) {
     if (bytes - at < 8) fail(KVEXP_HIP_FORMAT_ERROR, "truncated xkv block header");
     const uint8_t *p = blob + at;
@@ -140,7 +141,8 @@ HostBlock parse_block_host(const uint8_t *blob, size_t bytes, size_t at, int dim
         b.next = body + nb;
         return b;
     }
-    if (b.mode != 2 && b.mode != 4) fail(KVEXP_HIP_FORMAT_ERROR, "unknown xkv block mode");
+    if (b.mode != 2 && b.mode != 4 && !(b.mode == 3 && dim % 8 == 0))
+        fail(KVEXP_HIP_FORMAT_ERROR, "unknown xkv block mode");
     const size_t need = size_t(dim) + size_t(b.n_tokens) * size_t(dim) +
                         size_t((b.n_tokens * dim * b.mode + 7) / 8) + size_t(b.n_escape) * 2u;
     if (bytes - body < need) fail(KVEXP_HIP_FORMAT_ERROR, "truncated coded xkv block");
@@ -197,6 +199,7 @@ struct kvexp_hip_ctx {
     DevBuf enc_meta, enc_bases, enc_off, enc_first, app_jobs;
     size_t enc_meta_cap = 0, enc_bases_cap = 0, enc_index_cap = 0, app_jobs_cap = 0;
     int cu_count = 0;
+    int enc_modes = int(KVEXP_HIP_MODES_REFERENCE); // coded modes the encoders may choose
     // pinned host staging for the plan builder's reads of block indexes
     std::mutex pinned_mu;
     void *pinned = nullptr;
@@ -406,6 +409,19 @@ int kvexp_hip_ctx_destroy(kvexp_hip_ctx *ctx) {
     });
 }
 
+int kvexp_hip_set_encoder_modes(kvexp_hip_ctx *ctx, unsigned modes) {
+    return guarded([&] {
+        if (ctx == nullptr) fail(KVEXP_HIP_INVALID_ARGUMENT, "kvexp_hip_set_encoder_modes: null context");
+        const unsigned known = KVEXP_HIP_MODE_2BIT | KVEXP_HIP_MODE_3BIT | KVEXP_HIP_MODE_4BIT;
+        if (modes & ~known) fail(KVEXP_HIP_INVALID_ARGUMENT, "kvexp_hip_set_encoder_modes: unknown mode bits");
+        ctx->enc_modes = int(modes);
+    });
+}
+
+int kvexp_hip_get_encoder_modes(kvexp_hip_ctx *ctx) {
+    return ctx == nullptr ? -1 : ctx->enc_modes;
+}
+
 // ============================================================ size model ==
 int kvexp_hip_exp_payload_bytes(int n, int dim, int bits) { return (n * dim * bits + 7) / 8; }
 int kvexp_hip_coded_block_bytes(int n, int dim, int bits, int esc) {
@@ -458,7 +474,7 @@ int kvexp_hip_encode(kvexp_hip_ctx *ctx, const uint16_t *d_kv, int seq, int dim,
         hipStream_t s = static_cast<hipStream_t>(stream);
         const int nb = kvexp_hip_block_count(seq, bt);
         grow(ctx->enc_meta, ctx->enc_meta_cap, size_t(nb) * sizeof(EncBlockMeta));
-        grow(ctx->enc_bases, ctx->enc_bases_cap, size_t(nb) * 2u * size_t(dim));
+        grow(ctx->enc_bases, ctx->enc_bases_cap, size_t(nb) * 3u * size_t(dim));
         int64_t *offs = d_offsets;
         int32_t *first = d_first_token;
         if (offs == nullptr || first == nullptr) {
@@ -472,7 +488,8 @@ int kvexp_hip_encode(kvexp_hip_ctx *ctx, const uint16_t *d_kv, int seq, int dim,
             if (first == nullptr) first = ctx->enc_first.as<int32_t>();
         }
         HIPX(kvexp_launch::encode(d_kv, seq, dim, bt, nb, ctx->enc_meta.as<EncBlockMeta>(),
-                                  ctx->enc_bases.as<uint8_t>(), offs, first, d_out, ctx->status.as<uint32_t>(), s));
+                                  ctx->enc_bases.as<uint8_t>(), offs, first, d_out, ctx->status.as<uint32_t>(), s,
+                                  false, 0, ctx->enc_modes));
         if (bytes_out != nullptr) {
             int64_t total = 0;
             uint32_t st = 0;
@@ -554,13 +571,13 @@ void run_append(kvexp_hip_ctx *ctx, const kvexp_hip_append_job *jobs, int n_jobs
     // every job encodes at most one block (a decode step): one fused launch
     const bool one_block = std::all_of(dj.begin(), dj.end(), [](const AppendJobDev &j) { return j.nb <= 1; });
     grow(ctx->enc_meta, ctx->enc_meta_cap, size_t(std::max(blocks, 1)) * sizeof(EncBlockMeta));
-    grow(ctx->enc_bases, ctx->enc_bases_cap, size_t(std::max(blocks, 1)) * 2u * size_t(dim));
+    grow(ctx->enc_bases, ctx->enc_bases_cap, size_t(std::max(blocks, 1)) * 3u * size_t(dim));
     grow(ctx->app_jobs, ctx->app_jobs_cap, dj.size() * sizeof(AppendJobDev));
     // pageable source: the runtime has consumed it when the call returns
     HIPX(hipMemcpyAsync(ctx->app_jobs.p, dj.data(), dj.size() * sizeof(AppendJobDev), hipMemcpyHostToDevice, s));
     HIPX(kvexp_launch::append(ctx->app_jobs.as<AppendJobDev>(), int(dj.size()), blocks, dim, bt,
                               ctx->enc_meta.as<EncBlockMeta>(), ctx->enc_bases.as<uint8_t>(),
-                              ctx->status.as<uint32_t>(), s, one_block));
+                              ctx->status.as<uint32_t>(), s, one_block, ctx->enc_modes));
 }
 
 void check_encoder_status(kvexp_hip_ctx *ctx, hipStream_t s) {

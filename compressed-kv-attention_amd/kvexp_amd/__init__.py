@@ -23,6 +23,9 @@ HEADER = os.path.join(ROOT, "include", "kvexp_hip.h")
 
 ORDER_SCALAR = 0
 ORDER_DPBF16 = 1
+# coded block modes the encoders may choose (kvexp_hip_set_encoder_modes)
+MODE_2BIT, MODE_3BIT, MODE_4BIT = 4, 8, 16
+MODES_REFERENCE = MODE_2BIT | MODE_4BIT
 
 _KIND = {1: "invalid_argument", 2: "runtime_error", 3: "logic_error", 4: "unsupported", 5: "device_error",
          6: "capacity"}
@@ -105,6 +108,8 @@ def lib() -> C.CDLL:
     L.kvexp_hip_suggest_splits.argtypes = [vp, i32, i32, i32]
     L.kvexp_hip_suggest_splits_for.argtypes = [vp, i32, i32, i32, i32, i32, i32]
     L.kvexp_hip_suggest_splits_batch.argtypes = [vp, i32, vp, i32, i32, i32, i32]
+    L.kvexp_hip_set_encoder_modes.argtypes = [vp, C.c_uint]
+    L.kvexp_hip_get_encoder_modes.argtypes = [vp]
     L.kvexp_hip_attention_run.argtypes = [vp, vp, vp, vp, i32, vp]
     L.kvexp_hip_plan_status.argtypes = [vp, vp]
     L.kvexp_hip_plan_timing.argtypes = [vp, i32]
@@ -286,6 +291,16 @@ class Context:
             pass
 
     # codec ------------------------------------------------------------------
+    def set_encoder_modes(self, modes: int) -> None:
+        """Coded modes this context's encoders may choose: MODES_REFERENCE
+        (encode_bf16's containers, the default) or MODES_REFERENCE | MODE_3BIT
+        (the 3-bit format extension)."""
+        check(lib().kvexp_hip_set_encoder_modes(self.h, modes))
+
+    @property
+    def encoder_modes(self) -> int:
+        return int(lib().kvexp_hip_get_encoder_modes(self.h))
+
     def encode(self, kv, seq: int, dim: int, block: int = 128, stream=None, sync_size: bool = True) -> Encoded:
         """kv: device tensor holding [seq, dim] BF16 bits (int16/bfloat16)."""
         import torch

@@ -84,8 +84,30 @@ int kvexp_hip_build_index(const uint8_t *blob, size_t bytes, int dim, int seq, i
                           int32_t *first_token, int capacity, int *n_blocks);
 
 /* ------------------------------------------------------------- codec ---- */
+/* Coded block modes the context's encoders (kvexp_hip_encode,
+ * kvexp_hip_append, kvexp_hip_append_batch) may choose; raw blocks always
+ * may be chosen. The default, KVEXP_HIP_MODES_REFERENCE, gives encode_bf16's
+ * containers (codec.cpp:84-104). KVEXP_HIP_MODE_3BIT adds this library's
+ * format extension: mode byte 3, 3-bit codes over a 7-exponent window per
+ * channel (code 7 is the escape sentinel), element i of the block in bits
+ * [3i, 3i + 3) of the little-endian code bytes, taken only when head_dim is
+ * a multiple of 8; a block then takes the smallest of raw, 2-, 3- and 4-bit
+ * with ties to raw, fewer escapes, fewer bits (the 3-bit sizing of the
+ * reference's python/analyze_exponents.py:104-157, which its kernels do not
+ * implement). Every reader in this library (decode, index, plans, the
+ * attention kernels) accepts mode 3 blocks; the reference's readers reject
+ * them. Appends to a container should use the setting it was encoded with,
+ * or its blocks differ from a fresh encode. No counterpart in the reference. */
+#define KVEXP_HIP_MODE_2BIT 4u
+#define KVEXP_HIP_MODE_3BIT 8u
+#define KVEXP_HIP_MODE_4BIT 16u
+#define KVEXP_HIP_MODES_REFERENCE (KVEXP_HIP_MODE_2BIT | KVEXP_HIP_MODE_4BIT)
+int kvexp_hip_set_encoder_modes(kvexp_hip_ctx *ctx, unsigned modes);
+/* The context's encoder modes (-1 for a null context). */
+int kvexp_hip_get_encoder_modes(kvexp_hip_ctx *ctx);
+
 /* Encodes d_kv [seq, dim] BF16 (token-major) into d_out, byte-identical to
- * encode_bf16. d_out needs kvexp_hip_encode_bound() bytes. Writes the block
+ * encode_bf16 (with the default encoder modes). d_out needs kvexp_hip_encode_bound() bytes. Writes the block
  * index (n_blocks + 1 entries each) to d_offsets / d_first_token when they
  * are non-NULL. The container size is written to *bytes_out (host) after a
  * synchronisation of `stream` when bytes_out is non-NULL; it is also

@@ -110,16 +110,18 @@ static int window_base(const int *hist, int width, int *covered) {
 /* Mode choice (codec.cpp:75-103): raw first, then 2-bit, then 4-bit; a
  * candidate replaces the current best when strictly smaller, or on a size tie
  * when the best is not raw and it has fewer escapes (or equal escapes and
- * fewer bits). */
+ * fewer bits). With the 3-bit extension allowed (bit 3 of `modes`, head_dim
+ * a multiple of 8) it competes between them, which gives the order of the
+ * reference's sizer (analyze_exponents.py:117-143: smallest container, then
+ * raw, then fewer escapes, then narrower codes). */
 typedef struct {
     int mode, bytes, escapes;
 } mode_choice;
 
-static mode_choice choose_mode(const int *hist, int n, int dim) {
+static mode_choice choose_mode(const int *hist, int n, int dim, unsigned modes) {
     mode_choice best = {0, oracle_raw_block_bytes(n, dim), 0};
-    const int bits_list[2] = {2, 4};
-    for (int bi = 0; bi < 2; ++bi) {
-        const int bits = bits_list[bi];
+    for (int bits = 2; bits <= 4; ++bits) {
+        if (!(modes & (1u << bits)) || (bits == 3 && dim % 8 != 0)) continue;
         const int width = (1 << bits) - 1;
         int esc = 0;
         for (int d = 0; d < dim; ++d) {
@@ -136,9 +138,23 @@ static mode_choice choose_mode(const int *hist, int n, int dim) {
     return best;
 }
 
+/* Code `code` of element i at bits [bits i, bits i + bits) of the code bytes,
+ * least significant bit first (codec.hpp:27-31 for 4 and 2 bits; the same
+ * rule for the 3-bit extension, whose codes may straddle two bytes). */
+static inline void put_code(uint8_t *codes, int i, int bits, int code) {
+    const int bit = i * bits;
+    codes[bit >> 3] |= (uint8_t)(code << (bit & 7));
+    if ((bit & 7) + bits > 8) codes[(bit >> 3) + 1] |= (uint8_t)(code >> (8 - (bit & 7)));
+}
+
 /* encode_bf16 (codec.cpp:39-164), container layout codec.hpp:12-36. */
 int oracle_encode(const uint16_t *kv, int seq, int dim, int block, uint8_t *out, size_t cap,
                   size_t *out_bytes) {
+    return oracle_encode_modes(kv, seq, dim, block, ORACLE_MODES_REFERENCE, out, cap, out_bytes);
+}
+
+int oracle_encode_modes(const uint16_t *kv, int seq, int dim, int block, unsigned modes, uint8_t *out,
+                        size_t cap, size_t *out_bytes) {
     if (kv == NULL || seq <= 0 || dim <= 0 || block <= 0)
         return fail(ST_INVALID, "encode_bf16: empty input");
     if (dim % 4 != 0 || dim > KVEXP_MAX_DIM)
@@ -157,7 +173,7 @@ int oracle_encode(const uint16_t *kv, int seq, int dim, int block, uint8_t *out,
         memset(hist, 0, sizeof(int) * 256 * (size_t)dim);
         for (int t = 0; t < n; ++t)
             for (int d = 0; d < dim; ++d) ++hist[(size_t)d * 256 + bf16_exponent(src[(size_t)t * dim + d])];
-        const mode_choice mc = choose_mode(hist, n, dim);
+        const mode_choice mc = choose_mode(hist, n, dim, modes);
         if (pos + (size_t)mc.bytes > cap) {
             overflow = 1;
             pos += (size_t)mc.bytes;
@@ -197,10 +213,7 @@ int oracle_encode(const uint16_t *kv, int seq, int dim, int block, uint8_t *out,
                 wr_u16(escp + 2 * n_esc, h);
                 ++n_esc;
             }
-            if (bits == 4)
-                codes[i >> 1] |= (uint8_t)(code << ((i & 1) * 4));
-            else
-                codes[i >> 2] |= (uint8_t)(code << ((i & 3) * 2));
+            put_code(codes, i, bits, code);
         }
         if (n_esc != mc.escapes) {
             free(hist);
@@ -237,7 +250,9 @@ static int parse_block(const uint8_t *p, const uint8_t *end, int dim, block_view
         b->next = p + nbytes;
         return ST_OK;
     }
-    if (b->mode != 2 && b->mode != 4) return fail(ST_RUNTIME, "unknown xkv block mode");
+    /* mode 3: the 3-bit extension (head_dim a multiple of 8) */
+    if (b->mode != 2 && b->mode != 4 && !(b->mode == 3 && dim % 8 == 0))
+        return fail(ST_RUNTIME, "unknown xkv block mode");
     const size_t sm_bytes = (size_t)b->n_tokens * (size_t)dim;
     const size_t code_bytes = (size_t)oracle_exp_payload_bytes(b->n_tokens, dim, b->mode);
     const size_t esc_bytes = (size_t)b->n_escape * 2u;
@@ -251,11 +266,17 @@ static int parse_block(const uint8_t *p, const uint8_t *end, int dim, block_view
     return ST_OK;
 }
 
-/* residual_code (scan.hpp:68-75). */
+/* residual_code (scan.hpp:68-75); 3-bit codes as put_code writes them. */
 static inline int residual(const uint8_t *codes, int index, int bits) {
     if (bits == 4) {
         const uint8_t byte = codes[index >> 1];
         return (index & 1) ? (byte >> 4) : (byte & 0x0F);
+    }
+    if (bits == 3) {
+        const int bit = index * 3, sh = bit & 7;
+        unsigned w = codes[bit >> 3];
+        if (sh > 5) w |= (unsigned)codes[(bit >> 3) + 1] << 8;
+        return (int)((w >> sh) & 7u);
     }
     return (codes[index >> 2] >> ((index & 3) * 2)) & 0x03;
 }
@@ -381,6 +402,19 @@ int oracle_container_stats(const uint8_t *blob, size_t bytes, int dim, int64_t *
         if (b.mode == 2) ++*n_2bit;
         if (b.mode == 4) ++*n_4bit;
         if (b.mode != 0) *n_escapes += b.n_escape;
+        p = b.next;
+    }
+    return ST_OK;
+}
+
+int oracle_container_mode_counts(const uint8_t *blob, size_t bytes, int dim, int64_t *counts) {
+    const uint8_t *p = blob, *end = blob + bytes;
+    for (int i = 0; i < 5; ++i) counts[i] = 0;
+    while (p < end) {
+        block_view b;
+        int rc = parse_block(p, end, dim, &b);
+        if (rc) return rc;
+        ++counts[b.mode];
         p = b.next;
     }
     return ST_OK;

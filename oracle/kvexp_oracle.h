@@ -32,7 +32,18 @@ size_t oracle_encode_bound(int seq, int dim, int block);
 /* encode_bf16 (src/codec.cpp:39-164). */
 int oracle_encode(const uint16_t *kv, int seq, int dim, int block, uint8_t *out, size_t cap,
                   size_t *out_bytes);
-/* decode_bf16 (src/codec.cpp:166-174, scan.hpp:79-165). */
+/* encode_bf16 with a choice of coded modes (bit m set: mode m may be
+ * chosen; raw always may). ORACLE_MODES_REFERENCE (2- and 4-bit) is
+ * encode_bf16; adding bit 3 gives the 3-bit format extension (mode byte 3,
+ * codes 0..6 over the window [base, base + 6], 7 the escape sentinel, element
+ * i at bits [3i, 3i + 3) of the code bytes, head_dim a multiple of 8), sized
+ * and chosen as the reference's python/analyze_exponents.py:104-157 sizes it
+ * (its kernels and readers do not implement it). */
+#define ORACLE_MODES_REFERENCE 0x14u
+#define ORACLE_MODE_3BIT 0x08u
+int oracle_encode_modes(const uint16_t *kv, int seq, int dim, int block, unsigned modes, uint8_t *out,
+                        size_t cap, size_t *out_bytes);
+/* decode_bf16 (src/codec.cpp:166-174, scan.hpp:79-165); also reads mode 3. */
 int oracle_decode(const uint8_t *blob, size_t bytes, int seq, int dim, uint16_t *out);
 
 /* Block walk: byte offset and first token of every block the decode-side
@@ -45,6 +56,9 @@ int oracle_block_index(const uint8_t *blob, size_t bytes, int dim, int seq, int6
 /* Per-block statistics of a container: mode histogram and escape count. */
 int oracle_container_stats(const uint8_t *blob, size_t bytes, int dim, int64_t *n_raw,
                            int64_t *n_2bit, int64_t *n_4bit, int64_t *n_escapes);
+
+/* Blocks per mode byte: counts[m] for m in 0..4. */
+int oracle_container_mode_counts(const uint8_t *blob, size_t bytes, int dim, int64_t *counts);
 
 /* attention_decode (src/dispatch.cpp:27-104). backend: 0 scalar, 1 avx2
  * (bit-identical to scalar, attention.hpp:30-39), 2 avx512-bf16 score order

@@ -68,6 +68,8 @@ class Oracle:
         L.oracle_encode_bound.restype = sz
         L.oracle_encode_bound.argtypes = [i32, i32, i32]
         L.oracle_encode.argtypes = [vp, i32, i32, i32, vp, sz, C.POINTER(sz)]
+        L.oracle_encode_modes.argtypes = [vp, i32, i32, i32, C.c_uint, vp, sz, C.POINTER(sz)]
+        L.oracle_container_mode_counts.argtypes = [vp, sz, i32, vp]
         L.oracle_decode.argtypes = [vp, sz, i32, i32, vp]
         L.oracle_block_index.argtypes = [vp, sz, i32, i32, vp, vp, i32, C.POINTER(i32)]
         L.oracle_container_stats.argtypes = [vp, sz, i32] + [C.POINTER(C.c_int64)] * 4
@@ -105,14 +107,27 @@ class Oracle:
         return int(self.L.oracle_encode_bound(seq, dim, block))
 
     # codec ----------------------------------------------------------------
-    def encode(self, kv, seq: int, dim: int, block: int = 128) -> np.ndarray:
+    def encode(self, kv, seq: int, dim: int, block: int = 128, modes: int | None = None) -> np.ndarray:
+        """encode_bf16; with `modes` (bit m: coded mode m may be chosen), the
+        encoder with that choice of modes (0x14 = encode_bf16, 0x1c adds the
+        3-bit extension)."""
         kv = _u16(kv)
         cap = max(self.encode_bound(seq, dim, block), 1)
         out = np.zeros(cap, dtype=np.uint8)
         n = C.c_size_t(0)
-        self._check(self.L.oracle_encode(_p(kv) if kv.size else None, seq, dim, block, _p(out), cap,
-                                         C.byref(n)))
+        src = _p(kv) if kv.size else None
+        if modes is None:
+            self._check(self.L.oracle_encode(src, seq, dim, block, _p(out), cap, C.byref(n)))
+        else:
+            self._check(self.L.oracle_encode_modes(src, seq, dim, block, modes, _p(out), cap, C.byref(n)))
         return out[: n.value].copy()
+
+    def mode_counts(self, blob, dim: int) -> list:
+        """Blocks per mode byte 0..4."""
+        blob = _u8(blob)
+        c = np.zeros(5, dtype=np.int64)
+        self._check(self.L.oracle_container_mode_counts(_p(blob), blob.size, dim, _p(c)))
+        return [int(x) for x in c]
 
     def decode(self, blob, seq: int, dim: int) -> np.ndarray:
         blob = _u8(blob)

@@ -62,7 +62,7 @@ def test_build_index_errors_match_reference_messages(oracle):
     kv = random_kv(rng, 300, 64)
     blob = oracle.encode(kv, 300, 64, 128)
     bad_mode = blob.copy()
-    bad_mode[0] = 3
+    bad_mode[0] = 1  # 3 is the 3-bit extension (dim % 8 == 0), which this library reads
     zero_tok = blob.copy()
     zero_tok[1] = 0
     cases = [(blob[:5], 64, "truncated xkv block header"), (blob[:-3], 64, "truncated coded xkv block"),

@@ -114,7 +114,7 @@ def _damaged(ctx, oracle, mutate):
 
 def test_damaged_container_errors(ctx, oracle):
     def bad_mode(h, up):
-        h[int(up.offsets[1])] = 3
+        h[int(up.offsets[1])] = 5  # (3 is the 3-bit extension, read at dim 64)
 
     def bad_dim(h, up):
         h[int(up.offsets[0]) + 4] = 32

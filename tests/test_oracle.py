@@ -238,7 +238,7 @@ def _malformed_cases(oracle):
     cases.append(("truncated header", blob[:5], 300, 64))
     cases.append(("truncated body", blob[:-3], 300, 64))
     bad_mode = blob.copy()
-    bad_mode[0] = 3
+    bad_mode[0] = 1  # 3 is the 3-bit extension (dim % 8 == 0), which this library reads
     cases.append(("bad mode", bad_mode, 300, 64))
     cases.append(("wrong dim", blob, 300, 32))
     zero_tok = blob.copy()
