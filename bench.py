@@ -331,6 +331,9 @@ def main() -> int:
     ap.add_argument("--kvd", default="", help="KVD1 dump (--workload dump)")
     ap.add_argument("--qsnap", default="", help="QSN1 query snapshots (--workload dump)")
     ap.add_argument("--lengths", default="", help="comma-separated snapshot lengths (--workload dump)")
+    ap.add_argument("--three-bit", action="store_true",
+                    help="encode with the 3-bit format extension allowed (not the reference's containers; "
+                         "a side measurement, not the quoted line)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run a 256 MiB device copy (counter calibration under rocprofv3 --pmc)")
     a = ap.parse_args()
@@ -356,6 +359,8 @@ def main() -> int:
     H = L * KV
     dev = torch.device("cuda:0")
     ctx = kvexp_amd.Context(0)
+    if a.three_bit:
+        ctx.set_encoder_modes(kvexp_amd.MODES_REFERENCE | kvexp_amd.MODE_3BIT)
 
     # ---- inputs: generate per head, upload raw, encode on the GPU ---------------
     t0 = time.time()
@@ -378,7 +383,7 @@ def main() -> int:
         f"ratio {container / tight:.6f}")
 
     # block mode mix from the headers
-    stats = dict(raw=0, bits2=0, bits4=0, escapes=0)
+    stats = dict(raw=0, bits2=0, bits3=0, bits4=0, escapes=0)
     for e in enc_k + enc_v:
         off = e.offsets.cpu().numpy()
         blob = e.blob[: e.nbytes].cpu().numpy()
@@ -386,6 +391,7 @@ def main() -> int:
         modes = hdr[:, 0]
         stats["raw"] += int((modes == 0).sum())
         stats["bits2"] += int((modes == 2).sum())
+        stats["bits3"] += int((modes == 3).sum())
         stats["bits4"] += int((modes == 4).sum())
         stats["escapes"] += int((hdr[:, 2].astype(np.int64) | (hdr[:, 3].astype(np.int64) << 8)).sum())
 
@@ -455,7 +461,7 @@ def main() -> int:
     out_bytes = H * G * D * 4
     algo_bytes = container + q_bytes + out_bytes
     achieved = algo_bytes / (kern_avg_ms * 1e-3) / 1e9
-    traffic = measured_traffic()
+    traffic = None if a.three_bit else measured_traffic()  # the counters were read on encode_bf16's containers
     value = container / (ms_x * 1e-3) / 1e9
 
     if a.copy_probe:
@@ -510,7 +516,8 @@ def main() -> int:
         "data": "synthetic (seeded, kvexp_amd/synth.py config c2)",
         "config": {"workload": "c2: full 24-layer Qwen2.5-0.5B decode step, 48 KV heads x 7 queries, head_dim 64, "
                                "seq 32768, XKV 128-token blocks", "kv_heads": H, "group": G, "dim": D, "seq": S,
-                   "block": BT, "splits_per_head": splits, "copies": copies},
+                   "block": BT, "splits_per_head": splits, "copies": copies,
+                   "format": "XKV + 3-bit extension" if a.three_bit else "XKV (encode_bf16)"},
         "pct_hbm_peak": round(100.0 * value / HBM_PEAK_GBPS, 2),
         "container_bytes": container,
         "tight_bytes": tight,
