@@ -36,6 +36,15 @@ container in one call, GB/s of BF16 input) with its HBM roofline, and the
 reference's encode_bf16 on the host as the CPU baseline. Containers are
 checked byte for byte against kvexp_hip_encode of the same tokens.
 
+--config c1 | c3 | c4 measures the other configurations of BASELINE.json
+(parity cases, not the quoted line), one JSON line each: c1 (one KV head,
+seq 8192, one query; L2-resident, reported in µs), c3 (the ragged batch:
+32 sequences x 48 KV heads, split count from kvexp_hip_suggest_splits_batch)
+and c4 (256 KV heads x seq 131072, head_dim 128, 4 queries; K and V generated
+on the GPU with the config's distributions, torch's RNG, since the host
+generator would take minutes). c1 and c3 use the host generator
+(kvexp_amd/synth.py). XKV is checked bit for bit against raw before timing.
+
 --workload dump runs the reference bench's model scope on a real KV dump
 (KVD1 + QSN1 files written by the reference's python/dump_kv.py): every
 layer and KV head at each snapshot length, XKV checked bit for bit against
@@ -272,6 +281,91 @@ def bench_append(a, torch, np, kvexp_amd, synth) -> int:
     return 0
 
 
+def bench_config(a, torch, np, kvexp_amd, synth) -> int:
+    """--config c1 / c3 / c4 (see the module docstring)."""
+    name = a.config
+    cfg = synth.CONFIGS[name]
+    G, D, BT = cfg["group"], cfg["dim"], cfg["block"]
+    dev = torch.device("cuda:0")
+    ctx = kvexp_amd.Context(0)
+    t0 = time.time()
+    kx, vx, kr, vr, seqs = [], [], [], [], []
+    if name == "c4":
+        g = torch.Generator(device=dev)
+        g.manual_seed(cfg["seed"])
+        n_heads, lens = cfg["layers"] * cfg["kv_heads"], None
+    else:
+        lens = synth.c3_lengths(cfg["seed"], cfg["batch"]) if name == "c3" else [cfg["seq"]] * cfg["batch"]
+        n_heads = len(lens) * cfg["layers"] * cfg["kv_heads"]
+    for i in range(n_heads):
+        if name == "c4":
+            S = cfg["seq"]
+            scale = torch.exp2(torch.rand(D, generator=g, device=dev) * 8 - 5)
+            k = (torch.randn(S, D, generator=g, device=dev) * scale).to(torch.bfloat16).view(torch.int16).reshape(-1)
+            v = (torch.randn(S, D, generator=g, device=dev) * 0.5).to(torch.bfloat16).view(torch.int16).reshape(-1)
+        else:
+            per = cfg["layers"] * cfg["kv_heads"]
+            b, lh = divmod(i, per)
+            S = lens[b]
+            hk, hv = synth.head_kv(name, S, b, lh // cfg["kv_heads"], lh % cfg["kv_heads"])
+            k = torch.from_numpy(hk.view(np.int16)).to(dev)
+            v = torch.from_numpy(hv.view(np.int16)).to(dev)
+        kx.append(ctx.encode(k, S, D, BT, sync_size=False))
+        vx.append(ctx.encode(v, S, D, BT, sync_size=False))
+        kr.append(k)
+        vr.append(v)
+        seqs.append(S)
+        if (i + 1) % 256 == 0:
+            log(f"{name}: {i + 1} of {n_heads} heads generated and encoded ({time.time() - t0:.0f} s)")
+    torch.cuda.synchronize()
+    for e in kx + vx:
+        e.nbytes = int(e.offsets[-1])
+    container = sum(e.nbytes for e in kx + vx)
+    tight = 4 * D * sum(seqs)
+    splits = a.splits or (ctx.suggest_splits_batch(seqs, BT, D, G) if name == "c3"
+                          else ctx.suggest_splits(n_heads, seqs[0], BT, dim=D, n_q=G))
+    q = torch.randn(n_heads * G * D, device=dev).to(torch.bfloat16).view(torch.int16)
+    px = ctx.plan([dict(kx=kx[i], vx=vx[i], seq=seqs[i], splits=splits) for i in range(n_heads)], G, D, BT)
+    pr = ctx.plan([dict(k=kr[i], v=vr[i], seq=seqs[i], splits=splits) for i in range(n_heads)], G, D, BT)
+    ox = px.run(q, check_errors=True).clone()
+    orw = pr.run(q, check_errors=True).clone()
+    torch.cuda.synchronize()
+    same = bool(torch.equal(ox.view(torch.int32), orw.view(torch.int32)))
+    log(f"{name}: {n_heads} heads, {sum(seqs)} tokens, container {container} B (ratio {container / tight:.6f}), "
+        f"splits {splits}, XKV == raw: {same} ({time.time() - t0:.0f} s)")
+    out = torch.empty(n_heads * G * D, dtype=torch.float32, device=dev)
+
+    def timed(p):
+        for _ in range(a.warmup):
+            p.run(q, out)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(a.steps):
+            p.run(q, out)
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / a.steps
+
+    ms_x, ms_r = timed(px), timed(pr)
+    px.close()
+    pr.close()
+    gbps = container / (ms_x * 1e-3) / 1e9
+    log(f"{name}: xkv {ms_x * 1e3:.1f} us/step ({gbps:.0f} GB/s of containers), raw {ms_r * 1e3:.1f} us/step")
+    print(json.dumps({
+        "metric": f"decode-step µs + achieved HBM GB/s, BASELINE config {name} (parity case, not the quoted line)",
+        "value": round(gbps, 2), "unit": "GB/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
+        "us_per_step": round(ms_x * 1e3, 2), "higher_is_better": True, "dtype": "f32",
+        "data": "synthetic (GPU-generated, config distributions)" if name == "c4"
+                else f"synthetic (seeded, kvexp_amd/synth.py config {name})",
+        "config": {"workload": name, "kv_heads": n_heads, "group": G, "dim": D, "block": BT,
+                   "tokens": sum(seqs), "max_seq": max(seqs), "splits_per_head": splits},
+        "pct_hbm_peak": round(100.0 * gbps / HBM_PEAK_GBPS, 2), "container_bytes": container,
+        "tight_bytes": tight, "raw_us_per_step": round(ms_r * 1e3, 2), "xkv_bit_equal_raw": same,
+    }), flush=True)
+    return 0 if same else 1
+
+
 def bench_dump(a, torch, np, kvexp_amd) -> int:
     from kvexp_amd import dumps
 
@@ -352,8 +446,10 @@ def main() -> int:
         return bench_append(a, torch, np, kvexp_amd, synth)
     if a.workload == "dump":
         return bench_dump(a, torch, np, kvexp_amd)
+    if a.config in ("c1", "c3", "c4"):
+        return bench_config(a, torch, np, kvexp_amd, synth)
     if a.config != "c2":
-        raise SystemExit("the bench line is quoted on c2 (BASELINE.json configs[1]); other configs are test cases")
+        raise SystemExit("--config takes c1, c2 (the quoted line), c3 or c4 (c5 is a correctness case)")
     cfg = synth.CONFIGS["c2"]
     L, KV, G, D, S, BT = cfg["layers"], cfg["kv_heads"], cfg["group"], cfg["dim"], cfg["seq"], cfg["block"]
     H = L * KV
