@@ -146,35 +146,61 @@ __device__ __forceinline__ EncRows job_rows(const AppendJobDev &j, int b, int bt
 // m set for each coded mode m that may be chosen (raw always may): bits 2
 // and 4 give the reference's encoder; bit 3 adds the 3-bit extension, taken
 // only when dim % 8 == 0.
-// Thread i of the workgroup (at most 128 threads) owns channels i, i + 128:
-// it counts a channel's exponents in a private column of LDS byte counters
-// (four bins per dword; a block has at most 255 tokens, so a byte cannot
-// overflow into its neighbour) with fire-and-forget LDS adds, then slides
+// A channel's exponents are counted in a column of LDS byte counters (four
+// bins per dword; a block has at most 255 tokens, so a byte cannot overflow
+// into its neighbour) with fire-and-forget LDS adds by the threads of every
+// row slice; one thread per column then slides
 // each code window over the bins between its smallest and largest exponent
 // (windows outside them cover nothing) to find best_base: the most covered
 // exponents, then the smallest base (codec.cpp:18-35).
 constexpr int kHistStride = 65; // dwords per channel column (64 + 1: columns start on different banks)
 
+// LDS of the statistics: stats_cols(dim) channel columns, the per-wave
+// escape sums (3 per wave), each column's smallest and largest exponent.
+// The stats kernels run kThreads threads: 4 row slices at head_dim <= 64,
+// 2 above.
+__host__ __device__ constexpr int stats_cols(int dim) { return dim > 64 ? 128 : 64; }
+__host__ __device__ constexpr size_t stats_lds_bytes(int dim) {
+    return size_t(stats_cols(dim)) * kHistStride * sizeof(uint32_t) +
+           (3 * kWaves + 2 * stats_cols(dim)) * sizeof(int);
+}
+
 __device__ __forceinline__ void encode_stats_block(uint32_t *hist, int *esc_part, const EncRows src, int n, int dim,
                                                    EncBlockMeta *__restrict__ meta, uint8_t *__restrict__ bases,
                                                    int modes) {
     const int tid = int(threadIdx.x);
-    uint32_t *h = hist + tid * kHistStride;
+    // Channel columns: thread `own` of each row slice counts channels own,
+    // own + nthr, ... of rows slice, slice + nslices, ... into the column of
+    // `own` (LDS adds, so the slices share it); after a barrier the threads
+    // of slice 0 slide the windows. blockDim.x is a multiple of nthr.
+    const int nthr = min(int(blockDim.x), stats_cols(dim));
+    const int own = tid % nthr, slice = tid / nthr, nslices = int(blockDim.x) / nthr;
+    uint32_t *h = hist + own * kHistStride;
+    int *lohi = esc_part + 3 * kWaves; // [2][nthr]: smallest and largest exponent of each column
     int esc[3] = {0, 0, 0}; // escapes of the 2-, 3- and 4-bit codes
     const int nwin = (modes & 8) && dim % 8 == 0 ? 3 : 2; // windows computed (the 3-bit one only when allowed)
-    const int nthr = min(int(blockDim.x), 128); // threads owning channel columns
-    for (int d = tid; tid < nthr && d < dim; d += nthr) {
-        int e_lo = 255, e_hi = 0;
+    const int na = min(n, src.split / dim);
+    for (int d0 = 0; d0 < dim; d0 += nthr) {
+        const int d = d0 + own;
+        const bool has = d < dim;
+        if (slice == 0 && has) {
 #pragma unroll 16
-        for (int k = 0; k < 64; ++k) h[k] = 0u;
-        // rows from each source in a loop of its own (the counts do not
-        // depend on the order), 32 loads in flight before their adds
-        const int na = min(n, src.split / dim);
-        auto count_rows = [&](const uint16_t *p, int rows) {
-            for (int t0 = 0; t0 < rows; t0 += 32) {
+            for (int k = 0; k < 64; ++k) h[k] = 0u;
+            lohi[own] = 255;
+            lohi[nthr + own] = 0;
+        }
+        __syncthreads();
+        if (has) {
+            int e_lo = 255, e_hi = 0;
+            // this slice's rows, 32 loads in flight before their adds; rows
+            // [0, na) come from src.a, the rest from src.b
+            for (int r0 = slice; r0 < n; r0 += 32 * nslices) {
                 uint32_t x[32];
 #pragma unroll
-                for (int k = 0; k < 32; ++k) x[k] = t0 + k < rows ? uint32_t(p[(t0 + k) * dim + d]) : 0xFFFFFFFFu;
+                for (int k = 0; k < 32; ++k) {
+                    const int r = r0 + k * nslices;
+                    x[k] = r < n ? uint32_t(r < na ? src.a[r * dim + d] : src.b[(r - na) * dim + d]) : 0xFFFFFFFFu;
+                }
 #pragma unroll
                 for (int k = 0; k < 32; ++k) {
                     if (x[k] == 0xFFFFFFFFu) break;
@@ -184,28 +210,33 @@ __device__ __forceinline__ void encode_stats_block(uint32_t *hist, int *esc_part
                     e_hi = max(e_hi, int(e));
                 }
             }
-        };
-        count_rows(src.a, na);
-        count_rows(src.b, n - na);
-        auto count = [&](int b) { return int((h[b >> 2] >> (8 * (b & 3))) & 0xFFu); };
-        for (int wi = 0; wi < nwin; ++wi) {
-            const int bi = wi == 0 ? 0 : (wi == 1 && nwin == 2 ? 2 : wi); // 2-, (3-,) 4-bit
-            const int width = (4 << bi) - 1; // codes 0..2^bits-2
-            const int lo = min(max(0, e_lo - width + 1), 256 - width);
-            const int hi = min(e_hi, 256 - width);
-            int cov = 0;
-            for (int b = lo; b < lo + width; ++b) cov += count(b);
-            int best = cov, best_base = lo;
-            for (int b = lo + 1; b <= hi; ++b) {
-                cov += count(b + width - 1) - count(b - 1);
-                if (cov > best) {
-                    best = cov;
-                    best_base = b;
-                }
-            }
-            bases[size_t(bi) * size_t(dim) + size_t(d)] = uint8_t(best_base);
-            esc[bi] += n - best;
+            atomicMin(&lohi[own], e_lo);
+            atomicMax(&lohi[nthr + own], e_hi);
         }
+        __syncthreads();
+        if (slice == 0 && has) {
+            const int e_lo = lohi[own], e_hi = lohi[nthr + own];
+            auto count = [&](int b) { return int((h[b >> 2] >> (8 * (b & 3))) & 0xFFu); };
+            for (int wi = 0; wi < nwin; ++wi) {
+                const int bi = wi == 0 ? 0 : (wi == 1 && nwin == 2 ? 2 : wi); // 2-, (3-,) 4-bit
+                const int width = (4 << bi) - 1; // codes 0..2^bits-2
+                const int lo = min(max(0, e_lo - width + 1), 256 - width);
+                const int hi = min(e_hi, 256 - width);
+                int cov = 0;
+                for (int b = lo; b < lo + width; ++b) cov += count(b);
+                int best = cov, best_base = lo;
+                for (int b = lo + 1; b <= hi; ++b) {
+                    cov += count(b + width - 1) - count(b - 1);
+                    if (cov > best) {
+                        best = cov;
+                        best_base = b;
+                    }
+                }
+                bases[size_t(bi) * size_t(dim) + size_t(d)] = uint8_t(best_base);
+                esc[bi] += n - best;
+            }
+        }
+        __syncthreads(); // the columns are cleared again for the next channels
     }
     // escape counts of the whole block
     for (int o = 32; o > 0; o >>= 1) {
@@ -253,32 +284,27 @@ __device__ __forceinline__ void encode_stats_block(uint32_t *hist, int *esc_part
     }
 }
 
-// Threads and LDS of the stats kernels: one channel column per thread, then
-// the per-wave escape sums.
-__host__ __device__ constexpr int stats_threads(int dim) { return dim > 64 ? 128 : 64; }
-__host__ __device__ constexpr size_t stats_lds_bytes(int dim) {
-    return size_t(stats_threads(dim)) * kHistStride * sizeof(uint32_t) + 3 * kWaves * sizeof(int);
-}
 
-__global__ __launch_bounds__(128) void encode_stats_kernel(const uint16_t *__restrict__ kv, int seq, int dim,
+
+__global__ __launch_bounds__(kThreads) void encode_stats_kernel(const uint16_t *__restrict__ kv, int seq, int dim,
                                                                int bt, EncBlockMeta *__restrict__ meta,
                                                                uint8_t *__restrict__ bases, int modes) {
     const int b = int(blockIdx.x);
     const int t0 = b * bt;
     const EncRows src{kv + size_t(t0) * size_t(dim), kv + size_t(t0) * size_t(dim), 0};
     extern __shared__ uint32_t stats_lds[];
-    encode_stats_block(stats_lds, reinterpret_cast<int *>(stats_lds + blockDim.x * kHistStride), src,
+    encode_stats_block(stats_lds, reinterpret_cast<int *>(stats_lds + stats_cols(dim) * kHistStride), src,
                        min(bt, seq - t0), dim, meta + b, bases + size_t(b) * 3 * size_t(dim), modes);
 }
 
-__global__ __launch_bounds__(128) void append_stats_kernel(const AppendJobDev *__restrict__ jobs, int n_jobs,
+__global__ __launch_bounds__(kThreads) void append_stats_kernel(const AppendJobDev *__restrict__ jobs, int n_jobs,
                                                                int dim, int bt, EncBlockMeta *__restrict__ meta,
                                                                uint8_t *__restrict__ bases, int modes) {
     const int g = int(blockIdx.x);
     const AppendJobDev j = jobs[find_job(jobs, n_jobs, g)];
     const int b = g - j.blk0;
     extern __shared__ uint32_t stats_lds[];
-    encode_stats_block(stats_lds, reinterpret_cast<int *>(stats_lds + blockDim.x * kHistStride),
+    encode_stats_block(stats_lds, reinterpret_cast<int *>(stats_lds + stats_cols(dim) * kHistStride),
                        job_rows(j, b, bt, dim), min(bt, j.seq - b * bt), dim, meta + g,
                        bases + size_t(g) * 3 * size_t(dim), modes);
 }
@@ -485,8 +511,8 @@ __global__ __launch_bounds__(kThreads) void append_one_kernel(const AppendJobDev
     __shared__ EncBlockMeta meta_s;
     __shared__ int scan_tmp[kWaves];
     const AppendJobDev j = jobs[blockIdx.x];
-    int *esc_part = reinterpret_cast<int *>(one_lds + stats_threads(dim) * kHistStride);
-    uint8_t *bases_s = reinterpret_cast<uint8_t *>(esc_part + 3 * kWaves);
+    int *esc_part = reinterpret_cast<int *>(one_lds + stats_cols(dim) * kHistStride);
+    uint8_t *bases_s = reinterpret_cast<uint8_t *>(esc_part + 3 * kWaves + 2 * stats_cols(dim));
     const int64_t base = j.rebase ? j.offs[0] : 0;
     if (j.nb == 0) { // an empty container: its terminal index entry
         if (threadIdx.x == 0) {
@@ -715,7 +741,7 @@ hipError_t decode(const uint8_t *blob, uint64_t bytes, const int64_t *offs, cons
 hipError_t encode(const uint16_t *kv, int seq, int dim, int bt, int n_blocks, EncBlockMeta *meta, uint8_t *bases,
                   int64_t *offs, int32_t *first, uint8_t *out, uint32_t *status, hipStream_t s, bool rebase,
                   int tok0, int modes) {
-    hipLaunchKernelGGL(encode_stats_kernel, dim3(n_blocks), dim3(stats_threads(dim)), stats_lds_bytes(dim), s, kv, seq,
+    hipLaunchKernelGGL(encode_stats_kernel, dim3(n_blocks), dim3(kThreads), stats_lds_bytes(dim), s, kv, seq,
                        dim, bt, meta, bases, modes);
     hipLaunchKernelGGL(encode_scan_kernel, dim3(1), dim3(1024), 0, s, meta, n_blocks, bt, seq, offs, first,
                        rebase ? 1 : 0, tok0);
@@ -733,7 +759,7 @@ hipError_t append(const AppendJobDev *jobs, int n_jobs, int total_blocks, int di
         return hipGetLastError();
     }
     if (total_blocks > 0)
-        hipLaunchKernelGGL(append_stats_kernel, dim3(total_blocks), dim3(stats_threads(dim)), stats_lds_bytes(dim), s,
+        hipLaunchKernelGGL(append_stats_kernel, dim3(total_blocks), dim3(kThreads), stats_lds_bytes(dim), s,
                            jobs, n_jobs, dim, bt, meta, bases, modes);
     hipLaunchKernelGGL(append_scan_kernel, dim3(n_jobs), dim3(1024), 0, s, jobs, meta, bt);
     if (total_blocks > 0)
