@@ -1,4 +1,13 @@
-"""Builds lib/libkvexp_hip.so (gfx950) in-tree.
+"""Builds the libraries in-tree, under lib/:
+
+  libkvexp_hip.so      the C ABI (include/kvexp_hip.h) and the gfx950 kernels;
+                       exports C symbols only
+  libkvexp_hip_cxx.so  the reference's C++ API (include/kvexp/*.hpp) over it,
+                       for programs that use this library instead of the
+                       reference's (a separate library, so the C ABI links
+                       beside the reference's own kvexp:: symbols)
+  cxx_api_threads      the C++ caller used by tests/test_gpu_cxx_api.py,
+                       built with g++ and OpenMP as the reference's own code
 
     python compressed-kv-attention_amd/build.py [--jobs N] [--asm]
 
@@ -21,6 +30,9 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 LIB_DIR = os.path.join(HERE, "lib")
 LIB = os.path.join(LIB_DIR, "libkvexp_hip.so")
+LIB_CXX = os.path.join(LIB_DIR, "libkvexp_hip_cxx.so")
+CXX_TEST = os.path.join(LIB_DIR, "cxx_api_threads")
+CXX_TEST_SRC = os.path.join(ROOT, "tests", "csrc", "cxx_api_threads.cpp")
 OBJ_DIR = os.path.join(HERE, "_build", "obj")
 ASM_DIR = os.path.join(HERE, "_build", "asm")
 
@@ -30,8 +42,8 @@ SOURCES = [
     "csrc/hip/attention_kernels.hip",
     "csrc/hip/attention_wave.hip",
     "csrc/host/kvexp_hip_api.cpp",
-    "csrc/host/kvexp_cpp_api.cpp",
 ]
+CXX_SOURCES = ["csrc/host/kvexp_cpp_api.cpp"]
 HEADERS = [
     "csrc/hip/kvexp_device.h",
     "csrc/hip/kvexp_expf.h",
@@ -101,16 +113,25 @@ def build(force: bool = True, jobs: int = 4, asm: bool = False) -> str:
     os.makedirs(OBJ_DIR, exist_ok=True)
     os.makedirs(LIB_DIR, exist_ok=True)
     with cf.ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:
-        objs = list(ex.map(lambda s: _compile(s, force), SOURCES))
+        objs = list(ex.map(lambda s: _compile(s, force), SOURCES + CXX_SOURCES))
         if asm:
             list(ex.map(_asm, [s for s in SOURCES if s.endswith(".hip")]))
-    tmp = LIB + ".tmp"
-    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp] + objs
+    _link([hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC"] + objs[: len(SOURCES)], LIB)
+    _link([hipcc(), "-shared", "-fPIC"] + objs[len(SOURCES):] +
+          [f"-L{LIB_DIR}", "-lkvexp_hip", "-Wl,-rpath,$ORIGIN"], LIB_CXX)
+    # the C++ caller: plain g++ with OpenMP against the public headers only
+    _link(["g++", "-O2", "-std=c++17", "-fopenmp", "-pthread", f"-I{os.path.join(ROOT, 'include')}", CXX_TEST_SRC,
+           f"-L{LIB_DIR}", "-lkvexp_hip_cxx", "-lkvexp_hip", "-Wl,-rpath,$ORIGIN"], CXX_TEST)
+    return LIB
+
+
+def _link(cmd: list[str], out: str) -> None:
+    tmp = out + ".tmp"
+    cmd = cmd + ["-o", tmp]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed\n{' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
-    os.replace(tmp, LIB)
-    return LIB
+    os.replace(tmp, out)
 
 
 def main() -> int:

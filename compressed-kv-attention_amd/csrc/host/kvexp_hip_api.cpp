@@ -194,24 +194,39 @@ std::string status_message(uint32_t st) {
 // ================================================================ context ==
 struct kvexp_hip_ctx {
     int device = 0;
-    DevBuf status; // uint32 status word
-    // encoder scratch, grown on demand
+    DevBuf status; // uint32 status word of the encoders and the decoder
+    // encoder scratch, grown on demand; `scratch_done` is recorded on the
+    // stream of the last launch that used it, so growing it never frees
+    // memory that a kernel still in flight reads
     DevBuf enc_meta, enc_bases, enc_off, enc_first, app_jobs;
     size_t enc_meta_cap = 0, enc_bases_cap = 0, enc_index_cap = 0, app_jobs_cap = 0;
+    hipEvent_t scratch_done = nullptr;
+    // stream of the host-pointer entry (kvexp_hip_attention_decode_host): its
+    // copies and kernels wait for nothing outside this context
+    hipStream_t stream = nullptr;
     int cu_count = 0;
     int enc_modes = int(KVEXP_HIP_MODES_REFERENCE); // coded modes the encoders may choose
     // pinned host staging for the plan builder's reads of block indexes
-    std::mutex pinned_mu;
     void *pinned = nullptr;
     size_t pinned_cap = 0;
     ~kvexp_hip_ctx() {
+        if (stream) (void)hipStreamSynchronize(stream);
+        if (scratch_done) (void)hipEventSynchronize(scratch_done);
         if (pinned) (void)hipHostFree(pinned);
+        if (scratch_done) (void)hipEventDestroy(scratch_done);
+        if (stream) (void)hipStreamDestroy(stream);
     }
 };
 
 struct kvexp_hip_plan {
     kvexp_hip_ctx *ctx = nullptr;
     int n_heads = 0, n_q = 0, dim = 0, order = 0, split_tokens = 0;
+    // set when kvexp_hip_plan_update failed after the containers changed: the
+    // plan's descriptors no longer describe them, so runs are refused until
+    // an update succeeds
+    bool invalid = false;
+    std::string invalid_msg;
+    // ---- everything below is made by plan_build (swapped in whole by updates)
     bool xkv = false;
     // what kvexp_hip_plan_update needs: the heads as given and the per-tensor
     // escape-index jobs (host copy and device copy)
@@ -228,6 +243,7 @@ struct kvexp_hip_plan {
     int n_dev_heads = 0, n_items = 0, n_merge = 0;
     // wave kernel: items sorted by query-row count G; group_start[G] .. group_start[G+1]
     int group_start[10] = {0};
+    // ---- end of plan_build's part
     // split-kernel timing: one event pair per run while enabled
     bool timing = false;
     std::vector<std::pair<hipEvent_t, hipEvent_t>> events;
@@ -254,11 +270,26 @@ struct DeviceGuard {
     }
 };
 
-void grow(DevBuf &buf, size_t &cap, size_t need) {
+// Grows one of the context's scratch buffers. The old buffer may still be
+// read by the last launch that used it (on any stream): wait for it first.
+void grow(kvexp_hip_ctx *ctx, DevBuf &buf, size_t &cap, size_t need) {
     if (need <= cap) return;
+    if (ctx->scratch_done) HIPX(hipEventSynchronize(ctx->scratch_done));
     DevBuf nb(need);
     buf = std::move(nb);
     cap = need;
+}
+
+// Orders work about to be queued on `s` that writes the context's scratch
+// after the last work that used it (which may be on another stream).
+void scratch_acquire(kvexp_hip_ctx *ctx, hipStream_t s) {
+    if (ctx->scratch_done) HIPX(hipStreamWaitEvent(s, ctx->scratch_done, 0));
+}
+
+// Marks the context's scratch as in use by the work just queued on `s`.
+void scratch_used(kvexp_hip_ctx *ctx, hipStream_t s) {
+    if (ctx->scratch_done == nullptr) HIPX(hipEventCreateWithFlags(&ctx->scratch_done, hipEventDisableTiming));
+    HIPX(hipEventRecord(ctx->scratch_done, s));
 }
 
 void check_status_word(uint32_t *d_status, hipStream_t s) {
@@ -278,7 +309,7 @@ void check_status_word(uint32_t *d_status, hipStream_t s) {
 // the device from the containers, once per plan; the device heads of one
 // user head share it.
 void build_escape_index(kvexp_hip_plan &p, const kvexp_hip_head *heads, int n_heads, int n_q, int dim,
-                        std::vector<HeadDev> &hv) {
+                        std::vector<HeadDev> &hv, hipStream_t s) {
     std::vector<kvexp_dev::EscJob> jobs;
     std::vector<size_t> e0_at;
     size_t e0_total = 0;
@@ -300,22 +331,22 @@ void build_escape_index(kvexp_hip_plan &p, const kvexp_hip_head *heads, int n_he
     p.desc = DevBuf(e0_total * sizeof(kvexp_dev::BlockDesc));
     // HIP memory is not zeroed: the entry after each tensor's last block is
     // the zero-token sentinel until a plan update writes it again
-    HIPX(hipMemset(p.desc.p, 0, e0_total * sizeof(kvexp_dev::BlockDesc)));
+    HIPX(hipMemsetAsync(p.desc.p, 0, e0_total * sizeof(kvexp_dev::BlockDesc), s));
     for (size_t i = 0; i < jobs.size(); ++i) {
         jobs[i].esc0 = p.esc0.as<int32_t>() + e0_at[i];
         jobs[i].desc = p.desc.as<kvexp_dev::BlockDesc>() + e0_at[i];
     }
     DevBuf djobs(jobs.size() * sizeof(kvexp_dev::EscJob));
-    uint32_t *st = p.ctx->status.as<uint32_t>();
+    uint32_t *st = p.status.as<uint32_t>(); // the plan's own status word
     // pass 1: block checks and escape counts (descriptors need the position array)
     std::vector<kvexp_dev::EscJob> jobs1 = jobs;
     for (auto &j : jobs1) j.desc = nullptr;
-    HIPX(hipMemcpy(djobs.p, jobs1.data(), jobs1.size() * sizeof(kvexp_dev::EscJob), hipMemcpyHostToDevice));
-    HIPX(kvexp_launch::esc_start(djobs.as<kvexp_dev::EscJob>(), int(jobs.size()), st, nullptr));
-    HIPX(hipDeviceSynchronize());
-    check_status_word(st, nullptr);
+    HIPX(hipMemcpyAsync(djobs.p, jobs1.data(), jobs1.size() * sizeof(kvexp_dev::EscJob), hipMemcpyHostToDevice, s));
+    HIPX(kvexp_launch::esc_start(djobs.as<kvexp_dev::EscJob>(), int(jobs.size()), st, s));
+    check_status_word(st, s);
     std::vector<int32_t> e0(e0_total);
-    HIPX(hipMemcpy(e0.data(), p.esc0.p, e0_total * sizeof(int32_t), hipMemcpyDeviceToHost));
+    HIPX(hipMemcpyAsync(e0.data(), p.esc0.p, e0_total * sizeof(int32_t), hipMemcpyDeviceToHost, s));
+    HIPX(hipStreamSynchronize(s));
     p.esc_prefix = e0;
     p.esc_prefix_at = e0_at;
     // each tensor's positions, then room for its last block to grow to the
@@ -332,14 +363,13 @@ void build_escape_index(kvexp_hip_plan &p, const kvexp_hip_head *heads, int n_he
     }
     p.escpos = DevBuf(std::max<size_t>(pos_total, 1) * sizeof(uint16_t));
     for (size_t i = 0; i < jobs.size(); ++i) jobs[i].pos = p.escpos.as<uint16_t>() + pos_at[i];
-    HIPX(hipMemcpy(djobs.p, jobs.data(), jobs.size() * sizeof(kvexp_dev::EscJob), hipMemcpyHostToDevice));
+    HIPX(hipMemcpyAsync(djobs.p, jobs.data(), jobs.size() * sizeof(kvexp_dev::EscJob), hipMemcpyHostToDevice, s));
     // pass 2: descriptors (with the escape-position pointers)
-    HIPX(kvexp_launch::esc_start(djobs.as<kvexp_dev::EscJob>(), int(jobs.size()), st, nullptr));
+    HIPX(kvexp_launch::esc_start(djobs.as<kvexp_dev::EscJob>(), int(jobs.size()), st, s));
     DevBuf dblocks(std::max<size_t>(blocks.size(), 1) * sizeof(int2));
-    HIPX(hipMemcpy(dblocks.p, blocks.data(), blocks.size() * sizeof(int2), hipMemcpyHostToDevice));
-    HIPX(kvexp_launch::esc_pos(djobs.as<kvexp_dev::EscJob>(), dblocks.as<int2>(), int(blocks.size()), st, nullptr));
-    HIPX(hipDeviceSynchronize());
-    check_status_word(st, nullptr);
+    HIPX(hipMemcpyAsync(dblocks.p, blocks.data(), blocks.size() * sizeof(int2), hipMemcpyHostToDevice, s));
+    HIPX(kvexp_launch::esc_pos(djobs.as<kvexp_dev::EscJob>(), dblocks.as<int2>(), int(blocks.size()), st, s));
+    check_status_word(st, s); // synchronises s: the host vectors above may go
     p.jobs = jobs;
     p.djobs = std::move(djobs);
     const int per_head = (n_q + kMaxQPerLaunch - 1) / kMaxQPerLaunch;
@@ -392,7 +422,9 @@ int kvexp_hip_ctx_create(int device, kvexp_hip_ctx **out) {
         c->cu_count = prop.multiProcessorCount;
         try {
             c->status = DevBuf(sizeof(uint32_t));
-            HIPX(hipMemset(c->status.p, 0, sizeof(uint32_t)));
+            HIPX(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking));
+            HIPX(hipMemsetAsync(c->status.p, 0, sizeof(uint32_t), c->stream));
+            HIPX(hipStreamSynchronize(c->stream));
         } catch (...) {
             delete c;
             throw;
@@ -473,13 +505,14 @@ int kvexp_hip_encode(kvexp_hip_ctx *ctx, const uint16_t *d_kv, int seq, int dim,
         DeviceGuard g(ctx->device);
         hipStream_t s = static_cast<hipStream_t>(stream);
         const int nb = kvexp_hip_block_count(seq, bt);
-        grow(ctx->enc_meta, ctx->enc_meta_cap, size_t(nb) * sizeof(EncBlockMeta));
-        grow(ctx->enc_bases, ctx->enc_bases_cap, size_t(nb) * 3u * size_t(dim));
+        grow(ctx, ctx->enc_meta, ctx->enc_meta_cap, size_t(nb) * sizeof(EncBlockMeta));
+        grow(ctx, ctx->enc_bases, ctx->enc_bases_cap, size_t(nb) * 3u * size_t(dim));
         int64_t *offs = d_offsets;
         int32_t *first = d_first_token;
         if (offs == nullptr || first == nullptr) {
             const size_t need = size_t(nb + 1) * (sizeof(int64_t) + sizeof(int32_t));
             if (need > ctx->enc_index_cap) {
+                if (ctx->scratch_done) HIPX(hipEventSynchronize(ctx->scratch_done));
                 ctx->enc_off = DevBuf(size_t(nb + 1) * sizeof(int64_t));
                 ctx->enc_first = DevBuf(size_t(nb + 1) * sizeof(int32_t));
                 ctx->enc_index_cap = need;
@@ -487,9 +520,11 @@ int kvexp_hip_encode(kvexp_hip_ctx *ctx, const uint16_t *d_kv, int seq, int dim,
             if (offs == nullptr) offs = ctx->enc_off.as<int64_t>();
             if (first == nullptr) first = ctx->enc_first.as<int32_t>();
         }
+        scratch_acquire(ctx, s);
         HIPX(kvexp_launch::encode(d_kv, seq, dim, bt, nb, ctx->enc_meta.as<EncBlockMeta>(),
                                   ctx->enc_bases.as<uint8_t>(), offs, first, d_out, ctx->status.as<uint32_t>(), s,
                                   false, 0, ctx->enc_modes));
+        scratch_used(ctx, s);
         if (bytes_out != nullptr) {
             int64_t total = 0;
             uint32_t st = 0;
@@ -497,7 +532,8 @@ int kvexp_hip_encode(kvexp_hip_ctx *ctx, const uint16_t *d_kv, int seq, int dim,
             HIPX(hipMemcpyAsync(&st, ctx->status.p, sizeof st, hipMemcpyDeviceToHost, s));
             HIPX(hipStreamSynchronize(s));
             if (st != 0u) {
-                HIPX(hipMemset(ctx->status.p, 0, sizeof(uint32_t)));
+                HIPX(hipMemsetAsync(ctx->status.p, 0, sizeof(uint32_t), s));
+                HIPX(hipStreamSynchronize(s));
                 fail(KVEXP_HIP_LOGIC_ERROR, "escape count drifted from the size model");
             }
             *bytes_out = size_t(total);
@@ -570,14 +606,16 @@ void run_append(kvexp_hip_ctx *ctx, const kvexp_hip_append_job *jobs, int n_jobs
     if (dj.empty()) return;
     // every job encodes at most one block (a decode step): one fused launch
     const bool one_block = std::all_of(dj.begin(), dj.end(), [](const AppendJobDev &j) { return j.nb <= 1; });
-    grow(ctx->enc_meta, ctx->enc_meta_cap, size_t(std::max(blocks, 1)) * sizeof(EncBlockMeta));
-    grow(ctx->enc_bases, ctx->enc_bases_cap, size_t(std::max(blocks, 1)) * 3u * size_t(dim));
-    grow(ctx->app_jobs, ctx->app_jobs_cap, dj.size() * sizeof(AppendJobDev));
+    grow(ctx, ctx->enc_meta, ctx->enc_meta_cap, size_t(std::max(blocks, 1)) * sizeof(EncBlockMeta));
+    grow(ctx, ctx->enc_bases, ctx->enc_bases_cap, size_t(std::max(blocks, 1)) * 3u * size_t(dim));
+    grow(ctx, ctx->app_jobs, ctx->app_jobs_cap, dj.size() * sizeof(AppendJobDev));
+    scratch_acquire(ctx, s);
     // pageable source: the runtime has consumed it when the call returns
     HIPX(hipMemcpyAsync(ctx->app_jobs.p, dj.data(), dj.size() * sizeof(AppendJobDev), hipMemcpyHostToDevice, s));
     HIPX(kvexp_launch::append(ctx->app_jobs.as<AppendJobDev>(), int(dj.size()), blocks, dim, bt,
                               ctx->enc_meta.as<EncBlockMeta>(), ctx->enc_bases.as<uint8_t>(),
                               ctx->status.as<uint32_t>(), s, one_block, ctx->enc_modes));
+    scratch_used(ctx, s);
 }
 
 void check_encoder_status(kvexp_hip_ctx *ctx, hipStream_t s) {
@@ -585,7 +623,8 @@ void check_encoder_status(kvexp_hip_ctx *ctx, hipStream_t s) {
     HIPX(hipMemcpyAsync(&st, ctx->status.p, sizeof st, hipMemcpyDeviceToHost, s));
     HIPX(hipStreamSynchronize(s));
     if (st != 0u) {
-        HIPX(hipMemset(ctx->status.p, 0, sizeof(uint32_t)));
+        HIPX(hipMemsetAsync(ctx->status.p, 0, sizeof(uint32_t), s));
+        HIPX(hipStreamSynchronize(s));
         fail(KVEXP_HIP_LOGIC_ERROR, "escape count drifted from the size model");
     }
 }
@@ -654,8 +693,10 @@ int kvexp_hip_decode(kvexp_hip_ctx *ctx, const uint8_t *d_blob, size_t bytes, co
             HIPX(hipStreamSynchronize(s));
             if (have < seq) fail(KVEXP_HIP_FORMAT_ERROR, "xkv decode ran out of blocks");
         }
+        scratch_acquire(ctx, s); // the status word is shared with the encoders
         HIPX(kvexp_launch::decode(d_blob, bytes, d_offsets, d_first_token, n_blocks, seq, dim, d_out,
                                   ctx->status.as<uint32_t>(), s));
+        scratch_used(ctx, s);
         if (check) check_status_word(ctx->status.as<uint32_t>(), s);
     });
 }
@@ -766,12 +807,16 @@ void balance_items(kvexp_hip_plan &p, std::vector<WorkItem> &items, const int32_
     }
 }
 
-// Builds (or rebuilds) every device-side part of a plan from its heads: work
-// items (token_bounds splits, split starts checked against the block index),
-// device heads, merge work, and for the one-wave kernel the block descriptors
-// and escape-position index.
-void plan_build(kvexp_hip_plan *p, const kvexp_hip_head *heads, int n_heads) {
+// Builds every device-side part of a fresh plan from its heads: work items
+// (token_bounds splits, split starts checked against the block index), device
+// heads, merge work, and for the one-wave kernel the block descriptors and
+// escape-position index. Stream-ordered on `s`: it first waits for the work
+// already queued there (the encodes or appends that wrote the containers and
+// indexes it reads) and synchronises only `s`. Status words: the plan's own.
+void plan_build(kvexp_hip_plan *p, const kvexp_hip_head *heads, int n_heads, hipStream_t s) {
     kvexp_hip_ctx *ctx = p->ctx;
+    p->status = DevBuf(sizeof(uint32_t));
+    HIPX(hipMemsetAsync(p->status.p, 0, sizeof(uint32_t), s));
     const int n_q = p->n_q, dim = p->dim, split_tokens = p->split_tokens;
     const bool xkv = heads[0].k_xkv != nullptr;
     std::vector<HeadDev> hv;
@@ -783,7 +828,6 @@ void plan_build(kvexp_hip_plan *p, const kvexp_hip_head *heads, int n_heads) {
     std::vector<int32_t> firsts;
     const int32_t *first_all = nullptr;
     if (xkv) {
-        std::lock_guard<std::mutex> lock(ctx->pinned_mu);
         size_t total = 0;
         for (int h = 0; h < n_heads; ++h) {
             const kvexp_hip_head &H = heads[h];
@@ -809,11 +853,11 @@ void plan_build(kvexp_hip_plan *p, const kvexp_hip_head *heads, int n_heads) {
                 H.k_first_token == nullptr || H.v_first_token == nullptr || H.k_n_blocks <= 0 || H.v_n_blocks <= 0)
                 break;
             HIPX(hipMemcpyAsync(host + first_at[size_t(2 * h)], H.k_first_token, (size_t(H.k_n_blocks) + 1) * 4,
-                                hipMemcpyDeviceToHost, nullptr));
+                                hipMemcpyDeviceToHost, s));
             HIPX(hipMemcpyAsync(host + first_at[size_t(2 * h + 1)], H.v_first_token, (size_t(H.v_n_blocks) + 1) * 4,
-                                hipMemcpyDeviceToHost, nullptr));
+                                hipMemcpyDeviceToHost, s));
         }
-        HIPX(hipStreamSynchronize(nullptr));
+        HIPX(hipStreamSynchronize(s));
         firsts.assign(host, host + total);
         first_all = firsts.data();
     }
@@ -898,9 +942,9 @@ void plan_build(kvexp_hip_plan *p, const kvexp_hip_head *heads, int n_heads) {
         p->n_mitems = int(mi.size());
         p->mitems = DevBuf(std::max<size_t>(1, mi.size()) * sizeof(int2));
         if (!mi.empty())
-            HIPX(hipMemcpy(p->mitems.p, mi.data(), mi.size() * sizeof(int2), hipMemcpyHostToDevice));
+            HIPX(hipMemcpyAsync(p->mitems.p, mi.data(), mi.size() * sizeof(int2), hipMemcpyHostToDevice, s));
         if (xkv) {
-            build_escape_index(*p, heads, n_heads, n_q, dim, hv);
+            build_escape_index(*p, heads, n_heads, n_q, dim, hv, s);
             balance_items(*p, items, first_all, first_at, n_q, dim);
         }
     }
@@ -909,23 +953,49 @@ void plan_build(kvexp_hip_plan *p, const kvexp_hip_head *heads, int n_heads) {
     p->merge_ids = DevBuf(std::max<size_t>(1, merge.size()) * sizeof(int32_t));
     const size_t slot_floats = size_t(kMaxQPerLaunch) * size_t(dim + 2);
     p->ws = DevBuf(std::max<size_t>(1, size_t(ws_slots)) * slot_floats * sizeof(float));
-    p->status = DevBuf(sizeof(uint32_t));
-    HIPX(hipMemcpy(p->heads.p, hv.data(), hv.size() * sizeof(HeadDev), hipMemcpyHostToDevice));
-    HIPX(hipMemcpy(p->items.p, items.data(), items.size() * sizeof(WorkItem), hipMemcpyHostToDevice));
+    HIPX(hipMemcpyAsync(p->heads.p, hv.data(), hv.size() * sizeof(HeadDev), hipMemcpyHostToDevice, s));
+    HIPX(hipMemcpyAsync(p->items.p, items.data(), items.size() * sizeof(WorkItem), hipMemcpyHostToDevice, s));
     if (!merge.empty())
-        HIPX(hipMemcpy(p->merge_ids.p, merge.data(), merge.size() * sizeof(int32_t), hipMemcpyHostToDevice));
-    HIPX(hipMemset(p->status.p, 0, sizeof(uint32_t)));
+        HIPX(hipMemcpyAsync(p->merge_ids.p, merge.data(), merge.size() * sizeof(int32_t), hipMemcpyHostToDevice, s));
     if (!xkv) { // the job table kvexp_hip_plan_update sends lengths through
         p->jobs.assign(size_t(2 * n_heads), kvexp_dev::EscJob{});
         p->djobs = DevBuf(p->jobs.size() * sizeof(kvexp_dev::EscJob));
     }
     p->src.assign(heads, heads + n_heads);
+    HIPX(hipStreamSynchronize(s)); // the host vectors above are the copies' sources
+}
+
+// Moves a freshly built plan's device state into `dst` (an update that
+// succeeded); the old state goes to `src` and is freed with it.
+void swap_built(kvexp_hip_plan &dst, kvexp_hip_plan &src) {
+    using std::swap;
+    swap(dst.xkv, src.xkv);
+    swap(dst.src, src.src);
+    swap(dst.jobs, src.jobs);
+    swap(dst.esc_prefix, src.esc_prefix);
+    swap(dst.esc_prefix_at, src.esc_prefix_at);
+    swap(dst.djobs, src.djobs);
+    swap(dst.wave, src.wave);
+    swap(dst.heads, src.heads);
+    swap(dst.items, src.items);
+    swap(dst.merge_ids, src.merge_ids);
+    swap(dst.ws, src.ws);
+    swap(dst.status, src.status);
+    swap(dst.mitems, src.mitems);
+    swap(dst.esc0, src.esc0);
+    swap(dst.escpos, src.escpos);
+    swap(dst.desc, src.desc);
+    swap(dst.n_mitems, src.n_mitems);
+    swap(dst.n_dev_heads, src.n_dev_heads);
+    swap(dst.n_items, src.n_items);
+    swap(dst.n_merge, src.n_merge);
+    for (int i = 0; i < 10; ++i) swap(dst.group_start[i], src.group_start[i]);
 }
 
 } // namespace
 
 int kvexp_hip_plan_create(kvexp_hip_ctx *ctx, const kvexp_hip_head *heads, int n_heads, int n_q, int dim,
-                          int split_tokens, int order, kvexp_hip_plan **out) {
+                          int split_tokens, int order, void *stream, kvexp_hip_plan **out) {
     return guarded([&] {
         if (out == nullptr) fail(KVEXP_HIP_INVALID_ARGUMENT, "kvexp_hip_plan_create: null output");
         *out = nullptr;
@@ -947,7 +1017,7 @@ int kvexp_hip_plan_create(kvexp_hip_ctx *ctx, const kvexp_hip_head *heads, int n
             p->dim = dim;
             p->order = order;
             p->split_tokens = split_tokens;
-            plan_build(p, heads, n_heads);
+            plan_build(p, heads, n_heads, static_cast<hipStream_t>(stream));
         } catch (...) {
             delete p;
             throw;
@@ -983,26 +1053,57 @@ int kvexp_hip_plan_update(kvexp_hip_plan *plan, const kvexp_hip_head *heads, int
                 a.v_n_blocks != b.v_n_blocks)
                 fast = false;
         }
-        if (!fast) {
-            HIPX(hipStreamSynchronize(s)); // runs in flight still read the old buffers
-            plan_build(plan, heads, n_heads);
-            return;
-        }
-        // the device heads' lengths and byte counts and the last splits' ends
-        // are set on the GPU from the jobs, with the last blocks' descriptors
-        const int per_head = (plan->n_q + kMaxQPerLaunch - 1) / kMaxQPerLaunch;
-        for (int h = 0; h < n_heads; ++h)
-            for (int kv = 0; kv < 2; ++kv) {
-                kvexp_dev::EscJob &j = plan->jobs[size_t(2 * h + kv)];
-                j.bytes = kv ? heads[h].v_bytes : heads[h].k_bytes;
-                j.seq = heads[h].seq;
+        // From here on the containers have changed under the plan: a failure
+        // leaves the plan refusing runs until an update succeeds.
+        try {
+            if (!fast) {
+                // a new plan is built aside (its build first waits for the work
+                // queued on s, runs included, which still read the old buffers)
+                // and swapped in only when it is complete
+                kvexp_hip_plan np;
+                np.ctx = plan->ctx;
+                np.n_heads = plan->n_heads;
+                np.n_q = plan->n_q;
+                np.dim = plan->dim;
+                np.order = plan->order;
+                np.split_tokens = plan->split_tokens;
+                plan_build(&np, heads, n_heads, s);
+                swap_built(*plan, np);
+                plan->invalid = false;
+                plan->invalid_msg.clear();
+                return;
             }
-        HIPX(hipMemcpyAsync(plan->djobs.p, plan->jobs.data(), plan->jobs.size() * sizeof(kvexp_dev::EscJob),
-                            hipMemcpyHostToDevice, s));
-        HIPX(kvexp_launch::plan_refresh(plan->djobs.as<kvexp_dev::EscJob>(), plan->xkv ? int(plan->jobs.size()) : 0,
-                                        plan->heads.as<HeadDev>(), plan->n_dev_heads, plan->items.as<WorkItem>(),
-                                        plan->n_items, per_head, plan->status.as<uint32_t>(), s));
-        plan->src.assign(heads, heads + n_heads);
+            // the device heads' lengths and byte counts and the last splits' ends
+            // are set on the GPU from the jobs, with the last blocks' descriptors
+            const int per_head = (plan->n_q + kMaxQPerLaunch - 1) / kMaxQPerLaunch;
+            for (int h = 0; h < n_heads; ++h)
+                for (int kv = 0; kv < 2; ++kv) {
+                    kvexp_dev::EscJob &j = plan->jobs[size_t(2 * h + kv)];
+                    j.bytes = kv ? heads[h].v_bytes : heads[h].k_bytes;
+                    j.seq = heads[h].seq;
+                }
+            HIPX(hipMemcpyAsync(plan->djobs.p, plan->jobs.data(), plan->jobs.size() * sizeof(kvexp_dev::EscJob),
+                                hipMemcpyHostToDevice, s));
+            HIPX(kvexp_launch::plan_refresh(plan->djobs.as<kvexp_dev::EscJob>(),
+                                            plan->xkv ? int(plan->jobs.size()) : 0, plan->heads.as<HeadDev>(),
+                                            plan->n_dev_heads, plan->items.as<WorkItem>(), plan->n_items, per_head,
+                                            plan->status.as<uint32_t>(), s));
+            plan->src.assign(heads, heads + n_heads);
+            plan->invalid = false;
+            plan->invalid_msg.clear();
+        } catch (const KvexpFail &f) {
+            plan->invalid = true;
+            plan->invalid_msg = f.msg;
+            throw;
+        } catch (const HipFail &h) {
+            plan->invalid = true;
+            plan->invalid_msg = std::string(h.what) + ": " + hipGetErrorString(h.err);
+            throw;
+        } catch (...) {
+            plan->invalid = true;
+            plan->invalid_msg = "update failed";
+            throw;
+        }
     });
 }
 
@@ -1019,6 +1120,9 @@ int kvexp_hip_attention_run(kvexp_hip_plan *plan, const uint16_t *d_q, float *d_
     return guarded([&] {
         if (plan == nullptr || d_q == nullptr || d_out == nullptr)
             fail(KVEXP_HIP_INVALID_ARGUMENT, "attention_decode: bad argument");
+        if (plan->invalid)
+            fail(KVEXP_HIP_FORMAT_ERROR, "plan is stale after a failed kvexp_hip_plan_update (" + plan->invalid_msg +
+                                             "); update it again before running");
         DeviceGuard g(plan->ctx->device);
         hipStream_t s = static_cast<hipStream_t>(stream);
         hipEvent_t ev0 = nullptr, ev1 = nullptr;
@@ -1105,19 +1209,28 @@ int kvexp_hip_attention_decode_host(kvexp_hip_ctx *ctx, int order, const uint16_
         if (order == KVEXP_HIP_ORDER_DPBF16 && (dim % 32 != 0 || dim > kMaxDim))
             fail(KVEXP_HIP_INVALID_ARGUMENT, "avx512 attention: head_dim must be a multiple of 32");
         DeviceGuard g(ctx->device);
+        // everything on the context's own stream: concurrent calls on other
+        // contexts neither wait for this one nor see its status words
+        hipStream_t s = ctx->stream;
         const size_t qn = size_t(n_q) * size_t(dim);
         DevBuf dq(qn * 2), dout(qn * 4);
-        HIPX(hipMemcpy(dq.p, q, qn * 2, hipMemcpyHostToDevice));
+        HIPX(hipMemcpyAsync(dq.p, q, qn * 2, hipMemcpyHostToDevice, s));
         kvexp_hip_head H{};
         H.seq = seq;
         H.n_splits = n_threads;
         DevBuf dk, dv, kio, kif, vio, vif;
+        // declared after the buffers, so destroyed first: on an early failure
+        // the copies queued into them finish before they are freed
+        struct SyncOnExit {
+            hipStream_t s;
+            ~SyncOnExit() { (void)hipStreamSynchronize(s); }
+        } sync_on_exit{s};
         if (raw) {
             const size_t nb = size_t(seq) * size_t(dim) * 2u;
             dk = DevBuf(nb);
             dv = DevBuf(nb);
-            HIPX(hipMemcpy(dk.p, k_raw, nb, hipMemcpyHostToDevice));
-            HIPX(hipMemcpy(dv.p, v_raw, nb, hipMemcpyHostToDevice));
+            HIPX(hipMemcpyAsync(dk.p, k_raw, nb, hipMemcpyHostToDevice, s));
+            HIPX(hipMemcpyAsync(dv.p, v_raw, nb, hipMemcpyHostToDevice, s));
             H.k_raw = dk.as<uint16_t>();
             H.v_raw = dv.as<uint16_t>();
         } else {
@@ -1129,16 +1242,16 @@ int kvexp_hip_attention_decode_host(kvexp_hip_ctx *ctx, int order, const uint16_
                 fail(KVEXP_HIP_FORMAT_ERROR, "xkv ran out of tokens");
             dk = DevBuf(std::max<size_t>(k_bytes, 4));
             dv = DevBuf(std::max<size_t>(v_bytes, 4));
-            HIPX(hipMemcpy(dk.p, k_xkv, k_bytes, hipMemcpyHostToDevice));
-            HIPX(hipMemcpy(dv.p, v_xkv, v_bytes, hipMemcpyHostToDevice));
+            HIPX(hipMemcpyAsync(dk.p, k_xkv, k_bytes, hipMemcpyHostToDevice, s));
+            HIPX(hipMemcpyAsync(dv.p, v_xkv, v_bytes, hipMemcpyHostToDevice, s));
             kio = DevBuf(ko.size() * 8);
             kif = DevBuf(kf.size() * 4);
             vio = DevBuf(vo.size() * 8);
             vif = DevBuf(vf.size() * 4);
-            HIPX(hipMemcpy(kio.p, ko.data(), ko.size() * 8, hipMemcpyHostToDevice));
-            HIPX(hipMemcpy(kif.p, kf.data(), kf.size() * 4, hipMemcpyHostToDevice));
-            HIPX(hipMemcpy(vio.p, vo.data(), vo.size() * 8, hipMemcpyHostToDevice));
-            HIPX(hipMemcpy(vif.p, vf.data(), vf.size() * 4, hipMemcpyHostToDevice));
+            HIPX(hipMemcpyAsync(kio.p, ko.data(), ko.size() * 8, hipMemcpyHostToDevice, s));
+            HIPX(hipMemcpyAsync(kif.p, kf.data(), kf.size() * 4, hipMemcpyHostToDevice, s));
+            HIPX(hipMemcpyAsync(vio.p, vo.data(), vo.size() * 8, hipMemcpyHostToDevice, s));
+            HIPX(hipMemcpyAsync(vif.p, vf.data(), vf.size() * 4, hipMemcpyHostToDevice, s));
             H.k_xkv = dk.as<uint8_t>();
             H.v_xkv = dv.as<uint8_t>();
             H.k_bytes = k_bytes;
@@ -1151,13 +1264,14 @@ int kvexp_hip_attention_decode_host(kvexp_hip_ctx *ctx, int order, const uint16_
             H.v_n_blocks = int(vo.size()) - 1;
         }
         kvexp_hip_plan *plan = nullptr;
-        int rc = kvexp_hip_plan_create(ctx, &H, 1, n_q, dim, split_tokens, order, &plan);
+        int rc = kvexp_hip_plan_create(ctx, &H, 1, n_q, dim, split_tokens, order, s, &plan);
         if (rc) fail(rc, g_error);
-        rc = kvexp_hip_attention_run(plan, dq.as<uint16_t>(), dout.as<float>(), nullptr, 1, nullptr);
+        rc = kvexp_hip_attention_run(plan, dq.as<uint16_t>(), dout.as<float>(), nullptr, 1, s);
         const std::string msg = g_error;
         kvexp_hip_plan_destroy(plan);
         if (rc) fail(rc, msg);
-        HIPX(hipMemcpy(out, dout.p, qn * 4, hipMemcpyDeviceToHost));
+        HIPX(hipMemcpyAsync(out, dout.p, qn * 4, hipMemcpyDeviceToHost, s));
+        HIPX(hipStreamSynchronize(s));
     });
 }
 

@@ -102,7 +102,7 @@ def lib() -> C.CDLL:
     L.kvexp_hip_decode.argtypes = [vp, vp, sz, vp, vp, i32, i32, i32, vp, i32, vp]
     L.kvexp_hip_append.argtypes = [vp, vp, i32, i32, i32, i32, vp, vp, sz, vp, vp, i32, C.POINTER(sz), vp]
     L.kvexp_hip_append_batch.argtypes = [vp, C.POINTER(_AppendJob), i32, i32, i32, i32, vp]
-    L.kvexp_hip_plan_create.argtypes = [vp, C.POINTER(_Head), i32, i32, i32, i32, i32, C.POINTER(vp)]
+    L.kvexp_hip_plan_create.argtypes = [vp, C.POINTER(_Head), i32, i32, i32, i32, i32, vp, C.POINTER(vp)]
     L.kvexp_hip_plan_destroy.argtypes = [vp]
     L.kvexp_hip_plan_update.argtypes = [vp, C.POINTER(_Head), i32, vp]
     L.kvexp_hip_suggest_splits.argtypes = [vp, i32, i32, i32]
@@ -361,13 +361,17 @@ class Context:
         return out[: seq * enc.dim]
 
     # attention --------------------------------------------------------------
-    def plan(self, heads: list, n_q: int, dim: int, split: int = 128, order: int = ORDER_SCALAR) -> "Plan":
+    def plan(self, heads: list, n_q: int, dim: int, split: int = 128, order: int = ORDER_SCALAR,
+             stream=None) -> "Plan":
         """heads: dicts with 'seq', 'splits' and either 'k'/'v' (raw device tensors) or
         'kx'/'vx' (Encoded; a Cache.view() whose size was not read back passes
-        its capacity as the byte count)."""
+        its capacity as the byte count). The build is ordered on `stream`
+        (default: torch's current stream), after the work that wrote the
+        containers."""
         arr, keep = _heads_array(heads)
         p = C.c_void_p()
-        check(lib().kvexp_hip_plan_create(self.h, arr, len(heads), n_q, dim, split, order, C.byref(p)))
+        check(lib().kvexp_hip_plan_create(self.h, arr, len(heads), n_q, dim, split, order, _stream(stream),
+                                          C.byref(p)))
         plan = Plan(self, p, len(heads), n_q, dim, keep)
         plan._arr = arr
         plan._caps = [(h["kx"].blob.numel(), h["vx"].blob.numel()) if "kx" in h else (0, 0) for h in heads]

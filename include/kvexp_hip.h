@@ -57,9 +57,13 @@ const char *kvexp_hip_last_error(void);
 const char *kvexp_hip_version(void);
 
 /* ------------------------------------------------------------ context ---- */
-/* A context binds one device and owns its workspace (partial softmax states,
- * head/work descriptors, a status word). Contexts are independent; one
- * context may be used from one host thread at a time. */
+/* A context binds one device and owns the encoders' scratch memory, their
+ * status word and a non-blocking stream for the host-pointer entry
+ * (kvexp_hip_attention_decode_host). Contexts are independent: calls on
+ * different contexts may run concurrently from different host threads and
+ * share no mutable state. One context may be used from one host thread at a
+ * time; its encoders order their scratch reuse across streams themselves
+ * (a later call on another stream waits on the GPU for the earlier one). */
 typedef struct kvexp_hip_ctx kvexp_hip_ctx;
 
 int kvexp_hip_ctx_create(int device, kvexp_hip_ctx **out);
@@ -188,17 +192,20 @@ typedef struct kvexp_hip_head {
 } kvexp_hip_head;
 
 /* A plan fixes the heads, the split of each head and the kernel choice; it
- * owns the device-side descriptors, so running it launches kernels and
- * copies nothing from the host. Splits follow token_bounds
- * (dispatch.cpp:17-23) over `split_tokens`-token tiles with
+ * owns the device-side descriptors and its own status word, so running it
+ * launches kernels and copies nothing from the host. Splits follow
+ * token_bounds (dispatch.cpp:17-23) over `split_tokens`-token tiles with
  * min(max(1, n_splits), tiles) parts; XKV split starts must fall on block
  * starts of both K and V (else "token split is not aligned to an encoded
- * block"). Creating a plan reads the device first_token arrays (one
- * synchronous copy per tensor). */
+ * block"). Creating a plan is ordered on `stream` (the stream whose encodes
+ * or appends wrote the containers): it reads the block indexes and checks
+ * every block header after the work queued there, and synchronises only
+ * that stream. Plans of one context may be created from one thread at a
+ * time (they share its pinned staging buffer). */
 typedef struct kvexp_hip_plan kvexp_hip_plan;
 
 int kvexp_hip_plan_create(kvexp_hip_ctx *ctx, const kvexp_hip_head *heads, int n_heads, int n_q, int dim,
-                          int split_tokens, int order, kvexp_hip_plan **out);
+                          int split_tokens, int order, void *stream, kvexp_hip_plan **out);
 int kvexp_hip_plan_destroy(kvexp_hip_plan *plan);
 /* Re-targets a plan at its heads after their containers grew
  * (kvexp_hip_append): `heads` as at creation (same buffers, n_splits and
@@ -208,9 +215,13 @@ int kvexp_hip_plan_destroy(kvexp_hip_plan *plan);
  * positions are rewritten on the GPU) and the device heads and work items
  * are uploaded: stream-ordered on `stream` (the stream the plan runs on), no
  * synchronisation, no allocation; an index that does not cover seq is then
- * reported by the next checked run. Otherwise the plan is built again as by
- * kvexp_hip_plan_create (synchronising `stream` first). No counterpart in
- * the reference, which has no plans. */
+ * reported by the next checked run. Otherwise a new plan is built aside as
+ * by kvexp_hip_plan_create (ordered on `stream`, after the runs queued
+ * there) and replaces the old one only when complete. If an update fails
+ * after argument checks (a damaged container, a misaligned split, a device
+ * error), the plan refuses to run (KVEXP_HIP_FORMAT_ERROR naming the
+ * failure) until a later update succeeds; its memory stays valid. No
+ * counterpart in the reference, which has no plans. */
 int kvexp_hip_plan_update(kvexp_hip_plan *plan, const kvexp_hip_head *heads, int n_heads, void *stream);
 /* Suggested n_splits for a head of `seq` tokens so that a plan over
  * `n_heads` such heads fills the device (one wave group per split). */
@@ -248,7 +259,11 @@ int kvexp_hip_plan_kernel_time(kvexp_hip_plan *plan, double *ms, int *runs);
 
 /* The Backend::Hip case of attention_decode: the reference argument list
  * with host pointers. Copies the inputs to the device, builds indexes and a
- * plan with n_splits = n_threads, runs it and copies `out` back. */
+ * plan with n_splits = n_threads, runs it and copies `out` back, all on the
+ * context's own stream (synchronised before returning). Reentrant across
+ * contexts: the reference's attention_decode holds no shared state and its
+ * bench calls it from an OpenMP parallel for (bench.cpp:715-728); callers
+ * doing the same give each thread its own context. */
 int kvexp_hip_attention_decode_host(kvexp_hip_ctx *ctx, int order, const uint16_t *q, const uint16_t *k_raw,
                                     const uint16_t *v_raw, const uint8_t *k_xkv, size_t k_bytes,
                                     const uint8_t *v_xkv, size_t v_bytes, float *out, int n_q, int dim, int seq,

@@ -21,10 +21,17 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_cpp_api_symbols_exported():
-    out = os.popen(f"nm -D --defined-only {amd.LIB_PATH}").read()
+    """The C++ API lives in libkvexp_hip_cxx.so; libkvexp_hip.so exports C
+    symbols only, so it links beside the reference library (whose kvexp::
+    symbols the C++ API mirrors) without a clash."""
+    cxx = os.path.join(os.path.dirname(amd.LIB_PATH), "libkvexp_hip_cxx.so")
+    out = os.popen(f"nm -D --defined-only {cxx}").read()
     for sym in ("_ZN5kvexp16attention_decode", "_ZN5kvexp11encode_bf16", "_ZN5kvexp11decode_bf16",
-                "_ZN5kvexp10detect_cpuEv"):
+                "_ZN5kvexp10detect_cpuEv", "_ZN5kvexp10set_device"):
         assert sym in out, sym
+    c_only = os.popen(f"nm -D --defined-only {amd.LIB_PATH}").read()
+    assert "_ZN5kvexp" not in c_only
+    assert "kvexp_hip_attention_decode_host" in c_only
 
 
 def test_status_strings():
@@ -97,7 +104,7 @@ def test_null_arguments_rejected():
     nb = C.c_int(0)
     assert L.kvexp_hip_build_index(None, 10, 64, 10, None, None, 4, C.byref(nb)) == 1
     p = C.c_void_p()
-    assert L.kvexp_hip_plan_create(None, None, 0, 1, 64, 128, 0, C.byref(p)) == 1
+    assert L.kvexp_hip_plan_create(None, None, 0, 1, 64, 128, 0, None, C.byref(p)) == 1
     assert b"bad argument" in L.kvexp_hip_last_error()
     n = C.c_size_t(0)
     assert L.kvexp_hip_append(None, None, 1, 0, 64, 128, None, None, 0, None, None, 0, C.byref(n), None) == 1

@@ -386,3 +386,61 @@ def test_plan_update_raw_heads(ctx, oracle):
         want = ctx.plan(heads_at(seq), n_q, dim, block).run(q).cpu().numpy()
         say("raw plan update", step, dict(seq=seq))
         assert bits_equal(got, want), step
+
+
+def test_plan_update_failure_leaves_plan_refusing_runs(ctx, oracle):
+    """A plan update whose rebuild fails (a damaged block header found by the
+    rebuild's checks) keeps the plan's memory valid and makes every later run
+    fail without launching a kernel, until an update succeeds; the run after
+    that equals a new plan's."""
+    import torch
+
+    import kvexp_amd
+
+    rng = np.random.default_rng(31)
+    dim, n_q, block, splits = 64, 7, 128, 2
+    seq0, seq1 = 250, 260  # the append starts a block: the update rebuilds
+    k = random_kv(rng, seq1, dim, spread_lo=-6, spread_hi=4, outliers=2).reshape(-1, dim)
+    v = random_kv(rng, seq1, dim, sigma=0.5).reshape(-1, dim)
+    q = to_dev(random_kv(rng, n_q, dim), torch.int16)
+    caches = []
+    for x in (k, v):
+        c = ctx.cache(dim, seq1, block)
+        c.append(to_dev(x[:seq0].reshape(-1), torch.int16), seq0)
+        caches.append(c)
+
+    def heads(seq):
+        views = []
+        for c in caches:
+            e = c.view()
+            e.nbytes = -1
+            views.append(e)
+        return [dict(kx=views[0], vx=views[1], seq=seq, splits=splits)]
+
+    plan = ctx.plan(heads(seq0), n_q, dim, block)
+    for i, x in enumerate((k, v)):
+        caches[i].append(to_dev(x[seq0:seq1].reshape(-1), torch.int16), seq1 - seq0)
+    torch.cuda.synchronize()
+    saved = int(caches[0].blob[0].item())
+    caches[0].blob[0] = 5  # block 0 of K: mode byte 5 is no mode of the format
+    say("plan update failure: damaged update")
+    with pytest.raises(kvexp_amd.KvexpHipError) as ei:
+        plan.update(heads(seq1))
+    assert ei.value.kind == "runtime_error" and ei.value.msg == "unknown xkv block mode"
+    out = torch.full((n_q * dim,), 7.0, dtype=torch.float32, device="cuda:0")
+    say("plan update failure: run refused")
+    with pytest.raises(kvexp_amd.KvexpHipError) as ei:
+        plan.run(q, out=out)
+    assert ei.value.kind == "runtime_error" and "stale" in ei.value.msg
+    torch.cuda.synchronize()
+    assert bool((out == 7.0).all()), "a refused run wrote its output"
+    caches[0].blob[0] = saved
+    say("plan update failure: repaired update")
+    plan.update(heads(seq1))
+    got = plan.run(q, check_errors=True).cpu().numpy()
+    fresh = [ctx.encode(to_dev(x.reshape(-1), torch.int16), seq1, dim, block) for x in (k, v)]
+    want = ctx.plan([dict(kx=fresh[0], vx=fresh[1], seq=seq1, splits=splits)], n_q, dim, block).run(q).cpu().numpy()
+    assert bits_equal(got, want)
+    ref = oracle.attention("scalar", q.cpu().numpy().view(np.uint16), k.reshape(-1), v.reshape(-1), n_q=n_q, dim=dim,
+                           seq=seq1, threads=splits, split=block)
+    assert bits_equal(got, ref)
