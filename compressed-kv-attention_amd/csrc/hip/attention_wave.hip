@@ -440,6 +440,12 @@ __device__ __forceinline__ void scores(const uint8_t *row, const float (&qa)[kGr
 #pragma unroll
             for (int rg = 0; rg < NG; ++rg) ch[rg][J] = mfma_rank1<d % 16>(qa[rg][d / 16], k[J], ch[rg][J]);
         });
+        // the octet's eight widenings, then its products in one run: a
+        // product that reads a register the vector ALU has just written
+        // waits, and single products between vector instructions stall the
+        // SIMD more than one run of them
+        __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 8 * NG, 0);
     });
 #pragma unroll
     for (int rg = 0; rg < NG; ++rg) {
@@ -574,39 +580,39 @@ struct FoldIn {
 };
 
 // Token T of the ordered fold (attention_scalar.cpp:33-40), lane = channel
-// (channels lane + 64 h, h < D / 64),
-// for a whole chunk (tokens past the chunk's end carry e = 0, alpha = 1 and
-// V = -0, which leave acc and l exactly as they are). A token that moves no
-// running maximum (alpha == 1 for every row, exactly) takes
-// acc = fma(e, v, acc); a token that moves one (a uniform branch) scales by
-// alpha first: acc = fma(e, v, acc * alpha). acc[rg] register r is row
-// 4 rg + r (acc[rg][h]: channel lane + 64 h); the fma of every row of a
-// group is one rank-1 product per h whose A
-// operand is ea[rg][T / 16] (e[4 rg + r][T] at lane 4 (T % 16) + r). Lane
-// g < G carries l of row g through l = fma(l, alpha, e), which is l + e when
-// alpha is 1. Loads run ahead: V three tokens and e / alpha four tokens
-// before their use.
-template <int G, int D, int T>
-__device__ __forceinline__ void fold(const WaveLds<G, D> &S, lds_f32 *eb, lds_f32 *ab, const uint16_t *vb,
-                                     uint64_t amask, const float (&ea)[kGroups<G>][4], FoldIn<D / 64> &in,
-                                     f4 (&acc)[kGroups<G>][D / 64], float &lvec) {
+// (channels lane + 64 h, h < D / 64). Tokens past the chunk's end carry
+// e = 0, alpha = 1 and V = -0, which leave acc and l exactly as they are. A
+// token that moves no running maximum (alpha == 1 for every row, exactly)
+// takes acc = fma(e, v, acc); a token that moves one scales by alpha first:
+// acc = fma(e, v, acc * alpha) (MOVE: the caller found a move among this
+// token's group of four and tests the token's own bit; otherwise no test).
+// acc[rg] register r is row 4 rg + r (acc[rg][h]: channel lane + 64 h); the
+// fma of every row of a group is one rank-1 product per h whose A operand is
+// ea[rg][T / 16] (e[4 rg + r][T] at lane 4 (T % 16) + r). Lane g < G carries
+// l of row g through l = fma(l, alpha, e), which is l + e when alpha is 1.
+// Loads run ahead: V three tokens and e / alpha four tokens before their use.
+template <int G, int D, int T, bool MOVE>
+__device__ __forceinline__ void fold_token(const WaveLds<G, D> &S, lds_f32 *eb, lds_f32 *ab, const uint16_t *vb,
+                                           uint64_t amask, const float (&ea)[kGroups<G>][4], FoldIn<D / 64> &in,
+                                           f4 (&acc)[kGroups<G>][D / 64], float &lvec) {
     constexpr int NG = kGroups<G>, H = D / 64, TS = Shape<D>::kTileStride;
-    if constexpr (T < kChunk) {
-        if constexpr (T + 3 < kChunk) {
+    if constexpr (T + 3 < kChunk) {
 #pragma unroll
-            for (int h = 0; h < H; ++h) in.v[(T + 3) & 3][h] = vb[(T + 3) * (TS / 2) + 64 * h];
-        }
-        if constexpr (T % 4 == 0 && T + 4 < kChunk) {
-            in.e4[((T / 4) + 1) & 1] = *reinterpret_cast<lds_f4 *>(eb + T + 4);
-            in.a4[((T / 4) + 1) & 1] = *reinterpret_cast<lds_f4 *>(ab + T + 4);
-        }
-        float v[H];
+        for (int h = 0; h < H; ++h) in.v[(T + 3) & 3][h] = vb[(T + 3) * (TS / 2) + 64 * h];
+    }
+    if constexpr (T % 4 == 0 && T + 4 < kChunk) {
+        in.e4[((T / 4) + 1) & 1] = *reinterpret_cast<lds_f4 *>(eb + T + 4);
+        in.a4[((T / 4) + 1) & 1] = *reinterpret_cast<lds_f4 *>(ab + T + 4);
+    }
+    float v[H];
 #pragma unroll
-        for (int h = 0; h < H; ++h) v[h] = __uint_as_float(in.v[T & 3][h] << 16);
-        const f4 e4 = in.e4[(T / 4) & 1], a4 = in.a4[(T / 4) & 1];
-        const float el = (T % 4 == 0) ? e4.x : (T % 4 == 1) ? e4.y : (T % 4 == 2) ? e4.z : e4.w;
-        const float al = (T % 4 == 0) ? a4.x : (T % 4 == 1) ? a4.y : (T % 4 == 2) ? a4.z : a4.w;
-        if (((amask >> T) & 1ull) != 0) {
+    for (int h = 0; h < H; ++h) v[h] = __uint_as_float(in.v[T & 3][h] << 16);
+    const f4 e4 = in.e4[(T / 4) & 1], a4 = in.a4[(T / 4) & 1];
+    const float el = (T % 4 == 0) ? e4.x : (T % 4 == 1) ? e4.y : (T % 4 == 2) ? e4.z : e4.w;
+    const float al = (T % 4 == 0) ? a4.x : (T % 4 == 1) ? a4.y : (T % 4 == 2) ? a4.z : a4.w;
+    if constexpr (MOVE) {
+        const uint32_t mw = T < 32 ? uint32_t(amask) : uint32_t(amask >> 32);
+        if ((mw & (1u << (T % 32))) != 0) {
             float av[G];
 #pragma unroll
             for (int g = 0; g < G; ++g) av[g] = S.aT[g][T];
@@ -615,15 +621,45 @@ __device__ __forceinline__ void fold(const WaveLds<G, D> &S, lds_f32 *eb, lds_f3
 #pragma unroll
                 for (int h = 0; h < H; ++h) acc[g / 4][h][g % 4] *= av[g];
         }
-        lvec = fmaf(lvec, al, el);
-        // keeps the l chain in token order (otherwise it may be sunk to the
-        // end of the unrolled fold with every token's operands held live)
-        asm volatile("" : "+v"(lvec));
+    }
+    lvec = fmaf(lvec, al, el);
+    // keeps the l chain in token order (otherwise it may be sunk to the
+    // end of the unrolled fold with every token's operands held live)
+    asm volatile("" : "+v"(lvec));
 #pragma unroll
-        for (int rg = 0; rg < NG; ++rg)
+    for (int rg = 0; rg < NG; ++rg)
 #pragma unroll
-            for (int h = 0; h < H; ++h) acc[rg][h] = mfma_rank1<T % 16>(ea[rg][T / 16], v[h], acc[rg][h]);
-        fold<G, D, T + 1>(S, eb, ab, vb, amask, ea, in, acc, lvec);
+        for (int h = 0; h < H; ++h) acc[rg][h] = mfma_rank1<T % 16>(ea[rg][T / 16], v[h], acc[rg][h]);
+}
+
+// The chunk's fold in groups of 16 tokens: one uniform test of the group's
+// 16 bits of amask (tokens that move some running maximum) picks the straight
+// path or the one that tests each token. On the straight path each run of
+// four tokens issues its vector work (V widening, the l chain) and then its
+// eight products: a product right after a vector instruction, or the reverse,
+// stalls the SIMD, so few switches between the two pay.
+template <int G, int D, int T>
+__device__ __forceinline__ void fold(const WaveLds<G, D> &S, lds_f32 *eb, lds_f32 *ab, const uint16_t *vb,
+                                     uint64_t amask, const float (&ea)[kGroups<G>][4], FoldIn<D / 64> &in,
+                                     f4 (&acc)[kGroups<G>][D / 64], float &lvec) {
+    constexpr int GS = 16, NG = kGroups<G>, H = D / 64;
+    if constexpr (T < kChunk) {
+        const uint32_t mw = T < 32 ? uint32_t(amask) : uint32_t(amask >> 32);
+        constexpr uint32_t gm = uint32_t(((1ull << GS) - 1ull) << (T % 32));
+        if ((mw & gm) == 0) {
+            static_for<0, GS>([&](auto K) {
+                fold_token<G, D, T + decltype(K)::value, false>(S, eb, ab, vb, amask, ea, in, acc, lvec);
+            });
+            static_for<0, GS / 4>([&](auto) {
+                __builtin_amdgcn_sched_group_barrier(0x002, 4 * (H + 1), 0);
+                __builtin_amdgcn_sched_group_barrier(0x008, 4 * NG * H, 0);
+            });
+        } else {
+            static_for<0, GS>([&](auto K) {
+                fold_token<G, D, T + decltype(K)::value, true>(S, eb, ab, vb, amask, ea, in, acc, lvec);
+            });
+        }
+        fold<G, D, T + GS>(S, eb, ab, vb, amask, ea, in, acc, lvec);
     }
 }
 
