@@ -760,7 +760,26 @@ void attn_wave_kernel(const HeadDev *__restrict__ heads, const WorkItem *__restr
     }
     uint8_t *my_row = S.tile + lane * TS; // the lane's token
 
+    // Issue priority by progress: a SIMD issues from its oldest wave first, so
+    // the first workgroup placed on a CU would race ahead and the last finish
+    // alone at the end of the launch, with few loads in flight. Each wave
+    // instead lowers its priority as it gets through its split (3 for the
+    // first quarter of its tokens, then 2, 1, 0): the waves that are behind
+    // win the issue slots and all of a CU's waves finish at about the same
+    // time.
+    __builtin_amdgcn_s_setprio(3);
+    int prio = 3;
+    const int span = wi.tok_end - wi.tok_begin;
     while (t < wi.tok_end) {
+        {
+            const int want = 3 - min(3, ((t - wi.tok_begin) * 4) / max(span, 1));
+            if (want != prio) {
+                if (want == 2) __builtin_amdgcn_s_setprio(2);
+                else if (want == 1) __builtin_amdgcn_s_setprio(1);
+                else __builtin_amdgcn_s_setprio(0);
+                prio = want;
+            }
+        }
         int n = min(kChunk, wi.tok_end - t);
         if constexpr (XKV) n = min(n, min(kc.t1 - t, vc.t1 - t));
         if (n <= 0) break; // unreachable with plan-checked descriptors (n_tokens > 0)
