@@ -8,8 +8,12 @@
 //      (sm & 0x80) << 8 | (base + code) << 7 | (sm & 0x7F), built two at a
 //      time with v_perm_b32 / v_lshl_add_u32 / v_bfi_b32 on packed pairs;
 //      escape words are then written over their elements from the plan's
-//      escape-position index (an escape cursor per tensor: the window of 64
-//      loaded with the rows starts at the chunk's first escape);
+//      escape records (position and word in one dword; a cursor per tensor:
+//      the window of 256 loaded with the rows starts at the chunk's first
+//      escape, and a chunk is cut short where its escapes would not fit);
+//      raw blocks are copied in chunks of at most 48 rows (the registers of
+//      64 coded rows). Every lane issues the same loads on every path, so
+//      the compiler's waits for the K rows leave the V rows in flight;
 //   2. computes the G scores of each token in the reference order: 8 strided
 //      FMA chains over the head's channels, then the
 //      ((l0+l4)+(l1+l5))+((l2+l6)+(l3+l7)) tree. Every fmaf of the chains is
@@ -44,6 +48,8 @@ namespace kvexp_dev {
 namespace wave {
 
 constexpr int kChunk = 64;      // tokens per chunk (one per lane)
+constexpr int kEscWindow = 256; // escape records a chunk can patch: four per lane, loaded with its rows
+constexpr int kRawRows = 48;    // rows of a raw block per chunk: 64 lanes x 3D/2 bytes = 48 rows of 2D bytes
 constexpr uint16_t kNegZeroBf16 = 0x8000u; // V of a token past the chunk's end: fma(0, -0, acc) == acc exactly
 constexpr int kSlotQ = 8;       // partial-state slot: m[8], l[8], acc[8][head_dim]
 
@@ -123,26 +129,22 @@ __device__ __forceinline__ uint4 ld16(const uint8_t *p) {
 __device__ __forceinline__ uint32_t ldu16(const uint8_t *p) { return *(g_u16 *)(p); }
 
 // Position of one tensor inside its XKV container. The scalar fields are
-// wave-uniform; epos / eval hold the block's next escapes (lane
-// k < n_escape - ecur: element index and word of escape ecur + k).
+// wave-uniform; erec holds the block's next escape records (component j of
+// lane l: escape ecur + 4 l + j, meaningful below n_escape).
 struct Cursor {
     const BlockDesc *d;  // descriptor of the current block (the next one follows it)
     const uint8_t *blk;  // current block's header
-    const uint16_t *esc; // its escape positions
+    const uint32_t *esc; // its escape records
     int t0, t1;          // its token range
     uint32_t meta;       // mode | n_tokens << 8 | n_escape << 16
     int ecur;            // first escape of the block not yet written into a tile
-    uint32_t epos, eval;
+    int lrows;           // rows requested by the last load_rows (the raw piece layout depends on it)
+    uint4 erec;
     uint32_t base2;      // lane p < D / 2: base exponents 2p, 2p + 1 of the block
     __device__ int mode() const { return int(meta & 0xFFu); }
     __device__ int ntok() const { return int((meta >> 8) & 0xFFu); }
     __device__ int nesc() const { return int(meta >> 16); }
 };
-
-template <int D>
-__device__ __forceinline__ const uint8_t *esc_words(const Cursor &c) {
-    return c.blk + 8 + D + size_t(c.ntok()) * D + exp_payload_bytes(c.ntok(), D, c.mode());
-}
 
 // Enters the block of descriptor d, whose first token is t0: one scalar load
 // of the descriptor (checked against the container when the plan was built).
@@ -151,54 +153,76 @@ __device__ __forceinline__ void enter_block(Cursor &c, const BlockDesc *d, int t
     const u32x8 w = *(const __attribute__((address_space(4))) u32x8 *)(d);
     c.d = d;
     c.blk = reinterpret_cast<const uint8_t *>((uint64_t(w.s1) << 32) | w.s0);
-    c.esc = reinterpret_cast<const uint16_t *>((uint64_t(w.s3) << 32) | w.s2);
+    c.esc = reinterpret_cast<const uint32_t *>((uint64_t(w.s3) << 32) | w.s2);
     c.meta = w.s4;
     c.t0 = t0;
     c.t1 = t0 + c.ntok();
     c.ecur = 0;
 }
 
-// The block's base exponents (lane p < D / 2: pair p) and its next 64 escape
-// positions and words (lane k < n_escape - ecur: escape ecur + k). Every lane loads, from a
-// clamped and always valid address, and the call is made on every chunk
-// whether or not the block changed, so the number of loads in flight does
-// not depend on the path taken: a result is then never merged with a default
-// value, and waits for the row loads can leave later loads in flight. Lanes
-// >= n_escape are masked where the values are used.
+// The block's base exponents (lane p < D / 2: pair p) and its next 256
+// escape records (four per lane, one 16-byte load). Every lane loads, from an
+// always valid address (a records array ends with kEscPad spare records),
+// and the call is made on every chunk whether or not the block changed, so
+// the number of loads in flight never depends on the path taken: the
+// compiler's wait counts then stay exact, and a wait for the K rows leaves
+// the V rows in flight. Records at or past n_escape are masked where used.
 template <int D>
 __device__ __forceinline__ void block_vectors(Cursor &c) {
     const int lane = lane_id();
-    const int nesc = c.nesc();
-    const int k = min(c.ecur + lane, max(nesc - 1, 0));
     c.base2 = ldu16(c.blk + 8 + 2 * (lane & (D / 2 - 1)));
-    c.epos = *(g_u16 *)(nesc > 0 ? c.esc + k : reinterpret_cast<const uint16_t *>(c.blk));
-    c.eval = ldu16(nesc > 0 ? esc_words<D>(c) + 2 * k : c.blk);
+    const u32x4 r = *(g_u32x4 *)(c.esc + c.ecur + 4 * lane);
+    c.erec = make_uint4(r.x, r.y, r.z, r.w);
 }
 
-// Loads rows [r0 + lane] of the cursor's block (lanes < rows) into R: a
-// coded row's D sign/mantissa bytes and D/2 (4-bit), 3D/8 (3-bit: at D = 64
-// the second register holds bytes 8..23, at D = 128 the fourth repeats the
-// third) or D/4 (2-bit, its registers repeated) code bytes; a raw row's
-// first 3D/2 bytes (the rest is read at decode).
+// Rows of the cursor's block from row r0 on that the next chunk may take so
+// that its escapes all lie in the loaded window: when more than kEscWindow
+// escapes remain, the rows before the one holding window record 255 (its
+// position, read from lane 63). A row holds at most D <= 128 escapes, so the
+// answer is at least 1.
 template <int D>
-__device__ __forceinline__ void load_rows(const Cursor &c, int r0, int rows, uint4 (&R)[Shape<D>::kRowRegs]) {
-    // Lanes past `rows` load row rows - 1 again (their tile rows are not
-    // used): every load is unconditional, with the mode's layout picked by
-    // uniform selects, so the registers need no merge before their use.
-    constexpr int SM = Shape<D>::kSmRegs;
-    // (rows <= 0 only past a plan's zero-token sentinel block: row r0 then)
-    const int r = r0 + max(0, min(lane_id(), rows - 1));
+__device__ __forceinline__ int escape_rows(const Cursor &c, int r0) {
+    if (c.nesc() - c.ecur <= kEscWindow) return kChunk;
+    const uint32_t last = __builtin_amdgcn_readlane(c.erec.w, kWave - 1) & 0xFFFFu;
+    return max(1, int(last / D) - r0);
+}
+
+// First raw piece held by the lane: a raw chunk of `rows` rows is split into
+// 16-byte pieces (piece p: column p % (D / 8) of row p / (D / 8)), RR
+// consecutive pieces per lane, the last lanes' starts clamped so that every
+// lane's pieces lie inside the rows (lanes past the end repeat the last RR).
+template <int D>
+__device__ __forceinline__ int raw_start(int rows) {
+    constexpr int RR = Shape<D>::kRowRegs;
+    const int np = max(1, min(rows, kRawRows)) * (D / 8); // >= RR
+    return min(RR * lane_id(), np - RR);
+}
+
+// Loads rows r0 .. r0 + rows of the cursor's block into R. Coded block: lane
+// = row, its D sign/mantissa bytes and D/2 (4-bit), 3D/8 (3-bit: at D = 64
+// the second register holds bytes 8..23, at D = 128 the fourth repeats the
+// third) or D/4 (2-bit, its registers repeated) code bytes. Raw block (at
+// most kRawRows rows): the lane's RR pieces from raw_start. Lanes past the
+// rows load the last row again. Every load is unconditional, at the block's
+// (uniform) address plus one of two per-lane 32-bit offsets picked by uniform
+// selects, so the registers need no merge before their use.
+template <int D>
+__device__ __forceinline__ void load_rows(Cursor &c, int r0, int rows, uint4 (&R)[Shape<D>::kRowRegs]) {
+    constexpr int SM = Shape<D>::kSmRegs, RR = Shape<D>::kRowRegs;
     const int mode = c.mode();
     const bool raw = mode == 0;
-    // sign/mantissa bytes (or the first D raw bytes) of the row
-    const uint8_t *rowp = c.blk + 8 + (raw ? 0 : D) + size_t(r) * (raw ? 2 * D : D);
-    // codes of the row (or raw bytes D .. 3D/2 - 1)
+    c.lrows = rows;
+    // (rows <= 0 only past a plan's zero-token sentinel block: row r0 then)
+    const int r = r0 + max(0, min(lane_id(), rows - 1));
     const int cbytes = mode * (D / 8); // code bytes per coded row
-    const uint8_t *tail = raw ? rowp + D : c.blk + 8 + D + size_t(c.ntok()) * D + size_t(r) * cbytes;
+    const uint8_t *b = c.blk + 8;
+    // sign/mantissa bytes of the row, then its codes; raw: the lane's pieces
+    const uint32_t oa = raw ? uint32_t(r0 * (2 * D) + 16 * raw_start<D>(rows)) : uint32_t(D + r * D);
+    const uint32_t ob = raw ? oa + 16 * SM : uint32_t(D + c.ntok() * D + r * cbytes);
 #pragma unroll
-    for (int i = 0; i < SM; ++i) R[i] = ld16(rowp + 16 * i);
+    for (int i = 0; i < SM; ++i) R[i] = ld16(b + oa + 16 * i);
 #pragma unroll
-    for (int i = 0; i < D / 32; ++i) R[SM + i] = ld16(tail + (raw ? 16 * i : min(16 * i, cbytes - 16)));
+    for (int i = SM; i < RR; ++i) R[i] = ld16(b + ob + (raw ? 16 * (i - SM) : min(16 * (i - SM), cbytes - 16)));
 }
 
 __device__ __forceinline__ uint32_t comp(const uint4 &v, int i) {
@@ -256,13 +280,14 @@ __device__ __forceinline__ void fill_negzero(uint8_t *row) {
     for (int i = 0; i < D / 8; ++i) reinterpret_cast<uint4 *>(row)[i] = make_uint4(z, z, z, z);
 }
 
-// Decodes the lane's row held in R (cursor's block mode) into its tile row.
-// One uniform branch on the mode, then a straight-line body per mode. Lanes
-// >= rows (past the chunk's end) then store -0 in every channel (wanted for
-// V; harmless for K).
+// Decodes the rows held in R (cursor's block mode; see load_rows) into the
+// tile: a coded row into the lane's tile row, raw pieces to their rows. One
+// uniform branch on the mode, then a straight-line body per mode. Lanes
+// >= rows (past the chunk's end) then store -0 in every channel of their row
+// (wanted for V; harmless for K).
 template <int D>
 __device__ __forceinline__ void decode_row(const Cursor &c, const uint4 (&R)[Shape<D>::kRowRegs], const uint32_t *bp,
-                                           uint8_t *row, int r0, int rows) {
+                                           uint8_t *tile, uint8_t *row, int r0, int rows) {
     constexpr int SM = Shape<D>::kSmRegs, RR = Shape<D>::kRowRegs;
     uint4 *dst = reinterpret_cast<uint4 *>(row);
     const int mode = c.mode();
@@ -296,12 +321,15 @@ __device__ __forceinline__ void decode_row(const Cursor &c, const uint4 (&R)[Sha
             const uint32_t x = (w & 0x3Fu) | ((w << 2) & 0x3F00u) | ((w << 4) & 0x3F0000u) | ((w << 6) & 0x3F000000u);
             dst[dg] = octet(R, dg, x & 0x07070707u, (x >> 3) & 0x07070707u, bp);
         }
-    } else if (lane < rows) {
-        const uint8_t *src = c.blk + 8 + size_t(r0 + lane) * (2 * D);
+    } else {
+        // raw rows: register i holds piece raw_start + i of the rows loaded
+        // (c.lrows >= rows); pieces of rows >= rows are overwritten below
+        const int p0 = raw_start<D>(c.lrows);
 #pragma unroll
-        for (int i = 0; i < RR; ++i) dst[i] = R[i];
-#pragma unroll
-        for (int i = RR; i < D / 8; ++i) dst[i] = ld16(src + 16 * i);
+        for (int i = 0; i < RR; ++i) {
+            const int p = p0 + i;
+            *reinterpret_cast<uint4 *>(tile + (p / (D / 8)) * Shape<D>::kTileStride + (p % (D / 8)) * 16) = R[i];
+        }
     }
     if (rows < kChunk && lane >= rows) fill_negzero<D>(row);
 }
@@ -333,11 +361,11 @@ __device__ __forceinline__ float flush_tiny(float x) {
 // their elements in the tile and advances the cursor's escape index past
 // them. Positions ascend within a block and every escape before ecur lies in
 // an earlier chunk, so the chunk's escapes are the next ones from ecur whose
-// positions are below (r0 + n) * D: the 64 loaded with the chunk's rows
-// (block_vectors), and, only for a chunk with more than 64, further windows
-// loaded here, two at a time. With CHK, returns whether any of the words
-// written is a nonzero value whose exponent field lies below the threshold
-// that `low` encodes (see low_bf16).
+// positions are below (r0 + n) * D, all inside the window of records loaded
+// with the chunk's rows (the chunk's length was cut to escape_rows). No
+// loads here. With CHK, returns whether any of the words written is a
+// nonzero value whose exponent field lies below the threshold that `low`
+// encodes (see low_bf16).
 template <int D, bool CHK = false>
 __device__ __forceinline__ bool patch_escapes(Cursor &c, int r0, int n, uint8_t *tile, uint32_t low = 0) {
     constexpr int TS = Shape<D>::kTileStride;
@@ -345,38 +373,21 @@ __device__ __forceinline__ bool patch_escapes(Cursor &c, int r0, int n, uint8_t 
     if (c.ecur >= nesc) return false;
     const int lane = lane_id();
     const uint32_t hi = uint32_t((r0 + n) * D);
-    const bool mine = c.ecur + lane < nesc && c.epos < hi;
-    if (mine) {
-        const uint32_t row = c.epos / D - uint32_t(r0), col = c.epos % D;
-        *reinterpret_cast<uint16_t *>(tile + row * TS + col * 2) = uint16_t(c.eval);
+    const uint32_t rec[4] = {c.erec.x, c.erec.y, c.erec.z, c.erec.w};
+    bool bad = false;
+    int got = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const uint32_t pos = rec[j] & 0xFFFFu, word = rec[j] >> 16;
+        const bool mine = c.ecur + 4 * lane + j < nesc && pos < hi;
+        if (mine) {
+            const uint32_t row = pos / D - uint32_t(r0), col = pos % D;
+            *reinterpret_cast<uint16_t *>(tile + row * TS + col * 2) = uint16_t(word);
+        }
+        if (CHK) bad |= __ballot(mine && low_bf16(word, low)) != 0;
+        got += __popcll(__ballot(mine));
     }
-    bool bad = CHK && __ballot(mine && low_bf16(c.eval, low)) != 0;
-    const int got = __popcll(__ballot(mine));
     c.ecur += got;
-    if (got < kWave || c.ecur >= nesc) return bad;
-    const uint8_t *words = esc_words<D>(c);
-    for (;;) {
-        uint32_t pos[2], val[2];
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const int k = min(c.ecur + kWave * i + lane, nesc - 1);
-            pos[i] = *(g_u16 *)(c.esc + k);
-            val[i] = ldu16(words + 2 * k);
-        }
-        int more = 0;
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const bool m = c.ecur + kWave * i + lane < nesc && pos[i] < hi;
-            if (m) {
-                const uint32_t row = pos[i] / D - uint32_t(r0), col = pos[i] % D;
-                *reinterpret_cast<uint16_t *>(tile + row * TS + col * 2) = uint16_t(val[i]);
-            }
-            if (CHK) bad |= __ballot(m && low_bf16(val[i], low)) != 0;
-            more += __popcll(__ballot(m));
-        }
-        c.ecur += more;
-        if (more < 2 * kWave || c.ecur >= nesc) break;
-    }
     return bad;
 }
 
@@ -593,7 +604,7 @@ struct FoldIn {
 // Loads run ahead: V three tokens and e / alpha four tokens before their use.
 template <int G, int D, int T, bool MOVE>
 __device__ __forceinline__ void fold_token(const WaveLds<G, D> &S, lds_f32 *eb, lds_f32 *ab, const uint16_t *vb,
-                                           uint64_t amask, const float (&ea)[kGroups<G>][4], FoldIn<D / 64> &in,
+                                           const uint32_t (&am)[2], const float (&ea)[kGroups<G>][4], FoldIn<D / 64> &in,
                                            f4 (&acc)[kGroups<G>][D / 64], float &lvec) {
     constexpr int NG = kGroups<G>, H = D / 64, TS = Shape<D>::kTileStride;
     if constexpr (T + 3 < kChunk) {
@@ -611,7 +622,7 @@ __device__ __forceinline__ void fold_token(const WaveLds<G, D> &S, lds_f32 *eb, 
     const float el = (T % 4 == 0) ? e4.x : (T % 4 == 1) ? e4.y : (T % 4 == 2) ? e4.z : e4.w;
     const float al = (T % 4 == 0) ? a4.x : (T % 4 == 1) ? a4.y : (T % 4 == 2) ? a4.z : a4.w;
     if constexpr (MOVE) {
-        const uint32_t mw = T < 32 ? uint32_t(amask) : uint32_t(amask >> 32);
+        const uint32_t mw = am[T / 32];
         if ((mw & (1u << (T % 32))) != 0) {
             float av[G];
 #pragma unroll
@@ -640,15 +651,15 @@ __device__ __forceinline__ void fold_token(const WaveLds<G, D> &S, lds_f32 *eb, 
 // stalls the SIMD, so few switches between the two pay.
 template <int G, int D, int T>
 __device__ __forceinline__ void fold(const WaveLds<G, D> &S, lds_f32 *eb, lds_f32 *ab, const uint16_t *vb,
-                                     uint64_t amask, const float (&ea)[kGroups<G>][4], FoldIn<D / 64> &in,
+                                     const uint32_t (&am)[2], const float (&ea)[kGroups<G>][4], FoldIn<D / 64> &in,
                                      f4 (&acc)[kGroups<G>][D / 64], float &lvec) {
     constexpr int GS = 16, NG = kGroups<G>, H = D / 64;
     if constexpr (T < kChunk) {
-        const uint32_t mw = T < 32 ? uint32_t(amask) : uint32_t(amask >> 32);
+        const uint32_t mw = am[T / 32];
         constexpr uint32_t gm = uint32_t(((1ull << GS) - 1ull) << (T % 32));
         if ((mw & gm) == 0) {
             static_for<0, GS>([&](auto K) {
-                fold_token<G, D, T + decltype(K)::value, false>(S, eb, ab, vb, amask, ea, in, acc, lvec);
+                fold_token<G, D, T + decltype(K)::value, false>(S, eb, ab, vb, am, ea, in, acc, lvec);
             });
             static_for<0, GS / 4>([&](auto) {
                 __builtin_amdgcn_sched_group_barrier(0x002, 4 * (H + 1), 0);
@@ -656,10 +667,10 @@ __device__ __forceinline__ void fold(const WaveLds<G, D> &S, lds_f32 *eb, lds_f3
             });
         } else {
             static_for<0, GS>([&](auto K) {
-                fold_token<G, D, T + decltype(K)::value, true>(S, eb, ab, vb, amask, ea, in, acc, lvec);
+                fold_token<G, D, T + decltype(K)::value, true>(S, eb, ab, vb, am, ea, in, acc, lvec);
             });
         }
-        fold<G, D, T + GS>(S, eb, ab, vb, amask, ea, in, acc, lvec);
+        fold<G, D, T + GS>(S, eb, ab, vb, am, ea, in, acc, lvec);
     }
 }
 
@@ -781,7 +792,12 @@ void attn_wave_kernel(const HeadDev *__restrict__ heads, const WorkItem *__restr
             }
         }
         int n = min(kChunk, wi.tok_end - t);
-        if constexpr (XKV) n = min(n, min(kc.t1 - t, vc.t1 - t));
+        if constexpr (XKV) {
+            // within both blocks; raw rows as loaded; escapes inside the windows
+            n = min(n, min(kc.t1 - t, vc.t1 - t));
+            if (kc.mode() == 0 || vc.mode() == 0) n = min(n, kRawRows);
+            n = min(n, min(escape_rows<D>(kc, t - kc.t0), escape_rows<D>(vc, t - vc.t0)));
+        }
         if (n <= 0) break; // unreachable with plan-checked descriptors (n_tokens > 0)
         const int tn = t + n;
 
@@ -802,7 +818,7 @@ void attn_wave_kernel(const HeadDev *__restrict__ heads, const WorkItem *__restr
             } else {
                 flush = ORDER == 1;
             }
-            decode_row<D>(kc, RK, S.bp, my_row, t - kc.t0, n);
+            decode_row<D>(kc, RK, S.bp, S.tile, my_row, t - kc.t0, n);
             wave_sync();
             flush |= patch_escapes<D, ORDER == 1>(kc, t - kc.t0, n, S.tile, klow);
         } else {
@@ -845,7 +861,7 @@ void attn_wave_kernel(const HeadDev *__restrict__ heads, const WorkItem *__restr
                 base_pairs<D>(vc, S.bp);
                 wave_sync();
             }
-            decode_row<D>(vc, RV, S.bp, my_row, t - vc.t0, n);
+            decode_row<D>(vc, RV, S.bp, S.tile, my_row, t - vc.t0, n);
             wave_sync();
             patch_escapes<D>(vc, t - vc.t0, n, S.tile);
             // the loads are issued on every chunk (the last one re-reads its
@@ -883,40 +899,26 @@ void attn_wave_kernel(const HeadDev *__restrict__ heads, const WorkItem *__restr
         // alpha = exp(m_prev - m) (rows without such a token keep 1). Tokens
         // past the chunk's end get e = 0 and alpha = 1.
         const uint64_t nmask = n >= kChunk ? ~0ull : ((1ull << n) - 1ull);
-        float mi[G], d[G], ev[G];
-        uint64_t rmask[G];
+        float mi[G];
         uint64_t amask = 0;
 #pragma unroll
         for (int g = 0; g < G; ++g) mi[g] = s[g];
         wave_scan_max_rows<G>(mi);
+        // row by row, each row's values stored as soon as they are made (few
+        // registers live beside the rows in flight)
 #pragma unroll
         for (int g = 0; g < G; ++g) {
-            mi[g] = fmaxf(mi[g], msc[g]);
-            d[g] = wave_shift_up(mi[g], msc[g]) - mi[g];
+            const float m = fmaxf(mi[g], msc[g]);
+            const float dg = wave_shift_up(m, msc[g]) - m;
             // alpha != 1 exactly when m_prev - m is not zero (NaN included)
-            rmask[g] = __ballot(!(d[g] == 0.0f)) & nmask;
-            amask |= rmask[g];
-            ev[g] = kvexp_expf_nonpos_nb(s[g] - mi[g], tab);
-            msc[g] = readlane_f32(mi[g], n - 1);
-        }
-        if (n < kChunk) {
-#pragma unroll
-            for (int g = 0; g < G; ++g) ev[g] = lane < n ? ev[g] : 0.0f;
-        }
-        {
-            float al[G];
-#pragma unroll
-            for (int g = 0; g < G; ++g) al[g] = 1.0f;
-            if (amask != 0) {
-#pragma unroll
-                for (int g = 0; g < G; ++g)
-                    if (rmask[g] != 0) al[g] = lane < n ? kvexp_expf_nonpos_nb(d[g], tab) : 1.0f;
-            }
-#pragma unroll
-            for (int g = 0; g < G; ++g) {
-                S.eT[g][lane] = ev[g];
-                S.aT[g][lane] = al[g];
-            }
+            const uint64_t rmask = __ballot(!(dg == 0.0f)) & nmask;
+            amask |= rmask;
+            const float e = kvexp_expf_nonpos_nb(s[g] - m, tab);
+            S.eT[g][lane] = lane < n ? e : 0.0f;
+            float al = 1.0f;
+            if (rmask != 0) al = lane < n ? kvexp_expf_nonpos_nb(dg, tab) : 1.0f;
+            S.aT[g][lane] = al;
+            msc[g] = readlane_f32(m, n - 1);
         }
         wave_sync();
 
@@ -924,10 +926,14 @@ void attn_wave_kernel(const HeadDev *__restrict__ heads, const WorkItem *__restr
         {
             // e as the A operands: ea[rg][j] at lane 4b + r holds e[4 rg + r][16 j + b]
             // (rows past G repeat row G - 1; their results are not used)
+            // (the lane index passes through an empty asm so that these LDS
+            // addresses are made here, not kept live across the loop)
+            int lq = lane;
+            asm volatile("" : "+v"(lq));
             float ea[NG][4];
 #pragma unroll
             for (int rg = 0; rg < NG; ++rg) {
-                const int g = min(4 * rg + (lane & 3), G - 1);
+                const int g = min(4 * rg + (lq & 3), G - 1);
 #pragma unroll
                 for (int j = 0; j < 4; ++j) ea[rg][j] = S.eT[g][16 * j + (lane >> 2)];
             }
@@ -942,7 +948,12 @@ void attn_wave_kernel(const HeadDev *__restrict__ heads, const WorkItem *__restr
                 for (int h = 0; h < H; ++h) in.v[k][h] = vb[k * (TS / 2) + 64 * h];
             in.e4[0] = *reinterpret_cast<lds_f4 *>(eb);
             in.a4[0] = *reinterpret_cast<lds_f4 *>(ab);
-            fold<G, D, 0>(S, eb, ab, vb, amask, ea, in, acc, lvec);
+            // amask as two words behind an empty asm: the group tests stay
+            // 32-bit scalar compares (not a 64-bit vector compare against a
+            // constant held in registers)
+            uint32_t am[2] = {uint32_t(amask), uint32_t(amask >> 32)};
+            asm volatile("" : "+s"(am[0]), "+s"(am[1]));
+            fold<G, D, 0>(S, eb, ab, vb, am, ea, in, acc, lvec);
         }
         wave_sync();
         t = tn;

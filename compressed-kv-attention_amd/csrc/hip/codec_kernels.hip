@@ -539,14 +539,17 @@ __global__ __launch_bounds__(kThreads) void append_one_kernel(const AppendJobDev
     for (int i = int(threadIdx.x); i < total; i += kThreads) to[i] = from[i];
 }
 
-// -------------------------------------------------- escape-position index --
-// Element index of every escape of a coded block (mode 2, 3 or 4) whose
-// `total` codes start at `codes`, written to pos[0 .. n_escape); a sentinel
-// count other than n_escape raises kStEscape. All threads of the workgroup
-// call it.
+// ------------------------------------------------------------ escape records --
+// The escape record (element index | word << 16, kvexp_types.h) of every
+// escape of a coded block (mode 2, 3 or 4) whose `total` codes start at
+// `codes`, written to rec[0 .. n_escape): the i-th sentinel in scan order
+// takes the i-th escape word, which the format stores after the codes; a
+// sentinel count other than n_escape raises kStEscape. All threads of the
+// workgroup call it.
 __device__ __forceinline__ void escape_positions(const uint8_t *codes, int mode, int total, int n_escape,
-                                                 uint16_t *__restrict__ pos, int *scan_tmp,
+                                                 uint32_t *__restrict__ pos, int *scan_tmp,
                                                  uint32_t *__restrict__ status) {
+    const uint8_t *words = codes + (total * mode + 7) / 8;
     const int U = code_unit(mode);
     const uint32_t sentinel = (1u << mode) - 1u;
     const int units = total / U;
@@ -568,7 +571,10 @@ __device__ __forceinline__ void escape_positions(const uint8_t *codes, int mode,
             for (int k = 0; k < 8; ++k) {
                 if (k >= U) break;
                 if (unit_code(cw, mode, k) == sentinel) {
-                    if (rank < n_escape) pos[rank] = uint16_t(U * u + k);
+                    if (rank < n_escape) {
+                        const uint32_t w = uint32_t(words[2 * rank]) | (uint32_t(words[2 * rank + 1]) << 8);
+                        pos[rank] = uint32_t(U * u + k) | (w << 16);
+                    }
                     ++rank;
                 }
             }
@@ -647,7 +653,7 @@ __global__ __launch_bounds__(kThreads) void esc_pos_kernel(const EscJob *__restr
 
 // Plan update after appends. Workgroups [0, n_jobs), one per tensor: the
 // last block is checked against the index again and its descriptor and
-// escape positions are rewritten (blocks before it are unchanged by an
+// escape records are rewritten (blocks before it are unchanged by an
 // append); the entry after it becomes a zero-token sentinel (a split kernel
 // that reached it would stop there), and an index that ends before the
 // attended tokens raises kStIndex. The workgroups after them set each device

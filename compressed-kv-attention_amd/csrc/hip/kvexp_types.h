@@ -23,11 +23,10 @@ struct HeadDev {
     const int32_t *kfirst, *vfirst; // block first tokens (n_blocks + 1)
     const uint16_t *kraw, *vraw; // [seq, dim] BF16 (raw heads)
     // Plan-owned, XKV heads of the wave kernel: validated block descriptors
-    // and the escape-position index (block b's escape words are entries
-    // [desc[b].esc0, desc[b].esc0 + n_escape) and escpos[k] is the element
-    // index (row * dim + channel) of entry k inside its block).
+    // and the escape records (block b's escapes are records
+    // [desc[b].esc, desc[b].esc + n_escape), in scan order; format at kEscPad).
     const struct BlockDesc *kdesc, *vdesc;
-    const uint16_t *kescpos, *vescpos;
+    const uint32_t *kesc, *vesc;
     int32_t seq;
     int32_t n_splits;            // work items of this head, in merge order
     int32_t ws_base;             // first partial-state slot of this head
@@ -36,12 +35,20 @@ struct HeadDev {
     int32_t pad;
 };
 
+// An escape record: the escape's element index inside its block (row * dim
+// + channel) in bits 0..15 and its BF16 word in bits 16..31. The plan copies
+// each block's escape words out of the container next to their positions, so
+// the wave kernel reads a window of escapes with one 16-byte load per lane.
+// Every records array ends with kEscPad spare records, so such a window read
+// from any escape of any block stays inside the allocation.
+constexpr int kEscPad = 260;
+
 // One block of a container as the wave kernel reads it, built and checked
 // against the block index once per plan (esc_start_kernel). 32 bytes, so a
 // scalar load of one descriptor reads exactly one.
 struct BlockDesc {
     const uint8_t *data; // the block's header
-    const uint16_t *esc; // its entries in the tensor's escape-position index
+    const uint32_t *esc; // its escape records
     uint32_t meta;       // mode | n_tokens << 8 | n_escape << 16 (n_escape 0 for raw blocks)
     uint32_t pad[3];
 };
@@ -53,11 +60,11 @@ struct EscJob {
     const int64_t *offs;
     const int32_t *first; // block first tokens (n_blocks + 1)
     int32_t *esc0;        // out: n_blocks + 1 entries
-    uint16_t *pos;        // out: esc0[n_blocks] entries
+    uint32_t *pos;        // out: esc0[n_blocks] escape records
     BlockDesc *desc;      // out: n_blocks entries (nullable)
     int32_t n_blocks;
     int32_t dim;
-    int32_t pos_cap;      // entries of `pos` (the tensor's escapes plus room for its last block to grow)
+    int32_t pos_cap;      // records of `pos` (the tensor's escapes plus room for its last block to grow)
     int32_t seq;          // tokens a plan update attends (esc_tail_kernel checks the index covers them)
 };
 

@@ -237,7 +237,7 @@ struct kvexp_hip_plan {
     DevBuf djobs;
     bool wave = false; // one-wave-per-split kernel (dim 64 or 128)
     DevBuf heads, items, merge_ids, ws, status;
-    // wave kernel: merge work (head, row), escape-position index, block descriptors
+    // wave kernel: merge work (head, row), escape records, block descriptors
     DevBuf mitems, esc0, escpos, desc;
     int n_mitems = 0;
     int n_dev_heads = 0, n_items = 0, n_merge = 0;
@@ -302,7 +302,7 @@ void check_status_word(uint32_t *d_status, hipStream_t s) {
         fail(KVEXP_HIP_FORMAT_ERROR, status_message(st));
     }
 }
-// Block descriptors and escape-position index of every XKV tensor of a plan:
+// Block descriptors and escape records of every XKV tensor of a plan:
 // per block its address, first escape index and header fields (checked
 // against the block index; a mismatch fails the plan with the matching
 // format error), and per escape its element index inside the block. Built on
@@ -361,10 +361,13 @@ void build_escape_index(kvexp_hip_plan &p, const kvexp_hip_head *heads, int n_he
         pos_total += size_t(jobs[i].pos_cap);
         for (int b = 0; b < jobs[i].n_blocks; ++b) blocks.push_back(make_int2(int(i), b));
     }
-    p.escpos = DevBuf(std::max<size_t>(pos_total, 1) * sizeof(uint16_t));
-    for (size_t i = 0; i < jobs.size(); ++i) jobs[i].pos = p.escpos.as<uint16_t>() + pos_at[i];
+    // escape records, then kEscPad spare ones: a kernel's window of records
+    // read from any escape stays inside the allocation (zeroed, never used)
+    p.escpos = DevBuf((pos_total + size_t(kvexp_dev::kEscPad)) * sizeof(uint32_t));
+    HIPX(hipMemsetAsync(p.escpos.as<uint32_t>() + pos_total, 0, size_t(kvexp_dev::kEscPad) * sizeof(uint32_t), s));
+    for (size_t i = 0; i < jobs.size(); ++i) jobs[i].pos = p.escpos.as<uint32_t>() + pos_at[i];
     HIPX(hipMemcpyAsync(djobs.p, jobs.data(), jobs.size() * sizeof(kvexp_dev::EscJob), hipMemcpyHostToDevice, s));
-    // pass 2: descriptors (with the escape-position pointers)
+    // pass 2: descriptors (with the escape-record pointers)
     HIPX(kvexp_launch::esc_start(djobs.as<kvexp_dev::EscJob>(), int(jobs.size()), st, s));
     DevBuf dblocks(std::max<size_t>(blocks.size(), 1) * sizeof(int2));
     HIPX(hipMemcpyAsync(dblocks.p, blocks.data(), blocks.size() * sizeof(int2), hipMemcpyHostToDevice, s));
@@ -377,9 +380,9 @@ void build_escape_index(kvexp_hip_plan &p, const kvexp_hip_head *heads, int n_he
         for (int c = 0; c < per_head; ++c) {
             HeadDev &d = hv[size_t(h * per_head + c)];
             d.kdesc = jobs[size_t(2 * h)].desc;
-            d.kescpos = jobs[size_t(2 * h)].pos;
+            d.kesc = jobs[size_t(2 * h)].pos;
             d.vdesc = jobs[size_t(2 * h + 1)].desc;
-            d.vescpos = jobs[size_t(2 * h + 1)].pos;
+            d.vesc = jobs[size_t(2 * h + 1)].pos;
         }
     }
 }
@@ -810,7 +813,7 @@ void balance_items(kvexp_hip_plan &p, std::vector<WorkItem> &items, const int32_
 // Builds every device-side part of a fresh plan from its heads: work items
 // (token_bounds splits, split starts checked against the block index), device
 // heads, merge work, and for the one-wave kernel the block descriptors and
-// escape-position index. Stream-ordered on `s`: it first waits for the work
+// escape records. Stream-ordered on `s`: it first waits for the work
 // already queued there (the encodes or appends that wrote the containers and
 // indexes it reads) and synchronises only `s`. Status words: the plan's own.
 void plan_build(kvexp_hip_plan *p, const kvexp_hip_head *heads, int n_heads, hipStream_t s) {
@@ -1031,7 +1034,7 @@ int kvexp_hip_plan_create(kvexp_hip_ctx *ctx, const kvexp_hip_head *heads, int n
 // block_tokens tokens of a decode loop) the plan is built again. Otherwise
 // only the last split of each head ends later, and only the last block of
 // each container changed (kvexp_hip_append rewrites nothing before it): its
-// descriptor and escape positions are rewritten on the GPU, the device heads
+// descriptor and escape records are rewritten on the GPU, the device heads
 // and work items are uploaded again, all on `stream`.
 int kvexp_hip_plan_update(kvexp_hip_plan *plan, const kvexp_hip_head *heads, int n_heads, void *stream) {
     return guarded([&] {
