@@ -60,7 +60,6 @@ struct Shape {
     static constexpr int kSlotFloats = kSlotQ * (D + 2);
     static constexpr int kSmRegs = D / 16;          // 16-byte registers of a row's sign/mantissa bytes
     static constexpr int kRowRegs = kSmRegs + D / 32; // + its 4-bit codes: what a coded row needs
-    static constexpr int kRawRegs = D / 8;          // 16-byte registers of a raw BF16 row
     static constexpr int kOctets = D / 8;           // channel octets per row
     static constexpr int kHalves = D / 64;          // channels per lane in the fold (lane, lane + 64, ...)
     static constexpr int kWaves = D == 64 ? 4 : 2;  // waves per workgroup (LDS: see WaveLds)
@@ -674,6 +673,43 @@ __device__ __forceinline__ void fold(const WaveLds<G, D> &S, lds_f32 *eb, lds_f3
     }
 }
 
+// The lane index as an opaque value: the addresses derived from it are then
+// recomputed where they are used (a few instructions) instead of being
+// hoisted out of the chunk loop and held in registers across it.
+__device__ __forceinline__ int lane_here() {
+    int l = int(__lane_id());
+    asm volatile("" : "+v"(l));
+    return l;
+}
+
+// Rows of the plain BF16 kernel: register j of lane l holds bytes
+// [1024 j + 16 l, + 16) of the chunk's rows from token t (row
+// (1024 j + 16 l) / 2D), so every load reads one contiguous run; rows past
+// `avail` repeat the last one.
+template <int D>
+__device__ __forceinline__ void load_raw(const uint16_t *base, int t, int avail, uint4 (&R)[D / 8]) {
+    const uint8_t *b = reinterpret_cast<const uint8_t *>(base + size_t(t) * D);
+    const int lane = lane_here();
+#pragma unroll
+    for (int j = 0; j < D / 8; ++j) {
+        const int off = 1024 * j + 16 * lane;
+        R[j] = ld16(b + uint32_t(min(off / (2 * D), avail - 1) * (2 * D) + off % (2 * D)));
+    }
+}
+
+template <int D>
+__device__ __forceinline__ void store_raw(const uint4 (&R)[D / 8], uint8_t *tile) {
+    const int lane = lane_here();
+#pragma unroll
+    for (int j = 0; j < D / 8; ++j) {
+        const int off = 1024 * j + 16 * lane;
+        *reinterpret_cast<uint4 *>(tile + (off / (2 * D)) * Shape<D>::kTileStride + off % (2 * D)) = R[j];
+    }
+}
+
+template <bool XKV, int D> struct RegsOf { typedef uint4 T[Shape<D>::kRowRegs]; };
+template <int D> struct RegsOf<false, D> { typedef uint4 T[D / 8]; };
+
 // At D = 64 the XKV instantiations are held to three waves per SIMD (168
 // VGPRs), and LDS allows three workgroups of four waves per CU; at D = 128
 // two waves per SIMD (the rows in flight take twice the registers), and
@@ -749,7 +785,7 @@ void attn_wave_kernel(const HeadDev *__restrict__ heads, const WorkItem *__restr
     float lvec = 0.0f; // lane g < G holds l of query row g
 
     Cursor kc{}, vc{};
-    uint4 RK[XKV ? Shape<D>::kRowRegs : Shape<D>::kRawRegs], RV[XKV ? Shape<D>::kRowRegs : Shape<D>::kRawRegs];
+    typename RegsOf<XKV, D>::T RK, RV;
     int t = wi.tok_begin;
     if constexpr (XKV) {
         enter_block(kc, hd.kdesc + wi.kblk, t);
@@ -759,15 +795,9 @@ void attn_wave_kernel(const HeadDev *__restrict__ heads, const WorkItem *__restr
         block_vectors<D>(vc);
         load_rows<D>(vc, 0, min(kChunk, min(vc.t1, wi.tok_end) - t), RV);
     } else {
-        // unconditional loads (lanes past the chunk repeat its last row)
-        const int row = t + min(lane, min(kChunk, wi.tok_end - t) - 1);
-        const uint8_t *kr = reinterpret_cast<const uint8_t *>(hd.kraw + size_t(row) * D);
-        const uint8_t *vr = reinterpret_cast<const uint8_t *>(hd.vraw + size_t(row) * D);
-#pragma unroll
-        for (int i = 0; i < D / 8; ++i) {
-            RK[i] = ld16(kr + 16 * i);
-            RV[i] = ld16(vr + 16 * i);
-        }
+        // unconditional loads (rows past the split repeat its last row)
+        load_raw<D>(hd.kraw, t, min(kChunk, wi.tok_end - t), RK);
+        load_raw<D>(hd.vraw, t, min(kChunk, wi.tok_end - t), RV);
     }
     uint8_t *my_row = S.tile + lane * TS; // the lane's token
 
@@ -822,20 +852,20 @@ void attn_wave_kernel(const HeadDev *__restrict__ heads, const WorkItem *__restr
             wave_sync();
             flush |= patch_escapes<D, ORDER == 1>(kc, t - kc.t0, n, S.tile, klow);
         } else {
-            uint4 *dst = reinterpret_cast<uint4 *>(my_row);
-#pragma unroll
-            for (int i = 0; i < D / 8; ++i) dst[i] = RK[i];
+            store_raw<D>(RK, S.tile);
             if constexpr (ORDER == 1) {
+                // any element of the chunk's rows (pieces of rows < n) below the bound
                 u16x2 lo = {0xFFFFu, 0xFFFFu};
 #pragma unroll
-                for (int i = 0; i < D / 8; ++i) {
-                    const uint32_t c4[4] = {RK[i].x, RK[i].y, RK[i].z, RK[i].w};
+                for (int j = 0; j < D / 8; ++j) {
+                    if ((1024 * j + 16 * lane) / (2 * D) >= n) continue;
+                    const uint32_t c4[4] = {RK[j].x, RK[j].y, RK[j].z, RK[j].w};
 #pragma unroll
                     for (int k = 0; k < 4; ++k)
                         lo = __builtin_elementwise_min(lo, (__builtin_bit_cast(u16x2, c4[k]) & uint16_t(0x7FFF)) -
                                                                uint16_t(1));
                 }
-                flush = __ballot(lane < n && uint32_t(min(lo.x, lo.y)) < klow) != 0;
+                flush = __ballot(uint32_t(min(lo.x, lo.y)) < klow) != 0;
             }
         }
         wave_sync();
@@ -875,20 +905,13 @@ void attn_wave_kernel(const HeadDev *__restrict__ heads, const WorkItem *__restr
             block_vectors<D>(vc);
             load_rows<D>(vc, tp - vc.t0, min(kChunk, min(vc.t1, wi.tok_end) - tp), RV);
         } else {
-            uint4 *dst = reinterpret_cast<uint4 *>(my_row);
-#pragma unroll
-            for (int i = 0; i < D / 8; ++i) dst[i] = RV[i];
+            store_raw<D>(RV, S.tile);
             if (n < kChunk && lane >= n) fill_negzero<D>(my_row);
             {
                 // issued on every chunk (the last one re-reads its final row), K first
                 const int tp = min(tn, wi.tok_end - 1);
-                const int row = tp + min(lane, min(kChunk, wi.tok_end - tp) - 1);
-                const uint8_t *vr = reinterpret_cast<const uint8_t *>(hd.vraw + size_t(row) * D);
-                const uint8_t *kr = reinterpret_cast<const uint8_t *>(hd.kraw + size_t(row) * D);
-#pragma unroll
-                for (int i = 0; i < D / 8; ++i) RK[i] = ld16(kr + 16 * i);
-#pragma unroll
-                for (int i = 0; i < D / 8; ++i) RV[i] = ld16(vr + 16 * i);
+                load_raw<D>(hd.kraw, tp, min(kChunk, wi.tok_end - tp), RK);
+                load_raw<D>(hd.vraw, tp, min(kChunk, wi.tok_end - tp), RV);
             }
         }
 
