@@ -20,6 +20,7 @@
 // the new trailing partial block's raw tokens for the next append.
 #include "kvexp_device.h"
 #include <algorithm>
+#include <mutex>
 #include "kvexp_types.h"
 
 namespace kvexp_dev {
@@ -794,6 +795,42 @@ hipError_t esc_pos(const EscJob *jobs, const int2 *blocks, int n_blocks, uint32_
     if (n_blocks <= 0) return hipSuccess;
     hipLaunchKernelGGL(esc_pos_kernel, dim3(n_blocks), dim3(kThreads), 0, s, jobs, blocks, status);
     return hipGetLastError();
+}
+
+// ---------------------------------------------------- no-alloc scratch --
+// Device scratch of the no-allocation encoder entry point: a file-scope array
+// (each GPU the library runs on holds its own copy until the process ends),
+// addressed from the host only through the per-device pointer that
+// hipGetSymbolAddress returns (the array's name in host code is not a device
+// address). Calls that overlap on one GPU share it and race.
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+namespace {
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kMaxScratchDevices] = {};
+} // namespace
+
+// Looks the array up on `device` (which must be current) once; later calls
+// return the stored pointer.
+hipError_t noalloc_scratch_setup(int device, void **ptr) {
+    *ptr = nullptr;
+    if (device < 0 || device >= kMaxScratchDevices) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch_ptr[device] == nullptr) {
+        void *p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return e;
+        g_scratch_ptr[device] = p;
+    }
+    *ptr = g_scratch_ptr[device];
+    return hipSuccess;
+}
+
+void *noalloc_scratch(int device) {
+    if (device < 0 || device >= kMaxScratchDevices) return nullptr;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    return g_scratch_ptr[device];
 }
 
 hipError_t expf(const float *x, float *y, size_t n, hipStream_t s) {

@@ -78,6 +78,11 @@ struct WorkItem {
 };
 
 // Per-block result of the encoder's statistics pass.
+// Size of the no-allocation encoder's device scratch (per GPU): block
+// metadata and base-exponent candidates of up to about 20,000 blocks at
+// head_dim 64 (2.6M tokens of 128-token blocks) or 5,300 at head_dim 256.
+constexpr size_t kNoAllocScratchBytes = size_t(4) << 20;
+
 struct EncBlockMeta {
     int64_t bytes;
     int32_t mode;

@@ -47,6 +47,8 @@ hipError_t attention_wave(bool xkv, int order, int G, int dim, const HeadDev *he
 hipError_t wave_merge(int dim, const HeadDev *heads, const int2 *mitems, int n_mitems, float *out, float *lse,
                       const float *ws, hipStream_t s);
 int wave_waves_per_wg(int dim);
+hipError_t noalloc_scratch_setup(int device, void **ptr);
+void *noalloc_scratch(int device);
 } // namespace kvexp_launch
 
 namespace {
@@ -426,6 +428,9 @@ int kvexp_hip_ctx_create(int device, kvexp_hip_ctx **out) {
         try {
             c->status = DevBuf(sizeof(uint32_t));
             HIPX(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking));
+            // the no-allocation encoder's scratch on this device (looked up once per device)
+            void *scratch = nullptr;
+            HIPX(kvexp_launch::noalloc_scratch_setup(device, &scratch));
             HIPX(hipMemsetAsync(c->status.p, 0, sizeof(uint32_t), c->stream));
             HIPX(hipStreamSynchronize(c->stream));
         } catch (...) {
@@ -541,6 +546,48 @@ int kvexp_hip_encode(kvexp_hip_ctx *ctx, const uint16_t *d_kv, int seq, int dim,
             }
             *bytes_out = size_t(total);
         }
+    });
+}
+
+// kvexp_hip_encode with its scratch (block metadata and base-exponent
+// candidates) in the library's per-device static array instead of context
+// buffers grown with hipMalloc: no allocation, no synchronisation, and the
+// index is an output the caller provides. Rejects inputs whose scratch would
+// not fit the array.
+int kvexp_hip_encode_noalloc(kvexp_hip_ctx *ctx, const uint16_t *d_kv, int seq, int dim, int bt, uint8_t *d_out,
+                             size_t capacity, int64_t *d_offsets, int32_t *d_first_token, uint32_t *d_status,
+                             void *stream) {
+    return guarded([&] {
+        if (ctx == nullptr) fail(KVEXP_HIP_INVALID_ARGUMENT, "kvexp_hip_encode_noalloc: null context");
+        // codec.cpp:40-52, as kvexp_hip_encode
+        if (d_kv == nullptr || seq <= 0 || dim <= 0 || bt <= 0)
+            fail(KVEXP_HIP_INVALID_ARGUMENT, "encode_bf16: empty input");
+        if (dim % 4 != 0 || dim > kMaxDim)
+            fail(KVEXP_HIP_INVALID_ARGUMENT, "encode_bf16: head_dim must be a multiple of 4 and at most 256");
+        if (bt > 255) fail(KVEXP_HIP_INVALID_ARGUMENT, "encode_bf16: block_tokens must fit in a byte");
+        if (int64_t(bt) * dim > 65535)
+            fail(KVEXP_HIP_INVALID_ARGUMENT, "encode_bf16: block escape count would not fit in u16");
+        if (d_out == nullptr || d_offsets == nullptr || d_first_token == nullptr)
+            fail(KVEXP_HIP_INVALID_ARGUMENT, "kvexp_hip_encode_noalloc: null output or block index");
+        if (int64_t(capacity) < kvexp_hip_encode_bound(seq, dim, bt))
+            fail(KVEXP_HIP_CAPACITY, "kvexp_hip_encode_noalloc: capacity below kvexp_hip_encode_bound");
+        const int nb = kvexp_hip_block_count(seq, bt);
+        auto up = [](size_t n) { return (n + 255u) & ~size_t(255); };
+        const size_t meta_bytes = up(size_t(nb) * sizeof(EncBlockMeta));
+        const size_t base_bytes = up(size_t(nb) * 3u * size_t(dim));
+        const size_t need = meta_bytes + base_bytes + 256u; // + a status word when d_status is NULL
+        if (need > kvexp_dev::kNoAllocScratchBytes)
+            fail(KVEXP_HIP_CAPACITY, "kvexp_hip_encode_noalloc: " + std::to_string(nb) + " blocks of head_dim " +
+                                         std::to_string(dim) + " need " + std::to_string(need) +
+                                         " bytes of scratch, more than its " +
+                                         std::to_string(kvexp_dev::kNoAllocScratchBytes));
+        auto *sp = static_cast<uint8_t *>(kvexp_launch::noalloc_scratch(ctx->device));
+        if (sp == nullptr) fail(KVEXP_HIP_LOGIC_ERROR, "kvexp_hip_encode_noalloc: scratch not set up on this device");
+        DeviceGuard g(ctx->device);
+        uint32_t *st = d_status != nullptr ? d_status : reinterpret_cast<uint32_t *>(sp + meta_bytes + base_bytes);
+        HIPX(kvexp_launch::encode(d_kv, seq, dim, bt, nb, reinterpret_cast<EncBlockMeta *>(sp), sp + meta_bytes,
+                                  d_offsets, d_first_token, d_out, st, static_cast<hipStream_t>(stream), false, 0,
+                                  ctx->enc_modes));
     });
 }
 

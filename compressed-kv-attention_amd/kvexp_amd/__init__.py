@@ -99,6 +99,7 @@ def lib() -> C.CDLL:
     L.kvexp_hip_encode_bound.argtypes = [i32, i32, i32]
     L.kvexp_hip_build_index.argtypes = [vp, sz, i32, i32, vp, vp, i32, C.POINTER(i32)]
     L.kvexp_hip_encode.argtypes = [vp, vp, i32, i32, i32, vp, sz, vp, vp, C.POINTER(sz), vp]
+    L.kvexp_hip_encode_noalloc.argtypes = [vp, vp, i32, i32, i32, vp, sz, vp, vp, vp, vp]
     L.kvexp_hip_decode.argtypes = [vp, vp, sz, vp, vp, i32, i32, i32, vp, i32, vp]
     L.kvexp_hip_append.argtypes = [vp, vp, i32, i32, i32, i32, vp, vp, sz, vp, vp, i32, C.POINTER(sz), vp]
     L.kvexp_hip_append_batch.argtypes = [vp, C.POINTER(_AppendJob), i32, i32, i32, i32, vp]

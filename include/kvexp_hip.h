@@ -120,6 +120,25 @@ int kvexp_hip_encode(kvexp_hip_ctx *ctx, const uint16_t *d_kv, int seq, int dim,
                      uint8_t *d_out, size_t capacity, int64_t *d_offsets, int32_t *d_first_token,
                      size_t *bytes_out, void *stream);
 
+/* kvexp_hip_encode for callers that cannot allocate (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). No
+ * counterpart in the reference. It allocates nothing and does not
+ * synchronise: its scratch is a static device array of
+ * KVEXP_HIP_NOALLOC_SCRATCH_BYTES per GPU (looked up when a context is
+ * created on that GPU), so n_blocks * (16 + 3 * dim) bytes (each part rounded
+ * up to 256) plus 256 must fit in it, else KVEXP_HIP_CAPACITY; about 20,000
+ * blocks at head_dim 64. The block index is an output here: d_offsets and
+ * d_first_token (n_blocks + 1 entries) are required; the container size is
+ * d_offsets[n_blocks]. When d_status is not NULL, a nonzero value is OR-ed
+ * into it if the encoder's size model drifted (it is never cleared). All
+ * calls on one GPU share the scratch, which keeps the last call's contents:
+ * calls that overlap on one GPU (any contexts, any streams) race. Output is
+ * byte-identical to kvexp_hip_encode's. */
+#define KVEXP_HIP_NOALLOC_SCRATCH_BYTES 4194304
+int kvexp_hip_encode_noalloc(kvexp_hip_ctx *ctx, const uint16_t *d_kv, int seq, int dim, int block_tokens,
+                             uint8_t *d_out, size_t capacity, int64_t *d_offsets, int32_t *d_first_token,
+                             uint32_t *d_status, void *stream);
+
 /* Appends n_new tokens (d_new [n_new, dim] BF16) to a device container that
  * holds the first n_tokens tokens of a sequence, so that afterwards it is
  * byte-identical to encode_bf16 of all n_tokens + n_new tokens (blocks are
