@@ -567,9 +567,12 @@ def main() -> int:
         torch.cuda.synchronize()
         samples.append(e0.elapsed_time(e1))
     med_ms = float(np.median(samples))
-    dp_plans = [ctx.plan([dict(kx=ek[i], vx=ev[i], seq=S, splits=splits) for i in range(H)], G, D, BT, order=1)
+    # the AVX-512 order's own split count (its kernel may run fewer waves per SIMD)
+    dp_splits = a.splits or ctx.suggest_splits(H, S, BT, dim=D, n_q=G, order=1)
+    dp_plans = [ctx.plan([dict(kx=ek[i], vx=ev[i], seq=S, splits=dp_splits) for i in range(H)], G, D, BT, order=1)
                 for ek, ev in enc_copies]
-    dp_raw = ctx.plan([dict(k=raw_k[i], v=raw_v[i], seq=S, splits=splits) for i in range(H)], G, D, BT, order=1)
+    dp_raw = ctx.plan([dict(k=raw_k[i], v=raw_v[i], seq=S, splits=dp_splits) for i in range(H)], G, D, BT,
+                      order=1)
     odp = dp_plans[0].run(q, check_errors=True).clone()
     odr = dp_raw.run(q, check_errors=True).clone()
     torch.cuda.synchronize()
@@ -578,7 +581,7 @@ def main() -> int:
     for p in dp_plans + [dp_raw]:
         p.close()
     log(f"hot (one copy) {ms_hot * 1e3:.1f} us/step, median of 25 single steps {med_ms * 1e3:.1f} us; "
-        f"AVX-512 BF16 order {ms_dp * 1e3:.1f} us/step (XKV == raw: {dp_equal})")
+        f"AVX-512 BF16 order {ms_dp * 1e3:.1f} us/step at {dp_splits} splits (XKV == raw: {dp_equal})")
 
     q_bytes = H * G * D * 2
     out_bytes = H * G * D * 4
@@ -652,6 +655,7 @@ def main() -> int:
         "hot_us_per_step": round(ms_hot * 1e3, 2),
         "median_us_single_step": round(med_ms * 1e3, 2),
         "dpbf16_us_per_step": round(ms_dp * 1e3, 2),
+        "dpbf16_splits_per_head": dp_splits,
         "dpbf16_xkv_bit_equal_raw": dp_equal,
         "block_modes": stats,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",

@@ -127,6 +127,15 @@ __device__ __forceinline__ uint4 ld16(const uint8_t *p) {
 }
 __device__ __forceinline__ uint32_t ldu16(const uint8_t *p) { return *(g_u16 *)(p); }
 
+// The lane index as an opaque value: the addresses derived from it are then
+// recomputed where they are used (a few instructions) instead of being
+// hoisted out of the chunk loop and held in registers across it.
+__device__ __forceinline__ int lane_here() {
+    int l = int(__lane_id());
+    asm volatile("" : "+v"(l));
+    return l;
+}
+
 // Position of one tensor inside its XKV container. The scalar fields are
 // wave-uniform; erec holds the block's next escape records (component j of
 // lane l: escape ecur + 4 l + j, meaningful below n_escape).
@@ -168,7 +177,7 @@ __device__ __forceinline__ void enter_block(Cursor &c, const BlockDesc *d, int t
 // the V rows in flight. Records at or past n_escape are masked where used.
 template <int D>
 __device__ __forceinline__ void block_vectors(Cursor &c) {
-    const int lane = lane_id();
+    const int lane = lane_here();
     c.base2 = ldu16(c.blk + 8 + 2 * (lane & (D / 2 - 1)));
     const u32x4 r = *(g_u32x4 *)(c.esc + c.ecur + 4 * lane);
     c.erec = make_uint4(r.x, r.y, r.z, r.w);
@@ -194,7 +203,7 @@ template <int D>
 __device__ __forceinline__ int raw_start(int rows) {
     constexpr int RR = Shape<D>::kRowRegs;
     const int np = max(1, min(rows, kRawRows)) * (D / 8); // >= RR
-    return min(RR * lane_id(), np - RR);
+    return min(RR * lane_here(), np - RR);
 }
 
 // Loads rows r0 .. r0 + rows of the cursor's block into R. Coded block: lane
@@ -212,7 +221,7 @@ __device__ __forceinline__ void load_rows(Cursor &c, int r0, int rows, uint4 (&R
     const bool raw = mode == 0;
     c.lrows = rows;
     // (rows <= 0 only past a plan's zero-token sentinel block: row r0 then)
-    const int r = r0 + max(0, min(lane_id(), rows - 1));
+    const int r = r0 + max(0, min(lane_here(), rows - 1));
     const int cbytes = mode * (D / 8); // code bytes per coded row
     const uint8_t *b = c.blk + 8;
     // sign/mantissa bytes of the row, then its codes; raw: the lane's pieces
@@ -290,7 +299,7 @@ __device__ __forceinline__ void decode_row(const Cursor &c, const uint4 (&R)[Sha
     constexpr int SM = Shape<D>::kSmRegs, RR = Shape<D>::kRowRegs;
     uint4 *dst = reinterpret_cast<uint4 *>(row);
     const int mode = c.mode();
-    const int lane = lane_id();
+    const int lane = lane_here();
     if (mode == 4) {
 #pragma unroll
         for (int dg = 0; dg < D / 8; ++dg) {
@@ -481,66 +490,52 @@ __device__ __forceinline__ void scores(const uint8_t *row, const float (&qa)[kGr
 // reduced to its a_i before the next starts.
 template <int G, int D>
 __device__ __forceinline__ void scores_dp(const uint8_t *row, const float (&qa)[kGroups<G>][D / 16], float (&s)[G]) {
-    constexpr int NG = kGroups<G>, R = NG == 1 ? 2 : 1;
-    f4 a01[NG], a2[NG];
-    static_for<0, 4 / R>([&](auto RUN) {
-        constexpr int Q0 = R * decltype(RUN)::value;
-        f4 ch[NG][4 * R];
+    constexpr int NG = kGroups<G>;
+    // One row group at a time, one quad of chains at a time: at most four
+    // chains live beside the partial sums (the K words are read again per
+    // quad and row group; the reads are cheap next to the registers).
+    static_for<0, NG>([&](auto RG) {
+        constexpr int rg = decltype(RG)::value;
+        f4 a01, a2;
+        static_for<0, 4>([&](auto RUN) {
+            constexpr int Q0 = decltype(RUN)::value;
+            __builtin_amdgcn_sched_barrier(0);
+            f4 ch[4];
 #pragma unroll
-        for (int rg = 0; rg < NG; ++rg)
-#pragma unroll
-            for (int j = 0; j < 4 * R; ++j) ch[rg][j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-        static_for<0, D / 32>([&](auto S) {
-            constexpr int DG0 = 4 * decltype(S)::value + Q0; // octets DG0 .. DG0 + R - 1
-            uint32_t w[4 * R];
-#pragma unroll
-            for (int r = 0; r < R; ++r) {
-                const uint4 kb = *reinterpret_cast<const uint4 *>(row + 16 * (DG0 + r));
-                w[4 * r + 0] = kb.x;
-                w[4 * r + 1] = kb.y;
-                w[4 * r + 2] = kb.z;
-                w[4 * r + 3] = kb.w;
-            }
-            static_for<0, 4 * R>([&](auto J) { // odd channel of pair J first
-                constexpr int d = 8 * DG0 + 2 * decltype(J)::value + 1;
-#pragma unroll
-                for (int rg = 0; rg < NG; ++rg)
-                    ch[rg][J] = mfma_rank1<d % 16>(qa[rg][d / 16], hi_f32(w[J]), ch[rg][J]);
+            for (int j = 0; j < 4; ++j) ch[j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+            static_for<0, D / 32>([&](auto S) {
+                constexpr int DG0 = 4 * decltype(S)::value + Q0; // octet of this step
+                const uint4 kb = *reinterpret_cast<const uint4 *>(row + 16 * DG0);
+                const uint32_t w[4] = {kb.x, kb.y, kb.z, kb.w};
+                static_for<0, 4>([&](auto J) { // odd channel of pair J first
+                    constexpr int d = 8 * DG0 + 2 * decltype(J)::value + 1;
+                    ch[J] = mfma_rank1<d % 16>(qa[rg][d / 16], hi_f32(w[J]), ch[J]);
+                });
+                static_for<0, 4>([&](auto J) {
+                    constexpr int d = 8 * DG0 + 2 * decltype(J)::value;
+                    ch[J] = mfma_rank1<d % 16>(qa[rg][d / 16], lo_f32(w[J]), ch[J]);
+                });
             });
-            static_for<0, 4 * R>([&](auto J) {
-                constexpr int d = 8 * DG0 + 2 * decltype(J)::value;
-#pragma unroll
-                for (int rg = 0; rg < NG; ++rg)
-                    ch[rg][J] = mfma_rank1<d % 16>(qa[rg][d / 16], lo_f32(w[J]), ch[rg][J]);
-            });
-        });
-#pragma unroll
-        for (int rg = 0; rg < NG; ++rg) {
-            f4 a = (ch[rg][0] + ch[rg][1]) + (ch[rg][2] + ch[rg][3]); // a_Q0
-            if constexpr (R == 2) a = a + ((ch[rg][4] + ch[rg][5]) + (ch[rg][6] + ch[rg][7])); // a_Q0 + a_Q0+1
-            f4 t;
-            if constexpr (R == 2 && Q0 == 0) {
-                a01[rg] = a;
-                continue;
-            } else if constexpr (R == 2) {
-                t = a01[rg] + a;
-            } else if constexpr (Q0 == 0) {
-                a01[rg] = a;
-                continue;
+            const f4 a = (ch[0] + ch[1]) + (ch[2] + ch[3]); // a_Q0
+            // (the empty asm keeps each quad's sum here: sunk to the last
+            // quad, every quad's chains would stay live until then)
+            if constexpr (Q0 == 0) {
+                a01 = a;
+                asm volatile("" : "+v"(a01));
             } else if constexpr (Q0 == 1) {
-                a01[rg] = a01[rg] + a;
-                continue;
+                a01 = a01 + a;
+                asm volatile("" : "+v"(a01));
             } else if constexpr (Q0 == 2) {
-                a2[rg] = a;
-                continue;
+                a2 = a;
+                asm volatile("" : "+v"(a2));
             } else {
-                t = a01[rg] + (a2[rg] + a);
+                const f4 t = a01 + (a2 + a);
+                if (4 * rg + 0 < G) s[(4 * rg + 0) % G] = t.x;
+                if (4 * rg + 1 < G) s[(4 * rg + 1) % G] = t.y;
+                if (4 * rg + 2 < G) s[(4 * rg + 2) % G] = t.z;
+                if (4 * rg + 3 < G) s[(4 * rg + 3) % G] = t.w;
             }
-            if (4 * rg + 0 < G) s[(4 * rg + 0) % G] = t.x;
-            if (4 * rg + 1 < G) s[(4 * rg + 1) % G] = t.y;
-            if (4 * rg + 2 < G) s[(4 * rg + 2) % G] = t.z;
-            if (4 * rg + 3 < G) s[(4 * rg + 3) % G] = t.w;
-        }
+        });
     });
 }
 
@@ -673,14 +668,6 @@ __device__ __forceinline__ void fold(const WaveLds<G, D> &S, lds_f32 *eb, lds_f3
     }
 }
 
-// The lane index as an opaque value: the addresses derived from it are then
-// recomputed where they are used (a few instructions) instead of being
-// hoisted out of the chunk loop and held in registers across it.
-__device__ __forceinline__ int lane_here() {
-    int l = int(__lane_id());
-    asm volatile("" : "+v"(l));
-    return l;
-}
 
 // Rows of the plain BF16 kernel: register j of lane l holds bytes
 // [1024 j + 16 l, + 16) of the chunk's rows from token t (row
@@ -710,14 +697,13 @@ __device__ __forceinline__ void store_raw(const uint4 (&R)[D / 8], uint8_t *tile
 template <bool XKV, int D> struct RegsOf { typedef uint4 T[Shape<D>::kRowRegs]; };
 template <int D> struct RegsOf<false, D> { typedef uint4 T[D / 8]; };
 
-// At D = 64 the XKV instantiations are held to three waves per SIMD (168
-// VGPRs), and LDS allows three workgroups of four waves per CU; at D = 128
-// two waves per SIMD (the rows in flight take twice the registers), and
-// also for the AVX-512 order at D = 64 with six or more query rows (its
-// flush checks do not fit in 168 VGPRs there without spilling in the loop).
+// At D = 64 the XKV instantiations with up to seven query rows are held to
+// three waves per SIMD (168 VGPRs), and LDS allows three workgroups of four
+// waves per CU; at D = 128 (the rows in flight take twice the registers) and
+// at eight query rows two waves per SIMD.
 // ORDER 0: scalar/AVX2 score order; ORDER 1: AVX-512 BF16 order.
 template <int G, int D, bool XKV, int ORDER>
-constexpr int kWaveOcc = D == 64 && XKV && !(ORDER == 1 && G >= 6) ? 3 : 2;
+constexpr int kWaveOcc = D == 64 && XKV && G < 8 ? 3 : 2;
 
 template <int G, int D, bool XKV, int ORDER>
 __global__ __launch_bounds__(Shape<D>::kWaves * 64) __attribute__((amdgpu_waves_per_eu(kWaveOcc<G, D, XKV, ORDER>)))
@@ -799,7 +785,6 @@ void attn_wave_kernel(const HeadDev *__restrict__ heads, const WorkItem *__restr
         load_raw<D>(hd.kraw, t, min(kChunk, wi.tok_end - t), RK);
         load_raw<D>(hd.vraw, t, min(kChunk, wi.tok_end - t), RV);
     }
-    uint8_t *my_row = S.tile + lane * TS; // the lane's token
 
     // Issue priority by progress: a SIMD issues from its oldest wave first, so
     // the first workgroup placed on a CU would race ahead and the last finish
@@ -812,6 +797,7 @@ void attn_wave_kernel(const HeadDev *__restrict__ heads, const WorkItem *__restr
     int prio = 3;
     const int span = wi.tok_end - wi.tok_begin;
     while (t < wi.tok_end) {
+        const int ln = lane_here(); // this chunk's ln index (see lane_here)
         {
             const int want = 3 - min(3, ((t - wi.tok_begin) * 4) / max(span, 1));
             if (want != prio) {
@@ -841,14 +827,14 @@ void attn_wave_kernel(const HeadDev *__restrict__ heads, const WorkItem *__restr
                     // >= kmin when no base is below it or wraps
                     const uint32_t b0 = kc.base2 & 0xFFu, b1 = (kc.base2 >> 8) & 0xFFu;
                     const uint32_t top = 256u - (1u << kc.mode());
-                    flush = __ballot(lane < D / 2 && (min(b0, b1) < kmin || max(b0, b1) > top)) != 0;
+                    flush = __ballot(ln < D / 2 && (min(b0, b1) < kmin || max(b0, b1) > top)) != 0;
                 }
                 base_pairs<D>(kc, S.bp);
                 wave_sync();
             } else {
                 flush = ORDER == 1;
             }
-            decode_row<D>(kc, RK, S.bp, S.tile, my_row, t - kc.t0, n);
+            decode_row<D>(kc, RK, S.bp, S.tile, S.tile + ln * TS, t - kc.t0, n);
             wave_sync();
             flush |= patch_escapes<D, ORDER == 1>(kc, t - kc.t0, n, S.tile, klow);
         } else {
@@ -858,7 +844,7 @@ void attn_wave_kernel(const HeadDev *__restrict__ heads, const WorkItem *__restr
                 u16x2 lo = {0xFFFFu, 0xFFFFu};
 #pragma unroll
                 for (int j = 0; j < D / 8; ++j) {
-                    if ((1024 * j + 16 * lane) / (2 * D) >= n) continue;
+                    if ((1024 * j + 16 * ln) / (2 * D) >= n) continue;
                     const uint32_t c4[4] = {RK[j].x, RK[j].y, RK[j].z, RK[j].w};
 #pragma unroll
                     for (int k = 0; k < 4; ++k)
@@ -870,17 +856,17 @@ void attn_wave_kernel(const HeadDev *__restrict__ heads, const WorkItem *__restr
         }
         wave_sync();
 
-        // 2. scores, lane = token
+        // 2. scores, ln = token
         float s[G];
         if constexpr (ORDER == 0) {
-            scores<G, D>(my_row, qa, s);
+            scores<G, D>(S.tile + ln * TS, qa, s);
         } else if (!flush) {
-            scores_dp<G, D>(my_row, qa, s);
+            scores_dp<G, D>(S.tile + ln * TS, qa, s);
         } else {
-            scores_dp_flush<G, D>(my_row, q_all + size_t(hd.q_row) * D, &S.eT[0][0]);
+            scores_dp_flush<G, D>(S.tile + ln * TS, q_all + size_t(hd.q_row) * D, &S.eT[0][0]);
             wave_sync();
 #pragma unroll
-            for (int g = 0; g < G; ++g) s[g] = S.eT[g][lane];
+            for (int g = 0; g < G; ++g) s[g] = S.eT[g][ln];
         }
         wave_sync();
 
@@ -891,7 +877,7 @@ void attn_wave_kernel(const HeadDev *__restrict__ heads, const WorkItem *__restr
                 base_pairs<D>(vc, S.bp);
                 wave_sync();
             }
-            decode_row<D>(vc, RV, S.bp, S.tile, my_row, t - vc.t0, n);
+            decode_row<D>(vc, RV, S.bp, S.tile, S.tile + ln * TS, t - vc.t0, n);
             wave_sync();
             patch_escapes<D>(vc, t - vc.t0, n, S.tile);
             // the loads are issued on every chunk (the last one re-reads its
@@ -906,7 +892,7 @@ void attn_wave_kernel(const HeadDev *__restrict__ heads, const WorkItem *__restr
             load_rows<D>(vc, tp - vc.t0, min(kChunk, min(vc.t1, wi.tok_end) - tp), RV);
         } else {
             store_raw<D>(RV, S.tile);
-            if (n < kChunk && lane >= n) fill_negzero<D>(my_row);
+            if (n < kChunk && ln >= n) fill_negzero<D>(S.tile + ln * TS);
             {
                 // issued on every chunk (the last one re-reads its final row), K first
                 const int tp = min(tn, wi.tok_end - 1);
@@ -915,7 +901,7 @@ void attn_wave_kernel(const HeadDev *__restrict__ heads, const WorkItem *__restr
             }
         }
 
-        // 4. softmax coefficients, lane = token: the running maxima by an exact
+        // 4. softmax coefficients, ln = token: the running maxima by an exact
         // DPP prefix maximum (seeded with each row's maximum so far, held in
         // scalar registers), e = exp(s - m) for every token and row, and, for
         // the rows where some token of the chunk moves the maximum,
@@ -937,34 +923,34 @@ void attn_wave_kernel(const HeadDev *__restrict__ heads, const WorkItem *__restr
             const uint64_t rmask = __ballot(!(dg == 0.0f)) & nmask;
             amask |= rmask;
             const float e = kvexp_expf_nonpos_nb(s[g] - m, tab);
-            S.eT[g][lane] = lane < n ? e : 0.0f;
+            S.eT[g][ln] = ln < n ? e : 0.0f;
             float al = 1.0f;
-            if (rmask != 0) al = lane < n ? kvexp_expf_nonpos_nb(dg, tab) : 1.0f;
-            S.aT[g][lane] = al;
+            if (rmask != 0) al = ln < n ? kvexp_expf_nonpos_nb(dg, tab) : 1.0f;
+            S.aT[g][ln] = al;
             msc[g] = readlane_f32(m, n - 1);
         }
         wave_sync();
 
-        // 5. ordered fold, lane = channel, fully unrolled over the chunk
+        // 5. ordered fold, ln = channel, fully unrolled over the chunk
         {
-            // e as the A operands: ea[rg][j] at lane 4b + r holds e[4 rg + r][16 j + b]
+            // e as the A operands: ea[rg][j] at ln 4b + r holds e[4 rg + r][16 j + b]
             // (rows past G repeat row G - 1; their results are not used)
-            // (the lane index passes through an empty asm so that these LDS
+            // (the ln index passes through an empty asm so that these LDS
             // addresses are made here, not kept live across the loop)
-            int lq = lane;
+            int lq = ln;
             asm volatile("" : "+v"(lq));
             float ea[NG][4];
 #pragma unroll
             for (int rg = 0; rg < NG; ++rg) {
                 const int g = min(4 * rg + (lq & 3), G - 1);
 #pragma unroll
-                for (int j = 0; j < 4; ++j) ea[rg][j] = S.eT[g][16 * j + (lane >> 2)];
+                for (int j = 0; j < 4; ++j) ea[rg][j] = S.eT[g][16 * j + (ln >> 2)];
             }
-            const int gl = min(lane & 7, G - 1); // lanes >= G read a row they do not use
+            const int gl = min(ln & 7, G - 1); // lanes >= G read a row they do not use
             lds_f32 *eb = (lds_f32 *)&S.eT[gl][0];
             lds_f32 *ab = (lds_f32 *)&S.aT[gl][0];
             FoldIn<H> in;
-            const uint16_t *vb = reinterpret_cast<const uint16_t *>(S.tile) + lane; // channel lane of token 0
+            const uint16_t *vb = reinterpret_cast<const uint16_t *>(S.tile) + ln; // channel ln of token 0
 #pragma unroll
             for (int k = 0; k < 3; ++k)
 #pragma unroll
