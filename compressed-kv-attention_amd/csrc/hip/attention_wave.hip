@@ -491,51 +491,56 @@ __device__ __forceinline__ void scores(const uint8_t *row, const float (&qa)[kGr
 template <int G, int D>
 __device__ __forceinline__ void scores_dp(const uint8_t *row, const float (&qa)[kGroups<G>][D / 16], float (&s)[G]) {
     constexpr int NG = kGroups<G>;
-    // One row group at a time, one quad of chains at a time: at most four
-    // chains live beside the partial sums (the K words are read again per
-    // quad and row group; the reads are cheap next to the registers).
-    static_for<0, NG>([&](auto RG) {
-        constexpr int rg = decltype(RG)::value;
-        f4 a01, a2;
-        static_for<0, 4>([&](auto RUN) {
-            constexpr int Q0 = decltype(RUN)::value;
-            __builtin_amdgcn_sched_barrier(0);
-            f4 ch[4];
+    // One quad of chains at a time for every row group: at most 4 NG chains
+    // live beside the partial sums.
+    f4 a01[NG], a2[NG];
+    static_for<0, 4>([&](auto RUN) {
+        constexpr int Q0 = decltype(RUN)::value;
+        __builtin_amdgcn_sched_barrier(0);
+        f4 ch[NG][4];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) ch[j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-            static_for<0, D / 32>([&](auto S) {
-                constexpr int DG0 = 4 * decltype(S)::value + Q0; // octet of this step
-                const uint4 kb = *reinterpret_cast<const uint4 *>(row + 16 * DG0);
-                const uint32_t w[4] = {kb.x, kb.y, kb.z, kb.w};
-                static_for<0, 4>([&](auto J) { // odd channel of pair J first
-                    constexpr int d = 8 * DG0 + 2 * decltype(J)::value + 1;
-                    ch[J] = mfma_rank1<d % 16>(qa[rg][d / 16], hi_f32(w[J]), ch[J]);
-                });
-                static_for<0, 4>([&](auto J) {
-                    constexpr int d = 8 * DG0 + 2 * decltype(J)::value;
-                    ch[J] = mfma_rank1<d % 16>(qa[rg][d / 16], lo_f32(w[J]), ch[J]);
-                });
+        for (int rg = 0; rg < NG; ++rg)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) ch[rg][j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+        static_for<0, D / 32>([&](auto S) {
+            constexpr int DG0 = 4 * decltype(S)::value + Q0; // octet of this step
+            const uint4 kb = *reinterpret_cast<const uint4 *>(row + 16 * DG0);
+            const uint32_t w[4] = {kb.x, kb.y, kb.z, kb.w};
+            static_for<0, 4>([&](auto J) { // odd channel of pair J first
+                constexpr int d = 8 * DG0 + 2 * decltype(J)::value + 1;
+                const float k = hi_f32(w[J]);
+#pragma unroll
+                for (int rg = 0; rg < NG; ++rg) ch[rg][J] = mfma_rank1<d % 16>(qa[rg][d / 16], k, ch[rg][J]);
             });
-            const f4 a = (ch[0] + ch[1]) + (ch[2] + ch[3]); // a_Q0
+            static_for<0, 4>([&](auto J) {
+                constexpr int d = 8 * DG0 + 2 * decltype(J)::value;
+                const float k = lo_f32(w[J]);
+#pragma unroll
+                for (int rg = 0; rg < NG; ++rg) ch[rg][J] = mfma_rank1<d % 16>(qa[rg][d / 16], k, ch[rg][J]);
+            });
+        });
+#pragma unroll
+        for (int rg = 0; rg < NG; ++rg) {
+            const f4 a = (ch[rg][0] + ch[rg][1]) + (ch[rg][2] + ch[rg][3]); // a_Q0
             // (the empty asm keeps each quad's sum here: sunk to the last
             // quad, every quad's chains would stay live until then)
             if constexpr (Q0 == 0) {
-                a01 = a;
-                asm volatile("" : "+v"(a01));
+                a01[rg] = a;
+                asm volatile("" : "+v"(a01[rg]));
             } else if constexpr (Q0 == 1) {
-                a01 = a01 + a;
-                asm volatile("" : "+v"(a01));
+                a01[rg] = a01[rg] + a;
+                asm volatile("" : "+v"(a01[rg]));
             } else if constexpr (Q0 == 2) {
-                a2 = a;
-                asm volatile("" : "+v"(a2));
+                a2[rg] = a;
+                asm volatile("" : "+v"(a2[rg]));
             } else {
-                const f4 t = a01 + (a2 + a);
+                const f4 t = a01[rg] + (a2[rg] + a);
                 if (4 * rg + 0 < G) s[(4 * rg + 0) % G] = t.x;
                 if (4 * rg + 1 < G) s[(4 * rg + 1) % G] = t.y;
                 if (4 * rg + 2 < G) s[(4 * rg + 2) % G] = t.z;
                 if (4 * rg + 3 < G) s[(4 * rg + 3) % G] = t.w;
             }
-        });
+        }
     });
 }
 
