@@ -281,6 +281,31 @@ def bench_append(a, torch, np, kvexp_amd, synth) -> int:
     return 0
 
 
+# The split kernel's other bound: SIMD instruction issue. Per chunk of 64
+# tokens at head_dim 64 and 7 query rows a wave issues 256 FP32 matrix-core
+# products (128 score, 128 fold) and, on c2's containers, 983 other
+# vector-ALU instructions (SQ_INSTS_VALU - SQ_INSTS_MFMA per chunk,
+# profiles/attn_wave_c2_sq_counters.md); measured issue costs 8.4 and 2.5
+# SIMD cycles (profiles/mfma_valu_coexec.md), which do not overlap. Chunks
+# are spread over the 1,024 SIMDs at the 2.4 GHz peak clock. The ideal time
+# is what the SIMDs would take issuing back to back; achieved / ideal is the
+# fraction of that bound the kernel reaches.
+ISSUE_MFMA_PER_CHUNK, ISSUE_VALU_PER_CHUNK, ISSUE_MFMA_CYC, ISSUE_VALU_CYC = 256, 983, 8.4, 2.5
+SIMDS, CLOCK_GHZ = 1024, 2.4
+
+
+def issue_roofline(tokens: int, kernel_us: float, three_bit: bool):
+    if three_bit:
+        return None  # the vector instruction count was measured on encode_bf16's containers
+    chunks = tokens / 64
+    cycles = chunks / SIMDS * (ISSUE_MFMA_PER_CHUNK * ISSUE_MFMA_CYC + ISSUE_VALU_PER_CHUNK * ISSUE_VALU_CYC)
+    ideal_us = cycles / (CLOCK_GHZ * 1e3)
+    return {"bound": "simd-issue", "ideal_us": round(ideal_us, 2), "achieved_us": round(kernel_us, 2),
+            "frac": round(ideal_us / kernel_us, 4), "mfma_per_chunk": ISSUE_MFMA_PER_CHUNK,
+            "valu_per_chunk": ISSUE_VALU_PER_CHUNK, "mfma_cycles": ISSUE_MFMA_CYC, "valu_cycles": ISSUE_VALU_CYC,
+            "source": "profiles/attn_wave_c2_sq_counters.md, profiles/mfma_valu_coexec.md"}
+
+
 def bench_config(a, torch, np, kvexp_amd, synth) -> int:
     """--config c1 / c3 / c4 (see the module docstring)."""
     name = a.config
@@ -662,6 +687,7 @@ def main() -> int:
                      "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
                      "kernel": "attn_wave_kernel<7, 64, true, 0>", "kernel_us": round(kern_avg_ms * 1e3, 2),
                      "algorithmic_bytes": algo_bytes},
+        "issue": issue_roofline(H * S, kern_avg_ms * 1e3, a.three_bit),
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

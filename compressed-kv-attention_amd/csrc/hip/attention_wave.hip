@@ -47,6 +47,18 @@
 namespace kvexp_dev {
 namespace wave {
 
+// Phase trace (builds with KVEXP_PHASE_TRACE only; compressed-kv-attention_amd/
+// probes.py): per wave of the scalar-order XKV kernel, the cycles spent in
+// each phase of the chunk loop, summed over its chunks. A wait is measured
+// by a timestamp taken after an empty asm that reads the loaded register.
+#if defined(KVEXP_PHASE_TRACE)
+constexpr int kTraceWaves = 8192, kTraceWords = 10; // start, end, 7 phases, CU/SE id
+__device__ unsigned long long g_phase_trace[kTraceWaves * kTraceWords];
+#define KVEXP_TRACE_ON(X, O) ((X) && (O) == 0)
+#else
+#define KVEXP_TRACE_ON(X, O) false
+#endif
+
 constexpr int kChunk = 64;      // tokens per chunk (one per lane)
 constexpr int kEscWindow = 256; // escape records a chunk can patch: four per lane, loaded with its rows
 constexpr int kRawRows = 48;    // rows of a raw block per chunk: 64 lanes x 3D/2 bytes = 48 rows of 2D bytes
@@ -798,11 +810,28 @@ void attn_wave_kernel(const HeadDev *__restrict__ heads, const WorkItem *__restr
     // first quarter of its tokens, then 2, 1, 0): the waves that are behind
     // win the issue slots and all of a CU's waves finish at about the same
     // time.
+    constexpr bool TR = KVEXP_TRACE_ON(XKV, ORDER);
+    unsigned long long ph[7] = {0, 0, 0, 0, 0, 0, 0};
+    const unsigned long long tw0 = TR ? __builtin_readcyclecounter() : 0ull;
+    unsigned long long tprev = tw0;
+    auto stamp = [&](int i) {
+        if constexpr (TR) {
+            const unsigned long long tn_ = __builtin_readcyclecounter();
+            ph[i] += tn_ - tprev;
+            tprev = tn_;
+        }
+    };
+    auto after = [&](uint32_t x) {
+        if constexpr (TR) asm volatile("" ::"v"(x));
+    };
+    (void)stamp;
+    (void)after;
+
     __builtin_amdgcn_s_setprio(3);
     int prio = 3;
     const int span = wi.tok_end - wi.tok_begin;
     while (t < wi.tok_end) {
-        const int ln = lane_here(); // this chunk's ln index (see lane_here)
+        const int ln = lane_here(); // this chunk's lane index (see lane_here)
         {
             const int want = 3 - min(3, ((t - wi.tok_begin) * 4) / max(span, 1));
             if (want != prio) {
@@ -822,6 +851,8 @@ void attn_wave_kernel(const HeadDev *__restrict__ heads, const WorkItem *__restr
         if (n <= 0) break; // unreachable with plan-checked descriptors (n_tokens > 0)
         const int tn = t + n;
 
+        if constexpr (XKV) after(RK[Shape<D>::kRowRegs - 1].w); // K rows arrived
+        stamp(0);
         // 1. K rows -> tile (ORDER 1: and whether the chunk needs the flushing
         // score path)
         bool flush = false;
@@ -861,7 +892,8 @@ void attn_wave_kernel(const HeadDev *__restrict__ heads, const WorkItem *__restr
         }
         wave_sync();
 
-        // 2. scores, ln = token
+        stamp(1); // K decoded
+        // 2. scores, lane = token
         float s[G];
         if constexpr (ORDER == 0) {
             scores<G, D>(S.tile + ln * TS, qa, s);
@@ -875,6 +907,10 @@ void attn_wave_kernel(const HeadDev *__restrict__ heads, const WorkItem *__restr
         }
         wave_sync();
 
+        after(__float_as_uint(s[0]));
+        stamp(2); // scores done
+        if constexpr (XKV) after(RV[Shape<D>::kRowRegs - 1].w); // V rows arrived
+        stamp(3);
         // 3. V rows -> tile; request the next chunk's V and K rows (RK and RV
         // are then not live across the score and decode registers)
         if constexpr (XKV) {
@@ -906,7 +942,8 @@ void attn_wave_kernel(const HeadDev *__restrict__ heads, const WorkItem *__restr
             }
         }
 
-        // 4. softmax coefficients, ln = token: the running maxima by an exact
+        stamp(4); // V decoded, next rows requested
+        // 4. softmax coefficients, lane = token: the running maxima by an exact
         // DPP prefix maximum (seeded with each row's maximum so far, held in
         // scalar registers), e = exp(s - m) for every token and row, and, for
         // the rows where some token of the chunk moves the maximum,
@@ -936,11 +973,12 @@ void attn_wave_kernel(const HeadDev *__restrict__ heads, const WorkItem *__restr
         }
         wave_sync();
 
-        // 5. ordered fold, ln = channel, fully unrolled over the chunk
+        stamp(5); // softmax coefficients in LDS
+        // 5. ordered fold, lane = channel, fully unrolled over the chunk
         {
-            // e as the A operands: ea[rg][j] at ln 4b + r holds e[4 rg + r][16 j + b]
+            // e as the A operands: ea[rg][j] at lane 4b + r holds e[4 rg + r][16 j + b]
             // (rows past G repeat row G - 1; their results are not used)
-            // (the ln index passes through an empty asm so that these LDS
+            // (the lane index passes through an empty asm so that these LDS
             // addresses are made here, not kept live across the loop)
             int lq = ln;
             asm volatile("" : "+v"(lq));
@@ -955,7 +993,7 @@ void attn_wave_kernel(const HeadDev *__restrict__ heads, const WorkItem *__restr
             lds_f32 *eb = (lds_f32 *)&S.eT[gl][0];
             lds_f32 *ab = (lds_f32 *)&S.aT[gl][0];
             FoldIn<H> in;
-            const uint16_t *vb = reinterpret_cast<const uint16_t *>(S.tile) + ln; // channel ln of token 0
+            const uint16_t *vb = reinterpret_cast<const uint16_t *>(S.tile) + ln; // channel lane of token 0
 #pragma unroll
             for (int k = 0; k < 3; ++k)
 #pragma unroll
@@ -970,8 +1008,21 @@ void attn_wave_kernel(const HeadDev *__restrict__ heads, const WorkItem *__restr
             fold<G, D, 0>(S, eb, ab, vb, am, ea, in, acc, lvec);
         }
         wave_sync();
+        after(__float_as_uint(acc[0][0].x));
+        stamp(6); // fold done
         t = tn;
     }
+#if defined(KVEXP_PHASE_TRACE)
+    if constexpr (TR) {
+        if (lane == 0 && item < kTraceWaves) {
+            unsigned long long *o = g_phase_trace + size_t(item) * kTraceWords;
+            o[0] = tw0;
+            o[1] = __builtin_readcyclecounter();
+            for (int i = 0; i < 7; ++i) o[2 + i] = ph[i];
+            o[9] = (unsigned long long)__smid();
+        }
+    }
+#endif
 
     // ---- epilogue --------------------------------------------------------------
     float mv = msc[0]; // lane g < G: running maximum of row g
@@ -1156,3 +1207,10 @@ hipError_t attention_wave(bool xkv, int order, int G, int dim, const HeadDev *he
 }
 
 } // namespace kvexp_launch
+
+#if defined(KVEXP_PHASE_TRACE)
+// Copies the phase trace of the last traced launch (n words) to the host.
+extern "C" int kvexp_hip_phase_trace_read(unsigned long long *host, size_t n) {
+    return int(hipMemcpyFromSymbol(host, HIP_SYMBOL(kvexp_dev::wave::g_phase_trace), n * 8));
+}
+#endif
