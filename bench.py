@@ -102,7 +102,7 @@ def bench_append(a, torch, np, kvexp_amd, synth) -> int:
     dev = torch.device("cuda:0")
     ctx = kvexp_amd.Context(0)
     steps, warmup = a.steps, a.warmup
-    extra = 2 * steps + warmup + 1  # warmup + timed append steps, then the decode-loop steps
+    extra = 4 * steps + warmup + 1  # warmup + timed append steps, then the three decode loops
     t0 = time.time()
     src, host = [], []
     for l in range(L):
@@ -225,6 +225,71 @@ def bench_append(a, torch, np, kvexp_amd, synth) -> int:
     log(f"decode loop (append + plan update + attention): {loop_ms * 1e3:.1f} us per step (wall "
         f"{loop_wall * 1e3:.1f}) over {loop_steps} steps; last output equals fresh plan: {loop_same}")
 
+    # the same loop through the PyTorch operator (torch.ops.kvexp.decode_attention,
+    # reuse_plan=True: the op keeps the plan for these buffers and re-targets it)
+    import kvexp_amd.torch_ops as ops
+
+    dq3 = q.view(torch.bfloat16).view(H, G, D)
+    base2 = base + loop_steps
+    op_steps = loop_steps
+    seq_now = S + base2
+    kviews = [caches[2 * i].view() for i in range(H)]
+    vviews = [caches[2 * i + 1].view() for i in range(H)]
+    for e in kviews + vviews:
+        e.nbytes = -1
+    o_op = ops.decode_attention_containers(dq3, kviews, vviews, [seq_now] * H, splits, BT, 0, reuse_plan=True)
+    torch.cuda.synchronize()
+    t_op = time.perf_counter()
+    e0.record()
+    for i in range(base2, base2 + op_steps):
+        aset.append(one[i], 1)
+        seq_now = S + i + 1
+        kviews = [caches[2 * j].view() for j in range(H)]
+        vviews = [caches[2 * j + 1].view() for j in range(H)]
+        for e in kviews + vviews:
+            e.nbytes = -1
+        o_op = ops.decode_attention_containers(dq3, kviews, vviews, [seq_now] * H, splits, BT, 0, reuse_plan=True)
+    e1.record()
+    torch.cuda.synchronize()
+    op_ms = e0.elapsed_time(e1) / max(1, op_steps)
+    op_wall = (time.perf_counter() - t_op) * 1e3 / max(1, op_steps)
+    fresh2 = [ctx.encode(t[: seq_now * D], seq_now, D, BT) for t in src]
+    plan4 = ctx.plan([dict(kx=fresh2[2 * i], vx=fresh2[2 * i + 1], seq=seq_now, splits=splits) for i in range(H)],
+                     G, D, BT)
+    o4 = plan4.run(q, check_errors=True)
+    torch.cuda.synchronize()
+    op_same = bool(torch.equal(o_op.reshape(-1).view(torch.int32), o4.view(torch.int32)))
+    ops.clear_plan_cache()
+    # and through decode_attention_kv over the caches registered once (only the
+    # lengths cross the op each step)
+    handle = ops.register_kv([caches[2 * i] for i in range(H)], [caches[2 * i + 1] for i in range(H)], G, D, splits,
+                             BT, 0)
+    base3 = base2 + op_steps
+    seq_now = S + base3
+    o_kv = torch.ops.kvexp.decode_attention_kv(dq3, handle, [seq_now] * H)
+    torch.cuda.synchronize()
+    t_kv = time.perf_counter()
+    e0.record()
+    for i in range(base3, base3 + op_steps):
+        aset.append(one[i], 1)
+        seq_now = S + i + 1
+        o_kv = torch.ops.kvexp.decode_attention_kv(dq3, handle, [seq_now] * H)
+    e1.record()
+    torch.cuda.synchronize()
+    kv_ms = e0.elapsed_time(e1) / max(1, op_steps)
+    kv_wall = (time.perf_counter() - t_kv) * 1e3 / max(1, op_steps)
+    fresh3 = [ctx.encode(t[: seq_now * D], seq_now, D, BT) for t in src]
+    plan5 = ctx.plan([dict(kx=fresh3[2 * i], vx=fresh3[2 * i + 1], seq=seq_now, splits=splits) for i in range(H)],
+                     G, D, BT)
+    o5 = plan5.run(q, check_errors=True)
+    torch.cuda.synchronize()
+    kv_same = bool(torch.equal(o_kv.reshape(-1).view(torch.int32), o5.view(torch.int32)))
+    ops.unregister_kv(handle)
+    log(f"decode loop through torch.ops.kvexp.decode_attention (append + op): {op_ms * 1e3:.1f} us per step "
+        f"(wall {op_wall * 1e3:.1f}) over {op_steps} steps; last output equals fresh plan: {op_same}")
+    log(f"decode loop through torch.ops.kvexp.decode_attention_kv (append + op on registered caches): "
+        f"{kv_ms * 1e3:.1f} us per step (wall {kv_wall * 1e3:.1f}); last output equals fresh plan: {kv_same}")
+
     cpu = None
     if not a.no_cpu_baseline:
         try:
@@ -270,6 +335,12 @@ def bench_append(a, torch, np, kvexp_amd, synth) -> int:
         "decode_loop_us_per_step": round(loop_ms * 1e3, 2),
         "decode_loop_wall_us_per_step": round(loop_wall * 1e3, 2),
         "decode_loop_equal_fresh_plan": loop_same,
+        "op_decode_loop_us_per_step": round(op_ms * 1e3, 2),
+        "op_decode_loop_wall_us_per_step": round(op_wall * 1e3, 2),
+        "op_decode_loop_equal_fresh_plan": op_same,
+        "op_kv_decode_loop_us_per_step": round(kv_ms * 1e3, 2),
+        "op_kv_decode_loop_wall_us_per_step": round(kv_wall * 1e3, 2),
+        "op_kv_decode_loop_equal_fresh_plan": kv_same,
         "attention_equal_fresh_encode": attn_same,
         "roofline": {"bound": "hbm", "achieved": round(algo / (pre_ms * 1e-3) / 1e9, 2), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(algo / (pre_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),

@@ -442,6 +442,23 @@ def _heads_array(heads: list):
     return arr, keep
 
 
+_HEAD_DTYPE = None
+
+
+def _head_dtype():
+    """numpy view of kvexp_hip_head (edits a head table in place)."""
+    global _HEAD_DTYPE
+    if _HEAD_DTYPE is None:
+        import numpy as np
+
+        _HEAD_DTYPE = np.dtype({"names": [f for f, _ in _Head._fields_],
+                                "formats": ["<u8" if t in (C.c_void_p, C.c_uint64) else "<i4"
+                                            for _, t in _Head._fields_],
+                                "offsets": [getattr(_Head, f).offset for f, _ in _Head._fields_],
+                                "itemsize": C.sizeof(_Head)})
+    return _HEAD_DTYPE
+
+
 class Plan:
     def __init__(self, ctx: Context, h, n_heads: int, n_q: int, dim: int, keep):
         self.ctx, self.h, self.n_heads, self.n_q, self.dim, self._keep = ctx, h, n_heads, n_q, dim, keep
@@ -462,13 +479,7 @@ class Plan:
         import numpy as np
 
         n = self.n_heads
-        if not hasattr(self, "_view"):
-            dt = np.dtype({"names": [f for f, _ in _Head._fields_],
-                           "formats": ["<u8" if t in (C.c_void_p, C.c_uint64) else "<i4" for _, t in _Head._fields_],
-                           "offsets": [getattr(_Head, f).offset for f, _ in _Head._fields_],
-                           "itemsize": C.sizeof(_Head)})
-            self._view_dt = dt
-        v = np.frombuffer(self._arr, dtype=self._view_dt, count=n)
+        v = np.frombuffer(self._arr, dtype=_head_dtype(), count=n)
         seqs = np.full(n, int(seq), np.int64) if np.isscalar(seq) else np.asarray(seq, np.int64)
         nb = (seqs + block - 1) // block
         v["seq"] = seqs
@@ -476,6 +487,24 @@ class Plan:
             caps = np.asarray(self._caps, dtype=np.uint64)
             v["k_bytes"], v["v_bytes"] = caps[:, 0], caps[:, 1]
             v["k_n_blocks"], v["v_n_blocks"] = nb, nb
+        check(lib().kvexp_hip_plan_update(self.h, self._arr, n, _stream(stream)))
+
+    def update_heads(self, seqs, k_bytes=None, v_bytes=None, k_blocks=None, v_blocks=None, stream=None) -> None:
+        """kvexp_hip_plan_update with per-head lengths (and, for XKV heads, byte
+        and block counts; a negative byte count stands for the buffer's
+        capacity), edited in place in the head table of the last create or
+        update: the same buffers, grown by appends."""
+        import numpy as np
+
+        n = self.n_heads
+        v = np.frombuffer(self._arr, dtype=_head_dtype(), count=n)
+        v["seq"] = np.asarray(seqs, np.int64)
+        if k_bytes is not None:
+            caps = np.asarray(self._caps, dtype=np.int64)
+            kb, vb = np.asarray(k_bytes, np.int64), np.asarray(v_bytes, np.int64)
+            v["k_bytes"] = np.where(kb < 0, caps[:, 0], kb)
+            v["v_bytes"] = np.where(vb < 0, caps[:, 1], vb)
+            v["k_n_blocks"], v["v_n_blocks"] = np.asarray(k_blocks, np.int64), np.asarray(v_blocks, np.int64)
         check(lib().kvexp_hip_plan_update(self.h, self._arr, n, _stream(stream)))
 
     def run(self, q, out=None, lse=None, check_errors: bool = False, stream=None):
