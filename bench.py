@@ -352,6 +352,128 @@ def bench_append(a, torch, np, kvexp_amd, synth) -> int:
     return 0
 
 
+def host_info() -> dict:
+    """Logical CPUs, sockets, physical cores, the AVX512_BF16 flag and the
+    last-level cache of this host (Linux /proc and /sys)."""
+    info = {"nproc": os.cpu_count() or 1, "sockets": None, "physical_cores": None, "avx512_bf16": None,
+            "avx2": None, "model": None, "llc_bytes": None}
+    try:
+        cores, sockets, flags = set(), set(), ""
+        phys = core = None
+        for line in open("/proc/cpuinfo"):
+            k, _, v = line.partition(":")
+            k, v = k.strip(), v.strip()
+            if k == "physical id":
+                phys = v
+                sockets.add(v)
+            elif k == "core id":
+                core = v
+            elif k == "flags" and not flags:
+                flags = v
+            elif k == "model name" and info["model"] is None:
+                info["model"] = v
+            elif not k and phys is not None:
+                cores.add((phys, core))
+                phys = core = None
+        if phys is not None:
+            cores.add((phys, core))
+        info["sockets"] = len(sockets) or None
+        info["physical_cores"] = len(cores) or None
+        fl = set(flags.split())
+        info["avx512_bf16"], info["avx2"] = "avx512_bf16" in fl, "avx2" in fl
+    except OSError:
+        pass
+    try:  # sum of the distinct level-3 caches
+        seen, total = set(), 0
+        base = "/sys/devices/system/cpu"
+        for cpu in os.listdir(base):
+            d = os.path.join(base, cpu, "cache", "index3")
+            if not cpu.startswith("cpu") or not os.path.isdir(d):
+                continue
+            shared = open(os.path.join(d, "shared_cpu_list")).read().strip()
+            if shared in seen:
+                continue
+            seen.add(shared)
+            size = open(os.path.join(d, "size")).read().strip().upper()
+            mult = {"K": 1 << 10, "M": 1 << 20, "G": 1 << 30}.get(size[-1], 1)
+            total += int(size.rstrip("KMG")) * mult
+        info["llc_bytes"] = total or None
+    except OSError:
+        pass
+    return info
+
+
+def cpu_baseline_c2(R, np, a, q, ks, vs, kxs, vxs, G, D, S, BT) -> dict:
+    """The reference's own library (oracle/_ref) on this host, as its bench times
+    it (bench.cpp:189-218, 644-646, 711-728): every ISA the host has (AVX-512
+    BF16, AVX2), two scopes (model_heads: OpenMP over all KV heads of the step,
+    one thread each; head: KV head 0, sequence-parallel over the threads), raw
+    and XKV inputs whose outputs are compared bit for bit first, 2 untimed
+    calls, then the median of >= 5 samples, each after a sweep of a host buffer
+    of >= 2x the last-level cache (cold)."""
+    host = host_info()
+    phys = host["physical_cores"] or host["nproc"]
+    share = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)  # the box's CPU share, when set
+    threads = a.cpu_threads or (min(phys, share) if share > 0 else phys)
+    sweep_bytes = max(2 * (host["llc_bytes"] or 0), 1 << 30)
+    sweep = np.zeros(sweep_bytes // 8, dtype=np.uint64)
+
+    def cold():
+        np.add(sweep, 1, out=sweep)
+
+    def timed_cold(fn, n=5):
+        fn()
+        fn()
+        ts = []
+        for _ in range(n):
+            cold()
+            t1 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t1)
+        return float(np.median(ts))
+
+    H = len(ks)
+    container = sum(x.size for x in kxs) + sum(x.size for x in vxs)
+    tight = sum(x.size * 2 for x in ks) + sum(x.size * 2 for x in vs)
+    head_c = kxs[0].size + vxs[0].size
+    lines = []
+    isas = [i for i in ("avx512", "avx2") if R.has(i)] or ["scalar"]
+    for isa in isas:
+        ox = R.attention_heads(isa, q, kxs, vxs, xkv=True, n_q=G, dim=D, seq=S, split=BT, omp_threads=threads)
+        orw = R.attention_heads(isa, q, ks, vs, xkv=False, n_q=G, dim=D, seq=S, split=BT, omp_threads=threads)
+        same = bool(np.array_equal(ox.view(np.uint32), orw.view(np.uint32)))
+        tx = timed_cold(lambda: R.attention_heads(isa, q, kxs, vxs, xkv=True, n_q=G, dim=D, seq=S, split=BT,
+                                                  omp_threads=threads))
+        tr = timed_cold(lambda: R.attention_heads(isa, q, ks, vs, xkv=False, n_q=G, dim=D, seq=S, split=BT,
+                                                  omp_threads=threads))
+        lines.append({"isa": isa, "scope": "model_heads", "threads": threads, "heads": H,
+                      "xkv_ms": round(tx * 1e3, 3), "raw_ms": round(tr * 1e3, 3),
+                      "xkv_GBps": round(container / tx / 1e9, 3), "raw_GBps_tight": round(tight / tr / 1e9, 3),
+                      "xkv_over_raw": round(tx / tr, 4), "raw_equal_xkv": same})
+        q0 = q[: G * D]
+        hx = R.attention(isa, q0, kx=kxs[0], vx=vxs[0], n_q=G, dim=D, seq=S, threads=threads, split=BT)
+        hr = R.attention(isa, q0, k=ks[0], v=vs[0], n_q=G, dim=D, seq=S, threads=threads, split=BT)
+        hsame = bool(np.array_equal(hx.view(np.uint32), hr.view(np.uint32)))
+        thx = timed_cold(lambda: R.attention(isa, q0, kx=kxs[0], vx=vxs[0], n_q=G, dim=D, seq=S, threads=threads,
+                                             split=BT))
+        thr = timed_cold(lambda: R.attention(isa, q0, k=ks[0], v=vs[0], n_q=G, dim=D, seq=S, threads=threads,
+                                             split=BT))
+        lines.append({"isa": isa, "scope": "head", "threads": threads, "heads": 1,
+                      "xkv_ms": round(thx * 1e3, 3), "raw_ms": round(thr * 1e3, 3),
+                      "xkv_GBps": round(head_c / thx / 1e9, 3), "xkv_over_raw": round(thx / thr, 4),
+                      "raw_equal_xkv": hsame})
+    main = lines[0]
+    return {"value": main["xkv_GBps"], "unit": "GB/s", "cores": threads, "kind": "reference",
+            "sample": f"the whole c2 step on the host: all {H} KV heads x {G} queries, seq {S}, XKV, "
+                      f"{main['isa']} backend, OpenMP over heads with one thread each (bench.cpp model_heads), "
+                      f"{threads} threads; cold median of 5 after 2 untimed calls, a {sweep_bytes >> 20} MiB "
+                      f"host sweep before each sample; {main['xkv_ms']:.1f} ms per step "
+                      f"(raw {main['raw_ms']:.1f} ms, raw == XKV: {main['raw_equal_xkv']})",
+            "host": host, "threads_note": ("the box's CPU share (OMP_NUM_THREADS)" if share > 0 and share < phys
+                                           else "all physical cores"),
+            "lines": lines}
+
+
 # The split kernel's other bound: SIMD instruction issue. Per chunk of 64
 # tokens at head_dim 64 and 7 query rows a wave issues 256 FP32 matrix-core
 # products (128 score, 128 fold) and, on c2's containers, 983 other
@@ -633,6 +755,18 @@ def main() -> int:
         wall = time.perf_counter() - t_start
         return wall / steps * 1e3, e0.elapsed_time(e1) / steps
 
+    # The GPU's clock ramps up under load for some 100 ms: a settle period of
+    # untimed steps (XKV and raw alternating, about 300 ms) comes before the
+    # warm-up steps, so that a short --warmup does not time a cold clock.
+    t_settle, n_settle = time.perf_counter(), 0
+    while time.perf_counter() - t_settle < 0.3:
+        for i in range(copies):
+            xkv_plans[i].run(q, out_x)
+            raw_plans[i].run(q, out_r)
+        n_settle += 2 * copies
+        torch.cuda.synchronize()
+    log(f"clock settle: {n_settle} untimed steps in {(time.perf_counter() - t_settle) * 1e3:.0f} ms")
+
     ms_x, ev_x = timed(xkv_plans, out_x, a.steps, a.warmup)
     # the split kernel alone, in a separate pass: the library's event pair
     # around it adds a little time between the launches of a step
@@ -673,7 +807,7 @@ def main() -> int:
     odr = dp_raw.run(q, check_errors=True).clone()
     torch.cuda.synchronize()
     dp_equal = bool(torch.equal(odp.view(torch.int32), odr.view(torch.int32)))
-    ms_dp, _ = timed(dp_plans, out_x, max(20, a.steps // 2), a.warmup)
+    ms_dp, _ = timed(dp_plans, out_x, max(20, a.steps // 2), max(a.warmup, 8 * copies))  # new plans: settle too
     for p in dp_plans + [dp_raw]:
         p.close()
     log(f"hot (one copy) {ms_hot * 1e3:.1f} us/step, median of 25 single steps {med_ms * 1e3:.1f} us; "
@@ -689,7 +823,7 @@ def main() -> int:
     if a.copy_probe:
         copy_probe(torch, dev)
 
-    # ---- CPU baseline: the reference library, model_heads scope -------------------
+    # ---- CPU baseline: the compiled reference, both scopes, cold samples ----------
     cpu = None
     if not a.no_cpu_baseline:
         try:
@@ -697,27 +831,12 @@ def main() -> int:
             from oracle import Reference
 
             R = Reference()
-            be = "avx512" if R.avx512_bf16 else ("avx2" if R.avx2 else "scalar")
-            threads = a.cpu_threads or min(16, os.cpu_count() or 1)
-            n_sample = min(H, max(threads, 16))
-            kx = [e.blob[: e.nbytes].cpu().numpy() for e in enc_k[:n_sample]]
-            vx = [e.blob[: e.nbytes].cpu().numpy() for e in enc_v[:n_sample]]
-            qh = q[: n_sample * G * D].cpu().numpy().view(np.uint16)
-            sample_bytes = sum(x.size for x in kx) + sum(x.size for x in vx)
-            R.attention_heads(be, qh, kx, vx, xkv=True, n_q=G, dim=D, seq=S, split=BT, omp_threads=threads)
-            times = []
-            budget = time.perf_counter()
-            while len(times) < 3 or (time.perf_counter() - budget < 15.0 and len(times) < 25):
-                t1 = time.perf_counter()
-                R.attention_heads(be, qh, kx, vx, xkv=True, n_q=G, dim=D, seq=S, split=BT, omp_threads=threads)
-                times.append(time.perf_counter() - t1)
-            med = float(np.median(times))
-            cpu = {"value": round(sample_bytes / med / 1e9, 4), "unit": "GB/s", "cores": threads, "kind": "reference",
-                   "sample": f"{n_sample} of {H} KV heads of the same step (seq {S}, 7 queries each), XKV, "
-                             f"backend {be}, OpenMP over heads with 1 thread per head (bench.cpp model_heads), "
-                             f"median of {len(times)} runs; {med * 1e3:.1f} ms per sample "
-                             f"= {med * H / n_sample * 1e3:.1f} ms per full step"}
-            log("cpu baseline", cpu)
+            cpu = cpu_baseline_c2(
+                R, np, a, q.cpu().numpy().view(np.uint16),
+                [t.cpu().numpy().view(np.uint16) for t in raw_k], [t.cpu().numpy().view(np.uint16) for t in raw_v],
+                [e.blob[: e.nbytes].cpu().numpy() for e in enc_k], [e.blob[: e.nbytes].cpu().numpy() for e in enc_v],
+                G, D, S, BT)
+            log("cpu baseline", json.dumps(cpu))
         except FileNotFoundError:
             cpu = {"value": None, "unit": "GB/s", "cores": 0, "kind": "reference",
                    "sample": "oracle/_ref/libkvexp_ref.so not present on this host"}
