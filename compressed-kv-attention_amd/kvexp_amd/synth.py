@@ -8,8 +8,9 @@ its own. Values are FP32 rounded to BF16 (nearest even).
       0.3% of elements get their exponent moved 20 binades down (escapes).
   C2  Qwen2.5-0.5B step: 24 layers x 2 KV heads x 7 queries, dim 64, seq 32768.
       K = N(0,1) * 2^U(-6,4) per channel, 2 outlier channels x32; ~6% of K
-      blocks drawn from a 3-binade band (they encode as 2-bit). V = N(0, 0.5^2).
-      Q = N(0,1).
+      blocks drawn from a 3-binade band (they encode as 2-bit). V = N(0, 0.5^2)
+      with ~0.3% of its elements moved 20 binades down (escapes; K's own
+      escape rate is ~0.3%). Q = N(0,1).
   C3  C2 with 32 sequences of lengths round(exp(U(ln 1024, ln 32768))).
   C4  Llama-3-8B step: 32 layers x 8 KV heads x 4 queries, dim 128, seq 131072.
       K = N(0,1) * 2^U(-5,3), V = N(0, 0.5^2).
@@ -78,7 +79,14 @@ def head_kv(cfg: str, seq: int, b: int = 0, layer: int = 0, head: int = 0):
             sign = np.where(r.random((t1 - t0, dim)) < 0.5, -1.0, 1.0).astype(np.float32)
             k[t0:t1] = band * sign * scale
         v = r.standard_normal((seq, dim), dtype=np.float32) * np.float32(0.5)
-        return bf16(k.reshape(-1)), bf16(v.reshape(-1))
+        vb = bf16(v.reshape(-1))
+        # ~0.3 % of V elements moved 20 binades down (near-zero values that
+        # leave every 4-bit window): with K's own escapes (its 2-bit blocks
+        # and distribution tails, ~0.3 %) the step's escape rate is ~0.3 %
+        sel = np.nonzero(r.random(vb.size) < 0.003)[0]
+        e = (vb[sel] >> 7) & 0xFF
+        vb[sel] = (vb[sel] & 0x807F) | (np.where(e > 20, e - 20, e + 20).astype(np.uint16) << 7)
+        return bf16(k.reshape(-1)), vb
     if cfg == "c4":
         scale = np.exp2(r.uniform(-5, 3, dim)).astype(np.float32)
         k = r.standard_normal((seq, dim), dtype=np.float32) * scale
