@@ -48,6 +48,7 @@ HEADERS = [
     "csrc/hip/kvexp_device.h",
     "csrc/hip/kvexp_expf.h",
     "csrc/hip/kvexp_types.h",
+    "csrc/host/host_walk.hpp",
     "../include/kvexp_hip.h",
     "../include/kvexp/attention.hpp",
     "../include/kvexp/codec.hpp",

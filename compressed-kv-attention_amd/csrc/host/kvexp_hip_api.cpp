@@ -18,6 +18,7 @@
 #include <vector>
 
 #include "../hip/kvexp_types.h"
+#include "host_walk.hpp"
 
 using kvexp_dev::AppendJobDev;
 using kvexp_dev::EncBlockMeta;
@@ -53,6 +54,8 @@ void *noalloc_scratch(int device);
 
 namespace {
 
+using namespace kvexp_host; // KvexpFail, fail, the host walk, token_bounds
+
 constexpr int kMaxQPerLaunch = 8;
 constexpr int kMaxDim = 256;
 
@@ -78,12 +81,7 @@ struct HipFail {
         if (e_ != hipSuccess) throw HipFail{e_, #call};                                                               \
     } while (0)
 
-struct KvexpFail {
-    int code;
-    std::string msg;
-};
 
-[[noreturn]] void fail(int code, const std::string &msg) { throw KvexpFail{code, msg}; }
 
 template <class F> int guarded(F &&fn) {
     try {
@@ -119,67 +117,6 @@ struct DevBuf {
     }
     template <class T> T *as() const { return static_cast<T *>(p); }
 };
-
-// --------------------------------------------------------- host block walk --
-struct HostBlock {
-    int mode, n_tokens, n_escape;
-    size_t next;
-};
-
-inline unsigned rd16(const uint8_t *p) { return unsigned(p[0]) | (unsigned(p[1]) << 8); }
-
-// parse_block (scan.hpp:28-66): validation order and messages. Mode 3
-// (3-bit codes, head_dim a multiple of 8) is this library's extension.
-HostBlock parse_block_host(const uint8_t *blob, size_t bytes, size_t at, int dim) {
-    if (bytes - at < 8) fail(KVEXP_HIP_FORMAT_ERROR, "truncated xkv block header");
-    const uint8_t *p = blob + at;
-    HostBlock b{p[0], p[1], int(rd16(p + 2)), 0};
-    const int hdim = int(rd16(p + 4));
-    if (hdim != dim || b.n_tokens <= 0) fail(KVEXP_HIP_FORMAT_ERROR, "xkv block dimension or length mismatch");
-    const size_t body = at + 8;
-    if (b.mode == 0) {
-        const size_t nb = size_t(b.n_tokens) * size_t(dim) * 2u;
-        if (bytes - body < nb) fail(KVEXP_HIP_FORMAT_ERROR, "truncated raw xkv block");
-        b.next = body + nb;
-        return b;
-    }
-    if (b.mode != 2 && b.mode != 4 && !(b.mode == 3 && dim % 8 == 0))
-        fail(KVEXP_HIP_FORMAT_ERROR, "unknown xkv block mode");
-    const size_t need = size_t(dim) + size_t(b.n_tokens) * size_t(dim) +
-                        size_t((b.n_tokens * dim * b.mode + 7) / 8) + size_t(b.n_escape) * 2u;
-    if (bytes - body < need) fail(KVEXP_HIP_FORMAT_ERROR, "truncated coded xkv block");
-    b.next = body + need;
-    return b;
-}
-
-// Blocks that a reader consuming `seq` tokens touches, then the eager parse of
-// the following header (scan.hpp:144-151, 176-189).
-void walk_index(const uint8_t *blob, size_t bytes, int dim, int seq, std::vector<int64_t> &off,
-                std::vector<int32_t> &first) {
-    off.clear();
-    first.clear();
-    size_t at = 0;
-    int64_t tok = 0;
-    while (at < bytes) {
-        const HostBlock b = parse_block_host(blob, bytes, at, dim);
-        if (tok >= seq) break;
-        off.push_back(int64_t(at));
-        first.push_back(int32_t(tok));
-        tok += b.n_tokens;
-        at = b.next;
-    }
-    off.push_back(int64_t(at));
-    first.push_back(int32_t(std::min<int64_t>(tok, INT32_MAX)));
-}
-
-// token_bounds (dispatch.cpp:17-23).
-void token_bounds(int seq, int tile, int tid, int n, int &a, int &b) {
-    const int ntiles = (seq + tile - 1) / tile;
-    const int b0 = int((long long)tid * ntiles / n);
-    const int b1 = int((long long)(tid + 1) * ntiles / n);
-    a = std::min(seq, b0 * tile);
-    b = std::min(seq, b1 * tile);
-}
 
 std::string status_message(uint32_t st) {
     using namespace kvexp_dev;
