@@ -69,11 +69,11 @@ def log(*a):
     print("[bench]", *a, file=sys.stderr, flush=True)
 
 
-def measured_traffic():
-    """HBM bytes per launch of the split kernel from the committed counter
-    summary (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, scaled by a plain copy
-    kernel of known size), or None when there is none."""
-    path = os.path.join(ROOT, "profiles", "attn_wave_c2_traffic.md")
+def measured_traffic(profile: str = "attn_wave_c2_traffic.md"):
+    """HBM bytes per launch of a kernel from its committed counter summary
+    (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, scaled by a plain copy kernel of
+    known size): the split kernel's by default. None when there is none."""
+    path = os.path.join(ROOT, "profiles", profile)
     try:
         for line in open(path):
             if line.startswith("traffic_bytes_per_launch:"):
@@ -101,6 +101,8 @@ def bench_append(a, torch, np, kvexp_amd, synth) -> int:
     T = 2 * L * KV  # K and V containers
     dev = torch.device("cuda:0")
     ctx = kvexp_amd.Context(0)
+    if a.copy_probe:
+        copy_probe(torch, dev)
     steps, warmup = a.steps, a.warmup
     extra = 4 * steps + warmup + 1  # warmup + timed append steps, then the three decode loops
     t0 = time.time()
@@ -128,6 +130,7 @@ def bench_append(a, torch, np, kvexp_amd, synth) -> int:
     for _ in range(2):
         prefill()
     torch.cuda.synchronize()
+    # calls back to back between two HIP events on the stream
     n_pre = max(3, min(20, steps // 10))
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
@@ -344,7 +347,8 @@ def bench_append(a, torch, np, kvexp_amd, synth) -> int:
         "attention_equal_fresh_encode": attn_same,
         "roofline": {"bound": "hbm", "achieved": round(algo / (pre_ms * 1e-3) / 1e9, 2), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(algo / (pre_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
-                     "traffic": None, "kernel": "prefill append (stats + scan + write + tail launches)",
+                     "traffic": measured_traffic("encode_fused_c2_prefill.md"),
+                     "kernel": "prefill append (job-table copy + one-pass encoder + tail launches)",
                      "algorithmic_bytes": algo},
         "cpu_baseline": cpu,
     }

@@ -166,6 +166,36 @@ __host__ __device__ constexpr size_t stats_lds_bytes(int dim) {
            (3 * kWaves + 2 * stats_cols(dim)) * sizeof(int);
 }
 
+// The block's mode from the escape counts of the 2-, 3- and 4-bit windows
+// (codec.cpp:94-103): raw, then the coded modes by width; replace when
+// smaller, or on a tie when the best is not raw and has more escapes (or
+// equal escapes and more bits). With the 3-bit mode this is the order of the
+// reference's sizer (analyze_exponents.py:142-143: smaller, then raw, then
+// fewer escapes, then narrower codes).
+__device__ __forceinline__ EncBlockMeta choose_mode(const int (&cand_esc)[3], int n, int dim, int modes, int nwin) {
+    int best_mode = 0, best_esc = 0;
+    int64_t best_bytes = block_bytes(0, n, 0, dim);
+#pragma unroll
+    for (int bi = 0; bi < 3; ++bi) {
+        const int mode = bi + 2;
+        if (!(modes & (1 << mode)) || (mode == 3 && nwin < 3)) continue;
+        const int64_t by = block_bytes(mode, n, cand_esc[bi], dim);
+        const bool smaller = by < best_bytes;
+        const bool tie_win = by == best_bytes && best_mode != 0 &&
+                             (cand_esc[bi] < best_esc || (cand_esc[bi] == best_esc && mode < best_mode));
+        if (smaller || tie_win) {
+            best_mode = mode;
+            best_bytes = by;
+            best_esc = cand_esc[bi];
+        }
+    }
+    EncBlockMeta m;
+    m.bytes = best_bytes;
+    m.mode = best_mode;
+    m.n_escape = best_esc;
+    return m;
+}
+
 __device__ __forceinline__ void encode_stats_block(uint32_t *hist, int *esc_part, const EncRows src, int n, int dim,
                                                    EncBlockMeta *__restrict__ meta, uint8_t *__restrict__ bases,
                                                    int modes) {
@@ -256,32 +286,7 @@ __device__ __forceinline__ void encode_stats_block(uint32_t *hist, int *esc_part
 #pragma unroll
             for (int bi = 0; bi < 3; ++bi) cand_esc[bi] += esc_part[3 * i + bi];
         }
-        // codec.cpp:94-103: raw, then the coded modes by width; replace when
-        // smaller, or on a tie when the best is not raw and has more escapes
-        // (or equal escapes and more bits). With the 3-bit mode this is the
-        // order of the reference's sizer (analyze_exponents.py:142-143:
-        // smaller, then raw, then fewer escapes, then narrower codes).
-        int best_mode = 0, best_esc = 0;
-        int64_t best_bytes = block_bytes(0, n, 0, dim);
-#pragma unroll
-        for (int bi = 0; bi < 3; ++bi) {
-            const int mode = bi + 2;
-            if (!(modes & (1 << mode)) || (mode == 3 && nwin < 3)) continue;
-            const int64_t by = block_bytes(mode, n, cand_esc[bi], dim);
-            const bool smaller = by < best_bytes;
-            const bool tie_win = by == best_bytes && best_mode != 0 &&
-                                 (cand_esc[bi] < best_esc || (cand_esc[bi] == best_esc && mode < best_mode));
-            if (smaller || tie_win) {
-                best_mode = mode;
-                best_bytes = by;
-                best_esc = cand_esc[bi];
-            }
-        }
-        EncBlockMeta m;
-        m.bytes = best_bytes;
-        m.mode = best_mode;
-        m.n_escape = best_esc;
-        *meta = m;
+        *meta = choose_mode(cand_esc, n, dim, modes, nwin);
     }
 }
 
@@ -492,12 +497,528 @@ __global__ __launch_bounds__(kThreads) void append_write_kernel(const AppendJobD
 
 // The raw rows of each job's new trailing partial block that are not in
 // its tail buffer yet, copied there (after the write kernel has read it).
-__global__ __launch_bounds__(kThreads) void append_tail_kernel(const AppendJobDev *__restrict__ jobs, int dim) {
+// With `terminal` set (after the fused encoder, which writes the index of
+// the jobs with blocks), also the index entry of an empty container.
+__global__ __launch_bounds__(kThreads) void append_tail_kernel(const AppendJobDev *__restrict__ jobs, int dim,
+                                                              int terminal) {
     const AppendJobDev j = jobs[blockIdx.x];
+    if (terminal && j.nb == 0 && threadIdx.x == 0) {
+        j.offs[0] = j.rebase ? j.offs[0] : 0;
+        j.first[0] = j.tok0;
+    }
     const int total = j.copy_rows * dim;
     const uint16_t *from = j.src + size_t(j.copy_from) * size_t(dim);
     uint16_t *to = j.tail + size_t(j.copy_to) * size_t(dim);
     for (int i = int(threadIdx.x); i < total; i += kThreads) to[i] = from[i];
+}
+
+// ------------------------------------------------ encode: one fused pass --
+// Statistics, place and bytes of every block in one launch, reading the
+// tokens once (the three launches above read them twice). The grid is
+// [blocks of the longest job] x [jobs]; a workgroup takes the next block of
+// its job (blockIdx.y) from the job's ticket counter, so every earlier block
+// of the job has already started (workgroups past the job's blocks draw no
+// ticket and return at once); it holds the block's tokens in
+// registers (chunks of 8 elements of one row, 16 bytes, NL chunks per
+// thread), counts each channel's exponents into LDS byte counters, slides the
+// code windows (one (window, channel) pair per thread, so that every wave
+// works), chooses the mode, and finds its place in the container by a
+// decoupled look-back over the sizes of its job's earlier blocks: each block
+// publishes its own size as soon as its mode is known, and the job-relative
+// end of its bytes once its place is known; wave 0 reads up to 64 earlier
+// entries at a time and sums back to the nearest end, after the block's codes
+// and escape ranks are computed (so that the earlier blocks have had that
+// long to publish). Then the block is written from the registers.
+// head_dim % 8 == 0, at most kFusedMaxElems elements per block, sources
+// 16-byte aligned (the host checks; otherwise it uses the three launches).
+//
+// Look-back state: one ticket counter per job (reset to 0 by the workgroup
+// that takes the job's last ticket) and, in an array of its own, one entry
+// per block of the launch (the job's first block at jobs[i].blk0): bits
+// 63..48 the launch's epoch (1..65535, so entries of earlier launches never
+// match), 47..46 the kind (1: the block's size, 2: the job-relative end of
+// the block), 45..0 the value. The host clears the entries when the epoch
+// wraps and when the array is new, and the counters when their array is new.
+constexpr uint32_t kLookbackPolls = 1u << 20; // ~1 s of polling, then kStLookback
+
+// Phase trace of the one-pass encoder (builds with KVEXP_PHASE_TRACE only;
+// compressed-kv-attention_amd/probes.py): per block of a launch, wave 0's
+// clock at the start, after the ticket, the job, the tokens' arrival, the
+// histograms, the mode, the escape ranks, the look-back and the end; then
+// the look-back's polls, the CU that ran it and the workgroup's blockIdx.x.
+#if defined(KVEXP_PHASE_TRACE)
+constexpr int kEncTraceBlocks = 32768, kEncTraceWords = 12;
+__device__ unsigned long long g_enc_trace[kEncTraceBlocks * kEncTraceWords];
+#define KVEXP_ENC_MARK(i) (enc_tr[i] = __builtin_readcyclecounter())
+#else
+#define KVEXP_ENC_MARK(i) ((void)0)
+#endif
+constexpr uint64_t kLbValueMask = (uint64_t(1) << 46) - 1u;
+
+__device__ __forceinline__ uint64_t lb_word(uint32_t epoch, uint32_t kind, uint64_t value) {
+    return (uint64_t(epoch) << 48) | (uint64_t(kind) << 46) | (value & kLbValueMask);
+}
+
+__device__ __forceinline__ int64_t wave_sum_i64(int64_t v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef const __attribute__((address_space(1))) u32x4_t g_cu32x4; // 16-byte global loads
+
+// Exclusive prefix over the workgroup, in chunk order (chunk k * kThreads +
+// thread), of the sentinel counts packed two to a 32-bit word (16 bits
+// each: at most 8 per chunk, 2048 per chunk row of the workgroup, so no
+// field carries into the next). tmp: [kWaves][NP] words in LDS. Leaves in
+// excl[q] the thread's exclusive prefix within each chunk row and in
+// total[q] the rows' totals (field k % 2 of word k / 2 for chunk row k);
+// EscRanks::rank gives a chunk's first rank.
+template <int NL>
+struct EscRanks {
+    static constexpr int NP = (NL + 1) / 2;
+    uint32_t excl[NP], total[NP];
+    __device__ __forceinline__ int field(const uint32_t (&a)[NP], int k) const {
+        return int((a[k / 2] >> (16 * (k % 2))) & 0xFFFFu);
+    }
+    __device__ __forceinline__ int rank(int k) const {
+        int carry = 0;
+#pragma unroll
+        for (int i = 0; i < NL; ++i)
+            if (i < k) carry += field(total, i);
+        return carry + field(excl, k);
+    }
+    __device__ __forceinline__ int sum() const {
+        int t = 0;
+#pragma unroll
+        for (int i = 0; i < NL; ++i) t += field(total, i);
+        return t;
+    }
+};
+
+template <int NL>
+__device__ __forceinline__ EscRanks<NL> fused_escape_ranks(const uint32_t (&v)[EscRanks<NL>::NP], uint32_t *tmp) {
+    constexpr int NP = EscRanks<NL>::NP;
+    const int lane = lane_id(), w = int(threadIdx.x) >> 6;
+    EscRanks<NL> r;
+    uint32_t incl[NP];
+#pragma unroll
+    for (int q = 0; q < NP; ++q) {
+        incl[q] = uint32_t(wave_scan_add(int(v[q])));
+        if (lane == kWave - 1) tmp[w * NP + q] = incl[q];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < NP; ++q) {
+        uint32_t before = 0, total = 0;
+#pragma unroll
+        for (int x = 0; x < kWaves; ++x) {
+            const uint32_t t = tmp[x * NP + q];
+            before += x < w ? t : 0;
+            total += t;
+        }
+        r.excl[q] = before + incl[q] - v[q];
+        r.total[q] = total;
+    }
+    return r;
+}
+
+// Waves per SIMD the one-pass encoder is compiled for (its registers fit
+// 512 / waves without spilling): 8 with up to four chunk rows per thread.
+template <int NL>
+constexpr int kFusedWaves = NL <= 4 ? 8 : 4;
+
+// Dynamic LDS of the one-pass encoder: the histogram columns, or the
+// largest block (raw: header + 2 bytes per element) staged for its copy,
+// whichever is larger. At most 66,560 bytes (head_dim 256, 64-token blocks).
+__host__ __device__ constexpr size_t fused_lds_bytes(int dim, int bt) {
+    const size_t hist = size_t(dim) * kHistStride * sizeof(uint32_t);
+    const size_t raw = (8u + 2u * size_t(bt) * size_t(dim) + 15u) & ~size_t(15);
+    return hist > raw ? hist : raw;
+}
+
+// JOBS: the jobs are in device memory (appends); else the one job is a
+// kernel argument (an encode), read from the argument segment.
+template <int NL, bool JOBS>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(kFusedWaves<NL>, kFusedWaves<NL>))) void
+encode_fused_kernel(const AppendJobDev *__restrict__ jobs, AppendJobDev one, int dim, int bt, int modes,
+                    uint64_t *__restrict__ state, uint32_t *__restrict__ tickets, uint32_t epoch,
+                    uint32_t *__restrict__ status) {
+    // dynamic LDS: the exponent byte counters [dim][kHistStride], then the
+    // block's bytes staged for the copy to the container (fused_lds_bytes)
+    extern __shared__ uint32_t fz_lds[];
+    uint32_t *fz_hist = fz_lds;
+    uint8_t *stage = reinterpret_cast<uint8_t *>(fz_lds);
+    __shared__ uint32_t s_ticket;
+    __shared__ int s_lo[kWaves], s_hi[kWaves], s_esc[kWaves][3];
+    __shared__ __align__(16) uint8_t s_base[3][kMaxDim]; // window bases of the 2-, 3- and 4-bit codes
+    __shared__ uint16_t s_key[3 * kMaxDim];               // best (coverage, base) of the upper half of each range
+    __shared__ uint32_t s_scan[kWaves * EscRanks<NL>::NP];
+    __shared__ long long s_excl;
+    const int tid = int(threadIdx.x), lane = lane_id(), w = tid >> 6;
+    const int jx = int(blockIdx.y);
+    uint32_t polls = 0; // look-back reads that found a nearer block unpublished
+#if defined(KVEXP_PHASE_TRACE)
+    unsigned long long enc_tr[9];
+#endif
+    KVEXP_ENC_MARK(0);
+
+    // ---- ticket (every workgroup of the job's grid row draws one, so the
+    // one that draws the row's last resets the counter) while the job loads
+    if (tid == 0) {
+        const uint32_t t = atomicAdd(tickets + jx, 1u);
+        if (t == gridDim.x - 1u) atomicExch(tickets + jx, 0u);
+        s_ticket = t;
+    }
+    const AppendJobDev j = JOBS ? jobs[jx] : one;
+#pragma unroll 1
+    for (int i = tid; i < dim * kHistStride; i += kThreads) fz_hist[i] = 0u;
+    __syncthreads();
+    const int b = int(s_ticket);
+    if (b >= j.nb) { // past the job's blocks (or a counter not left at 0: then nothing of the job runs)
+        if (tid == 0 && b >= int(gridDim.x)) atomicOr(status, kStLookback);
+        return;
+    }
+    const int g = j.blk0 + b; // look-back entry of the block
+    KVEXP_ENC_MARK(1);
+    const int n = min(bt, j.seq - b * bt);
+#if defined(KVEXP_PHASE_TRACE)
+    asm volatile("" ::"v"(n));
+#endif
+    KVEXP_ENC_MARK(2);
+    const EncRows src = job_rows(j, b, bt, dim);
+    const int chunks = n * dim / 8, cpr = dim / 8, split = src.split / 8;
+    const float inv_cpr = __builtin_amdgcn_rcpf(float(cpr));
+
+    // ---- the block's tokens into registers; channel histograms
+    // first channel of chunk c (8 * (c mod dim / 8); the float quotient is
+    // exact to far below its distance from an integer, c < 4096)
+    auto chunk_d0 = [&](int c) {
+        const int row = int((float(c) + 0.5f) * inv_cpr);
+        return 8 * (c - row * cpr);
+    };
+    u32x4_t x[NL];
+    uint32_t pk_lo = 0xFFFFFFFFu, pk_hi = 0u; // exponent fields (bits 14..7 of each half), smallest and largest
+#pragma unroll
+    for (int k = 0; k < NL; ++k) { // all loads in flight together: chunks past the block read chunk 0
+        const int c = k * kThreads + tid < chunks ? k * kThreads + tid : 0;
+        const uint16_t *p = c < split ? src.a + 8 * size_t(c) : src.b + 8 * size_t(c - split);
+        x[k] = *(g_cu32x4 *)(p);
+    }
+#if defined(KVEXP_PHASE_TRACE)
+    asm volatile("" ::"v"(x[NL - 1][0]), "v"(x[0][0]));
+#endif
+    KVEXP_ENC_MARK(3);
+    // Lanes that share a chunk column (the rows of one chunk position) count
+    // their 8 elements in an order rotated by the row (step h takes element
+    // (h + row) % 8), so that the 64 lanes of an LDS add hit different
+    // channel columns rather than 8 lanes one counter.
+#pragma unroll
+    for (int k = 0; k < NL; ++k) {
+        const int c = k * kThreads + tid;
+        if (c < chunks) {
+            const int row = int((float(c) + 0.5f) * inv_cpr);
+            const int rot = row & 7;
+            uint32_t *col = fz_hist + 8 * (c - row * cpr) * kHistStride;
+            // the chunk rotated right by 16 * rot bits: element h of v is element (h + rot) % 8
+            u32x4_t v = x[k];
+            if (rot & 4) v = u32x4_t{v[2], v[3], v[0], v[1]};
+            if (rot & 2) v = u32x4_t{v[1], v[2], v[3], v[0]};
+            if (rot & 1)
+                v = u32x4_t{__builtin_amdgcn_alignbit(v[1], v[0], 16), __builtin_amdgcn_alignbit(v[2], v[1], 16),
+                            __builtin_amdgcn_alignbit(v[3], v[2], 16), __builtin_amdgcn_alignbit(v[0], v[3], 16)};
+#pragma unroll
+            for (int h = 0; h < 8; ++h) {
+                const uint32_t e = (v[h >> 1] >> (16 * (h & 1) + 7)) & 0xFFu;
+                atomicAdd(col + ((h + rot) & 7) * kHistStride + int(e >> 2), 1u << (8u * (e & 3u)));
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t ef = x[k][i] & 0x7F807F80u;
+                pk_lo = min(min(pk_lo, ef & 0xFFFFu), ef >> 16);
+                pk_hi = max(max(pk_hi, ef & 0xFFFFu), ef >> 16);
+            }
+        }
+    }
+    const int e_lo = wave_min_i32(pk_lo == 0xFFFFFFFFu ? 255 : int(pk_lo >> 7));
+    const int e_hi = wave_max_i32(int(pk_hi >> 7));
+    if (lane == 0) {
+        s_lo[w] = e_lo;
+        s_hi[w] = e_hi;
+    }
+    __syncthreads();
+    KVEXP_ENC_MARK(4);
+    int blk_lo = 255, blk_hi = 0;
+#pragma unroll
+    for (int i = 0; i < kWaves; ++i) {
+        blk_lo = min(blk_lo, s_lo[i]);
+        blk_hi = max(blk_hi, s_hi[i]);
+    }
+
+    // ---- best_base of each (window, channel) (codec.cpp:18-35): the most
+    // covered exponents, then the smallest base; bases outside
+    // [blk_lo - width + 1, blk_hi] cover nothing. Each range is split in two
+    // halves taken by different waves (tasks [0, pairs) the lower halves,
+    // [pairs, 2 pairs) the upper); a half's best is the key
+    // coverage * 256 + 255 - base, so the larger key is the better base.
+    const int nwin = (modes & 8) ? 3 : 2;
+    const int pairs = nwin * dim;
+    int key_lo[3] = {0, 0, 0}; // this thread's lower-half results (tasks tid, tid + 256, tid + 512)
+#pragma unroll
+    for (int r = 0; r < 6; ++r) {
+        const int t = tid + r * kThreads;
+        if (t >= 2 * pairs) break;
+        const int half = int(t >= pairs);
+        const int pt = t - half * pairs;
+        const int wi = int(pt >= dim) + int(pt >= 2 * dim);
+        const int d = pt - wi * dim;
+        const int bi = wi == 0 ? 0 : (nwin == 2 ? 2 : wi);
+        const int width = (4 << bi) - 1;
+        const int lo0 = min(max(0, blk_lo - width + 1), 256 - width);
+        const int hi0 = min(blk_hi, 256 - width);
+        const int mid = (lo0 + hi0 + 1) >> 1;
+        const int lo = half ? mid : lo0, hi = half ? hi0 : mid - 1;
+        int key = 0;
+        if (lo <= hi) {
+            const uint8_t *hb = reinterpret_cast<const uint8_t *>(fz_hist + d * kHistStride);
+            int cov = 0;
+            for (int e = lo; e < lo + width; ++e) cov += hb[e];
+            int best = cov, best_b = lo;
+#pragma unroll 4
+            for (int base = lo + 1; base <= hi; ++base) {
+                cov += int(hb[base + width - 1]) - int(hb[base - 1]);
+                if (cov > best) {
+                    best = cov;
+                    best_b = base;
+                }
+            }
+            key = best * 256 + 255 - best_b;
+        }
+        if (half) s_key[pt] = uint16_t(key);
+        else if (r < 3) key_lo[r] = key;
+    }
+    __syncthreads();
+    int esc[3] = {0, 0, 0};
+#pragma unroll
+    for (int r = 0; r < 3; ++r) {
+        const int pt = tid + r * kThreads;
+        if (pt >= pairs) break;
+        const int wi = int(pt >= dim) + int(pt >= 2 * dim);
+        const int d = pt - wi * dim;
+        const int bi = wi == 0 ? 0 : (nwin == 2 ? 2 : wi);
+        const int key = max(key_lo[r], int(s_key[pt]));
+        s_base[bi][d] = uint8_t(255 - (key & 255));
+        esc[bi] += n - (key >> 8);
+    }
+#pragma unroll
+    for (int bi = 0; bi < 3; ++bi) esc[bi] = wave_sum_i32(esc[bi]);
+    if (lane == 0) {
+#pragma unroll
+        for (int bi = 0; bi < 3; ++bi) s_esc[w][bi] = esc[bi];
+    }
+    __syncthreads();
+    int cand[3] = {0, 0, 0};
+#pragma unroll
+    for (int i = 0; i < kWaves; ++i) {
+#pragma unroll
+        for (int bi = 0; bi < 3; ++bi) cand[bi] += s_esc[i][bi];
+    }
+    const EncBlockMeta m = choose_mode(cand, n, dim, modes, nwin);
+    KVEXP_ENC_MARK(5);
+
+    // ---- publish the size
+    if (tid == 0)
+        __hip_atomic_store(state + g, lb_word(epoch, b == 0 ? 2u : 1u, uint64_t(m.bytes)), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+
+    // ---- codes and sentinel counts
+    const int mode = m.mode;
+    const uint32_t width = (1u << mode) - 1u;
+    uint32_t cw[NL];
+    uint32_t cnt_pk[EscRanks<NL>::NP] = {}; // sentinels per chunk, 16 bits each
+#pragma unroll
+    for (int k = 0; k < NL; ++k) {
+        cw[k] = 0u;
+        if (mode != 0 && k * kThreads + tid < chunks) {
+            int cnt = 0;
+            const uint2 bb = *reinterpret_cast<const uint2 *>(&s_base[mode - 2][chunk_d0(k * kThreads + tid)]);
+#pragma unroll
+            for (int h = 0; h < 8; ++h) {
+                const uint32_t e = (x[k][h >> 1] >> (16 * (h & 1) + 7)) & 0xFFu;
+                const uint32_t base = ((h < 4 ? bb.x : bb.y) >> (8 * (h & 3))) & 0xFFu;
+                const uint32_t delta = e - base; // wraps when e < base
+                const bool hit = delta < width;
+                cw[k] |= (hit ? delta : width) << (mode * h);
+                cnt += hit ? 0 : 1;
+            }
+            cnt_pk[k / 2] |= uint32_t(cnt) << (16 * (k % 2));
+        }
+    }
+    // the escape ranks; the barrier in it also ends every read of the
+    // histograms, whose LDS now takes the staged block
+    const EscRanks<NL> er = fused_escape_ranks<NL>(cnt_pk, s_scan);
+    KVEXP_ENC_MARK(6);
+
+    // ---- the block's bytes, staged in LDS in their final order
+    if (tid < 8) {
+        const int ne = mode == 0 ? 0 : m.n_escape;
+        const uint32_t hdr[8] = {uint32_t(mode), uint32_t(n), uint32_t(ne & 0xFF), uint32_t(ne >> 8),
+                                 uint32_t(dim & 0xFF), uint32_t(dim >> 8), 0u, 0u};
+        stage[tid] = uint8_t(hdr[tid]);
+    }
+    uint8_t *body = stage + 8;
+    if (mode == 0) {
+#pragma unroll
+        for (int k = 0; k < NL; ++k) {
+            const int c = k * kThreads + tid;
+            typedef u32x4_t __attribute__((aligned(8))) u32x4_a8;
+            if (c < chunks) *reinterpret_cast<u32x4_a8 *>(body + 16 * c) = x[k]; // 8 + 16c: 8-byte aligned
+        }
+    } else {
+        if (2 * tid < dim) // dim <= 256 = kThreads: one pair of bases per thread
+            *reinterpret_cast<uint16_t *>(body + 2 * tid) = *reinterpret_cast<const uint16_t *>(&s_base[mode - 2][2 * tid]);
+        uint8_t *sm = body + dim;
+        uint8_t *codes = sm + n * dim;
+        uint8_t *escw = codes + exp_payload_bytes(n, dim, mode);
+#pragma unroll
+        for (int k = 0; k < NL; ++k) {
+            const int c = k * kThreads + tid;
+            if (c >= chunks) continue;
+            // sign and mantissa bytes of the 8 elements: (h >> 8 & 0x80) | (h & 0x7F)
+            uint32_t s4[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t mm = x[k][i] & 0x807F807Fu;
+                s4[i] = mm | (mm >> 8); // bytes 0 and 2 hold the two elements' sm bytes
+            }
+            u32x2_t smv;
+            smv.x = __builtin_amdgcn_perm(s4[1], s4[0], 0x06040200u);
+            smv.y = __builtin_amdgcn_perm(s4[3], s4[2], 0x06040200u);
+            *reinterpret_cast<u32x2_t *>(sm + 8 * c) = smv; // 8 + dim + 8c: 8-byte aligned
+            if (mode == 4) {
+                *reinterpret_cast<uint32_t *>(codes + 4 * c) = cw[k];
+            } else if (mode == 2) {
+                *reinterpret_cast<uint16_t *>(codes + 2 * c) = uint16_t(cw[k]);
+            } else {
+                uint8_t *q = codes + 3 * c;
+                q[0] = uint8_t(cw[k]);
+                q[1] = uint8_t(cw[k] >> 8);
+                q[2] = uint8_t(cw[k] >> 16);
+            }
+            if (((cnt_pk[k / 2] >> (16 * (k % 2))) & 0xFFFFu) != 0) {
+                int r = er.rank(k);
+#pragma unroll
+                for (int h = 0; h < 8; ++h) {
+                    if (((cw[k] >> (mode * h)) & width) == width) {
+                        if (r < m.n_escape) { // escape words may sit at odd offsets (3-bit codes): bytes
+                            const uint32_t v = x[k][h >> 1] >> (16 * (h & 1));
+                            escw[2 * r] = uint8_t(v);
+                            escw[2 * r + 1] = uint8_t(v >> 8);
+                        }
+                        ++r;
+                    }
+                }
+            }
+        }
+    }
+
+    // ---- wave 0 finds the block's place while the others wait at the barrier
+    if (w == 0) {
+        int64_t excl = 0;
+        if (b > 0) {
+            int pos = g - 1;
+            auto lb_read = [&]() -> uint64_t {
+                const int idx = pos - lane;
+                return idx >= j.blk0 ? __hip_atomic_load(state + idx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                                     : 0u;
+            };
+            uint64_t wv = lb_read();
+            while (true) {
+                const bool in = pos - lane >= j.blk0;
+                const uint32_t kind = in && uint32_t(wv >> 48) == epoch ? uint32_t(wv >> 46) & 3u : 0u;
+                const uint64_t ends = __ballot(in && kind == 2u);
+                const uint64_t open = __ballot(in && kind == 0u);
+                const int fe = ends ? __ffsll((unsigned long long)ends) - 1 : kWave;
+                const int fo = open ? __ffsll((unsigned long long)open) - 1 : kWave;
+                if (fo < fe) { // a nearer block has not published its size yet
+                    if (++polls > kLookbackPolls) {
+                        if (lane == 0) atomicOr(status, kStLookback);
+                        break;
+                    }
+                    __builtin_amdgcn_s_sleep(2);
+                    wv = lb_read();
+                    continue;
+                }
+                excl += wave_sum_i64(in && lane <= fe ? int64_t(wv & kLbValueMask) : 0);
+                if (fe < kWave) break;
+                pos -= kWave;
+                wv = lb_read();
+            }
+            if (lane == 0)
+                __hip_atomic_store(state + g, lb_word(epoch, 2u, uint64_t(excl + m.bytes)), __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+        }
+        if (lane == 0) s_excl = excl;
+    }
+    __syncthreads();
+    KVEXP_ENC_MARK(7);
+
+    // ---- the staged bytes to the container: 16-byte aligned stores, the
+    // bytes before the first aligned address and after the last one alone
+    const int64_t off = (j.rebase ? j.offs[0] : 0) + s_excl;
+    uint8_t *p = j.out + off;
+    const int nbytes = int(m.bytes);
+    const int head = min(nbytes, int((16u - (uint32_t(reinterpret_cast<uintptr_t>(p)) & 15u)) & 15u));
+    const int n16 = (nbytes - head) >> 4;
+    const int tail0 = head + 16 * n16;
+    for (int i = tid; i < n16; i += kThreads) {
+        typedef const u32x4_t __attribute__((aligned(1))) u32x4_a1;
+        *(__attribute__((address_space(1))) u32x4_t *)(p + head + 16 * i) =
+            *reinterpret_cast<u32x4_a1 *>(stage + head + 16 * i);
+    }
+    if (tid < head) p[tid] = stage[tid];
+    else if (tid >= 16 && tid - 16 < nbytes - tail0) p[tail0 + tid - 16] = stage[tail0 + tid - 16];
+    if (tid == 0) {
+        j.offs[b] = off;
+        j.first[b] = j.tok0 + b * bt;
+        if (b == j.nb - 1) {
+            j.offs[b + 1] = off + m.bytes;
+            j.first[b + 1] = j.tok0 + j.seq;
+        }
+        if (er.sum() != (mode == 0 ? 0 : m.n_escape)) atomicOr(status, kStEscape);
+    }
+#if defined(KVEXP_PHASE_TRACE)
+    KVEXP_ENC_MARK(8);
+    if (w == 0 && lane == 0 && g < kEncTraceBlocks) {
+        unsigned long long *o = g_enc_trace + size_t(g) * kEncTraceWords;
+        for (int i = 0; i < 9; ++i) o[i] = enc_tr[i];
+        o[9] = polls;
+        o[10] = (unsigned long long)__smid();
+        o[11] = (unsigned long long)blockIdx.x; // the ticket (b) is the block: how often they agree
+    }
+#endif
+}
+
+#if defined(KVEXP_PHASE_TRACE)
+} // namespace kvexp_dev
+extern "C" int kvexp_hip_encode_trace_read(unsigned long long *host, size_t n) {
+    return int(hipMemcpyFromSymbol(host, HIP_SYMBOL(kvexp_dev::g_enc_trace), n * 8));
+}
+namespace kvexp_dev {
+#endif
+
+// Clear n 64-bit or 32-bit words (the look-back entries and ticket counters
+// of the fused encoder; kernels, not memsets, so that a captured graph
+// replays them).
+__global__ __launch_bounds__(256) void clear_u64_kernel(uint64_t *__restrict__ p, size_t n) {
+    const size_t i = size_t(blockIdx.x) * 256u + threadIdx.x;
+    if (i < n) p[i] = 0u;
+}
+__global__ __launch_bounds__(256) void clear_u32_kernel(uint32_t *__restrict__ p, size_t n) {
+    const size_t i = size_t(blockIdx.x) * 256u + threadIdx.x;
+    if (i < n) p[i] = 0u;
 }
 
 // Append jobs that encode one block each (a decode step: the trailing block
@@ -745,9 +1266,70 @@ hipError_t decode(const uint8_t *blob, uint64_t bytes, const int64_t *offs, cons
     return hipGetLastError();
 }
 
+bool encode_fused_supported(int dim, int bt) {
+    return dim >= 8 && dim % 8 == 0 && dim <= kMaxDim && bt >= 1 && int64_t(bt) * dim <= kFusedMaxElems;
+}
+
+namespace {
+template <int NL, bool JOBS>
+hipError_t launch_fused_j(const AppendJobDev *jobs, int n_jobs, const AppendJobDev &one, int max_job_blocks, int dim,
+                          int bt, int modes, const EncLookback &lb, uint32_t *status, hipStream_t s) {
+    // head_dim 256 needs 66,560 bytes of histogram columns, past the default
+    // 64 KiB of dynamic LDS (set once per instantiation)
+    static const hipError_t configured =
+        hipFuncSetAttribute(reinterpret_cast<const void *>(encode_fused_kernel<NL, JOBS>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, int(fused_lds_bytes(kMaxDim, 64)));
+    if (configured != hipSuccess) return configured;
+    const size_t lds = fused_lds_bytes(dim, bt);
+    hipLaunchKernelGGL((encode_fused_kernel<NL, JOBS>), dim3(unsigned(max_job_blocks), unsigned(n_jobs)),
+                       dim3(kThreads), lds, s, jobs, one, dim, bt, modes, lb.words, lb.tickets, lb.epoch, status);
+    return hipGetLastError();
+}
+
+template <int NL>
+hipError_t launch_fused(const AppendJobDev *jobs, int n_jobs, const AppendJobDev &one, int max_job_blocks, int dim,
+                        int bt, int modes, const EncLookback &lb, uint32_t *status, hipStream_t s) {
+    return jobs != nullptr
+               ? launch_fused_j<NL, true>(jobs, n_jobs, one, max_job_blocks, dim, bt, modes, lb, status, s)
+               : launch_fused_j<NL, false>(jobs, n_jobs, one, max_job_blocks, dim, bt, modes, lb, status, s);
+}
+
+// The fused encoder over the blocks of `jobs` (device; n_jobs of them, the
+// longest with max_job_blocks blocks), or of the one job `one` when jobs is
+// null (n_jobs 1).
+hipError_t encode_fused(const AppendJobDev *jobs, int n_jobs, const AppendJobDev &one, int max_job_blocks, int dim,
+                        int bt, int modes, const EncLookback &lb, uint32_t *status, hipStream_t s) {
+    if (lb.clear_words > 0)
+        hipLaunchKernelGGL(clear_u64_kernel, dim3(unsigned((lb.clear_words + 255) / 256)), dim3(256), 0, s, lb.words,
+                           lb.clear_words);
+    if (lb.clear_tickets > 0)
+        hipLaunchKernelGGL(clear_u32_kernel, dim3(unsigned((lb.clear_tickets + 255) / 256)), dim3(256), 0, s,
+                           lb.tickets, lb.clear_tickets);
+    const int chunks = (bt * dim) / 8;
+    if (chunks <= kThreads) return launch_fused<1>(jobs, n_jobs, one, max_job_blocks, dim, bt, modes, lb, status, s);
+    if (chunks <= 2 * kThreads)
+        return launch_fused<2>(jobs, n_jobs, one, max_job_blocks, dim, bt, modes, lb, status, s);
+    if (chunks <= 4 * kThreads)
+        return launch_fused<4>(jobs, n_jobs, one, max_job_blocks, dim, bt, modes, lb, status, s);
+    return launch_fused<8>(jobs, n_jobs, one, max_job_blocks, dim, bt, modes, lb, status, s);
+}
+} // namespace
+
 hipError_t encode(const uint16_t *kv, int seq, int dim, int bt, int n_blocks, EncBlockMeta *meta, uint8_t *bases,
                   int64_t *offs, int32_t *first, uint8_t *out, uint32_t *status, hipStream_t s, bool rebase,
-                  int tok0, int modes) {
+                  int tok0, int modes, const EncLookback *lb) {
+    if (lb != nullptr) { // one pass (the caller checked encode_fused_supported and the alignment)
+        AppendJobDev one{};
+        one.src = kv;
+        one.offs = offs;
+        one.first = first;
+        one.out = out;
+        one.seq = seq;
+        one.tok0 = tok0;
+        one.nb = n_blocks;
+        one.rebase = rebase ? 1 : 0;
+        return encode_fused(nullptr, 1, one, n_blocks, dim, bt, modes, *lb, status, s);
+    }
     hipLaunchKernelGGL(encode_stats_kernel, dim3(n_blocks), dim3(kThreads), stats_lds_bytes(dim), s, kv, seq,
                        dim, bt, meta, bases, modes);
     hipLaunchKernelGGL(encode_scan_kernel, dim3(1), dim3(1024), 0, s, meta, n_blocks, bt, seq, offs, first,
@@ -758,11 +1340,21 @@ hipError_t encode(const uint16_t *kv, int seq, int dim, int bt, int n_blocks, En
 }
 
 hipError_t append(const AppendJobDev *jobs, int n_jobs, int total_blocks, int dim, int bt, EncBlockMeta *meta,
-                  uint8_t *bases, uint32_t *status, hipStream_t s, bool one_block, int modes) {
+                  uint8_t *bases, uint32_t *status, hipStream_t s, bool one_block, int modes, const EncLookback *lb,
+                  int max_job_blocks) {
     if (n_jobs <= 0) return hipSuccess;
     if (one_block) {
         const size_t lds = stats_lds_bytes(dim) + 3 * size_t(dim);
         hipLaunchKernelGGL(append_one_kernel, dim3(n_jobs), dim3(kThreads), lds, s, jobs, dim, bt, status, modes);
+        return hipGetLastError();
+    }
+    if (lb != nullptr) { // one pass, then the tails (and the index of empty containers)
+        if (total_blocks > 0) {
+            const hipError_t e =
+                encode_fused(jobs, n_jobs, AppendJobDev{}, max_job_blocks, dim, bt, modes, *lb, status, s);
+            if (e != hipSuccess) return e;
+        }
+        hipLaunchKernelGGL(append_tail_kernel, dim3(n_jobs), dim3(kThreads), 0, s, jobs, dim, 1);
         return hipGetLastError();
     }
     if (total_blocks > 0)
@@ -772,7 +1364,7 @@ hipError_t append(const AppendJobDev *jobs, int n_jobs, int total_blocks, int di
     if (total_blocks > 0)
         hipLaunchKernelGGL(append_write_kernel, dim3(total_blocks), dim3(kThreads), 0, s, jobs, n_jobs, dim, bt, meta,
                            bases, status);
-    hipLaunchKernelGGL(append_tail_kernel, dim3(n_jobs), dim3(kThreads), 0, s, jobs, dim);
+    hipLaunchKernelGGL(append_tail_kernel, dim3(n_jobs), dim3(kThreads), 0, s, jobs, dim, 0);
     return hipGetLastError();
 }
 

@@ -11,6 +11,7 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <limits.h>
 #include <stdint.h>
 
 #include "kvexp_expf.h"
@@ -193,6 +194,29 @@ __device__ __forceinline__ int wave_scan_add(int x) {
     x += dpp_i32<0x143, 0xc>(0, x);
     return x;
 }
+
+// Minimum, maximum and sum over the 64 lanes, returned to every lane (the
+// scan pattern of wave_scan_add with the operation's identity shifted in,
+// then lane 63's value).
+__device__ __forceinline__ int wave_min_i32(int x) {
+    x = min(x, dpp_i32<0x111>(INT_MAX, x));
+    x = min(x, dpp_i32<0x112>(INT_MAX, x));
+    x = min(x, dpp_i32<0x114>(INT_MAX, x));
+    x = min(x, dpp_i32<0x118>(INT_MAX, x));
+    x = min(x, dpp_i32<0x142, 0xa>(INT_MAX, x));
+    x = min(x, dpp_i32<0x143, 0xc>(INT_MAX, x));
+    return __builtin_amdgcn_readlane(x, 63);
+}
+__device__ __forceinline__ int wave_max_i32(int x) {
+    x = max(x, dpp_i32<0x111>(INT_MIN, x));
+    x = max(x, dpp_i32<0x112>(INT_MIN, x));
+    x = max(x, dpp_i32<0x114>(INT_MIN, x));
+    x = max(x, dpp_i32<0x118>(INT_MIN, x));
+    x = max(x, dpp_i32<0x142, 0xa>(INT_MIN, x));
+    x = max(x, dpp_i32<0x143, 0xc>(INT_MIN, x));
+    return __builtin_amdgcn_readlane(x, 63);
+}
+__device__ __forceinline__ int wave_sum_i32(int x) { return __builtin_amdgcn_readlane(wave_scan_add(x), 63); }
 
 __device__ __forceinline__ int lane_id() { return int(__lane_id()); }
 

@@ -12,6 +12,7 @@ enum : uint32_t {
     kStTruncated = 1u << 2, // payload past the end of the container
     kStEscape = 1u << 3,    // more sentinels than n_escape
     kStIndex = 1u << 4,     // block index disagrees with the headers
+    kStLookback = 1u << 5,  // the fused encoder's wait for an earlier block's size ran out
 };
 
 
@@ -88,6 +89,22 @@ struct EncBlockMeta {
     int32_t mode;
     int32_t n_escape;
 };
+
+// Look-back state of the fused encoder: one entry per block of a launch
+// (`words`), one ticket counter per job (`tickets`, an array of its own, left
+// at 0 by every launch), the launch's epoch (1..65535), and how many entries
+// and counters to clear before the launch (all of them when an array is new,
+// the entries when the epoch wrapped, else 0).
+struct EncLookback {
+    uint64_t *words;
+    uint32_t *tickets;
+    uint32_t epoch;
+    size_t clear_words;
+    size_t clear_tickets;
+};
+
+// The fused encoder holds a block in registers: at most this many elements.
+constexpr int kFusedMaxElems = 16384;
 
 // Job of a batched append, as the kernels read it (built by the host API).
 struct AppendJobDev {

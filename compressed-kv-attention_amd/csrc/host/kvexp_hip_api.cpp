@@ -28,11 +28,13 @@ using kvexp_dev::WorkItem;
 namespace kvexp_launch {
 hipError_t decode(const uint8_t *blob, uint64_t bytes, const int64_t *offs, const int32_t *first, int n_blocks,
                   int seq, int dim, uint16_t *out, uint32_t *status, hipStream_t s);
+bool encode_fused_supported(int dim, int bt);
 hipError_t encode(const uint16_t *kv, int seq, int dim, int bt, int n_blocks, EncBlockMeta *meta, uint8_t *bases,
                   int64_t *offs, int32_t *first, uint8_t *out, uint32_t *status, hipStream_t s, bool rebase,
-                  int tok0, int modes);
+                  int tok0, int modes, const kvexp_dev::EncLookback *lb);
 hipError_t append(const kvexp_dev::AppendJobDev *jobs, int n_jobs, int total_blocks, int dim, int bt,
-                  EncBlockMeta *meta, uint8_t *bases, uint32_t *status, hipStream_t s, bool one_block, int modes);
+                  EncBlockMeta *meta, uint8_t *bases, uint32_t *status, hipStream_t s, bool one_block, int modes,
+                  const kvexp_dev::EncLookback *lb, int max_job_blocks);
 hipError_t attention(bool xkv, int order, const HeadDev *heads, const WorkItem *items, int n_items,
                      const int32_t *merge_ids, int n_merge, const uint16_t *q, float *out, float *lse, float *ws,
                      int dim, uint32_t *status, hipStream_t s);
@@ -128,6 +130,12 @@ std::string status_message(uint32_t st) {
     return "xkv container error";
 }
 
+// The encoders' status word as an error message.
+std::string encoder_status_message(uint32_t st) {
+    if (st & kvexp_dev::kStLookback) return "one-pass encoder: an earlier block's size never arrived";
+    return "escape count drifted from the size model";
+}
+
 } // namespace
 
 // ================================================================ context ==
@@ -139,6 +147,13 @@ struct kvexp_hip_ctx {
     // memory that a kernel still in flight reads
     DevBuf enc_meta, enc_bases, enc_off, enc_first, app_jobs;
     size_t enc_meta_cap = 0, enc_bases_cap = 0, enc_index_cap = 0, app_jobs_cap = 0;
+    // look-back entries and ticket counters of the one-pass encoder, the
+    // epoch of its last launch, and whether a launch reported a broken
+    // look-back (the next one then clears both arrays)
+    DevBuf enc_lb, enc_tk;
+    size_t enc_lb_cap = 0, enc_tk_cap = 0;
+    uint32_t enc_epoch = 0;
+    bool enc_lb_dirty = false;
     hipEvent_t scratch_done = nullptr;
     // stream of the host-pointer entry (kvexp_hip_attention_decode_host): its
     // copies and kernels wait for nothing outside this context
@@ -218,6 +233,34 @@ void grow(kvexp_hip_ctx *ctx, DevBuf &buf, size_t &cap, size_t need) {
     buf = std::move(nb);
     cap = need;
 }
+
+// The one-pass encoder's look-back state for a launch of `blocks` blocks
+// over `jobs` containers (an entry per block, a ticket counter per job):
+// grown on demand; the entries cleared (by the launcher, with a kernel) when
+// new and when the launch epoch wraps, so that no entry left by an earlier
+// launch carries the epoch of a later one; the counters when new (each
+// launch leaves them at 0) and after a launch reported a broken look-back.
+kvexp_dev::EncLookback lookback_for(kvexp_hip_ctx *ctx, int jobs, int blocks) {
+    size_t clear = 0, clear_tk = 0;
+    if (size_t(blocks) * sizeof(uint64_t) > ctx->enc_lb_cap) {
+        grow(ctx, ctx->enc_lb, ctx->enc_lb_cap, size_t(blocks) * sizeof(uint64_t));
+        clear = ctx->enc_lb_cap / sizeof(uint64_t);
+    }
+    if (size_t(jobs) * sizeof(uint32_t) > ctx->enc_tk_cap) {
+        grow(ctx, ctx->enc_tk, ctx->enc_tk_cap, size_t(jobs) * sizeof(uint32_t));
+        clear_tk = ctx->enc_tk_cap / sizeof(uint32_t);
+    }
+    if (++ctx->enc_epoch > 0xFFFFu || ctx->enc_lb_dirty) {
+        ctx->enc_epoch = 1;
+        clear = ctx->enc_lb_cap / sizeof(uint64_t);
+        if (ctx->enc_lb_dirty) clear_tk = ctx->enc_tk_cap / sizeof(uint32_t);
+        ctx->enc_lb_dirty = false;
+    }
+    return kvexp_dev::EncLookback{ctx->enc_lb.as<uint64_t>(), ctx->enc_tk.as<uint32_t>(), ctx->enc_epoch, clear,
+                                  clear_tk};
+}
+
+bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 // Orders work about to be queued on `s` that writes the context's scratch
 // after the last work that used it (which may be on another stream).
@@ -450,8 +493,11 @@ int kvexp_hip_encode(kvexp_hip_ctx *ctx, const uint16_t *d_kv, int seq, int dim,
         DeviceGuard g(ctx->device);
         hipStream_t s = static_cast<hipStream_t>(stream);
         const int nb = kvexp_hip_block_count(seq, bt);
-        grow(ctx, ctx->enc_meta, ctx->enc_meta_cap, size_t(nb) * sizeof(EncBlockMeta));
-        grow(ctx, ctx->enc_bases, ctx->enc_bases_cap, size_t(nb) * 3u * size_t(dim));
+        const bool fused = kvexp_launch::encode_fused_supported(dim, bt) && aligned16(d_kv);
+        if (!fused) {
+            grow(ctx, ctx->enc_meta, ctx->enc_meta_cap, size_t(nb) * sizeof(EncBlockMeta));
+            grow(ctx, ctx->enc_bases, ctx->enc_bases_cap, size_t(nb) * 3u * size_t(dim));
+        }
         int64_t *offs = d_offsets;
         int32_t *first = d_first_token;
         if (offs == nullptr || first == nullptr) {
@@ -465,10 +511,12 @@ int kvexp_hip_encode(kvexp_hip_ctx *ctx, const uint16_t *d_kv, int seq, int dim,
             if (offs == nullptr) offs = ctx->enc_off.as<int64_t>();
             if (first == nullptr) first = ctx->enc_first.as<int32_t>();
         }
+        kvexp_dev::EncLookback lb{};
+        if (fused) lb = lookback_for(ctx, 1, nb);
         scratch_acquire(ctx, s);
         HIPX(kvexp_launch::encode(d_kv, seq, dim, bt, nb, ctx->enc_meta.as<EncBlockMeta>(),
                                   ctx->enc_bases.as<uint8_t>(), offs, first, d_out, ctx->status.as<uint32_t>(), s,
-                                  false, 0, ctx->enc_modes));
+                                  false, 0, ctx->enc_modes, fused ? &lb : nullptr));
         scratch_used(ctx, s);
         if (bytes_out != nullptr) {
             int64_t total = 0;
@@ -479,12 +527,44 @@ int kvexp_hip_encode(kvexp_hip_ctx *ctx, const uint16_t *d_kv, int seq, int dim,
             if (st != 0u) {
                 HIPX(hipMemsetAsync(ctx->status.p, 0, sizeof(uint32_t), s));
                 HIPX(hipStreamSynchronize(s));
-                fail(KVEXP_HIP_LOGIC_ERROR, "escape count drifted from the size model");
+                if (st & kvexp_dev::kStLookback) ctx->enc_lb_dirty = true;
+        fail(KVEXP_HIP_LOGIC_ERROR, encoder_status_message(st));
             }
             *bytes_out = size_t(total);
         }
     });
 }
+
+// Epochs of the no-allocation encoder's look-back words in the per-device
+// static array. The whole array is cleared before the first one-pass call on
+// a device, when the epoch wraps, and after a three-launch call wrote other
+// data over the words.
+namespace {
+std::mutex g_noalloc_mu;
+uint32_t g_noalloc_epoch[64] = {};
+bool g_noalloc_dirty[64] = {};
+
+// Scratch layout of a one-pass call: the ticket counter in the first 256
+// bytes, then the look-back entries.
+kvexp_dev::EncLookback noalloc_lookback(int device, uint8_t *scratch) {
+    std::lock_guard<std::mutex> lock(g_noalloc_mu);
+    const int d = device & 63;
+    size_t clear = 0, clear_tk = 0;
+    if (g_noalloc_epoch[d] == 0 || g_noalloc_epoch[d] >= 0xFFFFu || g_noalloc_dirty[d]) {
+        g_noalloc_epoch[d] = 0;
+        clear = (kvexp_dev::kNoAllocScratchBytes - 256u) / sizeof(uint64_t);
+        clear_tk = 1;
+    }
+    g_noalloc_dirty[d] = false;
+    return kvexp_dev::EncLookback{reinterpret_cast<uint64_t *>(scratch + 256), reinterpret_cast<uint32_t *>(scratch),
+                                  ++g_noalloc_epoch[d], clear, clear_tk};
+}
+
+void noalloc_mark_dirty(int device) {
+    std::lock_guard<std::mutex> lock(g_noalloc_mu);
+    g_noalloc_dirty[device & 63] = true;
+}
+} // namespace
 
 // kvexp_hip_encode with its scratch (block metadata and base-exponent
 // candidates) in the library's per-device static array instead of context
@@ -510,8 +590,11 @@ int kvexp_hip_encode_noalloc(kvexp_hip_ctx *ctx, const uint16_t *d_kv, int seq, 
             fail(KVEXP_HIP_CAPACITY, "kvexp_hip_encode_noalloc: capacity below kvexp_hip_encode_bound");
         const int nb = kvexp_hip_block_count(seq, bt);
         auto up = [](size_t n) { return (n + 255u) & ~size_t(255); };
-        const size_t meta_bytes = up(size_t(nb) * sizeof(EncBlockMeta));
-        const size_t base_bytes = up(size_t(nb) * 3u * size_t(dim));
+        // one pass: a look-back word per block and the ticket; else block
+        // metadata and base-exponent candidates
+        const bool fused = kvexp_launch::encode_fused_supported(dim, bt) && aligned16(d_kv);
+        const size_t meta_bytes = fused ? 256u + up(size_t(nb) * sizeof(uint64_t)) : up(size_t(nb) * sizeof(EncBlockMeta));
+        const size_t base_bytes = fused ? 0 : up(size_t(nb) * 3u * size_t(dim));
         const size_t need = meta_bytes + base_bytes + 256u; // + a status word when d_status is NULL
         if (need > kvexp_dev::kNoAllocScratchBytes)
             fail(KVEXP_HIP_CAPACITY, "kvexp_hip_encode_noalloc: " + std::to_string(nb) + " blocks of head_dim " +
@@ -522,9 +605,12 @@ int kvexp_hip_encode_noalloc(kvexp_hip_ctx *ctx, const uint16_t *d_kv, int seq, 
         if (sp == nullptr) fail(KVEXP_HIP_LOGIC_ERROR, "kvexp_hip_encode_noalloc: scratch not set up on this device");
         DeviceGuard g(ctx->device);
         uint32_t *st = d_status != nullptr ? d_status : reinterpret_cast<uint32_t *>(sp + meta_bytes + base_bytes);
+        kvexp_dev::EncLookback lb{};
+        if (fused) lb = noalloc_lookback(ctx->device, sp);
+        else noalloc_mark_dirty(ctx->device);
         HIPX(kvexp_launch::encode(d_kv, seq, dim, bt, nb, reinterpret_cast<EncBlockMeta *>(sp), sp + meta_bytes,
                                   d_offsets, d_first_token, d_out, st, static_cast<hipStream_t>(stream), false, 0,
-                                  ctx->enc_modes));
+                                  ctx->enc_modes, fused ? &lb : nullptr));
     });
 }
 
@@ -593,15 +679,31 @@ void run_append(kvexp_hip_ctx *ctx, const kvexp_hip_append_job *jobs, int n_jobs
     if (dj.empty()) return;
     // every job encodes at most one block (a decode step): one fused launch
     const bool one_block = std::all_of(dj.begin(), dj.end(), [](const AppendJobDev &j) { return j.nb <= 1; });
-    grow(ctx, ctx->enc_meta, ctx->enc_meta_cap, size_t(std::max(blocks, 1)) * sizeof(EncBlockMeta));
-    grow(ctx, ctx->enc_bases, ctx->enc_bases_cap, size_t(std::max(blocks, 1)) * 3u * size_t(dim));
+    // several blocks: one pass when the shape fits it and every source is
+    // 16-byte aligned (the tails are allocated so; the new tokens' rows are
+    // then aligned too, since dim % 8 == 0)
+    int max_nb = 0;
+    for (const AppendJobDev &j : dj) max_nb = std::max(max_nb, j.nb);
+    const bool fused = !one_block && kvexp_launch::encode_fused_supported(dim, bt) && dj.size() <= 65535u &&
+                       std::all_of(dj.begin(), dj.end(), [](const AppendJobDev &j) {
+                           return aligned16(j.src) && aligned16(j.tail);
+                       });
+    if (!fused) {
+        grow(ctx, ctx->enc_meta, ctx->enc_meta_cap, size_t(std::max(blocks, 1)) * sizeof(EncBlockMeta));
+        grow(ctx, ctx->enc_bases, ctx->enc_bases_cap, size_t(std::max(blocks, 1)) * 3u * size_t(dim));
+    }
     grow(ctx, ctx->app_jobs, ctx->app_jobs_cap, dj.size() * sizeof(AppendJobDev));
+    kvexp_dev::EncLookback lb{};
+    if (fused) lb = lookback_for(ctx, int(dj.size()), blocks);
     scratch_acquire(ctx, s);
-    // pageable source: the runtime has consumed it when the call returns
+    // pageable source: the runtime has consumed it when the call returns (a
+    // copy from pinned memory measured slower in the stream: 433 against
+    // 342 us per c2 prefill call)
     HIPX(hipMemcpyAsync(ctx->app_jobs.p, dj.data(), dj.size() * sizeof(AppendJobDev), hipMemcpyHostToDevice, s));
     HIPX(kvexp_launch::append(ctx->app_jobs.as<AppendJobDev>(), int(dj.size()), blocks, dim, bt,
                               ctx->enc_meta.as<EncBlockMeta>(), ctx->enc_bases.as<uint8_t>(),
-                              ctx->status.as<uint32_t>(), s, one_block, ctx->enc_modes));
+                              ctx->status.as<uint32_t>(), s, one_block, ctx->enc_modes, fused ? &lb : nullptr,
+                              max_nb));
     scratch_used(ctx, s);
 }
 
@@ -612,7 +714,8 @@ void check_encoder_status(kvexp_hip_ctx *ctx, hipStream_t s) {
     if (st != 0u) {
         HIPX(hipMemsetAsync(ctx->status.p, 0, sizeof(uint32_t), s));
         HIPX(hipStreamSynchronize(s));
-        fail(KVEXP_HIP_LOGIC_ERROR, "escape count drifted from the size model");
+        if (st & kvexp_dev::kStLookback) ctx->enc_lb_dirty = true;
+        fail(KVEXP_HIP_LOGIC_ERROR, encoder_status_message(st));
     }
 }
 

@@ -4,10 +4,12 @@
     python compressed-kv-attention_amd/probes.py coexec         # GPU
     python compressed-kv-attention_amd/probes.py bf16-exact     # GPU
     python compressed-kv-attention_amd/probes.py phase-trace    # GPU
+    python compressed-kv-attention_amd/probes.py encode-trace   # GPU
 
 build        compiles csrc/probes/*.hip into lib/probes/ and a phase-traced
-             copy of the library (attention_wave.hip with KVEXP_PHASE_TRACE,
-             the other objects from build.py) as lib/probes/libkvexp_hip_trace.so.
+             copy of the library (attention_wave.hip and codec_kernels.hip with
+             KVEXP_PHASE_TRACE, the other objects from build.py) as
+             lib/probes/libkvexp_hip_trace.so.
 coexec       cycles per wave-iteration of MFMA and vector-ALU instruction mixes
              at 2 and 4 waves per SIMD (mfma_valu_coexec.hip).
 bf16-exact   whether a BF16 4x4x4 MFMA with one live K slot equals fmaf on
@@ -15,6 +17,8 @@ bf16-exact   whether a BF16 4x4x4 MFMA with one live K slot equals fmaf on
 phase-trace  c2 (48 KV heads x 7 queries, head_dim 64, 32K tokens, 64
              splits) through the traced library: cycles per wave in each
              phase of the chunk loop.
+encode-trace the c2 prefill through the traced library: cycles per block in
+             each phase of the one-pass encoder.
 """
 from __future__ import annotations
 
@@ -45,15 +49,17 @@ def build() -> None:
         _run([hipcc, *FLAGS, os.path.join(HERE, "csrc", "probes", name + ".hip"), "-o",
               os.path.join(PROBE_DIR, name)])
     inc = ["-I" + os.path.join(os.path.dirname(HERE), "include"), "-I" + os.path.join(HERE, "csrc", "hip")]
-    obj = os.path.join(PROBE_DIR, "attention_wave_trace.o")
-    _run([hipcc, *FLAGS, "-fPIC", "-DKVEXP_PHASE_TRACE", *inc, "-x", "hip", "-c",
-          os.path.join(HERE, "csrc", "hip", "attention_wave.hip"), "-o", obj])
-    others = [os.path.join(lib_build.OBJ_DIR, n + ".o") for n in
-              ("codec_kernels.hip", "attention_kernels.hip", "kvexp_hip_api.cpp")]
+    traced = []
+    for name in ("attention_wave", "codec_kernels"):
+        obj = os.path.join(PROBE_DIR, name + "_trace.o")
+        _run([hipcc, *FLAGS, "-fPIC", "-DKVEXP_PHASE_TRACE", *inc, "-x", "hip", "-c",
+              os.path.join(HERE, "csrc", "hip", name + ".hip"), "-o", obj])
+        traced.append(obj)
+    others = [os.path.join(lib_build.OBJ_DIR, n + ".o") for n in ("attention_kernels.hip", "kvexp_hip_api.cpp")]
     for o in others:
         if not os.path.exists(o):
             raise SystemExit(f"{o} missing: run compressed-kv-attention_amd/build.py first")
-    _run([hipcc, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", TRACE_LIB, *others, obj])
+    _run([hipcc, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", TRACE_LIB, *others, *traced])
 
 
 def coexec() -> None:
@@ -207,8 +213,64 @@ def phase_trace() -> None:
     print(f"  {'outside the chunk loop':32s} {(life - ph.sum(1)).mean():9.0f} cycles/wave")
 
 
+def encode_trace() -> None:
+    """The c2 prefill (96 containers from empty to 32,768 tokens in one
+    kvexp_hip_append_batch call: 24,576 blocks) through the traced library:
+    cycles per block in each phase of the one-pass encoder."""
+    import ctypes as C
+
+    import numpy as np
+
+    os.environ["KVEXP_HIP_LIBRARY"] = TRACE_LIB
+    sys.path.insert(0, HERE)
+    import torch
+
+    import kvexp_amd
+    from kvexp_amd import synth
+
+    L = kvexp_amd.lib()
+    cfg = synth.CONFIGS["c2"]
+    S, D, BT = cfg["seq"], cfg["dim"], cfg["block"]
+    ctx = kvexp_amd.Context(0)
+    dev = torch.device("cuda:0")
+    src = []
+    for layer in range(cfg["layers"]):
+        for h in range(cfg["kv_heads"]):
+            for x in synth.head_kv("c2", S, 0, layer, h):
+                src.append(torch.from_numpy(x.view(np.int16)).to(dev))
+    caches = [ctx.cache(D, S, BT) for _ in src]
+    for _ in range(5):
+        for c in caches:
+            c.seq = 0
+        ctx.append_batch(caches, src, S)
+    torch.cuda.synchronize()
+    nb = len(src) * (S // BT)
+    buf = np.zeros(32768 * 12, dtype=np.uint64)
+    L.kvexp_hip_encode_trace_read.argtypes = [C.c_void_p, C.c_size_t]
+    kvexp_amd.check(L.kvexp_hip_encode_trace_read(buf.ctypes.data_as(C.c_void_p), buf.size))
+    t = buf.reshape(32768, 12)[:nb].astype(np.int64)
+    life = t[:, 8] - t[:, 0]
+    names = ["job + ticket", "(none)", "tokens arrive", "histograms", "window bases + mode", "codes + escape ranks",
+             "look-back", "stores issued"]
+    print(f"c2 prefill: {nb} blocks; block life mean {life.mean():.0f} cycles "
+          f"(min {life.min()}, max {life.max()})")
+    for i, n in enumerate(names):
+        d = t[:, i + 1] - t[:, i]
+        print(f"  {n:22s} {d.mean():8.0f} cycles/block ({100 * d.mean() / life.mean():5.1f} %), "
+              f"p50 {np.percentile(d, 50):7.0f}, p99 {np.percentile(d, 99):7.0f}")
+    polls = t[:, 9]
+    print(f"  look-back waits: {np.mean(polls > 0) * 100:.1f} % of blocks polled again; mean {polls.mean():.2f}, "
+          f"max {polls.max()}")
+    blocks_per_job = S // BT
+    b = np.arange(nb) % blocks_per_job
+    same = np.mean(t[:, 11] == b)
+    near = np.mean(np.abs(t[:, 11] - b) <= 8)
+    print(f"  ticket equals blockIdx.x for {same * 100:.1f} % of blocks ({near * 100:.1f} % within 8)")
+
+
 if __name__ == "__main__":
-    cmds = {"build": build, "coexec": coexec, "bf16-exact": bf16_exact, "phase-trace": phase_trace}
+    cmds = {"build": build, "coexec": coexec, "bf16-exact": bf16_exact, "phase-trace": phase_trace,
+            "encode-trace": encode_trace}
     if len(sys.argv) != 2 or sys.argv[1] not in cmds:
         raise SystemExit(__doc__)
     cmds[sys.argv[1]]()

@@ -125,9 +125,12 @@ int kvexp_hip_encode(kvexp_hip_ctx *ctx, const uint16_t *d_kv, int seq, int dim,
  * counterpart in the reference. It allocates nothing and does not
  * synchronise: its scratch is a static device array of
  * KVEXP_HIP_NOALLOC_SCRATCH_BYTES per GPU (looked up when a context is
- * created on that GPU), so n_blocks * (16 + 3 * dim) bytes (each part rounded
- * up to 256) plus 256 must fit in it, else KVEXP_HIP_CAPACITY; about 20,000
- * blocks at head_dim 64. The block index is an output here: d_offsets and
+ * created on that GPU), which must hold 256 + 8 * n_blocks bytes (rounded up
+ * to 256) plus 256 where the one-pass encoder runs (head_dim % 8 == 0,
+ * block_tokens * dim <= 16384, d_kv 16-byte aligned: about 520,000 blocks),
+ * else n_blocks * (16 + 3 * dim) bytes (each part rounded up to 256) plus
+ * 256 (about 20,000 blocks at head_dim 64); larger inputs are refused with
+ * KVEXP_HIP_CAPACITY. The block index is an output here: d_offsets and
  * d_first_token (n_blocks + 1 entries) are required; the container size is
  * d_offsets[n_blocks]. When d_status is not NULL, a nonzero value is OR-ed
  * into it if the encoder's size model drifted (it is never cleared). All

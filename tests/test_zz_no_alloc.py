@@ -3,6 +3,7 @@ its scratch is the library's static per-GPU device array) called through the
 C ABI, checked byte for byte against kvexp_hip_encode on the same inputs:
 the container, its block index and the status word, on calls in a row whose
 later inputs are smaller (the scratch keeps the previous call's contents), on
+one-pass calls after a three-launch call, on
 the 3-bit encoder modes, and the oracle's encode_bf16 for the first call.
 Inputs too large for the scratch are refused before any GPU work."""
 import ctypes as C
@@ -59,8 +60,11 @@ def test_noalloc_encode_equals_encode(ctx, oracle, modes):
     rng = np.random.default_rng(77)
     ctx.set_encoder_modes(kvexp_amd.MODES_REFERENCE | (kvexp_amd.MODE_3BIT if modes == "3bit" else 0))
     try:
-        # larger first, then smaller: the second call runs on the first's leftovers
-        cases = [(20000, 64, 128, True), (1234, 64, 128, False), (3001, 128, 100, True), (5, 256, 255, False)]
+        # larger first, then smaller: the second call runs on the first's leftovers;
+        # the last call is one pass again after a three-launch call (head_dim 256,
+        # 255-token blocks) wrote its metadata over the one-pass look-back words
+        cases = [(20000, 64, 128, True), (1234, 64, 128, False), (3001, 128, 100, True), (5, 256, 255, False),
+                 (700, 64, 128, True)]
         for i, (seq, dim, block, with_status) in enumerate(cases):
             say("encode_noalloc", modes, seq, dim, block)
             kv = random_kv(rng, seq, dim)
