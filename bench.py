@@ -36,14 +36,16 @@ container in one call, GB/s of BF16 input) with its HBM roofline, and the
 reference's encode_bf16 on the host as the CPU baseline. Containers are
 checked byte for byte against kvexp_hip_encode of the same tokens.
 
---config c1 | c3 | c4 measures the other configurations of BASELINE.json
+--config c1 | c3 | c4 | c5 measures the other configurations of BASELINE.json
 (parity cases, not the quoted line), one JSON line each: c1 (one KV head,
 seq 8192, one query; L2-resident, reported in µs), c3 (the ragged batch:
-32 sequences x 48 KV heads, split count from kvexp_hip_suggest_splits_batch)
-and c4 (256 KV heads x seq 131072, head_dim 128, 4 queries; K and V generated
+32 sequences x 48 KV heads, split count from kvexp_hip_suggest_splits_batch),
+c4 (256 KV heads x seq 131072, head_dim 128, 4 queries; K and V generated
 on the GPU with the config's distributions, torch's RNG, since the host
-generator would take minutes). c1 and c3 use the host generator
-(kvexp_amd/synth.py). XKV is checked bit for bit against raw before timing.
+generator would take minutes) and c5 (batch 4 x 8 KV heads x seq 100003,
+head_dim 256, 255-token blocks, 8 queries). c1, c3 and c5 use the host
+generator (kvexp_amd/synth.py). XKV is checked bit for bit against raw
+before timing; each line carries the split kernel's HBM roofline.
 
 --workload dump runs the reference bench's model scope on a real KV dump
 (KVD1 + QSN1 files written by the reference's python/dump_kv.py): every
@@ -504,7 +506,7 @@ def issue_roofline(tokens: int, kernel_us: float, three_bit: bool):
 
 
 def bench_config(a, torch, np, kvexp_amd, synth) -> int:
-    """--config c1 / c3 / c4 (see the module docstring)."""
+    """--config c1 / c3 / c4 / c5 (see the module docstring)."""
     name = a.config
     cfg = synth.CONFIGS[name]
     G, D, BT = cfg["group"], cfg["dim"], cfg["block"]
@@ -570,10 +572,21 @@ def bench_config(a, torch, np, kvexp_amd, synth) -> int:
         return e0.elapsed_time(e1) / a.steps
 
     ms_x, ms_r = timed(px), timed(pr)
+    # the split kernel alone (HIP events on its stream around each launch)
+    px.timing(True)
+    timed(px)
+    kern_ms, kern_runs = px.kernel_time()
+    px.timing(False)
+    kern_avg_ms = kern_ms / max(1, kern_runs)
     px.close()
     pr.close()
     gbps = container / (ms_x * 1e-3) / 1e9
-    log(f"{name}: xkv {ms_x * 1e3:.1f} us/step ({gbps:.0f} GB/s of containers), raw {ms_r * 1e3:.1f} us/step")
+    # algorithmic bytes of one split-kernel launch: every container byte, Q
+    # (BF16) and the output (FP32) once
+    algo = container + n_heads * G * D * 2 + n_heads * G * D * 4
+    achieved = algo / (kern_avg_ms * 1e-3) / 1e9
+    log(f"{name}: xkv {ms_x * 1e3:.1f} us/step ({gbps:.0f} GB/s of containers; split kernel "
+        f"{kern_avg_ms * 1e3:.1f} us = {achieved:.0f} GB/s), raw {ms_r * 1e3:.1f} us/step")
     print(json.dumps({
         "metric": f"decode-step µs + achieved HBM GB/s, BASELINE config {name} (parity case, not the quoted line)",
         "value": round(gbps, 2), "unit": "GB/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
@@ -583,7 +596,12 @@ def bench_config(a, torch, np, kvexp_amd, synth) -> int:
         "config": {"workload": name, "kv_heads": n_heads, "group": G, "dim": D, "block": BT,
                    "tokens": sum(seqs), "max_seq": max(seqs), "splits_per_head": splits},
         "pct_hbm_peak": round(100.0 * gbps / HBM_PEAK_GBPS, 2), "container_bytes": container,
-        "tight_bytes": tight, "raw_us_per_step": round(ms_r * 1e3, 2), "xkv_bit_equal_raw": same,
+        "tight_bytes": tight, "raw_us_per_step": round(ms_r * 1e3, 2), "xkv_over_raw": round(ms_x / ms_r, 4),
+        "xkv_bit_equal_raw": same,
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "kernel": f"attn_wave_kernel<{G}, {D}, true, 0>", "kernel_us": round(kern_avg_ms * 1e3, 2),
+                     "algorithmic_bytes": algo},
     }), flush=True)
     return 0 if same else 1
 
@@ -668,10 +686,10 @@ def main() -> int:
         return bench_append(a, torch, np, kvexp_amd, synth)
     if a.workload == "dump":
         return bench_dump(a, torch, np, kvexp_amd)
-    if a.config in ("c1", "c3", "c4"):
+    if a.config in ("c1", "c3", "c4", "c5"):
         return bench_config(a, torch, np, kvexp_amd, synth)
     if a.config != "c2":
-        raise SystemExit("--config takes c1, c2 (the quoted line), c3 or c4 (c5 is a correctness case)")
+        raise SystemExit("--config takes c1, c2 (the quoted line), c3, c4 or c5")
     cfg = synth.CONFIGS["c2"]
     L, KV, G, D, S, BT = cfg["layers"], cfg["kv_heads"], cfg["group"], cfg["dim"], cfg["seq"], cfg["block"]
     H = L * KV

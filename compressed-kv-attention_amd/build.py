@@ -41,10 +41,12 @@ SOURCES = [
     "csrc/hip/codec_kernels.hip",
     "csrc/hip/attention_kernels.hip",
     "csrc/hip/attention_wave.hip",
+    "csrc/hip/attention_wave256.hip",
     "csrc/host/kvexp_hip_api.cpp",
 ]
 CXX_SOURCES = ["csrc/host/kvexp_cpp_api.cpp"]
 HEADERS = [
+    "csrc/hip/attention_wave.h",
     "csrc/hip/kvexp_device.h",
     "csrc/hip/kvexp_expf.h",
     "csrc/hip/kvexp_types.h",

@@ -811,7 +811,7 @@ int suggest_core(const kvexp_hip_ctx *ctx, int64_t total_tokens, int max_seq, in
     if (ctx == nullptr || total_tokens <= 0 || max_seq <= 0 || split_tokens <= 0) return 1;
     const int tiles = (max_seq + split_tokens - 1) / split_tokens;
     const int g = std::min(std::max(1, n_q), kMaxQPerLaunch);
-    const int per_simd = dim == 64 && g < 8 ? 3 : 2; // the wave kernel's occupancy (kWaveOcc)
+    const int per_simd = dim == 256 ? 1 : (dim == 64 && g < 8 ? 3 : 2); // the wave kernel's occupancy (kWaveOcc)
     (void)order;
     const int64_t groups = (std::max(1, n_q) + kMaxQPerLaunch - 1) / kMaxQPerLaunch; // device heads per head
     const int64_t slots = int64_t(4) * per_simd * std::max(1, ctx->cu_count);

@@ -55,7 +55,8 @@ def build() -> None:
         _run([hipcc, *FLAGS, "-fPIC", "-DKVEXP_PHASE_TRACE", *inc, "-x", "hip", "-c",
               os.path.join(HERE, "csrc", "hip", name + ".hip"), "-o", obj])
         traced.append(obj)
-    others = [os.path.join(lib_build.OBJ_DIR, n + ".o") for n in ("attention_kernels.hip", "kvexp_hip_api.cpp")]
+    others = [os.path.join(lib_build.OBJ_DIR, n + ".o")
+              for n in ("attention_kernels.hip", "attention_wave256.hip", "kvexp_hip_api.cpp")]
     for o in others:
         if not os.path.exists(o):
             raise SystemExit(f"{o} missing: run compressed-kv-attention_amd/build.py first")

@@ -164,9 +164,9 @@ def _max_block_escapes(oracle, blob, dim, seq):
 
 
 @pytest.mark.parametrize("backend", ["scalar", "avx512"])
-@pytest.mark.parametrize("dim", [64, 128])
+@pytest.mark.parametrize("dim", [64, 128, 256])
 def test_wave_kernel_groups_and_escapes(ctx, oracle, dim, backend):
-    """The one-wave kernel (head_dim 64 and 128, both score orders) for every
+    """The one-wave kernel (head_dim 64, 128 and 256, both score orders) for every
     query-row count G it is instantiated for, on containers whose blocks
     carry from 0 to several hundred escapes (blocks with more than 64 read
     the escape index in windows), block sizes that do and do not split into
@@ -214,7 +214,7 @@ def _scaled_blocks(rng, x, block, shifts, special_blocks=0.3):
     return b.reshape(-1)
 
 
-@pytest.mark.parametrize("dim", [64, 128])
+@pytest.mark.parametrize("dim", [64, 128, 256])
 def test_wave_dpbf16_flush_guard(ctx, oracle, dim):
     """AVX-512 BF16 order on the one-wave kernel where VDPBF16PS's flushes
     matter: K blocks scaled by 2^0 .. 2^-90 and query rows by 2^0 .. 2^-50,
