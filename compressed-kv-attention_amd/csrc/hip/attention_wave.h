@@ -3,8 +3,9 @@
 // and 128, the merges, the entry points) and attention_wave256.hip (head_dim
 // 256), compiled in parallel.
 #pragma once
-// gfx950 fused decode attention, head_dim 64 or 128, scalar/AVX2 score
-// order: one wave64 per split, no workgroup barriers on the hot path.
+// gfx950 fused decode attention, head_dim 64, 128 or 256, scalar/AVX2 and
+// AVX-512 BF16 score orders: one wave64 per split, no workgroup barriers on
+// the hot path.
 //
 // A split [tok_begin, tok_end) of one KV head is processed in chunks of up to
 // 64 tokens that never cross a K or V block. Per chunk the wave:
@@ -14,7 +15,7 @@
 //      time with v_perm_b32 / v_lshl_add_u32 / v_bfi_b32 on packed pairs;
 //      escape words are then written over their elements from the plan's
 //      escape records (position and word in one dword; a cursor per tensor:
-//      the window of 256 loaded with the rows starts at the chunk's first
+//      the window of 256 (1,024 at head_dim 256) loaded with the rows starts at the chunk's first
 //      escape, and a chunk is cut short where its escapes would not fit);
 //      raw blocks are copied in chunks of at most 48 rows (the registers of
 //      64 coded rows). Every lane issues the same loads on every path, so
@@ -76,7 +77,7 @@ constexpr int kRawRows = 48;    // rows of a raw block per chunk: 64 lanes x 3D/
 constexpr uint16_t kNegZeroBf16 = 0x8000u; // V of a token past the chunk's end: fma(0, -0, acc) == acc exactly
 constexpr int kSlotQ = 8;       // partial-state slot: m[8], l[8], acc[8][head_dim]
 
-// The kernel's sizes for head_dim D (64 or 128).
+// The kernel's sizes for head_dim D (64, 128 or 256).
 template <int D>
 struct Shape {
     static constexpr int kTileStride = 2 * D + 16;  // bytes per tile row: D BF16 + 16 (conflict-free 16-byte rows)
