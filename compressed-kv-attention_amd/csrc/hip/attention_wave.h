@@ -9,8 +9,10 @@
 //
 // A split [tok_begin, tok_end) of one KV head is processed in chunks of up to
 // 64 tokens that never cross a K or V block. Per chunk the wave:
-//   1. decodes the chunk's K rows (lane = token) from registers loaded one
-//      chunk ahead into a BF16 tile in its own LDS slice: a coded element is
+//   1. decodes the chunk's K rows from registers loaded one chunk ahead (16-
+//      channel pieces, consecutive lanes on consecutive bytes, so every load
+//      instruction reads a few whole cache lines) into a BF16 tile in its own
+//      LDS slice (row t: token t): a coded element is
 //      (sm & 0x80) << 8 | (base + code) << 7 | (sm & 0x7F), built two at a
 //      time with v_perm_b32 / v_lshl_add_u32 / v_bfi_b32 on packed pairs;
 //      escape words are then written over their elements from the plan's
@@ -58,7 +60,8 @@ namespace wave {
 // each phase of the chunk loop, summed over its chunks. A wait is measured
 // by a timestamp taken after an empty asm that reads the loaded register.
 #if defined(KVEXP_PHASE_TRACE)
-constexpr int kTraceWaves = 8192, kTraceWords = 10; // start, end, 7 phases, CU/SE id
+constexpr int kTracePhases = 12;
+constexpr int kTraceWaves = 8192, kTraceWords = kTracePhases + 3; // start, end, the phases, CU/SE id
 static __device__ unsigned long long g_phase_trace[kTraceWaves * kTraceWords];
 #define KVEXP_TRACE_ON(X, O) ((X) && (O) == 0)
 #else
@@ -82,9 +85,8 @@ template <int D>
 struct Shape {
     static constexpr int kTileStride = 2 * D + 16;  // bytes per tile row: D BF16 + 16 (conflict-free 16-byte rows)
     static constexpr int kSlotFloats = kSlotQ * (D + 2);
-    static constexpr int kSmRegs = D / 16;          // 16-byte registers of a row's sign/mantissa bytes
-    static constexpr int kRowRegs = kSmRegs + D / 32; // + its 4-bit codes: what a coded row needs
-    static constexpr int kOctets = D / 8;           // channel octets per row
+    static constexpr int kPieces = D / 16;          // 16-channel pieces per row, and pieces per lane per chunk
+    static constexpr int kPieceRows = kChunk / kPieces; // chunk rows between a lane's consecutive pieces
     static constexpr int kHalves = D / 64;          // channels per lane in the fold (lane, lane + 64, ...)
     static constexpr int kWaves = D == 64 ? 4 : (D == 128 ? 2 : 1); // waves per workgroup (LDS: see WaveLds)
     static constexpr int kMergeBatch = 128 / kHalves; // split slots whose loads are in flight together in the merge
@@ -105,7 +107,6 @@ struct alignas(16) WaveLds {
     uint8_t tile[kChunk * Shape<D>::kTileStride];
     float eT[G][kRowPad]; // e of token t, row g (0 past the chunk's end)
     float aT[G][kRowPad]; // alpha of token t, row g (1 where no running maximum moves)
-    uint32_t bp[D / 2];   // base pair words of the block being decoded
 };
 
 template <int G, int D>
@@ -119,6 +120,8 @@ struct alignas(16) WgLds {
 // alignment: gfx950 under ROCm runs in unaligned-access mode.
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4), aligned(2)));
 typedef const __attribute__((address_space(1))) u32x4 g_u32x4;
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2), aligned(2)));
+typedef const __attribute__((address_space(1))) u32x2 g_u32x2;
 typedef const __attribute__((address_space(1))) uint16_t g_u16;
 typedef const __attribute__((address_space(1))) uint32_t g_u32 __attribute__((aligned(2)));
 
@@ -150,7 +153,17 @@ __device__ __forceinline__ uint4 ld16(const uint8_t *p) {
     const u32x4 v = *(g_u32x4 *)(p);
     return make_uint4(v.x, v.y, v.z, v.w);
 }
-__device__ __forceinline__ uint32_t ldu16(const uint8_t *p) { return *(g_u16 *)(p); }
+__device__ __forceinline__ uint2 ld8(const uint8_t *p) {
+    const u32x2 v = *(g_u32x2 *)(p);
+    return make_uint2(v.x, v.y);
+}
+
+// x behind an empty asm: a value the compiler cannot see through, so loads
+// whose addresses use it are not merged with earlier ones.
+__device__ __forceinline__ int opaque(int x) {
+    asm volatile("" : "+v"(x));
+    return x;
+}
 
 // The lane index as an opaque value: the addresses derived from it are then
 // recomputed where they are used (a few instructions) instead of being
@@ -164,7 +177,10 @@ __device__ __forceinline__ int lane_here() {
 // Position of one tensor inside its XKV container. The scalar fields are
 // wave-uniform; erec holds the block's next escape records (component j of
 // erec[i] at lane l: escape ecur + 256 i + 4 l + j, meaningful below
-// n_escape; kEscLoads of them are loaded).
+// n_escape; kEscLoads of them are loaded); base4 holds four of the block's
+// base exponents: bytes 4j .. 4j + 3 of channel column c (channels 16 c ..
+// 16 c + 15, see Rows) at lane c + (D / 16) j, j < 4 (lanes past 4 D / 16
+// repeat them).
 struct Cursor {
     const BlockDesc *d;  // descriptor of the current block (the next one follows it)
     const uint8_t *blk;  // current block's header
@@ -174,7 +190,7 @@ struct Cursor {
     int ecur;            // first escape of the block not yet written into a tile
     int lrows;           // rows requested by the last load_rows (the raw piece layout depends on it)
     uint4 erec[4];
-    uint32_t base2;      // lane p < D / 2: base exponents 2p, 2p + 1 of the block (D = 256: 4p .. 4p + 3)
+    uint32_t base4;
     __device__ int mode() const { return int(meta & 0xFFu); }
     __device__ int ntok() const { return int((meta >> 8) & 0xFFu); }
     __device__ int nesc() const { return int(meta >> 16); }
@@ -194,9 +210,9 @@ __device__ __forceinline__ void enter_block(Cursor &c, const BlockDesc *d, int t
     c.ecur = 0;
 }
 
-// The block's base exponents (lane p < D / 2: pair p; at D = 256 lane p:
-// pairs 2p and 2p + 1, one 4-byte load) and its next kEscWindow escape
-// records (four per lane per 16-byte load). Every lane loads, from an
+// The block's base exponents (see Cursor: one 4-byte load) and its next
+// kEscWindow escape records (four per lane per 16-byte load). Every lane
+// loads, from an
 // always valid address (a records array ends with kEscPad spare records),
 // and the call is made on every chunk whether or not the block changed, so
 // the number of loads in flight never depends on the path taken: the
@@ -205,8 +221,8 @@ __device__ __forceinline__ void enter_block(Cursor &c, const BlockDesc *d, int t
 template <int D>
 __device__ __forceinline__ void block_vectors(Cursor &c) {
     const int lane = lane_here();
-    if constexpr (D == 256) c.base2 = *(g_u32 *)(c.blk + 8 + 4 * lane);
-    else c.base2 = ldu16(c.blk + 8 + 2 * (lane & (D / 2 - 1)));
+    constexpr int NP = Shape<D>::kPieces;
+    c.base4 = *(g_u32 *)(c.blk + 8 + 16 * (lane % NP) + 4 * ((lane / NP) & 3));
 #pragma unroll
     for (int i = 0; i < kEscLoads<D>; ++i) {
         const u32x4 r = *(g_u32x4 *)(c.esc + c.ecur + 256 * i + 4 * lane);
@@ -226,64 +242,80 @@ __device__ __forceinline__ int escape_rows(const Cursor &c, int r0) {
     return max(1, int(last / D) - r0);
 }
 
-// First raw piece held by the lane: a raw chunk of `rows` rows is split into
-// 16-byte pieces (piece p: column p % (D / 8) of row p / (D / 8)), RR
-// consecutive pieces per lane, the last lanes' starts clamped so that every
-// lane's pieces lie inside the rows (lanes past the end repeat the last RR).
+// A chunk's rows in registers, one piece per lane per register pair. Coded
+// block: piece p of the chunk is channels 16 (p % (D / 16)) .. + 16 of its
+// row p / (D / 16), and lane l holds pieces l + 64 k (k < D / 16): one
+// channel column c = l % (D / 16) in rows kPieceRows k + l / (D / 16). s[k]
+// holds the piece's 16 sign/mantissa bytes, c[k] the 8 bytes that end with
+// its last code byte (4-bit: its 8 code bytes; 3-bit: 2 bytes before its 6;
+// 2-bit: 4 bytes before its 4; so no load reaches past the block, and one
+// that starts before its first code byte still lies in the block's
+// sign/mantissa bytes). Consecutive lanes read consecutive bytes: each load
+// covers a few whole cache lines instead of one line per lane. Raw block (at
+// most kRawRows rows): s[k] holds bytes 1024 k + 16 l of the chunk's rows,
+// c[k] bytes 64 D + 512 k + 8 l (rows 32 .. 47), clamped to the last piece of
+// the rows loaded.
 template <int D>
-__device__ __forceinline__ int raw_start(int rows) {
-    constexpr int RR = Shape<D>::kRowRegs;
-    const int np = max(1, min(rows, kRawRows)) * (D / 8); // >= RR
-    return min(RR * lane_here(), np - RR);
-}
+struct Rows {
+    uint4 s[Shape<D>::kPieces];
+    uint2 c[Shape<D>::kPieces];
+};
 
-// Loads rows r0 .. r0 + rows of the cursor's block into R. Coded block: lane
-// = row, its D sign/mantissa bytes and D/2 (4-bit), 3D/8 (3-bit: at D = 64
-// the second register holds bytes 8..23, at D = 128 the fourth repeats the
-// third) or D/4 (2-bit, its registers repeated) code bytes. Raw block (at
-// most kRawRows rows): the lane's RR pieces from raw_start. Lanes past the
-// rows load the last row again. Every load is unconditional, at the block's
-// (uniform) address plus one of two per-lane 32-bit offsets picked by uniform
-// selects, so the registers need no merge before their use.
+// Loads rows r0 .. r0 + rows of the cursor's block into R (layout: Rows).
+// Both register streams (s and c) are runs of equal pieces: register k of
+// lane l reads from x0 + step k + w l (bytes from the block's data), clamped
+// to the stream's last piece e, which lanes whose piece lies past `rows`
+// read again, so no load leaves the rows asked for. The stream parameters
+// are picked once (coded or raw); per register the uniform part
+// min(x0 + step k, e) goes to the load's scalar base and the lane's part is
+// one v_min against e minus it (never negative, so the load takes a 32-bit
+// vector offset). Every load is unconditional, so the registers need no
+// merge before their use.
 template <int D>
-__device__ __forceinline__ void load_rows(Cursor &c, int r0, int rows, uint4 (&R)[Shape<D>::kRowRegs]) {
-    constexpr int SM = Shape<D>::kSmRegs, RR = Shape<D>::kRowRegs;
+__device__ __forceinline__ void load_rows(Cursor &c, int r0, int rows, Rows<D> &R) {
+    constexpr int NP = Shape<D>::kPieces;
     const int mode = c.mode();
     const bool raw = mode == 0;
     c.lrows = rows;
-    // (rows <= 0 only past a plan's zero-token sentinel block: row r0 then)
-    const int r = r0 + max(0, min(lane_here(), rows - 1));
-    const int cbytes = mode * (D / 8); // code bytes per coded row
+    rows = max(rows, 1); // (rows <= 0 only past a plan's zero-token sentinel block: row r0 then)
+    const int lane = lane_here();
     const uint8_t *b = c.blk + 8;
-    // sign/mantissa bytes of the row, then its codes; raw: the lane's pieces
-    const uint32_t oa = raw ? uint32_t(r0 * (2 * D) + 16 * raw_start<D>(rows)) : uint32_t(D + r * D);
-    const uint32_t ob = raw ? oa + 16 * SM : uint32_t(D + c.ntok() * D + r * cbytes);
+    // sign/mantissa stream: 16 bytes per lane, 1,024 per register
+    int s0, se;
+    // code stream: w bytes per lane (8 bytes loaded, ending with the piece's codes), cs per register
+    int c0, ce, cw;
+    if (!raw) {
+        const int cbytes = mode * (D / 8); // code bytes per coded row
+        s0 = D + r0 * D;
+        se = s0 + rows * D - 16;
+        cw = 2 * mode;
+        c0 = D + c.ntok() * D + r0 * cbytes + cw - 8;
+        ce = c0 + (rows * NP - 1) * cw;
+    } else {
+        const int rn = 2 * D * min(rows, kRawRows); // raw bytes loaded: rows [0, 32) in s, [32, 48) in c
+        s0 = r0 * (2 * D);
+        se = s0 + rn - 16;
+        cw = 8;
+        c0 = s0 + 64 * D;
+        ce = s0 + rn - 8;
+    }
+    const int cs = 64 * cw;
+    const uint32_t ls = uint32_t(16 * lane), lc = uint32_t(cw * lane);
 #pragma unroll
-    for (int i = 0; i < SM; ++i) R[i] = ld16(b + oa + 16 * i);
-#pragma unroll
-    for (int i = SM; i < RR; ++i) R[i] = ld16(b + ob + (raw ? 16 * (i - SM) : min(16 * (i - SM), cbytes - 16)));
+    for (int k = 0; k < NP; ++k) {
+        const int bs = min(s0 + 1024 * k, se), bc = min(c0 + cs * k, ce);
+        R.s[k] = ld16(b + bs + min(ls, uint32_t(se - bs)));
+        R.c[k] = ld8(b + bc + min(lc, uint32_t(ce - bc)));
+    }
 }
 
 __device__ __forceinline__ uint32_t comp(const uint4 &v, int i) {
     return i == 0 ? v.x : (i == 1 ? v.y : (i == 2 ? v.z : v.w));
 }
 
-// Base pair words of the cursor's block into LDS: word p = base[2p] << 7 |
-// base[2p+1] << 23 (lane p < D / 2 builds word p from the bytes loaded with
-// the block).
-template <int D>
-__device__ __forceinline__ void base_pairs(const Cursor &c, uint32_t *bp) {
-    const int lane = lane_id();
-    if constexpr (D == 256) {
-        bp[2 * lane] = ((c.base2 & 0xFFu) << 7) | (((c.base2 >> 8) & 0xFFu) << 23);
-        bp[2 * lane + 1] = (((c.base2 >> 16) & 0xFFu) << 7) | ((c.base2 >> 24) << 23);
-    } else {
-        if (lane < D / 2) bp[lane] = ((c.base2 & 0xFFu) << 7) | ((c.base2 >> 8) << 23);
-    }
-}
-
 // One BF16 pair from two sign/mantissa bytes (positions lb, lb+1 of sw), two
-// codes (byte p of lo and hi) and the channel pair's base word.
+// codes (byte p of lo and hi) and the channel pair's base word (bases at bits
+// 14:7 and 30:23).
 __device__ __forceinline__ uint32_t pair4(uint32_t sw, int lb, uint32_t lo, uint32_t hi, int p, uint32_t bpw) {
     const uint32_t code16 = __builtin_amdgcn_perm(hi, lo, 0x0c000c00u | (uint32_t(4 + p) << 16) | uint32_t(p));
     const uint32_t t = (code16 << 7) + bpw; // exponent pair at bits 14:7 / 30:23
@@ -292,28 +324,17 @@ __device__ __forceinline__ uint32_t pair4(uint32_t sw, int lb, uint32_t lo, uint
     return (s & 0x807F807Fu) | (t & ~0x807F807Fu);
 }
 
-// Octet dg (channels 8dg..8dg+7) of a coded row: four BF16 pairs from the
-// row's sign/mantissa bytes in R[0 .. D/16), its codes split into lo (byte p:
-// code 2p) and hi (byte p: code 2p+1), and the channel pairs' base words.
-template <int N>
-__device__ __forceinline__ uint4 octet(const uint4 (&R)[N], int dg, uint32_t lo, uint32_t hi, const uint32_t *bp) {
-    const uint32_t s0 = comp(R[dg >> 1], (dg & 1) * 2);
-    const uint32_t s1 = comp(R[dg >> 1], (dg & 1) * 2 + 1);
-    const uint4 b4 = *reinterpret_cast<const uint4 *>(bp + 4 * dg);
-    uint4 o;
-    o.x = pair4(s0, 0, lo, hi, 0, b4.x);
-    o.y = pair4(s0, 2, lo, hi, 1, b4.y);
-    o.z = pair4(s1, 0, lo, hi, 2, b4.z);
-    o.w = pair4(s1, 2, lo, hi, 3, b4.w);
-    return o;
-}
-
-// Dword i of a 3-bit coded row's code bytes as load_rows placed them in R.
-template <int D, int N>
-__device__ __forceinline__ uint32_t code_dword3(const uint4 (&R)[N], int i) {
-    constexpr int SM = Shape<D>::kSmRegs;
-    if (D == 64 && i >= 4) return comp(R[SM + 1], i - 2); // bytes 16..23 are dwords 2, 3 of the register at byte 8
-    return comp(R[SM + (i >> 2)], i & 3);
+// Octet o (channels 8o .. 8o + 7 of the piece) as four BF16 pairs: the
+// piece's sign/mantissa bytes sm, its codes split into lo (byte p: code 2p of
+// the octet) and hi (byte p: code 2p + 1), and the column's base pair words.
+__device__ __forceinline__ uint4 octet(const uint4 &sm, int o, uint32_t lo, uint32_t hi, const uint32_t (&bp)[8]) {
+    const uint32_t s0 = comp(sm, 2 * o), s1 = comp(sm, 2 * o + 1);
+    uint4 r;
+    r.x = pair4(s0, 0, lo, hi, 0, bp[4 * o]);
+    r.y = pair4(s0, 2, lo, hi, 1, bp[4 * o + 1]);
+    r.z = pair4(s1, 0, lo, hi, 2, bp[4 * o + 2]);
+    r.w = pair4(s1, 2, lo, hi, 3, bp[4 * o + 3]);
+    return r;
 }
 
 // -0 in every channel of the lane's tile row (a token past the chunk's end).
@@ -324,58 +345,79 @@ __device__ __forceinline__ void fill_negzero(uint8_t *row) {
     for (int i = 0; i < D / 8; ++i) reinterpret_cast<uint4 *>(row)[i] = make_uint4(z, z, z, z);
 }
 
-// Decodes the rows held in R (cursor's block mode; see load_rows) into the
-// tile: a coded row into the lane's tile row, raw pieces to their rows. One
-// uniform branch on the mode, then a straight-line body per mode. Lanes
-// >= rows (past the chunk's end) then store -0 in every channel of their row
-// (wanted for V; harmless for K).
+// Decodes the rows held in R (cursor's block mode; layout: Rows) into the
+// tile: each coded piece to its 32 bytes of its tile row (a coded element is
+// (sm & 0x80) << 8 | (base + code) << 7 | (sm & 0x7F)), raw pieces to their
+// rows. One uniform branch on the mode, then a straight-line body per mode.
+// Lanes >= rows (past the chunk's end) then store -0 in every channel of
+// their row (wanted for V; harmless for K).
 template <int D>
-__device__ __forceinline__ void decode_row(const Cursor &c, const uint4 (&R)[Shape<D>::kRowRegs], const uint32_t *bp,
-                                           uint8_t *tile, uint8_t *row, int r0, int rows) {
-    constexpr int SM = Shape<D>::kSmRegs, RR = Shape<D>::kRowRegs;
-    uint4 *dst = reinterpret_cast<uint4 *>(row);
+__device__ __forceinline__ void decode_rows(const Cursor &c, const Rows<D> &R, uint8_t *tile, int rows) {
+    constexpr int NP = Shape<D>::kPieces, RS = Shape<D>::kPieceRows, TS = Shape<D>::kTileStride;
     const int mode = c.mode();
     const int lane = lane_here();
-    if (mode == 4) {
+    if (mode != 0) {
+        // the column's base pair words: pair j (channels 2j, 2j + 1 of the
+        // column) at bits 14:7 and 30:23, from the four lanes that hold its
+        // base exponents
+        uint32_t bp[8];
 #pragma unroll
-        for (int dg = 0; dg < D / 8; ++dg) {
-            const uint32_t cw = comp(R[SM + (dg >> 2)], dg & 3);
-            dst[dg] = octet(R, dg, cw & 0x0F0F0F0Fu, (cw >> 4) & 0x0F0F0F0Fu, bp);
+        for (int m = 0; m < 4; ++m) {
+            const uint32_t w = uint32_t(__builtin_amdgcn_ds_bpermute(4 * (lane % NP + NP * m), int(c.base4)));
+            bp[2 * m] = __builtin_amdgcn_perm(w, w, 0x0c010c00u) << 7;
+            bp[2 * m + 1] = __builtin_amdgcn_perm(w, w, 0x0c030c02u) << 7;
         }
-    } else if (mode == 2) {
+        uint8_t *dst = tile + (lane / NP) * TS + 32 * (lane % NP); // piece 0's place; piece k is RS k rows below
+        if (mode == 4) {
 #pragma unroll
-        for (int dg = 0; dg < D / 8; ++dg) {
-            // 16 two-bit codes per dword; octet dg uses 16 bits. Byte p of
-            // lo/hi: codes 2p and 2p+1 of the octet.
-            const uint32_t cw = comp(R[SM + (dg >> 3)], (dg >> 1) & 3) >> (16 * (dg & 1));
-            const uint32_t lo =
-                (cw & 3u) | (((cw >> 4) & 3u) << 8) | (((cw >> 8) & 3u) << 16) | (((cw >> 12) & 3u) << 24);
-            const uint32_t hi = ((cw >> 2) & 3u) | (((cw >> 6) & 3u) << 8) | (((cw >> 10) & 3u) << 16) |
-                                (((cw >> 14) & 3u) << 24);
-            dst[dg] = octet(R, dg, lo, hi, bp);
-        }
-    } else if (mode == 3) {
-        // 3-bit codes: octet dg's 24 bits are bytes [3dg, 3dg + 3) of the
-        // row's codes; groups of two codes (6 bits) are spread to bytes first
+            for (int k = 0; k < NP; ++k) {
+                const uint32_t c0 = R.c[k].x, c1 = R.c[k].y;
+                uint4 *o = reinterpret_cast<uint4 *>(dst + RS * k * TS);
+                o[0] = octet(R.s[k], 0, c0 & 0x0F0F0F0Fu, (c0 >> 4) & 0x0F0F0F0Fu, bp);
+                o[1] = octet(R.s[k], 1, c1 & 0x0F0F0F0Fu, (c1 >> 4) & 0x0F0F0F0Fu, bp);
+            }
+        } else if (mode == 2) {
 #pragma unroll
-        for (int dg = 0; dg < D / 8; ++dg) {
-            const int q = (3 * dg) >> 2, b = (3 * dg) & 3;
-            const uint32_t w = __builtin_amdgcn_alignbyte(code_dword3<D>(R, q + (b > 1 ? 1 : 0)),
-                                                          code_dword3<D>(R, q), uint32_t(b));
-            const uint32_t x = (w & 0x3Fu) | ((w << 2) & 0x3F00u) | ((w << 4) & 0x3F0000u) | ((w << 6) & 0x3F000000u);
-            dst[dg] = octet(R, dg, x & 0x07070707u, (x >> 3) & 0x07070707u, bp);
+            for (int k = 0; k < NP; ++k) {
+                uint4 *o = reinterpret_cast<uint4 *>(dst + RS * k * TS);
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    // the octet's 16 bits: byte p of lo / hi holds codes 2p / 2p + 1
+                    const uint32_t cw = R.c[k].y >> (16 * h);
+                    const uint32_t lo =
+                        (cw & 3u) | (((cw >> 4) & 3u) << 8) | (((cw >> 8) & 3u) << 16) | (((cw >> 12) & 3u) << 24);
+                    const uint32_t hi = ((cw >> 2) & 3u) | (((cw >> 6) & 3u) << 8) | (((cw >> 10) & 3u) << 16) |
+                                        (((cw >> 14) & 3u) << 24);
+                    o[h] = octet(R.s[k], h, lo, hi, bp);
+                }
+            }
+        } else {
+            // 3-bit codes: octet h's 24 bits are bytes 2 + 3h .. 4 + 3h of
+            // c[k]; groups of two codes (6 bits) are spread to bytes first
+#pragma unroll
+            for (int k = 0; k < NP; ++k) {
+                uint4 *o = reinterpret_cast<uint4 *>(dst + RS * k * TS);
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const uint32_t w = h == 0 ? __builtin_amdgcn_alignbyte(R.c[k].y, R.c[k].x, 2u) : R.c[k].y >> 8;
+                    const uint32_t x =
+                        (w & 0x3Fu) | ((w << 2) & 0x3F00u) | ((w << 4) & 0x3F0000u) | ((w << 6) & 0x3F000000u);
+                    o[h] = octet(R.s[k], h, x & 0x07070707u, (x >> 3) & 0x07070707u, bp);
+                }
+            }
         }
     } else {
-        // raw rows: register i holds piece raw_start + i of the rows loaded
-        // (c.lrows >= rows); pieces of rows >= rows are overwritten below
-        const int p0 = raw_start<D>(c.lrows);
+        // raw rows: the pieces loaded (c.lrows >= rows; clamped pieces repeat
+        // the last one), to their rows; pieces of rows >= rows are overwritten below
+        const int rn = 2 * D * max(1, min(c.lrows, kRawRows));
 #pragma unroll
-        for (int i = 0; i < RR; ++i) {
-            const int p = p0 + i;
-            *reinterpret_cast<uint4 *>(tile + (p / (D / 8)) * Shape<D>::kTileStride + (p % (D / 8)) * 16) = R[i];
+        for (int k = 0; k < NP; ++k) {
+            const int os = min(1024 * k + 16 * lane, rn - 16), oc = min(64 * D + 512 * k + 8 * lane, rn - 8);
+            *reinterpret_cast<uint4 *>(tile + (os / (2 * D)) * TS + os % (2 * D)) = R.s[k];
+            *reinterpret_cast<uint2 *>(tile + (oc / (2 * D)) * TS + oc % (2 * D)) = R.c[k];
         }
     }
-    if (rows < kChunk && lane >= rows) fill_negzero<D>(row);
+    if (rows < kChunk && lane >= rows) fill_negzero<D>(tile + lane * TS);
 }
 
 // ---- AVX-512 BF16 order ------------------------------------------------------
@@ -736,7 +778,7 @@ __device__ __forceinline__ void store_raw(const uint4 (&R)[D / 8], uint8_t *tile
     }
 }
 
-template <bool XKV, int D> struct RegsOf { typedef uint4 T[Shape<D>::kRowRegs]; };
+template <bool XKV, int D> struct RegsOf { typedef Rows<D> T; };
 template <int D> struct RegsOf<false, D> { typedef uint4 T[D / 8]; };
 
 // At D = 64 the XKV instantiations with up to seven query rows are held to
@@ -838,7 +880,7 @@ void attn_wave_kernel(const HeadDev *__restrict__ heads, const WorkItem *__restr
     // win the issue slots and all of a CU's waves finish at about the same
     // time.
     constexpr bool TR = KVEXP_TRACE_ON(XKV, ORDER);
-    unsigned long long ph[7] = {0, 0, 0, 0, 0, 0, 0};
+    unsigned long long ph[12] = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
     const unsigned long long tw0 = TR ? __builtin_readcyclecounter() : 0ull;
     unsigned long long tprev = tw0;
     auto stamp = [&](int i) {
@@ -878,7 +920,7 @@ void attn_wave_kernel(const HeadDev *__restrict__ heads, const WorkItem *__restr
         if (n <= 0) break; // unreachable with plan-checked descriptors (n_tokens > 0)
         const int tn = t + n;
 
-        if constexpr (XKV) after(RK[Shape<D>::kRowRegs - 1].w); // K rows arrived
+        if constexpr (XKV) after(RK.c[Shape<D>::kPieces - 1].y); // K rows arrived
         stamp(0);
         // 1. K rows -> tile (ORDER 1: and whether the chunk needs the flushing
         // score path)
@@ -888,22 +930,18 @@ void attn_wave_kernel(const HeadDev *__restrict__ heads, const WorkItem *__restr
                 if constexpr (ORDER == 1) {
                     // coded exponents are base + code with code < 2^bits: all
                     // >= kmin when no base is below it or wraps
-                    const uint32_t b0 = kc.base2 & 0xFFu, b1 = (kc.base2 >> 8) & 0xFFu;
+                    // (the lanes' four bytes cover every channel; bytes as 16-bit halves)
+                    const uint32_t w = kc.base4;
+                    const u16x2 e = __builtin_bit_cast(u16x2, w & 0x00FF00FFu);
+                    const u16x2 o = __builtin_bit_cast(u16x2, (w >> 8) & 0x00FF00FFu);
+                    const u16x2 bmin = __builtin_elementwise_min(e, o), bmax = __builtin_elementwise_max(e, o);
                     const uint32_t top = 256u - (1u << kc.mode());
-                    uint32_t bmin = min(b0, b1), bmax = max(b0, b1);
-                    if constexpr (D == 256) {
-                        const uint32_t b2 = (kc.base2 >> 16) & 0xFFu, b3 = kc.base2 >> 24;
-                        bmin = min(bmin, min(b2, b3));
-                        bmax = max(bmax, max(b2, b3));
-                    }
-                    flush = __ballot(ln < D / 2 && (bmin < kmin || bmax > top)) != 0;
+                    flush = __ballot(uint32_t(min(bmin.x, bmin.y)) < kmin || uint32_t(max(bmax.x, bmax.y)) > top) != 0;
                 }
-                base_pairs<D>(kc, S.bp);
-                wave_sync();
             } else {
                 flush = ORDER == 1;
             }
-            decode_row<D>(kc, RK, S.bp, S.tile, S.tile + ln * TS, t - kc.t0, n);
+            decode_rows<D>(kc, RK, S.tile, n);
             wave_sync();
             flush |= patch_escapes<D, ORDER == 1>(kc, t - kc.t0, n, S.tile, klow);
         } else {
@@ -942,41 +980,7 @@ void attn_wave_kernel(const HeadDev *__restrict__ heads, const WorkItem *__restr
 
         after(__float_as_uint(s[0]));
         stamp(2); // scores done
-        if constexpr (XKV) after(RV[Shape<D>::kRowRegs - 1].w); // V rows arrived
-        stamp(3);
-        // 3. V rows -> tile; request the next chunk's V and K rows (RK and RV
-        // are then not live across the score and decode registers)
-        if constexpr (XKV) {
-            if (vc.mode() != 0) {
-                base_pairs<D>(vc, S.bp);
-                wave_sync();
-            }
-            decode_row<D>(vc, RV, S.bp, S.tile, S.tile + ln * TS, t - vc.t0, n);
-            wave_sync();
-            patch_escapes<D>(vc, t - vc.t0, n, S.tile);
-            // the loads are issued on every chunk (the last one re-reads its
-            // own final row), K first: the K decode can then wait for its
-            // loads while the V loads stay in flight
-            const int tp = min(tn, wi.tok_end - 1);
-            if (tp >= kc.t1) enter_block(kc, kc.d + 1, kc.t1);
-            block_vectors<D>(kc);
-            load_rows<D>(kc, tp - kc.t0, min(kChunk, min(kc.t1, wi.tok_end) - tp), RK);
-            if (tp >= vc.t1) enter_block(vc, vc.d + 1, vc.t1);
-            block_vectors<D>(vc);
-            load_rows<D>(vc, tp - vc.t0, min(kChunk, min(vc.t1, wi.tok_end) - tp), RV);
-        } else {
-            store_raw<D>(RV, S.tile);
-            if (n < kChunk && ln >= n) fill_negzero<D>(S.tile + ln * TS);
-            {
-                // issued on every chunk (the last one re-reads its final row), K first
-                const int tp = min(tn, wi.tok_end - 1);
-                load_raw<D>(hd.kraw, tp, min(kChunk, wi.tok_end - tp), RK);
-                load_raw<D>(hd.vraw, tp, min(kChunk, wi.tok_end - tp), RV);
-            }
-        }
-
-        stamp(4); // V decoded, next rows requested
-        // 4. softmax coefficients, lane = token: the running maxima by an exact
+        // 3. softmax coefficients, lane = token: the running maxima by an exact
         // DPP prefix maximum (seeded with each row's maximum so far, held in
         // scalar registers), e = exp(s - m) for every token and row, and, for
         // the rows where some token of the chunk moves the maximum,
@@ -989,7 +993,7 @@ void attn_wave_kernel(const HeadDev *__restrict__ heads, const WorkItem *__restr
         for (int g = 0; g < G; ++g) mi[g] = s[g];
         wave_scan_max_rows<G>(mi);
         // row by row, each row's values stored as soon as they are made (few
-        // registers live beside the rows in flight)
+        // registers live beside the V rows in flight)
 #pragma unroll
         for (int g = 0; g < G; ++g) {
             const float m = fmaxf(mi[g], msc[g]);
@@ -1006,7 +1010,43 @@ void attn_wave_kernel(const HeadDev *__restrict__ heads, const WorkItem *__restr
         }
         wave_sync();
 
-        stamp(5); // softmax coefficients in LDS
+        stamp(3); // softmax coefficients in LDS
+        if constexpr (XKV) after(RV.c[Shape<D>::kPieces - 1].y); // V rows arrived
+        stamp(4);
+        // 4. V rows -> tile (the scores are then no longer live); request the
+        // next chunk's K and V rows (RK and RV are then not live across the
+        // score and decode registers)
+        if constexpr (XKV) {
+            decode_rows<D>(vc, RV, S.tile, n);
+            wave_sync();
+            stamp(5); // V rows decoded
+            patch_escapes<D>(vc, t - vc.t0, n, S.tile);
+            stamp(6); // V escapes written
+            // the loads are issued on every chunk (the last one re-reads its
+            // own final row), K first: the K decode can then wait for its
+            // loads while the V loads stay in flight
+            const int tp = min(tn, wi.tok_end - 1);
+            if (tp >= kc.t1) enter_block(kc, kc.d + 1, kc.t1);
+            stamp(7); // next K block entered
+            block_vectors<D>(kc);
+            load_rows<D>(kc, tp - kc.t0, min(kChunk, min(kc.t1, wi.tok_end) - tp), RK);
+            stamp(8); // next K rows requested
+            if (tp >= vc.t1) enter_block(vc, vc.d + 1, vc.t1);
+            stamp(9); // next V block entered
+            block_vectors<D>(vc);
+            load_rows<D>(vc, tp - vc.t0, min(kChunk, min(vc.t1, wi.tok_end) - tp), RV);
+        } else {
+            store_raw<D>(RV, S.tile);
+            if (n < kChunk && ln >= n) fill_negzero<D>(S.tile + ln * TS);
+            {
+                // issued on every chunk (the last one re-reads its final row), K first
+                const int tp = min(tn, wi.tok_end - 1);
+                load_raw<D>(hd.kraw, tp, min(kChunk, wi.tok_end - tp), RK);
+                load_raw<D>(hd.vraw, tp, min(kChunk, wi.tok_end - tp), RV);
+            }
+        }
+
+        stamp(10); // next V rows requested
         // 5. ordered fold, lane = channel, fully unrolled over the chunk
         {
             // e as the A operands: ea[rg][j] at lane 4b + r holds e[4 rg + r][16 j + b]
@@ -1042,7 +1082,7 @@ void attn_wave_kernel(const HeadDev *__restrict__ heads, const WorkItem *__restr
         }
         wave_sync();
         after(__float_as_uint(acc[0][0].x));
-        stamp(6); // fold done
+        stamp(11); // fold done
         t = tn;
     }
 #if defined(KVEXP_PHASE_TRACE)
@@ -1051,8 +1091,8 @@ void attn_wave_kernel(const HeadDev *__restrict__ heads, const WorkItem *__restr
             unsigned long long *o = g_phase_trace + size_t(item) * kTraceWords;
             o[0] = tw0;
             o[1] = __builtin_readcyclecounter();
-            for (int i = 0; i < 7; ++i) o[2 + i] = ph[i];
-            o[9] = (unsigned long long)__smid();
+            for (int i = 0; i < kTracePhases; ++i) o[2 + i] = ph[i];
+            o[kTracePhases + 2] = (unsigned long long)__smid();
         }
     }
 #endif

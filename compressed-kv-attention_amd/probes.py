@@ -3,7 +3,7 @@
     python compressed-kv-attention_amd/probes.py build          # on the CPU, after build.py
     python compressed-kv-attention_amd/probes.py coexec         # GPU
     python compressed-kv-attention_amd/probes.py bf16-exact     # GPU
-    python compressed-kv-attention_amd/probes.py phase-trace    # GPU
+    python compressed-kv-attention_amd/probes.py phase-trace    # GPU (c2; phase-trace-c4: c4)
     python compressed-kv-attention_amd/probes.py encode-trace   # GPU
 
 build        compiles csrc/probes/*.hip into lib/probes/ and a phase-traced
@@ -16,7 +16,8 @@ bf16-exact   whether a BF16 4x4x4 MFMA with one live K slot equals fmaf on
              the widened inputs, by input class (bf16_mfma_exact.hip).
 phase-trace  c2 (48 KV heads x 7 queries, head_dim 64, 32K tokens, 64
              splits) through the traced library: cycles per wave in each
-             phase of the chunk loop.
+             phase of the chunk loop; phase-trace-c4 the same for c4 (256
+             KV heads x 4 queries, head_dim 128, 128K tokens, 8 splits).
 encode-trace the c2 prefill through the traced library: cycles per block in
              each phase of the one-pass encoder.
 """
@@ -168,7 +169,7 @@ def bf16_exact() -> None:
                 print(line, flush=True)
 
 
-def phase_trace() -> None:
+def phase_trace(config: str = "c2") -> None:
     import ctypes as C
 
     import numpy as np
@@ -181,32 +182,46 @@ def phase_trace() -> None:
     from kvexp_amd import synth
 
     L = kvexp_amd.lib()
-    cfg = synth.CONFIGS["c2"]
+    cfg = synth.CONFIGS[config]
     S, D, G, BT = cfg["seq"], cfg["dim"], cfg["group"], cfg["block"]
     ctx = kvexp_amd.Context(0)
     dev = torch.device("cuda:0")
     heads = []
-    for layer in range(24):
-        for h in range(2):
-            k, v = synth.head_kv("c2", S, 0, layer, h)
-            kx = ctx.encode(torch.from_numpy(k.view(np.int16)).to(dev), S, D, BT)
-            vx = ctx.encode(torch.from_numpy(v.view(np.int16)).to(dev), S, D, BT)
-            heads.append(dict(kx=kx, vx=vx, seq=S, splits=64))
-    q = torch.from_numpy(synth.queries("c2", 48).view(np.int16)).to(dev)
+    if config == "c2":
+        splits = 64
+        for layer in range(24):
+            for h in range(2):
+                k, v = synth.head_kv("c2", S, 0, layer, h)
+                kx = ctx.encode(torch.from_numpy(k.view(np.int16)).to(dev), S, D, BT)
+                vx = ctx.encode(torch.from_numpy(v.view(np.int16)).to(dev), S, D, BT)
+                heads.append(dict(kx=kx, vx=vx, seq=S, splits=splits))
+    else:  # c4: K and V from torch's generator on the GPU, as bench.py --config c4
+        splits = 8
+        g = torch.Generator(device=dev)
+        g.manual_seed(cfg["seed"])
+        for _ in range(cfg["layers"] * cfg["kv_heads"]):
+            scale = torch.exp2(torch.rand(D, generator=g, device=dev) * 8 - 5)
+            k = (torch.randn(S, D, generator=g, device=dev) * scale).to(torch.bfloat16).view(torch.int16).reshape(-1)
+            v = (torch.randn(S, D, generator=g, device=dev) * 0.5).to(torch.bfloat16).view(torch.int16).reshape(-1)
+            heads.append(dict(kx=ctx.encode(k, S, D, BT), vx=ctx.encode(v, S, D, BT), seq=S, splits=splits))
+    n_heads = len(heads)
+    q = torch.randn(n_heads * G * D, device=dev).to(torch.bfloat16).view(torch.int16)
     plan = ctx.plan(heads, G, D, BT)
-    for _ in range(100):
+    for _ in range(100 if config == "c2" else 10):
         plan.run(q)
     torch.cuda.synchronize()
-    buf = np.zeros(8192 * 10, dtype=np.uint64)
+    nph = 12
+    buf = np.zeros(8192 * (nph + 3), dtype=np.uint64)
     L.kvexp_hip_phase_trace_read.argtypes = [C.c_void_p, C.c_size_t]
     kvexp_amd.check(L.kvexp_hip_phase_trace_read(buf.ctypes.data_as(C.c_void_p), buf.size))
-    t = buf.reshape(8192, 10)[: 48 * 64].astype(np.int64)
+    t = buf.reshape(8192, nph + 3)[: n_heads * splits].astype(np.int64)
     life = t[:, 1] - t[:, 0]
-    ph = t[:, 2:9]
-    names = ["K rows wait", "K decode + escapes", "scores", "V rows wait", "V decode + escapes + next loads",
-             "softmax coefficients", "fold"]
-    chunks = S // 64 // 64  # chunks per wave
-    print(f"c2, 64 splits: {len(t)} waves of {chunks} chunks; wave life: mean {life.mean():.0f} cycles "
+    ph = t[:, 2:2 + nph]
+    names = ["K rows wait", "K decode + escapes", "scores", "softmax coefficients", "V rows wait", "V decode",
+             "V escapes", "next K block entered", "next K rows requested", "next V block entered",
+             "next V rows requested", "fold"]
+    chunks = S // splits // 64  # chunks per wave
+    print(f"{config}, {splits} splits: {len(t)} waves of {chunks} chunks; wave life: mean {life.mean():.0f} cycles "
           f"(min {life.min()}, max {life.max()})")
     for i, n in enumerate(names):
         print(f"  {n:32s} {ph[:, i].mean():9.0f} cycles/wave ({100 * ph[:, i].mean() / life.mean():5.1f} %), "
@@ -271,7 +286,7 @@ def encode_trace() -> None:
 
 if __name__ == "__main__":
     cmds = {"build": build, "coexec": coexec, "bf16-exact": bf16_exact, "phase-trace": phase_trace,
-            "encode-trace": encode_trace}
+            "phase-trace-c4": lambda: phase_trace("c4"), "encode-trace": encode_trace}
     if len(sys.argv) != 2 or sys.argv[1] not in cmds:
         raise SystemExit(__doc__)
     cmds[sys.argv[1]]()
