@@ -80,6 +80,15 @@ constexpr int kRawRows = 48;    // rows of a raw block per chunk: 64 lanes x 3D/
 constexpr uint16_t kNegZeroBf16 = 0x8000u; // V of a token past the chunk's end: fma(0, -0, acc) == acc exactly
 constexpr int kSlotQ = 8;       // partial-state slot: m[8], l[8], acc[8][head_dim]
 
+// How a chunk's coded rows are loaded (see Rows): whole rows (lane = row) at
+// head_dim 64, where a row's 64 sign/mantissa and 32 code bytes take six
+// 16-byte loads per lane; 16-channel pieces at 128 and 256, where whole rows
+// would put every load instruction on 64 different cache lines. Measured on
+// c2 (head_dim 64), whole rows: 93.7 us per step against 97.7 for pieces; on
+// c4 (head_dim 128), pieces: 2,726 against 3,323 for whole rows.
+template <int D>
+constexpr bool kWholeRows = D == 64;
+
 // The kernel's sizes for head_dim D (64, 128 or 256).
 template <int D>
 struct Shape {
@@ -87,6 +96,8 @@ struct Shape {
     static constexpr int kSlotFloats = kSlotQ * (D + 2);
     static constexpr int kPieces = D / 16;          // 16-channel pieces per row, and pieces per lane per chunk
     static constexpr int kPieceRows = kChunk / kPieces; // chunk rows between a lane's consecutive pieces
+    static constexpr int kSmRegs = D / 16;          // whole rows: 16-byte registers of a row's sign/mantissa bytes
+    static constexpr int kRowRegs = kSmRegs + D / 32; // + its 4-bit codes: what a coded row needs
     static constexpr int kHalves = D / 64;          // channels per lane in the fold (lane, lane + 64, ...)
     static constexpr int kWaves = D == 64 ? 4 : (D == 128 ? 2 : 1); // waves per workgroup (LDS: see WaveLds)
     static constexpr int kMergeBatch = 128 / kHalves; // split slots whose loads are in flight together in the merge
@@ -107,6 +118,7 @@ struct alignas(16) WaveLds {
     uint8_t tile[kChunk * Shape<D>::kTileStride];
     float eT[G][kRowPad]; // e of token t, row g (0 past the chunk's end)
     float aT[G][kRowPad]; // alpha of token t, row g (1 where no running maximum moves)
+    uint32_t bp[kWholeRows<D> ? D / 2 : 1]; // whole rows: base pair words of the block being decoded
 };
 
 template <int G, int D>
@@ -158,13 +170,6 @@ __device__ __forceinline__ uint2 ld8(const uint8_t *p) {
     return make_uint2(v.x, v.y);
 }
 
-// x behind an empty asm: a value the compiler cannot see through, so loads
-// whose addresses use it are not merged with earlier ones.
-__device__ __forceinline__ int opaque(int x) {
-    asm volatile("" : "+v"(x));
-    return x;
-}
-
 // The lane index as an opaque value: the addresses derived from it are then
 // recomputed where they are used (a few instructions) instead of being
 // hoisted out of the chunk loop and held in registers across it.
@@ -177,10 +182,10 @@ __device__ __forceinline__ int lane_here() {
 // Position of one tensor inside its XKV container. The scalar fields are
 // wave-uniform; erec holds the block's next escape records (component j of
 // erec[i] at lane l: escape ecur + 256 i + 4 l + j, meaningful below
-// n_escape; kEscLoads of them are loaded); base4 holds four of the block's
-// base exponents: bytes 4j .. 4j + 3 of channel column c (channels 16 c ..
-// 16 c + 15, see Rows) at lane c + (D / 16) j, j < 4 (lanes past 4 D / 16
-// repeat them).
+// n_escape; kEscLoads of them are loaded); basew holds base exponents of
+// the block: whole rows, lane p < D / 2: base[2p], base[2p + 1]; pieces,
+// bytes 4j .. 4j + 3 of channel column c (channels 16 c .. 16 c + 15, see
+// Rows) at lane c + (D / 16) j, j < 4 (lanes past 4 D / 16 repeat them).
 struct Cursor {
     const BlockDesc *d;  // descriptor of the current block (the next one follows it)
     const uint8_t *blk;  // current block's header
@@ -190,7 +195,7 @@ struct Cursor {
     int ecur;            // first escape of the block not yet written into a tile
     int lrows;           // rows requested by the last load_rows (the raw piece layout depends on it)
     uint4 erec[4];
-    uint32_t base4;
+    uint32_t basew;
     __device__ int mode() const { return int(meta & 0xFFu); }
     __device__ int ntok() const { return int((meta >> 8) & 0xFFu); }
     __device__ int nesc() const { return int(meta >> 16); }
@@ -222,7 +227,8 @@ template <int D>
 __device__ __forceinline__ void block_vectors(Cursor &c) {
     const int lane = lane_here();
     constexpr int NP = Shape<D>::kPieces;
-    c.base4 = *(g_u32 *)(c.blk + 8 + 16 * (lane % NP) + 4 * ((lane / NP) & 3));
+    if constexpr (kWholeRows<D>) c.basew = *(g_u16 *)(c.blk + 8 + 2 * (lane & (D / 2 - 1)));
+    else c.basew = *(g_u32 *)(c.blk + 8 + 16 * (lane % NP) + 4 * ((lane / NP) & 3));
 #pragma unroll
     for (int i = 0; i < kEscLoads<D>; ++i) {
         const u32x4 r = *(g_u32x4 *)(c.esc + c.ecur + 256 * i + 4 * lane);
@@ -242,7 +248,13 @@ __device__ __forceinline__ int escape_rows(const Cursor &c, int r0) {
     return max(1, int(last / D) - r0);
 }
 
-// A chunk's rows in registers, one piece per lane per register pair. Coded
+// A chunk's rows in registers. Whole rows (head_dim 64): lane = row, r[0 ..
+// D/16) its D sign/mantissa bytes, then its D/2 (4-bit), 3D/8 (3-bit: the
+// second code register holds bytes 8 .. 23) or D/4 (2-bit, the register
+// repeated) code bytes; a raw block (at most kRawRows rows) as 16-byte pieces
+// (piece p: column p % (D / 8) of row p / (D / 8)), kRowRegs consecutive ones
+// per lane from raw_start.
+// Pieces (head_dim 128, 256): one piece per lane per register pair. Coded
 // block: piece p of the chunk is channels 16 (p % (D / 16)) .. + 16 of its
 // row p / (D / 16), and lane l holds pieces l + 64 k (k < D / 16): one
 // channel column c = l % (D / 16) in rows kPieceRows k + l / (D / 16). s[k]
@@ -255,14 +267,51 @@ __device__ __forceinline__ int escape_rows(const Cursor &c, int r0) {
 // most kRawRows rows): s[k] holds bytes 1024 k + 16 l of the chunk's rows,
 // c[k] bytes 64 D + 512 k + 8 l (rows 32 .. 47), clamped to the last piece of
 // the rows loaded.
-template <int D>
+template <int D, bool W = kWholeRows<D>>
 struct Rows {
     uint4 s[Shape<D>::kPieces];
     uint2 c[Shape<D>::kPieces];
 };
+template <int D>
+struct Rows<D, true> {
+    uint4 r[Shape<D>::kRowRegs];
+};
 
-// Loads rows r0 .. r0 + rows of the cursor's block into R (layout: Rows).
-// Both register streams (s and c) are runs of equal pieces: register k of
+// Whole rows: the first raw piece held by the lane, the last lanes' starts
+// clamped so that every lane's pieces lie inside the rows (lanes past the end
+// repeat the last kRowRegs).
+template <int D>
+__device__ __forceinline__ int raw_start(int rows) {
+    constexpr int RR = Shape<D>::kRowRegs;
+    const int np = max(1, min(rows, kRawRows)) * (D / 8); // >= RR
+    return min(RR * lane_here(), np - RR);
+}
+
+// Whole rows: loads rows r0 .. r0 + rows of the cursor's block into R
+// (lanes past the rows load the last row again). Every load is
+// unconditional, at the block's (uniform) address plus one of two per-lane
+// 32-bit offsets picked by uniform selects.
+template <int D>
+__device__ __forceinline__ void load_whole_rows(Cursor &c, int r0, int rows, Rows<D, true> &R) {
+    constexpr int SM = Shape<D>::kSmRegs, RR = Shape<D>::kRowRegs;
+    const int mode = c.mode();
+    const bool raw = mode == 0;
+    c.lrows = rows;
+    // (rows <= 0 only past a plan's zero-token sentinel block: row r0 then)
+    const int r = r0 + max(0, min(lane_here(), rows - 1));
+    const int cbytes = mode * (D / 8); // code bytes per coded row
+    const uint8_t *b = c.blk + 8;
+    // sign/mantissa bytes of the row, then its codes; raw: the lane's pieces
+    const uint32_t oa = raw ? uint32_t(r0 * (2 * D) + 16 * raw_start<D>(rows)) : uint32_t(D + r * D);
+    const uint32_t ob = raw ? oa + 16 * SM : uint32_t(D + c.ntok() * D + r * cbytes);
+#pragma unroll
+    for (int i = 0; i < SM; ++i) R.r[i] = ld16(b + oa + 16 * i);
+#pragma unroll
+    for (int i = SM; i < RR; ++i) R.r[i] = ld16(b + ob + (raw ? 16 * (i - SM) : min(16 * (i - SM), cbytes - 16)));
+}
+
+// Pieces: loads rows r0 .. r0 + rows of the cursor's block into R. Both
+// register streams (s and c) are runs of equal pieces: register k of
 // lane l reads from x0 + step k + w l (bytes from the block's data), clamped
 // to the stream's last piece e, which lanes whose piece lies past `rows`
 // read again, so no load leaves the rows asked for. The stream parameters
@@ -272,7 +321,7 @@ struct Rows {
 // vector offset). Every load is unconditional, so the registers need no
 // merge before their use.
 template <int D>
-__device__ __forceinline__ void load_rows(Cursor &c, int r0, int rows, Rows<D> &R) {
+__device__ __forceinline__ void load_pieces(Cursor &c, int r0, int rows, Rows<D, false> &R) {
     constexpr int NP = Shape<D>::kPieces;
     const int mode = c.mode();
     const bool raw = mode == 0;
@@ -309,8 +358,30 @@ __device__ __forceinline__ void load_rows(Cursor &c, int r0, int rows, Rows<D> &
     }
 }
 
+template <int D>
+__device__ __forceinline__ void load_rows(Cursor &c, int r0, int rows, Rows<D> &R) {
+    if constexpr (kWholeRows<D>) load_whole_rows<D>(c, r0, rows, R);
+    else load_pieces<D>(c, r0, rows, R);
+}
+
+// A word that arrives with the last load of load_rows.
+template <int D>
+__device__ __forceinline__ uint32_t last_loaded(const Rows<D> &R) {
+    if constexpr (kWholeRows<D>) return R.r[Shape<D>::kRowRegs - 1].w;
+    else return R.c[Shape<D>::kPieces - 1].y;
+}
+
 __device__ __forceinline__ uint32_t comp(const uint4 &v, int i) {
     return i == 0 ? v.x : (i == 1 ? v.y : (i == 2 ? v.z : v.w));
+}
+
+// Whole rows: base pair words of the cursor's block into LDS, word p =
+// base[2p] << 7 | base[2p+1] << 23 (lane p < D / 2 builds word p from the
+// bytes loaded with the block).
+template <int D>
+__device__ __forceinline__ void base_pairs(const Cursor &c, uint32_t *bp) {
+    const int lane = lane_id();
+    if (lane < D / 2) bp[lane] = ((c.basew & 0xFFu) << 7) | ((c.basew >> 8) << 23);
 }
 
 // One BF16 pair from two sign/mantissa bytes (positions lb, lb+1 of sw), two
@@ -337,6 +408,33 @@ __device__ __forceinline__ uint4 octet(const uint4 &sm, int o, uint32_t lo, uint
     return r;
 }
 
+// Whole rows: octet dg (channels 8dg .. 8dg + 7) of a coded row, four BF16
+// pairs from the row's sign/mantissa bytes in R.r[0 .. D/16), its codes split
+// into lo (byte p: code 2p) and hi (byte p: code 2p + 1), and the channel
+// pairs' base words in LDS.
+template <int D>
+__device__ __forceinline__ uint4 octet_row(const Rows<D, true> &R, int dg, uint32_t lo, uint32_t hi,
+                                           const uint32_t *bp) {
+    const uint32_t s0 = comp(R.r[dg >> 1], (dg & 1) * 2);
+    const uint32_t s1 = comp(R.r[dg >> 1], (dg & 1) * 2 + 1);
+    const uint4 b4 = *reinterpret_cast<const uint4 *>(bp + 4 * dg);
+    uint4 o;
+    o.x = pair4(s0, 0, lo, hi, 0, b4.x);
+    o.y = pair4(s0, 2, lo, hi, 1, b4.y);
+    o.z = pair4(s1, 0, lo, hi, 2, b4.z);
+    o.w = pair4(s1, 2, lo, hi, 3, b4.w);
+    return o;
+}
+
+// Whole rows: dword i of a 3-bit coded row's code bytes as load_whole_rows
+// placed them.
+template <int D>
+__device__ __forceinline__ uint32_t code_dword3(const Rows<D, true> &R, int i) {
+    constexpr int SM = Shape<D>::kSmRegs;
+    if (D == 64 && i >= 4) return comp(R.r[SM + 1], i - 2); // bytes 16..23 are dwords 2, 3 of the register at byte 8
+    return comp(R.r[SM + (i >> 2)], i & 3);
+}
+
 // -0 in every channel of the lane's tile row (a token past the chunk's end).
 template <int D>
 __device__ __forceinline__ void fill_negzero(uint8_t *row) {
@@ -345,14 +443,67 @@ __device__ __forceinline__ void fill_negzero(uint8_t *row) {
     for (int i = 0; i < D / 8; ++i) reinterpret_cast<uint4 *>(row)[i] = make_uint4(z, z, z, z);
 }
 
-// Decodes the rows held in R (cursor's block mode; layout: Rows) into the
+// Whole rows: decodes the rows held in R into the tile, a coded row into the
+// lane's tile row with the base pair words in bp (base_pairs), raw pieces to
+// their rows. One uniform branch on the mode, then a straight-line body per
+// mode; lanes >= rows then store -0 in every channel of their row.
+template <int D>
+__device__ __forceinline__ void decode_whole_rows(const Cursor &c, const Rows<D, true> &R, const uint32_t *bp,
+                                                  uint8_t *tile, int rows) {
+    constexpr int SM = Shape<D>::kSmRegs, RR = Shape<D>::kRowRegs;
+    const int lane = lane_here();
+    uint4 *dst = reinterpret_cast<uint4 *>(tile + lane * Shape<D>::kTileStride);
+    const int mode = c.mode();
+    if (mode == 4) {
+#pragma unroll
+        for (int dg = 0; dg < D / 8; ++dg) {
+            const uint32_t cw = comp(R.r[SM + (dg >> 2)], dg & 3);
+            dst[dg] = octet_row<D>(R, dg, cw & 0x0F0F0F0Fu, (cw >> 4) & 0x0F0F0F0Fu, bp);
+        }
+    } else if (mode == 2) {
+#pragma unroll
+        for (int dg = 0; dg < D / 8; ++dg) {
+            // 16 two-bit codes per dword; octet dg uses 16 bits. Byte p of
+            // lo/hi: codes 2p and 2p+1 of the octet.
+            const uint32_t cw = comp(R.r[SM + (dg >> 3)], (dg >> 1) & 3) >> (16 * (dg & 1));
+            const uint32_t lo =
+                (cw & 3u) | (((cw >> 4) & 3u) << 8) | (((cw >> 8) & 3u) << 16) | (((cw >> 12) & 3u) << 24);
+            const uint32_t hi = ((cw >> 2) & 3u) | (((cw >> 6) & 3u) << 8) | (((cw >> 10) & 3u) << 16) |
+                                (((cw >> 14) & 3u) << 24);
+            dst[dg] = octet_row<D>(R, dg, lo, hi, bp);
+        }
+    } else if (mode == 3) {
+        // 3-bit codes: octet dg's 24 bits are bytes [3dg, 3dg + 3) of the
+        // row's codes; groups of two codes (6 bits) are spread to bytes first
+#pragma unroll
+        for (int dg = 0; dg < D / 8; ++dg) {
+            const int q = (3 * dg) >> 2, b = (3 * dg) & 3;
+            const uint32_t w = __builtin_amdgcn_alignbyte(code_dword3<D>(R, q + (b > 1 ? 1 : 0)),
+                                                          code_dword3<D>(R, q), uint32_t(b));
+            const uint32_t x = (w & 0x3Fu) | ((w << 2) & 0x3F00u) | ((w << 4) & 0x3F0000u) | ((w << 6) & 0x3F000000u);
+            dst[dg] = octet_row<D>(R, dg, x & 0x07070707u, (x >> 3) & 0x07070707u, bp);
+        }
+    } else {
+        // raw rows: register i holds piece raw_start + i of the rows loaded
+        // (c.lrows >= rows); pieces of rows >= rows are overwritten below
+        const int p0 = raw_start<D>(c.lrows);
+#pragma unroll
+        for (int i = 0; i < RR; ++i) {
+            const int p = p0 + i;
+            *reinterpret_cast<uint4 *>(tile + (p / (D / 8)) * Shape<D>::kTileStride + (p % (D / 8)) * 16) = R.r[i];
+        }
+    }
+    if (rows < kChunk && lane >= rows) fill_negzero<D>(tile + lane * Shape<D>::kTileStride);
+}
+
+// Pieces: decodes the rows held in R (cursor's block mode; layout: Rows) into the
 // tile: each coded piece to its 32 bytes of its tile row (a coded element is
 // (sm & 0x80) << 8 | (base + code) << 7 | (sm & 0x7F)), raw pieces to their
 // rows. One uniform branch on the mode, then a straight-line body per mode.
 // Lanes >= rows (past the chunk's end) then store -0 in every channel of
 // their row (wanted for V; harmless for K).
 template <int D>
-__device__ __forceinline__ void decode_rows(const Cursor &c, const Rows<D> &R, uint8_t *tile, int rows) {
+__device__ __forceinline__ void decode_pieces(const Cursor &c, const Rows<D, false> &R, uint8_t *tile, int rows) {
     constexpr int NP = Shape<D>::kPieces, RS = Shape<D>::kPieceRows, TS = Shape<D>::kTileStride;
     const int mode = c.mode();
     const int lane = lane_here();
@@ -363,7 +514,7 @@ __device__ __forceinline__ void decode_rows(const Cursor &c, const Rows<D> &R, u
         uint32_t bp[8];
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
-            const uint32_t w = uint32_t(__builtin_amdgcn_ds_bpermute(4 * (lane % NP + NP * m), int(c.base4)));
+            const uint32_t w = uint32_t(__builtin_amdgcn_ds_bpermute(4 * (lane % NP + NP * m), int(c.basew)));
             bp[2 * m] = __builtin_amdgcn_perm(w, w, 0x0c010c00u) << 7;
             bp[2 * m + 1] = __builtin_amdgcn_perm(w, w, 0x0c030c02u) << 7;
         }
@@ -418,6 +569,15 @@ __device__ __forceinline__ void decode_rows(const Cursor &c, const Rows<D> &R, u
         }
     }
     if (rows < kChunk && lane >= rows) fill_negzero<D>(tile + lane * TS);
+}
+
+// The chunk's rows into the tile in the layout of head_dim D; bp: the base
+// pair words that base_pairs wrote (whole rows only).
+template <int D>
+__device__ __forceinline__ void decode_rows(const Cursor &c, const Rows<D> &R, const uint32_t *bp, uint8_t *tile,
+                                            int rows) {
+    if constexpr (kWholeRows<D>) decode_whole_rows<D>(c, R, bp, tile, rows);
+    else decode_pieces<D>(c, R, tile, rows);
 }
 
 // ---- AVX-512 BF16 order ------------------------------------------------------
@@ -920,7 +1080,7 @@ void attn_wave_kernel(const HeadDev *__restrict__ heads, const WorkItem *__restr
         if (n <= 0) break; // unreachable with plan-checked descriptors (n_tokens > 0)
         const int tn = t + n;
 
-        if constexpr (XKV) after(RK.c[Shape<D>::kPieces - 1].y); // K rows arrived
+        if constexpr (XKV) after(last_loaded<D>(RK)); // K rows arrived
         stamp(0);
         // 1. K rows -> tile (ORDER 1: and whether the chunk needs the flushing
         // score path)
@@ -929,19 +1089,25 @@ void attn_wave_kernel(const HeadDev *__restrict__ heads, const WorkItem *__restr
             if (kc.mode() != 0) {
                 if constexpr (ORDER == 1) {
                     // coded exponents are base + code with code < 2^bits: all
-                    // >= kmin when no base is below it or wraps
-                    // (the lanes' four bytes cover every channel; bytes as 16-bit halves)
-                    const uint32_t w = kc.base4;
+                    // >= kmin when no base is below it or wraps (whole rows:
+                    // every lane two bases, pieces: four, together every
+                    // channel); bytes as 16-bit halves
+                    const uint32_t w = kc.basew;
                     const u16x2 e = __builtin_bit_cast(u16x2, w & 0x00FF00FFu);
                     const u16x2 o = __builtin_bit_cast(u16x2, (w >> 8) & 0x00FF00FFu);
-                    const u16x2 bmin = __builtin_elementwise_min(e, o), bmax = __builtin_elementwise_max(e, o);
+                    u16x2 bmin = __builtin_elementwise_min(e, o), bmax = __builtin_elementwise_max(e, o);
+                    if constexpr (kWholeRows<D>) bmin.y = bmin.x, bmax.y = bmax.x; // the upper halves hold no base
                     const uint32_t top = 256u - (1u << kc.mode());
                     flush = __ballot(uint32_t(min(bmin.x, bmin.y)) < kmin || uint32_t(max(bmax.x, bmax.y)) > top) != 0;
+                }
+                if constexpr (kWholeRows<D>) {
+                    base_pairs<D>(kc, S.bp);
+                    wave_sync();
                 }
             } else {
                 flush = ORDER == 1;
             }
-            decode_rows<D>(kc, RK, S.tile, n);
+            decode_rows<D>(kc, RK, S.bp, S.tile, n);
             wave_sync();
             flush |= patch_escapes<D, ORDER == 1>(kc, t - kc.t0, n, S.tile, klow);
         } else {
@@ -1011,13 +1177,19 @@ void attn_wave_kernel(const HeadDev *__restrict__ heads, const WorkItem *__restr
         wave_sync();
 
         stamp(3); // softmax coefficients in LDS
-        if constexpr (XKV) after(RV.c[Shape<D>::kPieces - 1].y); // V rows arrived
+        if constexpr (XKV) after(last_loaded<D>(RV)); // V rows arrived
         stamp(4);
         // 4. V rows -> tile (the scores are then no longer live); request the
         // next chunk's K and V rows (RK and RV are then not live across the
         // score and decode registers)
         if constexpr (XKV) {
-            decode_rows<D>(vc, RV, S.tile, n);
+            if constexpr (kWholeRows<D>) {
+                if (vc.mode() != 0) {
+                    base_pairs<D>(vc, S.bp);
+                    wave_sync();
+                }
+            }
+            decode_rows<D>(vc, RV, S.bp, S.tile, n);
             wave_sync();
             stamp(5); // V rows decoded
             patch_escapes<D>(vc, t - vc.t0, n, S.tile);
