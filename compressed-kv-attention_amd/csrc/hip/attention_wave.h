@@ -954,6 +954,7 @@ constexpr int kWaveOcc = D == 256 ? 1 : (D == 64 && XKV && G < 8 ? 3 : 2);
 template <int G, int D, bool XKV, int ORDER>
 __global__ __launch_bounds__(Shape<D>::kWaves * 64) __attribute__((amdgpu_waves_per_eu(kWaveOcc<G, D, XKV, ORDER>)))
 void attn_wave_kernel(const HeadDev *__restrict__ heads, const WorkItem *__restrict__ items, int n_items,
+                      const BlockDesc *__restrict__ desc,
                       const uint16_t *__restrict__ q_all, float *__restrict__ out_all, float *__restrict__ lse_all,
                       float *__restrict__ ws) {
     constexpr int TS = Shape<D>::kTileStride, H = D / 64;
@@ -1020,8 +1021,8 @@ void attn_wave_kernel(const HeadDev *__restrict__ heads, const WorkItem *__restr
     typename RegsOf<XKV, D>::T RK, RV;
     int t = wi.tok_begin;
     if constexpr (XKV) {
-        enter_block(kc, hd.kdesc + wi.kblk, t);
-        enter_block(vc, hd.vdesc + wi.vblk, t);
+        enter_block(kc, desc + wi.kdi, t);
+        enter_block(vc, desc + wi.vdi, t);
         block_vectors<D>(kc);
         load_rows<D>(kc, 0, min(kChunk, min(kc.t1, wi.tok_end) - t), RK);
         block_vectors<D>(vc);
@@ -1297,8 +1298,8 @@ void attn_wave_kernel(const HeadDev *__restrict__ heads, const WorkItem *__restr
 
 // Ordered merge of a head's split states (softmax.hpp:16-30 merge_state,
 // left to right in split order), then out = acc * (1/l) and lse = m + log l.
-// One wave per (device head, query row): lane = channel (channels lane +
-// 64 h). A separate launch, so the slots written by the split kernel are
+// One wave per merge item (device head, query row): lane = channel
+// (channels lane + 64 h). A separate launch, so the slots written by the split kernel are
 // visible without fences.
 // One batch of the merge: splits [s0, s0 + cnt) (cnt <= B), every load
 // issued before any use (indices clamped), then folded in split order.
@@ -1344,7 +1345,7 @@ __device__ __forceinline__ void merge_batch(const float *slots, int g, int s0, i
 
 template <int D>
 __global__ __launch_bounds__(4 * 64) void wave_merge_kernel(
-    const HeadDev *__restrict__ heads, const int2 *__restrict__ mitems, int n_mitems, float *__restrict__ out_all,
+    const MergeItem *__restrict__ mitems, int n_mitems, float *__restrict__ out_all,
     float *__restrict__ lse_all, const float *__restrict__ ws) {
     constexpr int H = D / 64, B = Shape<D>::kMergeBatch, SF = Shape<D>::kSlotFloats;
     __shared__ uint64_t tab[32];
@@ -1353,11 +1354,10 @@ __global__ __launch_bounds__(4 * 64) void wave_merge_kernel(
     const int lane = lane_id();
     const int mi = __builtin_amdgcn_readfirstlane(int(blockIdx.x) * 4 + (int(threadIdx.x) >> 6));
     if (mi >= n_mitems) return;
-    const int2 it = mitems[mi];
-    const HeadDev hd = heads[it.x];
-    const int g = it.y;
-    const float *slots = ws + size_t(hd.ws_base) * SF;
-    const int n = hd.n_splits;
+    const MergeItem it = load_scalar(mitems + mi);
+    const int g = it.g;
+    const float *slots = ws + size_t(it.ws_base) * SF;
+    const int n = it.n_splits;
     float a[H];
 #pragma unroll
     for (int c = 0; c < H; ++c) a[c] = slots[2 * kSlotQ + g * D + 64 * c + lane];
@@ -1372,8 +1372,8 @@ __global__ __launch_bounds__(4 * 64) void wave_merge_kernel(
             merge_batch<D, B>(slots, g, s0, cnt, tab, a, mf, lf);
     }
 #pragma unroll
-    for (int c = 0; c < H; ++c) out_all[(size_t(hd.q_row) + g) * D + 64 * c + lane] = a[c] * (1.0f / lf);
-    if (lse_all != nullptr && lane == 0) lse_all[hd.q_row + g] = mf + logf(lf);
+    for (int c = 0; c < H; ++c) out_all[(size_t(it.q_row) + g) * D + 64 * c + lane] = a[c] * (1.0f / lf);
+    if (lse_all != nullptr && lane == 0) lse_all[it.q_row + g] = mf + logf(lf);
 }
 
 } // namespace wave
@@ -1383,40 +1383,42 @@ namespace kvexp_launch {
 using namespace kvexp_dev;
 
 template <int G, int D, bool XKV, int ORDER>
-static hipError_t launch_wave_g(const HeadDev *heads, const WorkItem *items, int n_items, const uint16_t *q,
-                                float *out, float *lse, float *ws, hipStream_t s) {
+static hipError_t launch_wave_g(const HeadDev *heads, const WorkItem *items, int n_items, const BlockDesc *desc,
+                                const uint16_t *q, float *out, float *lse, float *ws, hipStream_t s) {
     constexpr int W = wave::Shape<D>::kWaves;
     const int grid = (n_items + W - 1) / W;
     hipLaunchKernelGGL((wave::attn_wave_kernel<G, D, XKV, ORDER>), dim3(grid), dim3(W * 64), 0, s, heads, items,
-                       n_items, q, out, lse, ws);
+                       n_items, desc, q, out, lse, ws);
     return hipGetLastError();
 }
 
 template <int D, bool XKV, int ORDER>
-static hipError_t launch_wave_x(int G, const HeadDev *heads, const WorkItem *items, int n_items, const uint16_t *q,
-                                float *out, float *lse, float *ws, hipStream_t s) {
+static hipError_t launch_wave_x(int G, const HeadDev *heads, const WorkItem *items, int n_items,
+                                const BlockDesc *desc, const uint16_t *q, float *out, float *lse, float *ws,
+                                hipStream_t s) {
     switch (G) {
-    case 1: return launch_wave_g<1, D, XKV, ORDER>(heads, items, n_items, q, out, lse, ws, s);
-    case 2: return launch_wave_g<2, D, XKV, ORDER>(heads, items, n_items, q, out, lse, ws, s);
-    case 3: return launch_wave_g<3, D, XKV, ORDER>(heads, items, n_items, q, out, lse, ws, s);
-    case 4: return launch_wave_g<4, D, XKV, ORDER>(heads, items, n_items, q, out, lse, ws, s);
-    case 5: return launch_wave_g<5, D, XKV, ORDER>(heads, items, n_items, q, out, lse, ws, s);
-    case 6: return launch_wave_g<6, D, XKV, ORDER>(heads, items, n_items, q, out, lse, ws, s);
-    case 7: return launch_wave_g<7, D, XKV, ORDER>(heads, items, n_items, q, out, lse, ws, s);
-    case 8: return launch_wave_g<8, D, XKV, ORDER>(heads, items, n_items, q, out, lse, ws, s);
+    case 1: return launch_wave_g<1, D, XKV, ORDER>(heads, items, n_items, desc, q, out, lse, ws, s);
+    case 2: return launch_wave_g<2, D, XKV, ORDER>(heads, items, n_items, desc, q, out, lse, ws, s);
+    case 3: return launch_wave_g<3, D, XKV, ORDER>(heads, items, n_items, desc, q, out, lse, ws, s);
+    case 4: return launch_wave_g<4, D, XKV, ORDER>(heads, items, n_items, desc, q, out, lse, ws, s);
+    case 5: return launch_wave_g<5, D, XKV, ORDER>(heads, items, n_items, desc, q, out, lse, ws, s);
+    case 6: return launch_wave_g<6, D, XKV, ORDER>(heads, items, n_items, desc, q, out, lse, ws, s);
+    case 7: return launch_wave_g<7, D, XKV, ORDER>(heads, items, n_items, desc, q, out, lse, ws, s);
+    case 8: return launch_wave_g<8, D, XKV, ORDER>(heads, items, n_items, desc, q, out, lse, ws, s);
     default: return hipErrorInvalidValue;
     }
 }
 
 template <int D>
 static hipError_t launch_wave_d(bool xkv, int order, int G, const HeadDev *heads, const WorkItem *items, int n_items,
-                                const uint16_t *q, float *out, float *lse, float *ws, hipStream_t s) {
+                                const BlockDesc *desc, const uint16_t *q, float *out, float *lse, float *ws,
+                                hipStream_t s) {
     if (order == 0)
-        return xkv ? launch_wave_x<D, true, 0>(G, heads, items, n_items, q, out, lse, ws, s)
-                   : launch_wave_x<D, false, 0>(G, heads, items, n_items, q, out, lse, ws, s);
+        return xkv ? launch_wave_x<D, true, 0>(G, heads, items, n_items, desc, q, out, lse, ws, s)
+                   : launch_wave_x<D, false, 0>(G, heads, items, n_items, desc, q, out, lse, ws, s);
     if (order == 1)
-        return xkv ? launch_wave_x<D, true, 1>(G, heads, items, n_items, q, out, lse, ws, s)
-                   : launch_wave_x<D, false, 1>(G, heads, items, n_items, q, out, lse, ws, s);
+        return xkv ? launch_wave_x<D, true, 1>(G, heads, items, n_items, desc, q, out, lse, ws, s)
+                   : launch_wave_x<D, false, 1>(G, heads, items, n_items, desc, q, out, lse, ws, s);
     return hipErrorInvalidValue;
 }
 

@@ -6,7 +6,8 @@ namespace kvexp_launch {
 using namespace kvexp_dev;
 
 hipError_t attention_wave_256(bool xkv, int order, int G, const HeadDev *heads, const WorkItem *items, int n_items,
-                              const uint16_t *q, float *out, float *lse, float *ws, hipStream_t s);
+                              const BlockDesc *desc, const uint16_t *q, float *out, float *lse, float *ws,
+                              hipStream_t s);
 
 // head_dim 64, 128 and 256, both score orders (the host sends other sizes
 // to the general kernel).
@@ -18,30 +19,31 @@ int wave_waves_per_wg(int dim) {
     return dim == 64 ? wave::Shape<64>::kWaves : (dim == 128 ? wave::Shape<128>::kWaves : wave::Shape<256>::kWaves);
 }
 
-hipError_t wave_merge(int dim, const HeadDev *heads, const int2 *mitems, int n_mitems, float *out, float *lse,
-                      const float *ws, hipStream_t s) {
+hipError_t wave_merge(int dim, const MergeItem *mitems, int n_mitems, float *out, float *lse, const float *ws,
+                      hipStream_t s) {
     if (n_mitems <= 0) return hipSuccess;
     const int grid = (n_mitems + 3) / 4;
     if (dim == 64)
-        hipLaunchKernelGGL(wave::wave_merge_kernel<64>, dim3(grid), dim3(4 * 64), 0, s, heads, mitems, n_mitems, out,
-                           lse, ws);
+        hipLaunchKernelGGL(wave::wave_merge_kernel<64>, dim3(grid), dim3(4 * 64), 0, s, mitems, n_mitems, out, lse,
+                           ws);
     else if (dim == 128)
-        hipLaunchKernelGGL(wave::wave_merge_kernel<128>, dim3(grid), dim3(4 * 64), 0, s, heads, mitems, n_mitems, out,
-                           lse, ws);
+        hipLaunchKernelGGL(wave::wave_merge_kernel<128>, dim3(grid), dim3(4 * 64), 0, s, mitems, n_mitems, out, lse,
+                           ws);
     else if (dim == 256)
-        hipLaunchKernelGGL(wave::wave_merge_kernel<256>, dim3(grid), dim3(4 * 64), 0, s, heads, mitems, n_mitems, out,
-                           lse, ws);
+        hipLaunchKernelGGL(wave::wave_merge_kernel<256>, dim3(grid), dim3(4 * 64), 0, s, mitems, n_mitems, out, lse,
+                           ws);
     else
         return hipErrorInvalidValue;
     return hipGetLastError();
 }
 
 hipError_t attention_wave(bool xkv, int order, int G, int dim, const HeadDev *heads, const WorkItem *items,
-                          int n_items, const uint16_t *q, float *out, float *lse, float *ws, hipStream_t s) {
+                          int n_items, const BlockDesc *desc, const uint16_t *q, float *out, float *lse, float *ws,
+                          hipStream_t s) {
     if (n_items <= 0) return hipSuccess;
-    if (dim == 64) return launch_wave_d<64>(xkv, order, G, heads, items, n_items, q, out, lse, ws, s);
-    if (dim == 128) return launch_wave_d<128>(xkv, order, G, heads, items, n_items, q, out, lse, ws, s);
-    if (dim == 256) return attention_wave_256(xkv, order, G, heads, items, n_items, q, out, lse, ws, s);
+    if (dim == 64) return launch_wave_d<64>(xkv, order, G, heads, items, n_items, desc, q, out, lse, ws, s);
+    if (dim == 128) return launch_wave_d<128>(xkv, order, G, heads, items, n_items, desc, q, out, lse, ws, s);
+    if (dim == 256) return attention_wave_256(xkv, order, G, heads, items, n_items, desc, q, out, lse, ws, s);
     return hipErrorInvalidValue;
 }
 

@@ -6,8 +6,9 @@
 namespace kvexp_launch {
 
 hipError_t attention_wave_256(bool xkv, int order, int G, const HeadDev *heads, const WorkItem *items, int n_items,
-                              const uint16_t *q, float *out, float *lse, float *ws, hipStream_t s) {
-    return launch_wave_d<256>(xkv, order, G, heads, items, n_items, q, out, lse, ws, s);
+                              const BlockDesc *desc, const uint16_t *q, float *out, float *lse, float *ws,
+                              hipStream_t s) {
+    return launch_wave_d<256>(xkv, order, G, heads, items, n_items, desc, q, out, lse, ws, s);
 }
 
 } // namespace kvexp_launch

@@ -71,12 +71,25 @@ struct EscJob {
 };
 
 // One split: tokens [tok_begin, tok_end) of a head; for XKV the blocks that
-// hold tok_begin in K and V.
+// hold tok_begin in K and V, as block indexes of the head's tensors and (one-
+// wave kernel plans) as indexes into the plan's descriptor array (-1
+// otherwise), so that the split's first descriptors load without waiting for
+// the head. 32 bytes: one scalar load.
 struct WorkItem {
     int32_t head;
     int32_t split;
     int32_t tok_begin, tok_end;
     int32_t kblk, vblk;
+    int32_t kdi, vdi;
+};
+
+// One (device head, query row) of the one-wave kernel's merge: the head's
+// first partial-state slot, its split count and output row, and the row.
+struct MergeItem {
+    int32_t ws_base;
+    int32_t n_splits;
+    int32_t q_row;
+    int32_t g;
 };
 
 // Per-block result of the encoder's statistics pass.

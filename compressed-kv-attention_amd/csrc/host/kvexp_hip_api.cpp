@@ -46,8 +46,9 @@ hipError_t plan_refresh(const kvexp_dev::EscJob *jobs, int n_jobs, HeadDev *head
                         int n_items, int per_head, uint32_t *status, hipStream_t s);
 bool wave_supports(int dim);
 hipError_t attention_wave(bool xkv, int order, int G, int dim, const HeadDev *heads, const WorkItem *items,
-                          int n_items, const uint16_t *q, float *out, float *lse, float *ws, hipStream_t s);
-hipError_t wave_merge(int dim, const HeadDev *heads, const int2 *mitems, int n_mitems, float *out, float *lse,
+                          int n_items, const kvexp_dev::BlockDesc *desc, const uint16_t *q, float *out, float *lse,
+                          float *ws, hipStream_t s);
+hipError_t wave_merge(int dim, const kvexp_dev::MergeItem *mitems, int n_mitems, float *out, float *lse,
                       const float *ws, hipStream_t s);
 int wave_waves_per_wg(int dim);
 hipError_t noalloc_scratch_setup(int device, void **ptr);
@@ -996,6 +997,7 @@ void plan_build(kvexp_hip_plan *p, const kvexp_hip_head *heads, int n_heads, hip
                 wi.split = sp;
                 token_bounds(H.seq, split_tokens, sp, n_splits, wi.tok_begin, wi.tok_end);
                 wi.kblk = wi.vblk = -1;
+                wi.kdi = wi.vdi = -1;
                 if (x) {
                     const int32_t *kit = std::lower_bound(kf0, kf1, wi.tok_begin);
                     const int32_t *vit = std::lower_bound(vf0, vf1, wi.tok_begin);
@@ -1027,16 +1029,27 @@ void plan_build(kvexp_hip_plan *p, const kvexp_hip_head *heads, int n_heads, hip
             p->group_start[G + 1] =
                 int(std::count_if(items.begin(), items.end(),
                                   [&](const WorkItem &w) { return hv[size_t(w.head)].n_q <= G; }));
-        std::vector<int2> mi;
-        for (int32_t dh : merge)
-            for (int g = 0; g < hv[size_t(dh)].n_q; ++g) mi.push_back(make_int2(dh, g));
+        std::vector<kvexp_dev::MergeItem> mi;
+        for (int32_t dh : merge) {
+            const HeadDev &d = hv[size_t(dh)];
+            for (int g = 0; g < d.n_q; ++g) mi.push_back(kvexp_dev::MergeItem{d.ws_base, d.n_splits, d.q_row, g});
+        }
         p->n_mitems = int(mi.size());
-        p->mitems = DevBuf(std::max<size_t>(1, mi.size()) * sizeof(int2));
+        p->mitems = DevBuf(std::max<size_t>(1, mi.size()) * sizeof(kvexp_dev::MergeItem));
         if (!mi.empty())
-            HIPX(hipMemcpyAsync(p->mitems.p, mi.data(), mi.size() * sizeof(int2), hipMemcpyHostToDevice, s));
+            HIPX(hipMemcpyAsync(p->mitems.p, mi.data(), mi.size() * sizeof(kvexp_dev::MergeItem),
+                                hipMemcpyHostToDevice, s));
         if (xkv) {
             build_escape_index(*p, heads, n_heads, n_q, dim, hv, s);
             balance_items(*p, items, first_all, first_at, n_q, dim);
+            // the split's first descriptors as indexes into the plan's array
+            // (device head dh belongs to user head dh / per_head)
+            const int per_head = (n_q + kMaxQPerLaunch - 1) / kMaxQPerLaunch;
+            for (WorkItem &w : items) {
+                const int h = w.head / per_head;
+                w.kdi = int(p->esc_prefix_at[size_t(2 * h)]) + w.kblk;
+                w.vdi = int(p->esc_prefix_at[size_t(2 * h + 1)]) + w.vblk;
+            }
         }
     }
     p->heads = DevBuf(hv.size() * sizeof(HeadDev));
@@ -1231,12 +1244,13 @@ int kvexp_hip_attention_run(kvexp_hip_plan *plan, const uint16_t *d_q, float *d_
                 const int b = plan->group_start[G], e = plan->group_start[G + 1];
                 if (e > b)
                     HIPX(kvexp_launch::attention_wave(plan->xkv, plan->order, G, plan->dim, plan->heads.as<HeadDev>(),
-                                                      plan->items.as<WorkItem>() + b, e - b, d_q, d_out, d_lse,
+                                                      plan->items.as<WorkItem>() + b, e - b,
+                                                      plan->desc.as<kvexp_dev::BlockDesc>(), d_q, d_out, d_lse,
                                                       plan->ws.as<float>(), s));
             }
             if (ev1) HIPX(hipEventRecord(ev1, s));
-            HIPX(kvexp_launch::wave_merge(plan->dim, plan->heads.as<HeadDev>(), plan->mitems.as<int2>(),
-                                          plan->n_mitems, d_out, d_lse, plan->ws.as<float>(), s));
+            HIPX(kvexp_launch::wave_merge(plan->dim, plan->mitems.as<kvexp_dev::MergeItem>(), plan->n_mitems, d_out,
+                                          d_lse, plan->ws.as<float>(), s));
         } else {
             if (ev0) HIPX(hipEventRecord(ev0, s));
             HIPX(kvexp_launch::attention(plan->xkv, plan->order, plan->heads.as<HeadDev>(),

@@ -197,6 +197,55 @@ def test_wave_kernel_groups_and_escapes(ctx, oracle, dim, backend):
     assert seen_big
 
 
+def _mixed_block_kv(rng, seq, dim, block, kinds):
+    """Tokens whose blocks cycle through `kinds`: "raw" (values spread over 60
+    binades: the encoder stores the block raw), "coded" (4-bit codes, a few
+    escapes) and "narrow" (2-bit codes)."""
+    parts = []
+    for b0 in range(0, seq, block):
+        n = min(block, seq - b0)
+        kind = kinds[(b0 // block) % len(kinds)]
+        if kind == "raw":
+            parts.append(random_kv(rng, n, dim, wide=True))
+        else:
+            parts.append(_escape_heavy_kv(rng, n, dim, 0.01, narrow=kind == "narrow"))
+    return np.concatenate(parts)
+
+
+def _block_modes(oracle, blob, dim, seq):
+    offs, _ = oracle.block_index(blob, dim, seq)
+    return set(int(m) for m in np.asarray(blob)[np.asarray(offs[:-1])])
+
+
+@pytest.mark.parametrize("dim", [64, 128, 256])
+def test_wave_kernel_mixed_raw_and_coded_blocks(ctx, oracle, dim):
+    """Raw, 4-bit and 2-bit blocks interleaved in K and, in another order, in
+    V, so that a chunk ends where either tensor's block ends, raw chunks are
+    cut at 48 rows, and block sizes of 100 and 255 tokens leave partial
+    chunks; blocks start at every even byte offset of the container (the
+    piece loads at head_dim 128 and 256 clamp to the last piece of a cut
+    chunk). XKV equals raw and the oracle bit for bit."""
+    rng = np.random.default_rng(707 + dim)
+    for trial, (n_q, block) in enumerate([(4, 100), (7, 255), (1, 128), (8, 100)]):
+        heads = []
+        for h in range(3):
+            seq = int(rng.integers(200, 1400))
+            k = _mixed_block_kv(rng, seq, dim, block, ["raw", "coded", "narrow", "coded"])
+            v = _mixed_block_kv(rng, seq, dim, block, ["coded", "raw", "raw", "narrow"])
+            heads.append(dict(k=k, v=v, seq=seq, splits=int(rng.integers(1, 5)), block=block))
+            if h == 0:
+                modes = _block_modes(oracle, oracle.encode(k, seq, dim, block), dim, seq)
+                assert {0, 4}.issubset(modes), modes
+        q = random_kv(rng, len(heads) * n_q, dim, spread_lo=-1, spread_hi=1)
+        say("mixed blocks", dim, trial, dict(n_q=n_q, block=block, seqs=[h["seq"] for h in heads]))
+        want = oracle.attention_heads("scalar", q, [dict(k=h["k"], v=h["v"], seq=h["seq"], threads=h["splits"])
+                                                    for h in heads], n_q=n_q, dim=dim, split=block)
+        raw = run_gpu(ctx, ORDER["scalar"], q, heads, n_q, dim, block, False)
+        xkv = run_gpu(ctx, ORDER["scalar"], q, heads, n_q, dim, block, True)
+        assert bits_equal(raw, xkv), trial
+        assert bits_equal(raw, want), (trial, max_rel_err(raw, want))
+
+
 def _scaled_blocks(rng, x, block, shifts, special_blocks=0.3):
     """x [seq, dim] float32 with each block of `block` rows scaled by 2^s, s
     drawn from `shifts` per block; a fraction `special_blocks` of the blocks
