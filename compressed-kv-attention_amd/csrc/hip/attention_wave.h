@@ -503,8 +503,15 @@ __device__ __forceinline__ void decode_whole_rows(const Cursor &c, const Rows<D,
 // Lanes >= rows (past the chunk's end) then store -0 in every channel of
 // their row (wanted for V; harmless for K).
 template <int D>
-__device__ __forceinline__ void decode_pieces(const Cursor &c, const Rows<D, false> &R, uint8_t *tile, int rows) {
+__device__ __forceinline__ void decode_pieces(const Cursor &c, Rows<D, false> &R, uint8_t *tile, int rows) {
     constexpr int NP = Shape<D>::kPieces, RS = Shape<D>::kPieceRows, TS = Shape<D>::kTileStride;
+    // At head_dim 256 the coded pieces go in two passes of eight, the last
+    // eight registers moved into the first eight in between: one copy of each
+    // mode's body instead of two keeps the chunk loop within the instruction
+    // cache (64 KiB; the kernel's code, 149 KiB fully unrolled, is now 63 KiB
+    // at eight query rows). Four passes of four cost more in register moves
+    // than they save (c5: 1,992 against 1,936 us per step).
+    constexpr int NPASS = D == 256 ? 2 : 1, PP = NP / NPASS;
     const int mode = c.mode();
     const int lane = lane_here();
     if (mode != 0) {
@@ -519,42 +526,54 @@ __device__ __forceinline__ void decode_pieces(const Cursor &c, const Rows<D, fal
             bp[2 * m + 1] = __builtin_amdgcn_perm(w, w, 0x0c030c02u) << 7;
         }
         uint8_t *dst = tile + (lane / NP) * TS + 32 * (lane % NP); // piece 0's place; piece k is RS k rows below
-        if (mode == 4) {
+#pragma unroll 1
+        for (int pass = 0; pass < NPASS; ++pass) {
+            if (mode == 4) {
 #pragma unroll
-            for (int k = 0; k < NP; ++k) {
-                const uint32_t c0 = R.c[k].x, c1 = R.c[k].y;
-                uint4 *o = reinterpret_cast<uint4 *>(dst + RS * k * TS);
-                o[0] = octet(R.s[k], 0, c0 & 0x0F0F0F0Fu, (c0 >> 4) & 0x0F0F0F0Fu, bp);
-                o[1] = octet(R.s[k], 1, c1 & 0x0F0F0F0Fu, (c1 >> 4) & 0x0F0F0F0Fu, bp);
-            }
-        } else if (mode == 2) {
+                for (int k = 0; k < PP; ++k) {
+                    const uint32_t c0 = R.c[k].x, c1 = R.c[k].y;
+                    uint4 *o = reinterpret_cast<uint4 *>(dst + RS * k * TS);
+                    o[0] = octet(R.s[k], 0, c0 & 0x0F0F0F0Fu, (c0 >> 4) & 0x0F0F0F0Fu, bp);
+                    o[1] = octet(R.s[k], 1, c1 & 0x0F0F0F0Fu, (c1 >> 4) & 0x0F0F0F0Fu, bp);
+                }
+            } else if (mode == 2) {
 #pragma unroll
-            for (int k = 0; k < NP; ++k) {
-                uint4 *o = reinterpret_cast<uint4 *>(dst + RS * k * TS);
+                for (int k = 0; k < PP; ++k) {
+                    uint4 *o = reinterpret_cast<uint4 *>(dst + RS * k * TS);
 #pragma unroll
-                for (int h = 0; h < 2; ++h) {
-                    // the octet's 16 bits: byte p of lo / hi holds codes 2p / 2p + 1
-                    const uint32_t cw = R.c[k].y >> (16 * h);
-                    const uint32_t lo =
-                        (cw & 3u) | (((cw >> 4) & 3u) << 8) | (((cw >> 8) & 3u) << 16) | (((cw >> 12) & 3u) << 24);
-                    const uint32_t hi = ((cw >> 2) & 3u) | (((cw >> 6) & 3u) << 8) | (((cw >> 10) & 3u) << 16) |
-                                        (((cw >> 14) & 3u) << 24);
-                    o[h] = octet(R.s[k], h, lo, hi, bp);
+                    for (int h = 0; h < 2; ++h) {
+                        // the octet's 16 bits: byte p of lo / hi holds codes 2p / 2p + 1
+                        const uint32_t cw = R.c[k].y >> (16 * h);
+                        const uint32_t lo = (cw & 3u) | (((cw >> 4) & 3u) << 8) | (((cw >> 8) & 3u) << 16) |
+                                            (((cw >> 12) & 3u) << 24);
+                        const uint32_t hi = ((cw >> 2) & 3u) | (((cw >> 6) & 3u) << 8) | (((cw >> 10) & 3u) << 16) |
+                                            (((cw >> 14) & 3u) << 24);
+                        o[h] = octet(R.s[k], h, lo, hi, bp);
+                    }
+                }
+            } else {
+                // 3-bit codes: octet h's 24 bits are bytes 2 + 3h .. 4 + 3h of
+                // c[k]; groups of two codes (6 bits) are spread to bytes first
+#pragma unroll
+                for (int k = 0; k < PP; ++k) {
+                    uint4 *o = reinterpret_cast<uint4 *>(dst + RS * k * TS);
+#pragma unroll
+                    for (int h = 0; h < 2; ++h) {
+                        const uint32_t w =
+                            h == 0 ? __builtin_amdgcn_alignbyte(R.c[k].y, R.c[k].x, 2u) : R.c[k].y >> 8;
+                        const uint32_t x =
+                            (w & 0x3Fu) | ((w << 2) & 0x3F00u) | ((w << 4) & 0x3F0000u) | ((w << 6) & 0x3F000000u);
+                        o[h] = octet(R.s[k], h, x & 0x07070707u, (x >> 3) & 0x07070707u, bp);
+                    }
                 }
             }
-        } else {
-            // 3-bit codes: octet h's 24 bits are bytes 2 + 3h .. 4 + 3h of
-            // c[k]; groups of two codes (6 bits) are spread to bytes first
+            if constexpr (NPASS > 1) {
 #pragma unroll
-            for (int k = 0; k < NP; ++k) {
-                uint4 *o = reinterpret_cast<uint4 *>(dst + RS * k * TS);
-#pragma unroll
-                for (int h = 0; h < 2; ++h) {
-                    const uint32_t w = h == 0 ? __builtin_amdgcn_alignbyte(R.c[k].y, R.c[k].x, 2u) : R.c[k].y >> 8;
-                    const uint32_t x =
-                        (w & 0x3Fu) | ((w << 2) & 0x3F00u) | ((w << 4) & 0x3F0000u) | ((w << 6) & 0x3F000000u);
-                    o[h] = octet(R.s[k], h, x & 0x07070707u, (x >> 3) & 0x07070707u, bp);
+                for (int k = 0; k < NP - PP; ++k) {
+                    R.s[k] = R.s[k + PP];
+                    R.c[k] = R.c[k + PP];
                 }
+                dst += PP * RS * TS;
             }
         }
     } else {
@@ -574,7 +593,7 @@ __device__ __forceinline__ void decode_pieces(const Cursor &c, const Rows<D, fal
 // The chunk's rows into the tile in the layout of head_dim D; bp: the base
 // pair words that base_pairs wrote (whole rows only).
 template <int D>
-__device__ __forceinline__ void decode_rows(const Cursor &c, const Rows<D> &R, const uint32_t *bp, uint8_t *tile,
+__device__ __forceinline__ void decode_rows(const Cursor &c, Rows<D> &R, const uint32_t *bp, uint8_t *tile,
                                             int rows) {
     if constexpr (kWholeRows<D>) decode_whole_rows<D>(c, R, bp, tile, rows);
     else decode_pieces<D>(c, R, tile, rows);
@@ -887,6 +906,58 @@ __device__ __forceinline__ void fold_token(const WaveLds<G, D> &S, lds_f32 *eb, 
 // four tokens issues its vector work (V widening, the l chain) and then its
 // eight products: a product right after a vector instruction, or the reverse,
 // stalls the SIMD, so few switches between the two pay.
+// Group J (tokens 16 J .. 16 J + 15) of the fold with a runtime token index,
+// for a group where some token moves a running maximum at head_dim 256: there
+// the unrolled form (32 accumulator scalings per token, through the matrix
+// registers) would put the chunk loop far beyond the instruction cache. The
+// same operations in the same order as fold_token: the A operand of token
+// 16 J + b (e of the group's rows, lanes 4b .. 4b + 3 of ea[rg][J]) is moved
+// to lanes 0 .. 3 by ds_bpermute and taken from block 0; V, e and alpha are
+// read per token. Then the next group's operands are loaded as the unrolled
+// fold would have left them.
+template <int G, int D, int J>
+__device__ __forceinline__ void fold_group_dyn(const WaveLds<G, D> &S, lds_f32 *eb, lds_f32 *ab, const uint16_t *vb,
+                                               const uint32_t (&am)[2], const float (&ea)[kGroups<G>][4],
+                                               FoldIn<D / 64> &in, f4 (&acc)[kGroups<G>][D / 64], float &lvec) {
+    constexpr int NG = kGroups<G>, H = D / 64, TS = Shape<D>::kTileStride;
+    const int lane = lane_id();
+    const uint32_t mw = am[J / 2];
+#pragma unroll 1
+    for (int b = 0; b < 16; ++b) {
+        const int T = 16 * J + b;
+        float v[H];
+#pragma unroll
+        for (int h = 0; h < H; ++h) v[h] = __uint_as_float(uint32_t(vb[T * (TS / 2) + 64 * h]) << 16);
+        const float el = eb[T], al = ab[T];
+        if ((mw >> (T % 32)) & 1u) {
+            float av[G];
+#pragma unroll
+            for (int g = 0; g < G; ++g) av[g] = S.aT[g][T];
+#pragma unroll
+            for (int g = 0; g < G; ++g)
+#pragma unroll
+                for (int h = 0; h < H; ++h) acc[g / 4][h][g % 4] *= av[g];
+        }
+        lvec = fmaf(lvec, al, el);
+        asm volatile("" : "+v"(lvec));
+#pragma unroll
+        for (int rg = 0; rg < NG; ++rg) {
+            const float a = __int_as_float(__builtin_amdgcn_ds_bpermute(4 * (4 * b + (lane & 3)), __float_as_int(ea[rg][J])));
+#pragma unroll
+            for (int h = 0; h < H; ++h) acc[rg][h] = mfma_rank1<0>(a, v[h], acc[rg][h]);
+        }
+    }
+    constexpr int T0 = 16 * (J + 1);
+    if constexpr (T0 < kChunk) {
+#pragma unroll
+        for (int k = 0; k < 3; ++k)
+#pragma unroll
+            for (int h = 0; h < H; ++h) in.v[(T0 + k) & 3][h] = vb[(T0 + k) * (TS / 2) + 64 * h];
+        in.e4[(T0 / 4) & 1] = *reinterpret_cast<lds_f4 *>(eb + T0);
+        in.a4[(T0 / 4) & 1] = *reinterpret_cast<lds_f4 *>(ab + T0);
+    }
+}
+
 template <int G, int D, int T>
 __device__ __forceinline__ void fold(const WaveLds<G, D> &S, lds_f32 *eb, lds_f32 *ab, const uint16_t *vb,
                                      const uint32_t (&am)[2], const float (&ea)[kGroups<G>][4], FoldIn<D / 64> &in,
@@ -903,6 +974,8 @@ __device__ __forceinline__ void fold(const WaveLds<G, D> &S, lds_f32 *eb, lds_f3
                 __builtin_amdgcn_sched_group_barrier(0x002, 4 * (H + 1), 0);
                 __builtin_amdgcn_sched_group_barrier(0x008, 4 * NG * H, 0);
             });
+        } else if constexpr (D == 256) {
+            fold_group_dyn<G, D, T / GS>(S, eb, ab, vb, am, ea, in, acc, lvec);
         } else {
             static_for<0, GS>([&](auto K) {
                 fold_token<G, D, T + decltype(K)::value, true>(S, eb, ab, vb, am, ea, in, acc, lvec);
