@@ -17,7 +17,7 @@
 //      time with v_perm_b32 / v_lshl_add_u32 / v_bfi_b32 on packed pairs;
 //      escape words are then written over their elements from the plan's
 //      escape records (position and word in one dword; a cursor per tensor:
-//      the window of 256 (1,024 at head_dim 256) loaded with the rows starts at the chunk's first
+//      the window of 256 (2,048 at head_dim 256) loaded with the rows starts at the chunk's first
 //      escape, and a chunk is cut short where its escapes would not fit);
 //      raw blocks are copied in chunks of at most 48 rows (the registers of
 //      64 coded rows). Every lane issues the same loads on every path, so
@@ -70,10 +70,11 @@ static __device__ unsigned long long g_phase_trace[kTraceWaves * kTraceWords];
 
 constexpr int kChunk = 64;      // tokens per chunk (one per lane)
 // Escape records a chunk can patch, loaded with its rows: four per lane per
-// 16-byte load, one load at head_dim 64 and 128, four at 256 (where escape-
-// dense blocks would otherwise cut chunks to a few rows).
+// 16-byte load, one load at head_dim 64 and 128, eight at 256 (where escape-
+// dense blocks would otherwise cut chunks short: c5's 4-bit K blocks hold
+// about 1,300 escapes per 64 rows).
 template <int D>
-constexpr int kEscLoads = D == 256 ? 4 : 1;
+constexpr int kEscLoads = D == 256 ? 8 : 1;
 template <int D>
 constexpr int kEscWindow = 256 * kEscLoads<D>;
 constexpr int kRawRows = 48;    // rows of a raw block per chunk: 64 lanes x 3D/2 bytes = 48 rows of 2D bytes
@@ -194,7 +195,7 @@ struct Cursor {
     uint32_t meta;       // mode | n_tokens << 8 | n_escape << 16
     int ecur;            // first escape of the block not yet written into a tile
     int lrows;           // rows requested by the last load_rows (the raw piece layout depends on it)
-    uint4 erec[4];
+    uint4 erec[8];
     uint32_t basew;
     __device__ int mode() const { return int(meta & 0xFFu); }
     __device__ int ntok() const { return int((meta >> 8) & 0xFFu); }
@@ -643,6 +644,7 @@ __device__ __forceinline__ bool patch_escapes(Cursor &c, int r0, int n, uint8_t 
 #pragma unroll
     for (int ij = 0; ij < 4 * kEscLoads<D>; ++ij) {
         const int i = ij >> 2, j = ij & 3;
+        if (kEscLoads<D> > 1 && j == 0 && c.ecur + 256 * i >= nesc) break; // the block's records end before load i
         const uint32_t rj = comp(c.erec[i], j);
         const uint32_t pos = rj & 0xFFFFu, word = rj >> 16;
         const bool mine = c.ecur + 256 * i + 4 * lane + j < nesc && pos < hi;

@@ -40,10 +40,10 @@ struct HeadDev {
 // + channel) in bits 0..15 and its BF16 word in bits 16..31. The plan copies
 // each block's escape words out of the container next to their positions, so
 // the wave kernel reads a window of escapes with 16-byte loads per lane (up
-// to 1,024 records). Every records array ends with kEscPad spare records, so
+// to 2,048 records). Every records array ends with kEscPad spare records, so
 // such a window read from any escape of any block stays inside the
 // allocation.
-constexpr int kEscPad = 1028;
+constexpr int kEscPad = 2052;
 
 // One block of a container as the wave kernel reads it, built and checked
 // against the block index once per plan (esc_start_kernel). 32 bytes, so a
