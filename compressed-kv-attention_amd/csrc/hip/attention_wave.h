@@ -8,7 +8,9 @@
 // the hot path.
 //
 // A split [tok_begin, tok_end) of one KV head is processed in chunks of up to
-// 64 tokens that never cross a K or V block. Per chunk the wave:
+// 64 tokens that never cross a K or V block; the order below is the loop's,
+// except that the softmax (4) runs before the V decode (3), so that the
+// scores are no longer live while V is decoded. Per chunk the wave:
 //   1. decodes the chunk's K rows from registers loaded one chunk ahead (16-
 //      channel pieces, consecutive lanes on consecutive bytes, so every load
 //      instruction reads a few whole cache lines) into a BF16 tile in its own
@@ -36,7 +38,9 @@
 //      exact DPP prefix maximum seeded by the maxima held in scalar registers
 //      and the glibc-identical expf; e and alpha go to LDS by query row;
 //   5. folds the chunk's tokens in order (lane = channel; at head_dim 128
-//      each lane holds channels lane and lane + 64), fully unrolled:
+//      each lane holds channels lane and lane + 64), unrolled (at head_dim
+//      256 a group of 16 tokens that moves a maximum runs as a loop, to keep
+//      the code within the instruction cache):
 //      acc = fma(e, v, acc) as one rank-1 product per token and row group
 //      (e of four rows in A, picked per token by the block broadcast; the
 //      token's V row in B), with acc scaled by alpha first only on the tokens
