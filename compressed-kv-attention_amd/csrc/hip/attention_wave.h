@@ -1263,6 +1263,22 @@ void attn_wave_kernel(const HeadDev *__restrict__ heads, const WorkItem *__restr
         // next chunk's K and V rows (RK and RV are then not live across the
         // score and decode registers)
         if constexpr (XKV) {
+            // the loads are issued on every chunk (the last one re-reads its
+            // own final row), the next K rows before the next V rows: the K
+            // decode can then wait for its loads while the V loads stay in
+            // flight. At head_dim 64 and 128 the K rows are requested before
+            // this chunk's V decode (which waits only for the older V rows;
+            // c2 and c4 about 1 % faster), at 256 after it (no gain measured
+            // there, where one wave per SIMD has registers to spare).
+            const int tp = min(tn, wi.tok_end - 1);
+            auto request_k = [&]() {
+                if (tp >= kc.t1) enter_block(kc, kc.d + 1, kc.t1);
+                stamp(7); // next K block entered
+                block_vectors<D>(kc);
+                load_rows<D>(kc, tp - kc.t0, min(kChunk, min(kc.t1, wi.tok_end) - tp), RK);
+                stamp(8); // next K rows requested
+            };
+            if constexpr (D <= 128) request_k();
             if constexpr (kWholeRows<D>) {
                 if (vc.mode() != 0) {
                     base_pairs<D>(vc, S.bp);
@@ -1274,15 +1290,7 @@ void attn_wave_kernel(const HeadDev *__restrict__ heads, const WorkItem *__restr
             stamp(5); // V rows decoded
             patch_escapes<D>(vc, t - vc.t0, n, S.tile);
             stamp(6); // V escapes written
-            // the loads are issued on every chunk (the last one re-reads its
-            // own final row), K first: the K decode can then wait for its
-            // loads while the V loads stay in flight
-            const int tp = min(tn, wi.tok_end - 1);
-            if (tp >= kc.t1) enter_block(kc, kc.d + 1, kc.t1);
-            stamp(7); // next K block entered
-            block_vectors<D>(kc);
-            load_rows<D>(kc, tp - kc.t0, min(kChunk, min(kc.t1, wi.tok_end) - tp), RK);
-            stamp(8); // next K rows requested
+            if constexpr (D > 128) request_k();
             if (tp >= vc.t1) enter_block(vc, vc.d + 1, vc.t1);
             stamp(9); // next V block entered
             block_vectors<D>(vc);
