@@ -47,6 +47,13 @@ head_dim 256, 255-token blocks, 8 queries). c1, c3 and c5 use the host
 generator (kvexp_amd/synth.py). XKV is checked bit for bit against raw
 before timing; each line carries the split kernel's HBM roofline.
 
+--phase-trace (after `build.py --trace`) loads the trace build of the
+library and prints, instead of a bench line, where the split kernel's waves
+spend their cycles (c2 or --config c4: cycles per wave in each phase of the
+chunk loop) or, with --workload append, where the one-pass encoder's blocks
+spend theirs during the c2 prefill. Its kernels record clock stamps, so its
+times are not the library's.
+
 --workload dump runs the reference bench's model scope on a real KV dump
 (KVD1 + QSN1 files written by the reference's python/dump_kv.py): every
 layer and KV head at each snapshot length, XKV checked bit for bit against
@@ -485,7 +492,7 @@ def cpu_baseline_c2(R, np, a, q, ks, vs, kxs, vxs, G, D, S, BT) -> dict:
 # products (128 score, 128 fold) and, on c2's containers, 983 other
 # vector-ALU instructions (SQ_INSTS_VALU - SQ_INSTS_MFMA per chunk,
 # profiles/attn_wave_c2_sq_counters.md); measured issue costs 8.4 and 2.5
-# SIMD cycles (profiles/mfma_valu_coexec.md), which do not overlap. Chunks
+# SIMD cycles (measured per instruction on gfx950), which do not overlap. Chunks
 # are spread over the 1,024 SIMDs at the 2.4 GHz peak clock. The ideal time
 # is what the SIMDs would take issuing back to back; achieved / ideal is the
 # fraction of that bound the kernel reaches.
@@ -502,7 +509,7 @@ def issue_roofline(tokens: int, kernel_us: float, three_bit: bool):
     return {"bound": "simd-issue", "ideal_us": round(ideal_us, 2), "achieved_us": round(kernel_us, 2),
             "frac": round(ideal_us / kernel_us, 4), "mfma_per_chunk": ISSUE_MFMA_PER_CHUNK,
             "valu_per_chunk": ISSUE_VALU_PER_CHUNK, "mfma_cycles": ISSUE_MFMA_CYC, "valu_cycles": ISSUE_VALU_CYC,
-            "source": "profiles/attn_wave_c2_sq_counters.md, profiles/mfma_valu_coexec.md"}
+            "source": "profiles/attn_wave_c2_sq_counters.md"}
 
 
 def bench_config(a, torch, np, kvexp_amd, synth) -> int:
@@ -650,6 +657,108 @@ def bench_dump(a, torch, np, kvexp_amd) -> int:
     return 0
 
 
+TRACE_LIB = os.path.join(ROOT, "compressed-kv-attention_amd", "lib", "trace", "libkvexp_hip_trace.so")
+
+
+def phase_trace(a) -> int:
+    """Cycles per wave in each phase of the split kernel's chunk loop (c2 or
+    c4), or per block in each phase of the one-pass encoder (--workload
+    append: the c2 prefill), from the trace build of the library."""
+    import ctypes as C
+
+    if not os.path.exists(TRACE_LIB):
+        raise SystemExit(f"{TRACE_LIB} missing: run compressed-kv-attention_amd/build.py --trace")
+    os.environ["KVEXP_HIP_LIBRARY"] = TRACE_LIB
+    import numpy as np
+    import torch
+
+    import kvexp_amd
+    from kvexp_amd import synth
+
+    L = kvexp_amd.lib()
+    ctx = kvexp_amd.Context(0)
+    dev = torch.device("cuda:0")
+    if a.workload == "append":
+        cfg = synth.CONFIGS["c2"]
+        S, D, BT = cfg["seq"], cfg["dim"], cfg["block"]
+        src = [torch.from_numpy(x.view(np.int16)).to(dev)
+               for layer in range(cfg["layers"]) for h in range(cfg["kv_heads"])
+               for x in synth.head_kv("c2", S, 0, layer, h)]
+        caches = [ctx.cache(D, S, BT) for _ in src]
+        for _ in range(5):
+            for c in caches:
+                c.seq = 0
+            ctx.append_batch(caches, src, S)
+        torch.cuda.synchronize()
+        nb = len(src) * (S // BT)
+        buf = np.zeros(32768 * 12, dtype=np.uint64)
+        L.kvexp_hip_encode_trace_read.argtypes = [C.c_void_p, C.c_size_t]
+        kvexp_amd.check(L.kvexp_hip_encode_trace_read(buf.ctypes.data_as(C.c_void_p), buf.size))
+        t = buf.reshape(32768, 12)[:nb].astype(np.int64)
+        life = t[:, 8] - t[:, 0]
+        names = ["job + ticket", "(none)", "tokens arrive", "histograms", "window bases + mode",
+                 "codes + escape ranks", "look-back", "stores issued"]
+        print(f"c2 prefill: {nb} blocks; block life mean {life.mean():.0f} cycles (min {life.min()}, max {life.max()})")
+        for i, n in enumerate(names):
+            d = t[:, i + 1] - t[:, i]
+            print(f"  {n:22s} {d.mean():8.0f} cycles/block ({100 * d.mean() / life.mean():5.1f} %), "
+                  f"p50 {np.percentile(d, 50):7.0f}, p99 {np.percentile(d, 99):7.0f}")
+        polls = t[:, 9]
+        print(f"  look-back waits: {np.mean(polls > 0) * 100:.1f} % of blocks polled again; "
+              f"mean {polls.mean():.2f}, max {polls.max()}")
+        b = np.arange(nb) % (S // BT)
+        print(f"  ticket equals blockIdx.x for {np.mean(t[:, 11] == b) * 100:.1f} % of blocks "
+              f"({np.mean(np.abs(t[:, 11] - b) <= 8) * 100:.1f} % within 8)")
+        return 0
+    config = a.config
+    if config not in ("c2", "c4"):
+        raise SystemExit("--phase-trace takes --config c2 or c4")
+    cfg = synth.CONFIGS[config]
+    S, D, G, BT = cfg["seq"], cfg["dim"], cfg["group"], cfg["block"]
+    heads = []
+    if config == "c2":
+        splits = 64
+        for layer in range(cfg["layers"]):
+            for h in range(cfg["kv_heads"]):
+                k, v = synth.head_kv("c2", S, 0, layer, h)
+                kx = ctx.encode(torch.from_numpy(k.view(np.int16)).to(dev), S, D, BT)
+                vx = ctx.encode(torch.from_numpy(v.view(np.int16)).to(dev), S, D, BT)
+                heads.append(dict(kx=kx, vx=vx, seq=S, splits=splits))
+    else:  # K and V from torch's generator on the GPU, as --config c4
+        splits = 8
+        g = torch.Generator(device=dev)
+        g.manual_seed(cfg["seed"])
+        for _ in range(cfg["layers"] * cfg["kv_heads"]):
+            scale = torch.exp2(torch.rand(D, generator=g, device=dev) * 8 - 5)
+            k = (torch.randn(S, D, generator=g, device=dev) * scale).to(torch.bfloat16).view(torch.int16).reshape(-1)
+            v = (torch.randn(S, D, generator=g, device=dev) * 0.5).to(torch.bfloat16).view(torch.int16).reshape(-1)
+            heads.append(dict(kx=ctx.encode(k, S, D, BT), vx=ctx.encode(v, S, D, BT), seq=S, splits=splits))
+    n_heads = len(heads)
+    q = torch.randn(n_heads * G * D, device=dev).to(torch.bfloat16).view(torch.int16)
+    plan = ctx.plan(heads, G, D, BT)
+    for _ in range(100 if config == "c2" else 10):
+        plan.run(q)
+    torch.cuda.synchronize()
+    nph = 12
+    buf = np.zeros(8192 * (nph + 3), dtype=np.uint64)
+    L.kvexp_hip_phase_trace_read.argtypes = [C.c_void_p, C.c_size_t, C.c_int]
+    kvexp_amd.check(L.kvexp_hip_phase_trace_read(buf.ctypes.data_as(C.c_void_p), buf.size, D))
+    t = buf.reshape(8192, nph + 3)[: n_heads * splits].astype(np.int64)
+    life = t[:, 1] - t[:, 0]
+    ph = t[:, 2:2 + nph]
+    names = ["K rows wait", "K decode + escapes", "scores", "softmax coefficients", "V rows wait", "V decode",
+             "V escapes", "next K block entered", "next K rows requested", "next V block entered",
+             "next V rows requested", "fold"]
+    chunks = S // splits // 64
+    print(f"{config}, {splits} splits: {len(t)} waves of {chunks} chunks; wave life: mean {life.mean():.0f} cycles "
+          f"(min {life.min()}, max {life.max()})")
+    for i, n in enumerate(names):
+        print(f"  {n:32s} {ph[:, i].mean():9.0f} cycles/wave ({100 * ph[:, i].mean() / life.mean():5.1f} %), "
+              f"{ph[:, i].mean() / chunks:6.0f} per chunk")
+    print(f"  {'outside the chunk loop':32s} {(life - ph.sum(1)).mean():9.0f} cycles/wave")
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -670,7 +779,12 @@ def main() -> int:
                          "a side measurement, not the quoted line)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run a 256 MiB device copy (counter calibration under rocprofv3 --pmc)")
+    ap.add_argument("--phase-trace", action="store_true",
+                    help="with the trace build (build.py --trace): cycles by phase of the split kernel's chunk "
+                         "loop (c2, --config c4) or of the one-pass encoder (--workload append)")
     a = ap.parse_args()
+    if a.phase_trace:
+        return phase_trace(a)
     if a.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
                                    "(multi-GPU sharding is a design note, not a measured path)"}))

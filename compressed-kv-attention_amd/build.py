@@ -9,13 +9,21 @@
   cxx_api_threads      the C++ caller used by tests/test_gpu_cxx_api.py,
                        built with g++ and OpenMP as the reference's own code
 
-    python compressed-kv-attention_amd/build.py [--jobs N] [--asm]
+    python compressed-kv-attention_amd/build.py [--jobs N] [--asm] [--trace]
+
+(N defaults to the host's CPU count, at most 8.)
 
 Every source is compiled with hipcc for gfx950 only, with the numeric flags
 the reference uses for its own code (-ffp-contract=off, no fast math), and
 with packed FP32 instructions disabled (-packed-fp32-ops target feature).
 ``--asm`` also writes the device assembly of each kernel file to
-``_build/asm/`` for inspection.
+``_build/asm/`` for inspection. ``--trace`` builds, instead of the library
+above, lib/trace/libkvexp_hip_trace.so: the same sources compiled with
+KVEXP_PHASE_TRACE, whose split kernel (scalar order, XKV) and one-pass
+encoder record per-wave / per-block cycle counts by phase, read back with
+kvexp_hip_phase_trace_read / kvexp_hip_encode_trace_read
+(``bench.py --phase-trace``). It is a measurement build, never loaded unless
+KVEXP_HIP_LIBRARY names it.
 """
 from __future__ import annotations
 
@@ -34,14 +42,23 @@ LIB_CXX = os.path.join(LIB_DIR, "libkvexp_hip_cxx.so")
 CXX_TEST = os.path.join(LIB_DIR, "cxx_api_threads")
 CXX_TEST_SRC = os.path.join(ROOT, "tests", "csrc", "cxx_api_threads.cpp")
 OBJ_DIR = os.path.join(HERE, "_build", "obj")
+TRACE_OBJ_DIR = os.path.join(HERE, "_build", "obj_trace")
+TRACE_LIB = os.path.join(LIB_DIR, "trace", "libkvexp_hip_trace.so")
 ASM_DIR = os.path.join(HERE, "_build", "asm")
 
 ARCH = "gfx950"
+# the split kernel's instantiation units first (the longest compiles), so
+# that a parallel build starts them at once
 SOURCES = [
+    "csrc/hip/attention_wave_d256_o1.hip",
+    "csrc/hip/attention_wave_d256_o0.hip",
+    "csrc/hip/attention_wave_d128_o1.hip",
+    "csrc/hip/attention_wave_d128_o0.hip",
+    "csrc/hip/attention_wave_d64_o1.hip",
+    "csrc/hip/attention_wave_d64_o0.hip",
+    "csrc/hip/attention_wave.hip",
     "csrc/hip/codec_kernels.hip",
     "csrc/hip/attention_kernels.hip",
-    "csrc/hip/attention_wave.hip",
-    "csrc/hip/attention_wave256.hip",
     "csrc/host/kvexp_hip_api.cpp",
 ]
 CXX_SOURCES = ["csrc/host/kvexp_cpp_api.cpp"]
@@ -85,8 +102,8 @@ def _newest(paths) -> float:
     return max(os.path.getmtime(os.path.join(HERE, p)) for p in paths)
 
 
-def _compile(src: str, force: bool) -> str:
-    obj = os.path.join(OBJ_DIR, os.path.basename(src) + ".o")
+def _compile(src: str, force: bool, trace: bool = False) -> str:
+    obj = os.path.join(TRACE_OBJ_DIR if trace else OBJ_DIR, os.path.basename(src) + ".o")
     dep_time = max(_newest([src]), _newest(HEADERS), os.path.getmtime(__file__))
     if not force and os.path.exists(obj) and os.path.getmtime(obj) >= dep_time:
         return obj
@@ -96,6 +113,8 @@ def _compile(src: str, force: bool) -> str:
         cmd = [hipcc()] + [f for f in common_flags() if not f.startswith("--offload-arch")] + ["-x", "c++"]
         cmd = [c for c in cmd if c not in ("-Xclang", "-target-feature", "-packed-fp32-ops")]
         cmd += ["-D__HIP_PLATFORM_AMD__=1", "-I/opt/rocm/include"]
+    if trace:
+        cmd += ["-DKVEXP_PHASE_TRACE"]
     cmd += ["-c", os.path.join(HERE, src), "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
@@ -111,11 +130,16 @@ def _asm(src: str) -> None:
     subprocess.run(cmd, check=True, capture_output=True, text=True)
 
 
-def build(force: bool = True, jobs: int = 4, asm: bool = False) -> str:
+def default_jobs() -> int:
+    return max(1, min(8, os.cpu_count() or 1))
+
+
+def build(force: bool = True, jobs: int = 0, asm: bool = False) -> str:
     """Compiles every source (``force``: even when up to date) and links the library."""
     os.makedirs(OBJ_DIR, exist_ok=True)
     os.makedirs(LIB_DIR, exist_ok=True)
-    with cf.ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:
+    jobs = jobs if jobs > 0 else default_jobs()
+    with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
         objs = list(ex.map(lambda s: _compile(s, force), SOURCES + CXX_SOURCES))
         if asm:
             list(ex.map(_asm, [s for s in SOURCES if s.endswith(".hip")]))
@@ -126,6 +150,17 @@ def build(force: bool = True, jobs: int = 4, asm: bool = False) -> str:
     _link(["g++", "-O2", "-std=c++17", "-fopenmp", "-pthread", f"-I{os.path.join(ROOT, 'include')}", CXX_TEST_SRC,
            f"-L{LIB_DIR}", "-lkvexp_hip_cxx", "-lkvexp_hip", "-Wl,-rpath,$ORIGIN"], CXX_TEST)
     return LIB
+
+
+def build_trace(jobs: int = 0) -> str:
+    """Compiles every kernel source with KVEXP_PHASE_TRACE into the trace library."""
+    os.makedirs(TRACE_OBJ_DIR, exist_ok=True)
+    os.makedirs(os.path.dirname(TRACE_LIB), exist_ok=True)
+    jobs = jobs if jobs > 0 else default_jobs()
+    with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
+        objs = list(ex.map(lambda s: _compile(s, True, trace=True), SOURCES))
+    _link([hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC"] + objs, TRACE_LIB)
+    return TRACE_LIB
 
 
 def _link(cmd: list[str], out: str) -> None:
@@ -139,10 +174,14 @@ def _link(cmd: list[str], out: str) -> None:
 
 def main() -> int:
     ap = argparse.ArgumentParser()
-    ap.add_argument("--jobs", type=int, default=4)
+    ap.add_argument("--jobs", type=int, default=0)
     ap.add_argument("--asm", action="store_true")
     ap.add_argument("--incremental", action="store_true", help="skip up-to-date objects")
+    ap.add_argument("--trace", action="store_true", help="build the phase-trace library instead")
     a = ap.parse_args()
+    if a.trace:
+        print(build_trace(jobs=a.jobs))
+        return 0
     print(build(force=not a.incremental, jobs=a.jobs, asm=a.asm))
     return 0
 

@@ -59,9 +59,9 @@
 namespace kvexp_dev {
 namespace wave {
 
-// Phase trace (builds with KVEXP_PHASE_TRACE only; compressed-kv-attention_amd/
-// probes.py): per wave of the scalar-order XKV kernel, the cycles spent in
-// each phase of the chunk loop, summed over its chunks. A wait is measured
+// Phase trace (builds with KVEXP_PHASE_TRACE only: build.py --trace, read
+// by bench.py --phase-trace): per wave of the scalar-order XKV kernel, the
+// cycles spent in each phase of the chunk loop, summed over its chunks. A wait is measured
 // by a timestamp taken after an empty asm that reads the loaded register.
 #if defined(KVEXP_PHASE_TRACE)
 constexpr int kTracePhases = 12;
@@ -1496,17 +1496,27 @@ static hipError_t launch_wave_x(int G, const HeadDev *heads, const WorkItem *ite
     }
 }
 
-template <int D>
-static hipError_t launch_wave_d(bool xkv, int order, int G, const HeadDev *heads, const WorkItem *items, int n_items,
-                                const BlockDesc *desc, const uint16_t *q, float *out, float *lse, float *ws,
-                                hipStream_t s) {
-    if (order == 0)
-        return xkv ? launch_wave_x<D, true, 0>(G, heads, items, n_items, desc, q, out, lse, ws, s)
-                   : launch_wave_x<D, false, 0>(G, heads, items, n_items, desc, q, out, lse, ws, s);
-    if (order == 1)
-        return xkv ? launch_wave_x<D, true, 1>(G, heads, items, n_items, desc, q, out, lse, ws, s)
-                   : launch_wave_x<D, false, 1>(G, heads, items, n_items, desc, q, out, lse, ws, s);
-    return hipErrorInvalidValue;
-}
+// The split kernels of one head_dim D and score order O (both the XKV and the
+// plain BF16 instantiation, every query-row count), launched by G. Each
+// (D, O) pair is instantiated in a translation unit of its own
+// (attention_wave_d<D>_o<O>.hip), so that they compile in parallel.
+// In a phase-trace build each unit also exports a reader of its own copy of
+// the trace array (a file-scope device array exists once per unit).
+#if defined(KVEXP_PHASE_TRACE)
+#define KVEXP_WAVE_TRACE_READER(D, O)                                                                                \
+    hipError_t attention_wave_d##D##_o##O##_trace_read(unsigned long long *host, size_t n) {                       \
+        return hipMemcpyFromSymbol(host, HIP_SYMBOL(kvexp_dev::wave::g_phase_trace), n * 8);                        \
+    }
+#else
+#define KVEXP_WAVE_TRACE_READER(D, O)
+#endif
+#define KVEXP_WAVE_UNIT(D, O)                                                                                        \
+    hipError_t attention_wave_d##D##_o##O(bool xkv, int G, const HeadDev *heads, const WorkItem *items,             \
+                                         int n_items, const BlockDesc *desc, const uint16_t *q, float *out,        \
+                                         float *lse, float *ws, hipStream_t s) {                                   \
+        return xkv ? launch_wave_x<D, true, O>(G, heads, items, n_items, desc, q, out, lse, ws, s)                  \
+                   : launch_wave_x<D, false, O>(G, heads, items, n_items, desc, q, out, lse, ws, s);                \
+    }                                                                                                                \
+    KVEXP_WAVE_TRACE_READER(D, O)
 
 } // namespace kvexp_launch
