@@ -542,7 +542,7 @@ __global__ __launch_bounds__(kThreads) void append_tail_kernel(const AppendJobDe
 constexpr uint32_t kLookbackPolls = 1u << 20; // ~1 s of polling, then kStLookback
 
 // Phase trace of the one-pass encoder (builds with KVEXP_PHASE_TRACE only;
-// compressed-kv-attention_amd/probes.py): per block of a launch, wave 0's
+// build.py --trace, read by bench.py --phase-trace): per block of a launch, wave 0's
 // clock at the start, after the ticket, the job, the tokens' arrival, the
 // histograms, the mode, the escape ranks, the look-back and the end; then
 // the look-back's polls, the CU that ran it and the workgroup's blockIdx.x.
@@ -1009,16 +1009,14 @@ extern "C" int kvexp_hip_encode_trace_read(unsigned long long *host, size_t n) {
 namespace kvexp_dev {
 #endif
 
-// Clear n 64-bit or 32-bit words (the look-back entries and ticket counters
-// of the fused encoder; kernels, not memsets, so that a captured graph
-// replays them).
-__global__ __launch_bounds__(256) void clear_u64_kernel(uint64_t *__restrict__ p, size_t n) {
+// Clears the first nw look-back entries and nt ticket counters of the fused
+// encoder in one launch (a kernel, not a memset, so that a captured graph
+// replays it).
+__global__ __launch_bounds__(256) void clear_lookback_kernel(uint64_t *__restrict__ words, size_t nw,
+                                                             uint32_t *__restrict__ tickets, size_t nt) {
     const size_t i = size_t(blockIdx.x) * 256u + threadIdx.x;
-    if (i < n) p[i] = 0u;
-}
-__global__ __launch_bounds__(256) void clear_u32_kernel(uint32_t *__restrict__ p, size_t n) {
-    const size_t i = size_t(blockIdx.x) * 256u + threadIdx.x;
-    if (i < n) p[i] = 0u;
+    if (i < nw) words[i] = 0u;
+    if (i < nt) tickets[i] = 0u;
 }
 
 // Append jobs that encode one block each (a decode step: the trailing block
@@ -1299,12 +1297,10 @@ hipError_t launch_fused(const AppendJobDev *jobs, int n_jobs, const AppendJobDev
 // null (n_jobs 1).
 hipError_t encode_fused(const AppendJobDev *jobs, int n_jobs, const AppendJobDev &one, int max_job_blocks, int dim,
                         int bt, int modes, const EncLookback &lb, uint32_t *status, hipStream_t s) {
-    if (lb.clear_words > 0)
-        hipLaunchKernelGGL(clear_u64_kernel, dim3(unsigned((lb.clear_words + 255) / 256)), dim3(256), 0, s, lb.words,
-                           lb.clear_words);
-    if (lb.clear_tickets > 0)
-        hipLaunchKernelGGL(clear_u32_kernel, dim3(unsigned((lb.clear_tickets + 255) / 256)), dim3(256), 0, s,
-                           lb.tickets, lb.clear_tickets);
+    const size_t nclear = std::max(lb.clear_words, lb.clear_tickets);
+    if (nclear > 0)
+        hipLaunchKernelGGL(clear_lookback_kernel, dim3(unsigned((nclear + 255) / 256)), dim3(256), 0, s, lb.words,
+                           lb.clear_words, lb.tickets, lb.clear_tickets);
     const int chunks = (bt * dim) / 8;
     if (chunks <= kThreads) return launch_fused<1>(jobs, n_jobs, one, max_job_blocks, dim, bt, modes, lb, status, s);
     if (chunks <= 2 * kThreads)

@@ -8,9 +8,12 @@
 // is reentrant: a call leases a context (device workspace, status words and
 // a non-blocking stream) from a per-device pool for its whole duration, so
 // concurrent calls never share mutable device state, and every copy and
-// launch of a call is ordered on its lease's stream alone (no device-wide
-// synchronisation). The pool grows to the largest number of concurrent
-// calls and keeps its contexts until the process ends.
+// launch of a call is ordered on its lease's stream alone. Device memory is
+// grow-only (the lease's staging buffers here; the context's buffer pool in
+// the attention entry): after the first calls of a shape no call allocates
+// or frees device memory, so none waits on the implicit device-wide
+// synchronisation of hipFree. The pool grows to the largest number of
+// concurrent calls and keeps its contexts until the process ends.
 #include "kvexp/attention.hpp"
 #include "kvexp/codec.hpp"
 #include "kvexp_hip.h"
@@ -18,6 +21,9 @@
 #include <hip/hip_runtime.h>
 
 #include <atomic>
+#if defined(__x86_64__)
+#include <cpuid.h>
+#endif
 #include <mutex>
 #include <stdexcept>
 #include <string>
@@ -45,9 +51,30 @@ void hip(hipError_t e) {
     if (e != hipSuccess) throw std::runtime_error(std::string("HIP: ") + hipGetErrorString(e));
 }
 
+// A grow-only device buffer of a slot: reallocated only when a call needs
+// more than it holds (the slot's stream is then idle: a lease synchronises
+// it before the slot is handed on), so after warm-up no call allocates or
+// frees device memory.
+struct Stage {
+    void *p = nullptr;
+    size_t cap = 0;
+    void *get(size_t n) {
+        n = n ? n : 4;
+        if (n > cap) {
+            if (p) hip(hipFree(p));
+            p = nullptr;
+            cap = 0;
+            hip(hipMalloc(&p, n));
+            cap = n;
+        }
+        return p;
+    }
+};
+
 struct Slot {
     kvexp_hip_ctx *ctx = nullptr;
     hipStream_t stream = nullptr; // copies and codec launches of the lease holder
+    Stage *stage = nullptr;       // four staging buffers of the codec calls
 };
 
 // Idle contexts per device. Contexts are created outside the lock; a slot is
@@ -65,6 +92,7 @@ class Pool {
         }
         Slot s;
         check(kvexp_hip_ctx_create(dev, &s.ctx));
+        s.stage = new Stage[4]; // kept with the slot until the process ends
         int prev = 0;
         hip(hipGetDevice(&prev));
         hip(hipSetDevice(dev));
@@ -114,32 +142,51 @@ struct Lease {
     Lease &operator=(const Lease &) = delete;
 };
 
-// Device allocation of one call; the lease's stream is synchronised before
-// it is freed (declared after the Lease, so destroyed first, and every
-// early exit syncs explicitly).
-struct Dev {
-    void *p = nullptr;
-    hipStream_t s;
-    Dev(size_t n, hipStream_t stream) : s(stream) { hip(hipMalloc(&p, n ? n : 4)); }
-    ~Dev() {
-        (void)hipStreamSynchronize(s);
-        (void)hipFree(p);
-    }
-    Dev(const Dev &) = delete;
-    Dev &operator=(const Dev &) = delete;
-};
 
 } // namespace
 
 void set_device(int device) { g_device.store(device); }
 
+// The host's features with the reference's gates (src/cpu.cpp:35-61), which
+// follow the Intel SDM: the OS must save the vector state (CPUID.1:ECX
+// OSXSAVE and AVX, then XCR0 from xgetbv: bits 1-2 for YMM, and 5-7 as well
+// for ZMM), and the instruction sets are CPUID.(7,0):EBX bit 5 (AVX2), bits
+// 16, 30, 31 (AVX-512 F, BW, VL) and CPUID.(7,1):EAX bit 5 (AVX512_BF16).
+// The GPU backends do not depend on it; it reports what the reference's
+// CPU backends would accept on this host.
+namespace {
+struct CpuidBit {
+    unsigned leaf, sub;
+    int reg; // 0 eax, 1 ebx, 2 ecx, 3 edx
+    unsigned bit;
+};
+
+#if defined(__x86_64__)
+bool cpuid_has(const CpuidBit &b) {
+    unsigned r[4] = {0, 0, 0, 0};
+    if (__get_cpuid_max(0, nullptr) < b.leaf) return false;
+    __cpuid_count(b.leaf, b.sub, r[0], r[1], r[2], r[3]);
+    return (r[b.reg] >> b.bit) & 1u;
+}
+
+unsigned long long xcr0() {
+    unsigned lo = 0, hi = 0;
+    __asm__ volatile("xgetbv" : "=a"(lo), "=d"(hi) : "c"(0));
+    return (static_cast<unsigned long long>(hi) << 32) | lo;
+}
+#endif
+} // namespace
+
 CpuFeatures detect_cpu() {
     CpuFeatures f;
 #if defined(__x86_64__)
-    __builtin_cpu_init();
-    f.avx2 = __builtin_cpu_supports("avx2");
-    f.avx512_bf16 = __builtin_cpu_supports("avx512f") && __builtin_cpu_supports("avx512bw") &&
-                    __builtin_cpu_supports("avx512vl") && __builtin_cpu_supports("avx512bf16");
+    if (!cpuid_has({1, 0, 2, 27}) || !cpuid_has({1, 0, 2, 28})) return f; // OSXSAVE, AVX
+    const unsigned long long x = xcr0();
+    const bool ymm_state = (x & 0x06u) == 0x06u;
+    const bool zmm_state = (x & 0xE6u) == 0xE6u;
+    f.avx2 = ymm_state && cpuid_has({7, 0, 1, 5});
+    f.avx512_bf16 = zmm_state && cpuid_has({7, 0, 1, 16}) && cpuid_has({7, 0, 1, 30}) && cpuid_has({7, 0, 1, 31}) &&
+                    cpuid_has({7, 1, 0, 5});
 #endif
     return f;
 }
@@ -149,18 +196,18 @@ EncodedTensor encode_bf16(const uint16_t *kv, int seq_len, int head_dim, int blo
     const hipStream_t s = L.slot.stream;
     const int64_t bound = kvexp_hip_encode_bound(seq_len, head_dim, block_tokens);
     const size_t in_bytes = (seq_len > 0 && head_dim > 0) ? size_t(seq_len) * size_t(head_dim) * 2u : 0u;
-    Dev din(in_bytes, s), dout(size_t(bound > 0 ? bound : 0), s);
-    if (kv != nullptr && in_bytes) hip(hipMemcpyAsync(din.p, kv, in_bytes, hipMemcpyHostToDevice, s));
+    void *din = L.slot.stage[0].get(in_bytes), *dout = L.slot.stage[1].get(size_t(bound > 0 ? bound : 0));
+    if (kv != nullptr && in_bytes) hip(hipMemcpyAsync(din, kv, in_bytes, hipMemcpyHostToDevice, s));
     size_t n = 0;
-    check(kvexp_hip_encode(L.slot.ctx, kv ? static_cast<const uint16_t *>(din.p) : nullptr, seq_len, head_dim,
-                           block_tokens, static_cast<uint8_t *>(dout.p), size_t(bound > 0 ? bound : 0), nullptr,
+    check(kvexp_hip_encode(L.slot.ctx, kv ? static_cast<const uint16_t *>(din) : nullptr, seq_len, head_dim,
+                           block_tokens, static_cast<uint8_t *>(dout), size_t(bound > 0 ? bound : 0), nullptr,
                            nullptr, &n, s));
     EncodedTensor e;
     e.seq_len = seq_len;
     e.head_dim = head_dim;
     e.block_tokens = block_tokens;
     e.bytes.resize(n);
-    if (n) hip(hipMemcpyAsync(e.bytes.data(), dout.p, n, hipMemcpyDeviceToHost, s));
+    if (n) hip(hipMemcpyAsync(e.bytes.data(), dout, n, hipMemcpyDeviceToHost, s));
     hip(hipStreamSynchronize(s));
     return e;
 }
@@ -176,14 +223,15 @@ void decode_bf16(const uint8_t *blob, size_t bytes, int seq_len, int head_dim, u
     Lease L;
     const hipStream_t s = L.slot.stream;
     const size_t out_bytes = size_t(seq_len) * size_t(head_dim) * 2u;
-    Dev db(bytes, s), doff(size_t(nb + 1) * 8, s), dfirst(size_t(nb + 1) * 4, s), dout(out_bytes, s);
-    hip(hipMemcpyAsync(db.p, blob, bytes, hipMemcpyHostToDevice, s));
-    hip(hipMemcpyAsync(doff.p, off.data(), size_t(nb + 1) * 8, hipMemcpyHostToDevice, s));
-    hip(hipMemcpyAsync(dfirst.p, first.data(), size_t(nb + 1) * 4, hipMemcpyHostToDevice, s));
-    check(kvexp_hip_decode(L.slot.ctx, static_cast<const uint8_t *>(db.p), bytes,
-                           static_cast<const int64_t *>(doff.p), static_cast<const int32_t *>(dfirst.p), nb, seq_len,
-                           head_dim, static_cast<uint16_t *>(dout.p), 1, s));
-    hip(hipMemcpyAsync(out, dout.p, out_bytes, hipMemcpyDeviceToHost, s));
+    void *db = L.slot.stage[0].get(bytes), *doff = L.slot.stage[1].get(size_t(nb + 1) * 8),
+         *dfirst = L.slot.stage[2].get(size_t(nb + 1) * 4), *dout = L.slot.stage[3].get(out_bytes);
+    hip(hipMemcpyAsync(db, blob, bytes, hipMemcpyHostToDevice, s));
+    hip(hipMemcpyAsync(doff, off.data(), size_t(nb + 1) * 8, hipMemcpyHostToDevice, s));
+    hip(hipMemcpyAsync(dfirst, first.data(), size_t(nb + 1) * 4, hipMemcpyHostToDevice, s));
+    check(kvexp_hip_decode(L.slot.ctx, static_cast<const uint8_t *>(db), bytes, static_cast<const int64_t *>(doff),
+                           static_cast<const int32_t *>(dfirst), nb, seq_len, head_dim, static_cast<uint16_t *>(dout),
+                           1, s));
+    hip(hipMemcpyAsync(out, dout, out_bytes, hipMemcpyDeviceToHost, s));
     hip(hipStreamSynchronize(s));
 }
 

@@ -101,22 +101,93 @@ template <class F> int guarded(F &&fn) {
     }
 }
 
-// Device allocation released on scope exit unless kept.
+// Device buffers kept for reuse by a context: hipFree synchronises the whole
+// device, so a call path that allocated and freed on every call would wait
+// for every other caller's work. Blocks are kept by size class (four classes
+// per power of two), at most kMaxHeld bytes in all, and returned to the
+// device when the context is destroyed. Only buffers whose last use is known
+// to be finished when they are released go back to a pool.
+class DevPool {
+  public:
+    static size_t size_class(size_t n) {
+        size_t c = 256;
+        while (c < n) c *= 2;
+        if (c <= 256) return c;
+        const size_t q = c / 8; // c/2 + q, c/2 + 2q, c/2 + 3q, c
+        for (size_t k = 5; k <= 8; ++k)
+            if (q * k >= n) return q * k;
+        return c;
+    }
+    void *get(size_t n, size_t &cap) {
+        cap = size_class(n);
+        {
+            std::lock_guard<std::mutex> lock(mu_);
+            for (size_t i = 0; i < free_.size(); ++i)
+                if (free_[i].first == cap) {
+                    void *p = free_[i].second;
+                    free_[i] = free_.back();
+                    free_.pop_back();
+                    held_ -= cap;
+                    return p;
+                }
+        }
+        void *p = nullptr;
+        HIPX(hipMalloc(&p, cap));
+        return p;
+    }
+    void put(void *p, size_t cap) {
+        {
+            std::lock_guard<std::mutex> lock(mu_);
+            if (held_ + cap <= kMaxHeld) {
+                free_.emplace_back(cap, p);
+                held_ += cap;
+                return;
+            }
+        }
+        (void)hipFree(p);
+    }
+    ~DevPool() {
+        for (auto &f : free_) (void)hipFree(f.second);
+    }
+
+  private:
+    static constexpr size_t kMaxHeld = size_t(1) << 30;
+    std::mutex mu_;
+    std::vector<std::pair<size_t, void *>> free_;
+    size_t held_ = 0;
+};
+
+// Device allocation released on scope exit unless kept: back to its pool
+// when it came from one, else to the device.
 struct DevBuf {
     void *p = nullptr;
+    DevPool *pool = nullptr;
+    size_t cap = 0;
     DevBuf() = default;
     explicit DevBuf(size_t n) {
         if (n) HIPX(hipMalloc(&p, n));
     }
+    DevBuf(DevPool *from, size_t n) {
+        if (from == nullptr) {
+            if (n) HIPX(hipMalloc(&p, n));
+        } else if (n) {
+            p = from->get(n, cap);
+            pool = from;
+        }
+    }
     DevBuf(const DevBuf &) = delete;
     DevBuf &operator=(const DevBuf &) = delete;
-    DevBuf(DevBuf &&o) noexcept : p(o.p) { o.p = nullptr; }
+    DevBuf(DevBuf &&o) noexcept : p(o.p), pool(o.pool), cap(o.cap) { o.p = nullptr; }
     DevBuf &operator=(DevBuf &&o) noexcept {
         std::swap(p, o.p);
+        std::swap(pool, o.pool);
+        std::swap(cap, o.cap);
         return *this;
     }
     ~DevBuf() {
-        if (p) (void)hipFree(p);
+        if (p == nullptr) return;
+        if (pool) pool->put(p, cap);
+        else (void)hipFree(p);
     }
     template <class T> T *as() const { return static_cast<T *>(p); }
 };
@@ -142,6 +213,9 @@ std::string encoder_status_message(uint32_t st) {
 // ================================================================ context ==
 struct kvexp_hip_ctx {
     int device = 0;
+    // buffers of the host-pointer entry and of the plans it builds (declared
+    // first: destroyed after everything that may return buffers to it)
+    DevPool pool;
     DevBuf status; // uint32 status word of the encoders and the decoder
     // encoder scratch, grown on demand; `scratch_done` is recorded on the
     // stream of the last launch that used it, so growing it never frees
@@ -175,6 +249,10 @@ struct kvexp_hip_ctx {
 
 struct kvexp_hip_plan {
     kvexp_hip_ctx *ctx = nullptr;
+    // buffers from the context's pool (plans of the host-pointer entry, which
+    // synchronises its stream before destroying them); others are freed
+    bool pooled = false;
+    DevBuf alloc(size_t n) const { return DevBuf(pooled ? &ctx->pool : nullptr, n); }
     int n_heads = 0, n_q = 0, dim = 0, order = 0, split_tokens = 0;
     // set when kvexp_hip_plan_update failed after the containers changed: the
     // plan's descriptors no longer describe them, so runs are refused until
@@ -310,8 +388,8 @@ void build_escape_index(kvexp_hip_plan &p, const kvexp_hip_head *heads, int n_he
             jobs.push_back(j);
         }
     }
-    p.esc0 = DevBuf(e0_total * sizeof(int32_t));
-    p.desc = DevBuf(e0_total * sizeof(kvexp_dev::BlockDesc));
+    p.esc0 = p.alloc(e0_total * sizeof(int32_t));
+    p.desc = p.alloc(e0_total * sizeof(kvexp_dev::BlockDesc));
     // HIP memory is not zeroed: the entry after each tensor's last block is
     // the zero-token sentinel until a plan update writes it again
     HIPX(hipMemsetAsync(p.desc.p, 0, e0_total * sizeof(kvexp_dev::BlockDesc), s));
@@ -319,7 +397,7 @@ void build_escape_index(kvexp_hip_plan &p, const kvexp_hip_head *heads, int n_he
         jobs[i].esc0 = p.esc0.as<int32_t>() + e0_at[i];
         jobs[i].desc = p.desc.as<kvexp_dev::BlockDesc>() + e0_at[i];
     }
-    DevBuf djobs(jobs.size() * sizeof(kvexp_dev::EscJob));
+    DevBuf djobs = p.alloc(jobs.size() * sizeof(kvexp_dev::EscJob));
     uint32_t *st = p.status.as<uint32_t>(); // the plan's own status word
     // pass 1: block checks and escape counts (descriptors need the position array)
     std::vector<kvexp_dev::EscJob> jobs1 = jobs;
@@ -346,13 +424,13 @@ void build_escape_index(kvexp_hip_plan &p, const kvexp_hip_head *heads, int n_he
     }
     // escape records, then kEscPad spare ones: a kernel's window of records
     // read from any escape stays inside the allocation (zeroed, never used)
-    p.escpos = DevBuf((pos_total + size_t(kvexp_dev::kEscPad)) * sizeof(uint32_t));
+    p.escpos = p.alloc((pos_total + size_t(kvexp_dev::kEscPad)) * sizeof(uint32_t));
     HIPX(hipMemsetAsync(p.escpos.as<uint32_t>() + pos_total, 0, size_t(kvexp_dev::kEscPad) * sizeof(uint32_t), s));
     for (size_t i = 0; i < jobs.size(); ++i) jobs[i].pos = p.escpos.as<uint32_t>() + pos_at[i];
     HIPX(hipMemcpyAsync(djobs.p, jobs.data(), jobs.size() * sizeof(kvexp_dev::EscJob), hipMemcpyHostToDevice, s));
     // pass 2: descriptors (with the escape-record pointers)
     HIPX(kvexp_launch::esc_start(djobs.as<kvexp_dev::EscJob>(), int(jobs.size()), st, s));
-    DevBuf dblocks(std::max<size_t>(blocks.size(), 1) * sizeof(int2));
+    DevBuf dblocks = p.alloc(std::max<size_t>(blocks.size(), 1) * sizeof(int2));
     HIPX(hipMemcpyAsync(dblocks.p, blocks.data(), blocks.size() * sizeof(int2), hipMemcpyHostToDevice, s));
     HIPX(kvexp_launch::esc_pos(djobs.as<kvexp_dev::EscJob>(), dblocks.as<int2>(), int(blocks.size()), st, s));
     check_status_word(st, s); // synchronises s: the host vectors above may go
@@ -536,34 +614,17 @@ int kvexp_hip_encode(kvexp_hip_ctx *ctx, const uint16_t *d_kv, int seq, int dim,
     });
 }
 
-// Epochs of the no-allocation encoder's look-back words in the per-device
-// static array. The whole array is cleared before the first one-pass call on
-// a device, when the epoch wraps, and after a three-launch call wrote other
-// data over the words.
+// Look-back state of a no-allocation one-pass call in the per-device static
+// array: the ticket counter in the first 256 bytes, then one entry per block.
+// Every call clears its own entries and the ticket with a kernel queued
+// before the encoder, and every call uses epoch 1: a call (or a replay of a
+// captured graph that holds one) then never takes an entry that an earlier
+// call left behind for a published one, whatever the earlier call's input
+// was. The cost is one small launch (8 bytes per block).
 namespace {
-std::mutex g_noalloc_mu;
-uint32_t g_noalloc_epoch[64] = {};
-bool g_noalloc_dirty[64] = {};
-
-// Scratch layout of a one-pass call: the ticket counter in the first 256
-// bytes, then the look-back entries.
-kvexp_dev::EncLookback noalloc_lookback(int device, uint8_t *scratch) {
-    std::lock_guard<std::mutex> lock(g_noalloc_mu);
-    const int d = device & 63;
-    size_t clear = 0, clear_tk = 0;
-    if (g_noalloc_epoch[d] == 0 || g_noalloc_epoch[d] >= 0xFFFFu || g_noalloc_dirty[d]) {
-        g_noalloc_epoch[d] = 0;
-        clear = (kvexp_dev::kNoAllocScratchBytes - 256u) / sizeof(uint64_t);
-        clear_tk = 1;
-    }
-    g_noalloc_dirty[d] = false;
+kvexp_dev::EncLookback noalloc_lookback(uint8_t *scratch, int blocks) {
     return kvexp_dev::EncLookback{reinterpret_cast<uint64_t *>(scratch + 256), reinterpret_cast<uint32_t *>(scratch),
-                                  ++g_noalloc_epoch[d], clear, clear_tk};
-}
-
-void noalloc_mark_dirty(int device) {
-    std::lock_guard<std::mutex> lock(g_noalloc_mu);
-    g_noalloc_dirty[device & 63] = true;
+                                  1u, size_t(blocks), 1u};
 }
 } // namespace
 
@@ -607,8 +668,7 @@ int kvexp_hip_encode_noalloc(kvexp_hip_ctx *ctx, const uint16_t *d_kv, int seq, 
         DeviceGuard g(ctx->device);
         uint32_t *st = d_status != nullptr ? d_status : reinterpret_cast<uint32_t *>(sp + meta_bytes + base_bytes);
         kvexp_dev::EncLookback lb{};
-        if (fused) lb = noalloc_lookback(ctx->device, sp);
-        else noalloc_mark_dirty(ctx->device);
+        if (fused) lb = noalloc_lookback(sp, nb);
         HIPX(kvexp_launch::encode(d_kv, seq, dim, bt, nb, reinterpret_cast<EncBlockMeta *>(sp), sp + meta_bytes,
                                   d_offsets, d_first_token, d_out, st, static_cast<hipStream_t>(stream), false, 0,
                                   ctx->enc_modes, fused ? &lb : nullptr));
@@ -907,7 +967,7 @@ void balance_items(kvexp_hip_plan &p, std::vector<WorkItem> &items, const int32_
 // indexes it reads) and synchronises only `s`. Status words: the plan's own.
 void plan_build(kvexp_hip_plan *p, const kvexp_hip_head *heads, int n_heads, hipStream_t s) {
     kvexp_hip_ctx *ctx = p->ctx;
-    p->status = DevBuf(sizeof(uint32_t));
+    p->status = p->alloc(sizeof(uint32_t));
     HIPX(hipMemsetAsync(p->status.p, 0, sizeof(uint32_t), s));
     const int n_q = p->n_q, dim = p->dim, split_tokens = p->split_tokens;
     const bool xkv = heads[0].k_xkv != nullptr;
@@ -1035,7 +1095,7 @@ void plan_build(kvexp_hip_plan *p, const kvexp_hip_head *heads, int n_heads, hip
             for (int g = 0; g < d.n_q; ++g) mi.push_back(kvexp_dev::MergeItem{d.ws_base, d.n_splits, d.q_row, g});
         }
         p->n_mitems = int(mi.size());
-        p->mitems = DevBuf(std::max<size_t>(1, mi.size()) * sizeof(kvexp_dev::MergeItem));
+        p->mitems = p->alloc(std::max<size_t>(1, mi.size()) * sizeof(kvexp_dev::MergeItem));
         if (!mi.empty())
             HIPX(hipMemcpyAsync(p->mitems.p, mi.data(), mi.size() * sizeof(kvexp_dev::MergeItem),
                                 hipMemcpyHostToDevice, s));
@@ -1052,18 +1112,18 @@ void plan_build(kvexp_hip_plan *p, const kvexp_hip_head *heads, int n_heads, hip
             }
         }
     }
-    p->heads = DevBuf(hv.size() * sizeof(HeadDev));
-    p->items = DevBuf(items.size() * sizeof(WorkItem));
-    p->merge_ids = DevBuf(std::max<size_t>(1, merge.size()) * sizeof(int32_t));
+    p->heads = p->alloc(hv.size() * sizeof(HeadDev));
+    p->items = p->alloc(items.size() * sizeof(WorkItem));
+    p->merge_ids = p->alloc(std::max<size_t>(1, merge.size()) * sizeof(int32_t));
     const size_t slot_floats = size_t(kMaxQPerLaunch) * size_t(dim + 2);
-    p->ws = DevBuf(std::max<size_t>(1, size_t(ws_slots)) * slot_floats * sizeof(float));
+    p->ws = p->alloc(std::max<size_t>(1, size_t(ws_slots)) * slot_floats * sizeof(float));
     HIPX(hipMemcpyAsync(p->heads.p, hv.data(), hv.size() * sizeof(HeadDev), hipMemcpyHostToDevice, s));
     HIPX(hipMemcpyAsync(p->items.p, items.data(), items.size() * sizeof(WorkItem), hipMemcpyHostToDevice, s));
     if (!merge.empty())
         HIPX(hipMemcpyAsync(p->merge_ids.p, merge.data(), merge.size() * sizeof(int32_t), hipMemcpyHostToDevice, s));
     if (!xkv) { // the job table kvexp_hip_plan_update sends lengths through
         p->jobs.assign(size_t(2 * n_heads), kvexp_dev::EscJob{});
-        p->djobs = DevBuf(p->jobs.size() * sizeof(kvexp_dev::EscJob));
+        p->djobs = p->alloc(p->jobs.size() * sizeof(kvexp_dev::EscJob));
     }
     p->src.assign(heads, heads + n_heads);
     HIPX(hipStreamSynchronize(s)); // the host vectors above are the copies' sources
@@ -1098,35 +1158,46 @@ void swap_built(kvexp_hip_plan &dst, kvexp_hip_plan &src) {
 
 } // namespace
 
+namespace {
+// kvexp_hip_plan_create's checks and build (throws); `pooled`: the plan's
+// buffers come from and return to the context's pool.
+kvexp_hip_plan *plan_create(kvexp_hip_ctx *ctx, const kvexp_hip_head *heads, int n_heads, int n_q, int dim,
+                            int split_tokens, int order, hipStream_t stream, bool pooled) {
+    if (ctx == nullptr || heads == nullptr || n_heads <= 0 || n_q <= 0 || dim <= 0 || split_tokens <= 0)
+        fail(KVEXP_HIP_INVALID_ARGUMENT, "attention_decode: bad argument");
+    if (order != KVEXP_HIP_ORDER_SCALAR && order != KVEXP_HIP_ORDER_DPBF16)
+        fail(KVEXP_HIP_INVALID_ARGUMENT, "kvexp_hip_plan_create: unknown score order");
+    // attention_scalar.cpp:47-49 / attention_avx512.cpp:155-157
+    if (order == KVEXP_HIP_ORDER_SCALAR && (dim % 8 != 0 || dim > kMaxDim))
+        fail(KVEXP_HIP_INVALID_ARGUMENT, "scalar attention: bad shape");
+    if (order == KVEXP_HIP_ORDER_DPBF16 && (dim % 32 != 0 || dim > kMaxDim))
+        fail(KVEXP_HIP_INVALID_ARGUMENT, "avx512 attention: head_dim must be a multiple of 32");
+    DeviceGuard g(ctx->device);
+    auto *p = new kvexp_hip_plan();
+    try {
+        p->ctx = ctx;
+        p->pooled = pooled;
+        p->n_heads = n_heads;
+        p->n_q = n_q;
+        p->dim = dim;
+        p->order = order;
+        p->split_tokens = split_tokens;
+        plan_build(p, heads, n_heads, stream);
+    } catch (...) {
+        delete p;
+        throw;
+    }
+    return p;
+}
+} // namespace
+
 int kvexp_hip_plan_create(kvexp_hip_ctx *ctx, const kvexp_hip_head *heads, int n_heads, int n_q, int dim,
                           int split_tokens, int order, void *stream, kvexp_hip_plan **out) {
     return guarded([&] {
         if (out == nullptr) fail(KVEXP_HIP_INVALID_ARGUMENT, "kvexp_hip_plan_create: null output");
         *out = nullptr;
-        if (ctx == nullptr || heads == nullptr || n_heads <= 0 || n_q <= 0 || dim <= 0 || split_tokens <= 0)
-            fail(KVEXP_HIP_INVALID_ARGUMENT, "attention_decode: bad argument");
-        if (order != KVEXP_HIP_ORDER_SCALAR && order != KVEXP_HIP_ORDER_DPBF16)
-            fail(KVEXP_HIP_INVALID_ARGUMENT, "kvexp_hip_plan_create: unknown score order");
-        // attention_scalar.cpp:47-49 / attention_avx512.cpp:155-157
-        if (order == KVEXP_HIP_ORDER_SCALAR && (dim % 8 != 0 || dim > kMaxDim))
-            fail(KVEXP_HIP_INVALID_ARGUMENT, "scalar attention: bad shape");
-        if (order == KVEXP_HIP_ORDER_DPBF16 && (dim % 32 != 0 || dim > kMaxDim))
-            fail(KVEXP_HIP_INVALID_ARGUMENT, "avx512 attention: head_dim must be a multiple of 32");
-        DeviceGuard g(ctx->device);
-        auto *p = new kvexp_hip_plan();
-        try {
-            p->ctx = ctx;
-            p->n_heads = n_heads;
-            p->n_q = n_q;
-            p->dim = dim;
-            p->order = order;
-            p->split_tokens = split_tokens;
-            plan_build(p, heads, n_heads, static_cast<hipStream_t>(stream));
-        } catch (...) {
-            delete p;
-            throw;
-        }
-        *out = p;
+        *out = plan_create(ctx, heads, n_heads, n_q, dim, split_tokens, order, static_cast<hipStream_t>(stream),
+                           false);
     });
 }
 
@@ -1166,6 +1237,7 @@ int kvexp_hip_plan_update(kvexp_hip_plan *plan, const kvexp_hip_head *heads, int
                 // and swapped in only when it is complete
                 kvexp_hip_plan np;
                 np.ctx = plan->ctx;
+                np.pooled = plan->pooled;
                 np.n_heads = plan->n_heads;
                 np.n_q = plan->n_q;
                 np.dim = plan->dim;
@@ -1315,25 +1387,30 @@ int kvexp_hip_attention_decode_host(kvexp_hip_ctx *ctx, int order, const uint16_
             fail(KVEXP_HIP_INVALID_ARGUMENT, "avx512 attention: head_dim must be a multiple of 32");
         DeviceGuard g(ctx->device);
         // everything on the context's own stream: concurrent calls on other
-        // contexts neither wait for this one nor see its status words
+        // contexts neither wait for this one nor see its status words. Device
+        // buffers (staging and the plan's) come from the context's pool and go
+        // back to it once the stream is synchronised: after the first calls of
+        // a shape no call allocates or frees device memory.
         hipStream_t s = ctx->stream;
+        DevPool *pool = &ctx->pool;
         const size_t qn = size_t(n_q) * size_t(dim);
-        DevBuf dq(qn * 2), dout(qn * 4);
+        DevBuf dq(pool, qn * 2), dout(pool, qn * 4);
         HIPX(hipMemcpyAsync(dq.p, q, qn * 2, hipMemcpyHostToDevice, s));
         kvexp_hip_head H{};
         H.seq = seq;
         H.n_splits = n_threads;
         DevBuf dk, dv, kio, kif, vio, vif;
         // declared after the buffers, so destroyed first: on an early failure
-        // the copies queued into them finish before they are freed
+        // the copies and kernels queued with them finish before they are
+        // released (and the plan is destroyed before the buffers it reads)
         struct SyncOnExit {
             hipStream_t s;
             ~SyncOnExit() { (void)hipStreamSynchronize(s); }
         } sync_on_exit{s};
         if (raw) {
             const size_t nb = size_t(seq) * size_t(dim) * 2u;
-            dk = DevBuf(nb);
-            dv = DevBuf(nb);
+            dk = DevBuf(pool, nb);
+            dv = DevBuf(pool, nb);
             HIPX(hipMemcpyAsync(dk.p, k_raw, nb, hipMemcpyHostToDevice, s));
             HIPX(hipMemcpyAsync(dv.p, v_raw, nb, hipMemcpyHostToDevice, s));
             H.k_raw = dk.as<uint16_t>();
@@ -1345,14 +1422,14 @@ int kvexp_hip_attention_decode_host(kvexp_hip_ctx *ctx, int order, const uint16_
             walk_index(v_xkv, v_bytes, dim, seq, vo, vf);
             if (kf.back() < seq || vf.back() < seq)
                 fail(KVEXP_HIP_FORMAT_ERROR, "xkv ran out of tokens");
-            dk = DevBuf(std::max<size_t>(k_bytes, 4));
-            dv = DevBuf(std::max<size_t>(v_bytes, 4));
+            dk = DevBuf(pool, std::max<size_t>(k_bytes, 4));
+            dv = DevBuf(pool, std::max<size_t>(v_bytes, 4));
             HIPX(hipMemcpyAsync(dk.p, k_xkv, k_bytes, hipMemcpyHostToDevice, s));
             HIPX(hipMemcpyAsync(dv.p, v_xkv, v_bytes, hipMemcpyHostToDevice, s));
-            kio = DevBuf(ko.size() * 8);
-            kif = DevBuf(kf.size() * 4);
-            vio = DevBuf(vo.size() * 8);
-            vif = DevBuf(vf.size() * 4);
+            kio = DevBuf(pool, ko.size() * 8);
+            kif = DevBuf(pool, kf.size() * 4);
+            vio = DevBuf(pool, vo.size() * 8);
+            vif = DevBuf(pool, vf.size() * 4);
             HIPX(hipMemcpyAsync(kio.p, ko.data(), ko.size() * 8, hipMemcpyHostToDevice, s));
             HIPX(hipMemcpyAsync(kif.p, kf.data(), kf.size() * 4, hipMemcpyHostToDevice, s));
             HIPX(hipMemcpyAsync(vio.p, vo.data(), vo.size() * 8, hipMemcpyHostToDevice, s));
@@ -1368,13 +1445,18 @@ int kvexp_hip_attention_decode_host(kvexp_hip_ctx *ctx, int order, const uint16_
             H.k_n_blocks = int(ko.size()) - 1;
             H.v_n_blocks = int(vo.size()) - 1;
         }
-        kvexp_hip_plan *plan = nullptr;
-        int rc = kvexp_hip_plan_create(ctx, &H, 1, n_q, dim, split_tokens, order, s, &plan);
+        struct PlanOnExit {
+            kvexp_hip_plan *p = nullptr;
+            hipStream_t s;
+            ~PlanOnExit() {
+                if (p == nullptr) return;
+                (void)hipStreamSynchronize(s); // its runs are finished before its buffers go back
+                delete p;
+            }
+        } plan{nullptr, s};
+        plan.p = plan_create(ctx, &H, 1, n_q, dim, split_tokens, order, s, true);
+        const int rc = kvexp_hip_attention_run(plan.p, dq.as<uint16_t>(), dout.as<float>(), nullptr, 1, s);
         if (rc) fail(rc, g_error);
-        rc = kvexp_hip_attention_run(plan, dq.as<uint16_t>(), dout.as<float>(), nullptr, 1, s);
-        const std::string msg = g_error;
-        kvexp_hip_plan_destroy(plan);
-        if (rc) fail(rc, msg);
         HIPX(hipMemcpyAsync(out, dout.p, qn * 4, hipMemcpyDeviceToHost, s));
         HIPX(hipStreamSynchronize(s));
     });

@@ -135,8 +135,10 @@ int kvexp_hip_encode(kvexp_hip_ctx *ctx, const uint16_t *d_kv, int seq, int dim,
  * d_offsets[n_blocks]. When d_status is not NULL, a nonzero value is OR-ed
  * into it if the encoder's size model drifted (it is never cleared). All
  * calls on one GPU share the scratch, which keeps the last call's contents:
- * calls that overlap on one GPU (any contexts, any streams) race. Output is
- * byte-identical to kvexp_hip_encode's. */
+ * calls that overlap on one GPU (any contexts, any streams) race. Each call
+ * clears the look-back state it uses with a kernel launched ahead of the
+ * encoder (no memset), so a call captured in a graph may be replayed over
+ * new inputs. Output is byte-identical to kvexp_hip_encode's. */
 #define KVEXP_HIP_NOALLOC_SCRATCH_BYTES 4194304
 int kvexp_hip_encode_noalloc(kvexp_hip_ctx *ctx, const uint16_t *d_kv, int seq, int dim, int block_tokens,
                              uint8_t *d_out, size_t capacity, int64_t *d_offsets, int32_t *d_first_token,

@@ -5,7 +5,11 @@ Backend::HipDpbf16, raw and XKV inputs) and encode_bf16 / decode_bf16 as the
 jobs of an OpenMP parallel for over 8 host threads, as the reference's bench
 calls attention_decode (src/bench.cpp:715-728). Every result is compared bit
 for bit with the reference's golden outputs and containers, and every thread
-checks the exception classes and messages of bad calls."""
+checks the exception classes and messages of bad calls.
+
+KVEXP_CXX_CASES_DIR, when set, names a directory the fixture files are
+written to (and kept), so that the same program can be run again over them,
+e.g. under rocprofv3 --hip-trace to count the device allocations per call."""
 import os
 import subprocess
 
@@ -47,9 +51,11 @@ def write_cases(d, oracle, golden) -> int:
 def test_cxx_api_from_eight_threads(tmp_path, oracle, golden):
     if not os.path.exists(BIN):
         pytest.fail(f"{BIN} is missing: run compressed-kv-attention_amd/build.py")
-    n = write_cases(str(tmp_path), oracle, golden)
+    d = os.environ.get("KVEXP_CXX_CASES_DIR") or str(tmp_path)
+    os.makedirs(d, exist_ok=True)
+    n = write_cases(d, oracle, golden)
     say("cxx api: cases", n)
-    r = subprocess.run([BIN, str(tmp_path), "8", "2"], capture_output=True, text=True, timeout=240)
+    r = subprocess.run([BIN, d, "8", "2"], capture_output=True, text=True, timeout=240)
     print(r.stdout, r.stderr)
     assert r.returncode == 0, r.stdout + r.stderr
     assert "8 threads (8 ran jobs)" in r.stdout and " 0 failures" in r.stdout
