@@ -183,16 +183,28 @@ def register_kv(ks: list, vs: list, n_q: int, dim: int, n_splits: int, split_tok
     then follows from the length: `split_tokens`-token blocks)."""
     if len(ks) != len(vs) or not ks:
         raise ValueError("kvexp.register_kv: one K and one V cache per head")
+    for c in list(ks) + list(vs):
+        # the block index of a cache is derived from its length in
+        # split_tokens-token blocks, so every cache must use that block size
+        if int(getattr(c, "block", split_tokens)) != int(split_tokens):
+            raise ValueError(f"kvexp.register_kv: a cache of {c.block}-token blocks with split_tokens "
+                             f"{split_tokens} (they must be equal)")
+        if int(getattr(c, "dim", dim)) != int(dim):
+            raise ValueError(f"kvexp.register_kv: a cache of head_dim {c.dim}, registered as {dim}")
     h = 1 + max(_kv_sets, default=0)
     _kv_sets[h] = dict(ks=list(ks), vs=list(vs), n_q=int(n_q), dim=int(dim), n_splits=int(n_splits),
-                       split=int(split_tokens), order=int(order), plan=None, seqs=None)
+                       split=int(split_tokens), order=int(order), plan=None, seqs=None, stream=None)
     return h
 
 
 def unregister_kv(handle: int) -> None:
     e = _kv_sets.pop(int(handle), None)
     if e is not None and e["plan"] is not None:
-        torch.cuda.current_stream().synchronize()  # the plan's buffers outlive queued runs
+        # the plan's buffers outlive its queued runs: wait for the stream of
+        # its last update or run (and the current one)
+        if e["stream"] is not None:
+            e["stream"].synchronize()
+        torch.cuda.current_stream().synchronize()
         e["plan"].close()
 
 
@@ -226,6 +238,7 @@ def decode_attention_kv(q: Tensor, kv: int, seqs: list[int]) -> Tensor:
         e["seqs"] = seqs
     out = torch.empty((n_heads, n_q, dim), dtype=torch.float32, device=q.device)
     e["plan"].run(q.contiguous(), out, stream=stream)
+    e["stream"] = stream
     return out
 
 

@@ -39,3 +39,21 @@ def test_ops_reject_cpu_tensors():
     k = torch.zeros(1, 10, 64, dtype=torch.bfloat16)
     with pytest.raises(ValueError, match="ROCm device tensor"):
         torch.ops.kvexp.decode_attention_raw(q, k, k, 1, 128, 0, False)
+
+
+def test_register_kv_rejects_other_block_sizes():
+    """register_kv derives each cache's block index from its length in
+    split_tokens-token blocks, so caches of another block size (or head_dim)
+    are refused when registered, not misread later."""
+    from types import SimpleNamespace
+
+    from kvexp_amd import torch_ops
+
+    good = SimpleNamespace(block=128, dim=64)
+    odd = SimpleNamespace(block=64, dim=64)
+    with pytest.raises(ValueError, match="64-token blocks with split_tokens 128"):
+        torch_ops.register_kv([good, odd], [good, good], 7, 64, 4, 128)
+    with pytest.raises(ValueError, match="head_dim 64, registered as 128"):
+        torch_ops.register_kv([good], [good], 7, 128, 4, 128)
+    h = torch_ops.register_kv([good], [good], 7, 64, 4, 128)
+    torch_ops.unregister_kv(h)  # no plan was built: nothing to wait for
