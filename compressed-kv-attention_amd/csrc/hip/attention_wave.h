@@ -844,13 +844,43 @@ __device__ __forceinline__ void scores_dp_flush(const uint8_t *row, const uint16
     }
 }
 
+// Transposed read of four tokens' V for the fold (ds_read_b64_tr_b16): in
+// each group of 16 lanes, lane 16 g + 4 k + i points at the 8 bytes of
+// channels 16 g + 4 i .. + 3 of token T0 + k, and every lane c then receives
+// V[T0 + k][c] as 16-bit element k of its result (a 4 x 4 transpose of
+// 16-bit elements within the group). One LDS read per four tokens and
+// channel half instead of four.
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+// The lane's byte offset in the tile for load_tr (token T0 = 0, channels 0 .. 63).
+template <int D>
+__device__ __forceinline__ uint32_t tr_lane_offset(int lane) {
+    const int s = lane & 15;
+    return uint32_t((s >> 2) * Shape<D>::kTileStride + 32 * (lane >> 4) + 8 * (s & 3));
+}
+
+__device__ __forceinline__ uint2 load_tr(const uint8_t *p) {
+    const s16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)(p));
+    return __builtin_bit_cast(uint2, r);
+}
+
+// Token k (0 .. 3) of a load_tr quad as FP32.
+template <int K>
+__device__ __forceinline__ float quad_f32(const uint2 &q) {
+    if constexpr (K == 0) return lo_f32(q.x);
+    else if constexpr (K == 1) return hi_f32(q.x);
+    else if constexpr (K == 2) return lo_f32(q.y);
+    else return hi_f32(q.y);
+}
+
 // Operands of the fold in flight: V of the lane's channels (lane + 64 h) for
-// the next tokens (BF16 in the low half) and e / alpha of four tokens (lane
-// g < G: its row).
+// the next quads of four tokens (quad Q in vq[Q % 3], requested two quads
+// ahead) and e of four tokens (lane g < G: its row; the next quad's).
 template <int H>
 struct FoldIn {
-    uint32_t v[4][H];
-    f4 e4[2], a4[2];
+    uint2 vq[3][H];
+    f4 e4[2];
 };
 
 // Token T of the ordered fold (attention_scalar.cpp:33-40), lane = channel
@@ -859,31 +889,31 @@ struct FoldIn {
 // token that moves no running maximum (alpha == 1 for every row, exactly)
 // takes acc = fma(e, v, acc); a token that moves one scales by alpha first:
 // acc = fma(e, v, acc * alpha) (MOVE: the caller found a move among this
-// token's group of four and tests the token's own bit; otherwise no test).
+// token's group of 16 and tests the token's own bit; otherwise no test).
 // acc[rg] register r is row 4 rg + r (acc[rg][h]: channel lane + 64 h); the
 // fma of every row of a group is one rank-1 product per h whose A operand is
 // ea[rg][T / 16] (e[4 rg + r][T] at lane 4 (T % 16) + r). Lane g < G carries
-// l of row g through l = fma(l, alpha, e), which is l + e when alpha is 1.
-// Loads run ahead: V three tokens and e / alpha four tokens before their use.
+// l of row g: l = fma(l, alpha, e), which is l + e exactly where every
+// alpha of the group is 1 (so only groups with a move read alpha, a quad at a
+// time). V arrives by quads (load_tr) two quads ahead, e a quad ahead.
 template <int G, int D, int T, bool MOVE>
-__device__ __forceinline__ void fold_token(const WaveLds<G, D> &S, lds_f32 *eb, lds_f32 *ab, const uint16_t *vb,
+__device__ __forceinline__ void fold_token(const WaveLds<G, D> &S, lds_f32 *eb, lds_f32 *ab, const uint8_t *trb,
                                            const uint32_t (&am)[2], const float (&ea)[kGroups<G>][4], FoldIn<D / 64> &in,
-                                           f4 (&acc)[kGroups<G>][D / 64], float &lvec) {
-    constexpr int NG = kGroups<G>, H = D / 64, TS = Shape<D>::kTileStride;
-    if constexpr (T + 3 < kChunk) {
+                                           f4 &a4, f4 (&acc)[kGroups<G>][D / 64], float &lvec) {
+    constexpr int NG = kGroups<G>, H = D / 64, TS = Shape<D>::kTileStride, Q = T / 4;
+    if constexpr (T % 4 == 0) {
+        if constexpr (4 * (Q + 2) < kChunk) {
 #pragma unroll
-        for (int h = 0; h < H; ++h) in.v[(T + 3) & 3][h] = vb[(T + 3) * (TS / 2) + 64 * h];
-    }
-    if constexpr (T % 4 == 0 && T + 4 < kChunk) {
-        in.e4[((T / 4) + 1) & 1] = *reinterpret_cast<lds_f4 *>(eb + T + 4);
-        in.a4[((T / 4) + 1) & 1] = *reinterpret_cast<lds_f4 *>(ab + T + 4);
+            for (int h = 0; h < H; ++h) in.vq[(Q + 2) % 3][h] = load_tr(trb + 4 * (Q + 2) * TS + 128 * h);
+        }
+        if constexpr (4 * (Q + 1) < kChunk) in.e4[(Q + 1) & 1] = *reinterpret_cast<lds_f4 *>(eb + 4 * (Q + 1));
+        if constexpr (MOVE) a4 = *reinterpret_cast<lds_f4 *>(ab + 4 * Q);
     }
     float v[H];
 #pragma unroll
-    for (int h = 0; h < H; ++h) v[h] = __uint_as_float(in.v[T & 3][h] << 16);
-    const f4 e4 = in.e4[(T / 4) & 1], a4 = in.a4[(T / 4) & 1];
+    for (int h = 0; h < H; ++h) v[h] = quad_f32<T % 4>(in.vq[Q % 3][h]);
+    const f4 e4 = in.e4[Q & 1];
     const float el = (T % 4 == 0) ? e4.x : (T % 4 == 1) ? e4.y : (T % 4 == 2) ? e4.z : e4.w;
-    const float al = (T % 4 == 0) ? a4.x : (T % 4 == 1) ? a4.y : (T % 4 == 2) ? a4.z : a4.w;
     if constexpr (MOVE) {
         const uint32_t mw = am[T / 32];
         if ((mw & (1u << (T % 32))) != 0) {
@@ -895,8 +925,11 @@ __device__ __forceinline__ void fold_token(const WaveLds<G, D> &S, lds_f32 *eb, 
 #pragma unroll
                 for (int h = 0; h < H; ++h) acc[g / 4][h][g % 4] *= av[g];
         }
+        const float al = (T % 4 == 0) ? a4.x : (T % 4 == 1) ? a4.y : (T % 4 == 2) ? a4.z : a4.w;
+        lvec = fmaf(lvec, al, el);
+    } else {
+        lvec = lvec + el;
     }
-    lvec = fmaf(lvec, al, el);
     // keeps the l chain in token order (otherwise it may be sunk to the
     // end of the unrolled fold with every token's operands held live)
     asm volatile("" : "+v"(lvec));
@@ -918,13 +951,14 @@ __device__ __forceinline__ void fold_token(const WaveLds<G, D> &S, lds_f32 *eb, 
 // registers) would put the chunk loop far beyond the instruction cache. The
 // same operations in the same order as fold_token: the A operand of token
 // 16 J + b (e of the group's rows, lanes 4b .. 4b + 3 of ea[rg][J]) is moved
-// to lanes 0 .. 3 by ds_bpermute and taken from block 0; V, e and alpha are
-// read per token. Then the next group's operands are loaded as the unrolled
-// fold would have left them.
+// to lanes 0 .. 3 by ds_bpermute and taken from block 0; V (by channel from
+// the tile), e and alpha are read per token. Then the next group's operands
+// are requested as the unrolled fold would have left them.
 template <int G, int D, int J>
 __device__ __forceinline__ void fold_group_dyn(const WaveLds<G, D> &S, lds_f32 *eb, lds_f32 *ab, const uint16_t *vb,
-                                               const uint32_t (&am)[2], const float (&ea)[kGroups<G>][4],
-                                               FoldIn<D / 64> &in, f4 (&acc)[kGroups<G>][D / 64], float &lvec) {
+                                               const uint8_t *trb, const uint32_t (&am)[2],
+                                               const float (&ea)[kGroups<G>][4], FoldIn<D / 64> &in,
+                                               f4 (&acc)[kGroups<G>][D / 64], float &lvec) {
     constexpr int NG = kGroups<G>, H = D / 64, TS = Shape<D>::kTileStride;
     const int lane = lane_id();
     const uint32_t mw = am[J / 2];
@@ -953,41 +987,41 @@ __device__ __forceinline__ void fold_group_dyn(const WaveLds<G, D> &S, lds_f32 *
             for (int h = 0; h < H; ++h) acc[rg][h] = mfma_rank1<0>(a, v[h], acc[rg][h]);
         }
     }
-    constexpr int T0 = 16 * (J + 1);
-    if constexpr (T0 < kChunk) {
+    constexpr int Q0 = 4 * (J + 1); // the next group's first quad
+    if constexpr (4 * Q0 < kChunk) {
 #pragma unroll
-        for (int k = 0; k < 3; ++k)
+        for (int k = 0; k < 2; ++k)
 #pragma unroll
-            for (int h = 0; h < H; ++h) in.v[(T0 + k) & 3][h] = vb[(T0 + k) * (TS / 2) + 64 * h];
-        in.e4[(T0 / 4) & 1] = *reinterpret_cast<lds_f4 *>(eb + T0);
-        in.a4[(T0 / 4) & 1] = *reinterpret_cast<lds_f4 *>(ab + T0);
+            for (int h = 0; h < H; ++h) in.vq[(Q0 + k) % 3][h] = load_tr(trb + 4 * (Q0 + k) * TS + 128 * h);
+        in.e4[Q0 & 1] = *reinterpret_cast<lds_f4 *>(eb + 4 * Q0);
     }
 }
 
 template <int G, int D, int T>
 __device__ __forceinline__ void fold(const WaveLds<G, D> &S, lds_f32 *eb, lds_f32 *ab, const uint16_t *vb,
-                                     const uint32_t (&am)[2], const float (&ea)[kGroups<G>][4], FoldIn<D / 64> &in,
-                                     f4 (&acc)[kGroups<G>][D / 64], float &lvec) {
+                                     const uint8_t *trb, const uint32_t (&am)[2], const float (&ea)[kGroups<G>][4],
+                                     FoldIn<D / 64> &in, f4 (&acc)[kGroups<G>][D / 64], float &lvec) {
     constexpr int GS = 16, NG = kGroups<G>, H = D / 64;
     if constexpr (T < kChunk) {
         const uint32_t mw = am[T / 32];
         constexpr uint32_t gm = uint32_t(((1ull << GS) - 1ull) << (T % 32));
+        f4 a4;
         if ((mw & gm) == 0) {
             static_for<0, GS>([&](auto K) {
-                fold_token<G, D, T + decltype(K)::value, false>(S, eb, ab, vb, am, ea, in, acc, lvec);
+                fold_token<G, D, T + decltype(K)::value, false>(S, eb, ab, trb, am, ea, in, a4, acc, lvec);
             });
             static_for<0, GS / 4>([&](auto) {
                 __builtin_amdgcn_sched_group_barrier(0x002, 4 * (H + 1), 0);
                 __builtin_amdgcn_sched_group_barrier(0x008, 4 * NG * H, 0);
             });
         } else if constexpr (D == 256) {
-            fold_group_dyn<G, D, T / GS>(S, eb, ab, vb, am, ea, in, acc, lvec);
+            fold_group_dyn<G, D, T / GS>(S, eb, ab, vb, trb, am, ea, in, acc, lvec);
         } else {
             static_for<0, GS>([&](auto K) {
-                fold_token<G, D, T + decltype(K)::value, true>(S, eb, ab, vb, am, ea, in, acc, lvec);
+                fold_token<G, D, T + decltype(K)::value, true>(S, eb, ab, trb, am, ea, in, a4, acc, lvec);
             });
         }
-        fold<G, D, T + GS>(S, eb, ab, vb, am, ea, in, acc, lvec);
+        fold<G, D, T + GS>(S, eb, ab, vb, trb, am, ea, in, acc, lvec);
     }
 }
 
@@ -1327,18 +1361,18 @@ void attn_wave_kernel(const HeadDev *__restrict__ heads, const WorkItem *__restr
             lds_f32 *ab = (lds_f32 *)&S.aT[gl][0];
             FoldIn<H> in;
             const uint16_t *vb = reinterpret_cast<const uint16_t *>(S.tile) + ln; // channel lane of token 0
+            const uint8_t *trb = S.tile + tr_lane_offset<D>(ln);                   // the lane's load_tr address
 #pragma unroll
-            for (int k = 0; k < 3; ++k)
+            for (int k = 0; k < 2; ++k)
 #pragma unroll
-                for (int h = 0; h < H; ++h) in.v[k][h] = vb[k * (TS / 2) + 64 * h];
+                for (int h = 0; h < H; ++h) in.vq[k][h] = load_tr(trb + 4 * k * TS + 128 * h);
             in.e4[0] = *reinterpret_cast<lds_f4 *>(eb);
-            in.a4[0] = *reinterpret_cast<lds_f4 *>(ab);
             // amask as two words behind an empty asm: the group tests stay
             // 32-bit scalar compares (not a 64-bit vector compare against a
             // constant held in registers)
             uint32_t am[2] = {uint32_t(amask), uint32_t(amask >> 32)};
             asm volatile("" : "+s"(am[0]), "+s"(am[1]));
-            fold<G, D, 0>(S, eb, ab, vb, am, ea, in, acc, lvec);
+            fold<G, D, 0>(S, eb, ab, vb, trb, am, ea, in, acc, lvec);
         }
         wave_sync();
         after(__float_as_uint(acc[0][0].x));
