@@ -891,17 +891,22 @@ def main() -> int:
         wall = time.perf_counter() - t_start
         return wall / steps * 1e3, e0.elapsed_time(e1) / steps
 
-    # The GPU's clock ramps up under load for some 100 ms: a settle period of
-    # untimed steps (XKV and raw alternating, about 300 ms) comes before the
-    # warm-up steps, so that a short --warmup does not time a cold clock.
-    t_settle, n_settle = time.perf_counter(), 0
-    while time.perf_counter() - t_settle < 0.3:
-        for i in range(copies):
-            xkv_plans[i].run(q, out_x)
-            raw_plans[i].run(q, out_r)
-        n_settle += 2 * copies
-        torch.cuda.synchronize()
-    log(f"clock settle: {n_settle} untimed steps in {(time.perf_counter() - t_settle) * 1e3:.0f} ms")
+    # The GPU's clock ramps up under load for some 100 ms (and drops again
+    # while the host builds plans): a settle period of untimed steps (about
+    # 300 ms) comes before each timed pass that follows idle time, so that a
+    # short --warmup does not time a cold clock.
+    def settle(plan_sets, outs):
+        t_settle, n_settle = time.perf_counter(), 0
+        while time.perf_counter() - t_settle < 0.3:
+            for plans, out in zip(plan_sets, outs):
+                for p in plans:
+                    p.run(q, out)
+                n_settle += len(plans)
+            torch.cuda.synchronize()
+        return n_settle, (time.perf_counter() - t_settle) * 1e3
+
+    n_settle, t_settle = settle([xkv_plans, raw_plans], [out_x, out_r])
+    log(f"clock settle: {n_settle} untimed steps in {t_settle:.0f} ms")
 
     ms_x, ev_x = timed(xkv_plans, out_x, a.steps, a.warmup)
     # the split kernel alone, in a separate pass: the library's event pair
@@ -943,7 +948,8 @@ def main() -> int:
     odr = dp_raw.run(q, check_errors=True).clone()
     torch.cuda.synchronize()
     dp_equal = bool(torch.equal(odp.view(torch.int32), odr.view(torch.int32)))
-    ms_dp, _ = timed(dp_plans, out_x, max(20, a.steps // 2), max(a.warmup, 8 * copies))  # new plans: settle too
+    settle([dp_plans], [out_x])  # the plan builds left the GPU idle
+    ms_dp, _ = timed(dp_plans, out_x, max(20, a.steps // 2), max(a.warmup, 8 * copies))
     for p in dp_plans + [dp_raw]:
         p.close()
     log(f"hot (one copy) {ms_hot * 1e3:.1f} us/step, median of 25 single steps {med_ms * 1e3:.1f} us; "

@@ -389,27 +389,40 @@ __device__ __forceinline__ void base_pairs(const Cursor &c, uint32_t *bp) {
     if (lane < D / 2) bp[lane] = ((c.basew & 0xFFu) << 7) | ((c.basew >> 8) << 23);
 }
 
+// The sign/mantissa bit mask of a BF16 pair, 0x807F807F, in a vector
+// register (made once per chunk): as the mask operand of v_bitop3_b32 from a
+// vector register it keeps that instruction at the fast issue rate, where a
+// scalar operand or v_bfi_b32 would take the slow one.
+__device__ __forceinline__ uint32_t sm_mask_vgpr() {
+    uint32_t m = 0x807F807Fu;
+    asm volatile("" : "+v"(m));
+    return m;
+}
+
 // One BF16 pair from two sign/mantissa bytes (positions lb, lb+1 of sw), two
 // codes (byte p of lo and hi) and the channel pair's base word (bases at bits
-// 14:7 and 30:23).
-__device__ __forceinline__ uint32_t pair4(uint32_t sw, int lb, uint32_t lo, uint32_t hi, int p, uint32_t bpw) {
+// 14:7 and 30:23); smm is sm_mask_vgpr(). The sign and mantissa bits come from
+// the spread bytes, the exponents from base + code (bitop3 0xE4: S2 ? S0 : S1).
+__device__ __forceinline__ uint32_t pair4(uint32_t sw, int lb, uint32_t lo, uint32_t hi, int p, uint32_t bpw,
+                                          uint32_t smm) {
     const uint32_t code16 = __builtin_amdgcn_perm(hi, lo, 0x0c000c00u | (uint32_t(4 + p) << 16) | uint32_t(p));
     const uint32_t t = (code16 << 7) + bpw; // exponent pair at bits 14:7 / 30:23
     const uint32_t hb = uint32_t(lb + 1);
     const uint32_t s = __builtin_amdgcn_perm(sw, sw, (hb << 24) | (hb << 16) | (uint32_t(lb) << 8) | uint32_t(lb));
-    return (s & 0x807F807Fu) | (t & ~0x807F807Fu);
+    return __builtin_amdgcn_bitop3_b32(s, t, smm, 0xE4);
 }
 
 // Octet o (channels 8o .. 8o + 7 of the piece) as four BF16 pairs: the
 // piece's sign/mantissa bytes sm, its codes split into lo (byte p: code 2p of
 // the octet) and hi (byte p: code 2p + 1), and the column's base pair words.
-__device__ __forceinline__ uint4 octet(const uint4 &sm, int o, uint32_t lo, uint32_t hi, const uint32_t (&bp)[8]) {
+__device__ __forceinline__ uint4 octet(const uint4 &sm, int o, uint32_t lo, uint32_t hi, const uint32_t (&bp)[8],
+                                       uint32_t smm) {
     const uint32_t s0 = comp(sm, 2 * o), s1 = comp(sm, 2 * o + 1);
     uint4 r;
-    r.x = pair4(s0, 0, lo, hi, 0, bp[4 * o]);
-    r.y = pair4(s0, 2, lo, hi, 1, bp[4 * o + 1]);
-    r.z = pair4(s1, 0, lo, hi, 2, bp[4 * o + 2]);
-    r.w = pair4(s1, 2, lo, hi, 3, bp[4 * o + 3]);
+    r.x = pair4(s0, 0, lo, hi, 0, bp[4 * o], smm);
+    r.y = pair4(s0, 2, lo, hi, 1, bp[4 * o + 1], smm);
+    r.z = pair4(s1, 0, lo, hi, 2, bp[4 * o + 2], smm);
+    r.w = pair4(s1, 2, lo, hi, 3, bp[4 * o + 3], smm);
     return r;
 }
 
@@ -419,15 +432,15 @@ __device__ __forceinline__ uint4 octet(const uint4 &sm, int o, uint32_t lo, uint
 // pairs' base words in LDS.
 template <int D>
 __device__ __forceinline__ uint4 octet_row(const Rows<D, true> &R, int dg, uint32_t lo, uint32_t hi,
-                                           const uint32_t *bp) {
+                                           const uint32_t *bp, uint32_t smm) {
     const uint32_t s0 = comp(R.r[dg >> 1], (dg & 1) * 2);
     const uint32_t s1 = comp(R.r[dg >> 1], (dg & 1) * 2 + 1);
     const uint4 b4 = *reinterpret_cast<const uint4 *>(bp + 4 * dg);
     uint4 o;
-    o.x = pair4(s0, 0, lo, hi, 0, b4.x);
-    o.y = pair4(s0, 2, lo, hi, 1, b4.y);
-    o.z = pair4(s1, 0, lo, hi, 2, b4.z);
-    o.w = pair4(s1, 2, lo, hi, 3, b4.w);
+    o.x = pair4(s0, 0, lo, hi, 0, b4.x, smm);
+    o.y = pair4(s0, 2, lo, hi, 1, b4.y, smm);
+    o.z = pair4(s1, 0, lo, hi, 2, b4.z, smm);
+    o.w = pair4(s1, 2, lo, hi, 3, b4.w, smm);
     return o;
 }
 
@@ -454,7 +467,7 @@ __device__ __forceinline__ void fill_negzero(uint8_t *row) {
 // mode; lanes >= rows then store -0 in every channel of their row.
 template <int D>
 __device__ __forceinline__ void decode_whole_rows(const Cursor &c, const Rows<D, true> &R, const uint32_t *bp,
-                                                  uint8_t *tile, int rows) {
+                                                  uint8_t *tile, int rows, uint32_t smm) {
     constexpr int SM = Shape<D>::kSmRegs, RR = Shape<D>::kRowRegs;
     const int lane = lane_here();
     uint4 *dst = reinterpret_cast<uint4 *>(tile + lane * Shape<D>::kTileStride);
@@ -463,7 +476,7 @@ __device__ __forceinline__ void decode_whole_rows(const Cursor &c, const Rows<D,
 #pragma unroll
         for (int dg = 0; dg < D / 8; ++dg) {
             const uint32_t cw = comp(R.r[SM + (dg >> 2)], dg & 3);
-            dst[dg] = octet_row<D>(R, dg, cw & 0x0F0F0F0Fu, (cw >> 4) & 0x0F0F0F0Fu, bp);
+            dst[dg] = octet_row<D>(R, dg, cw & 0x0F0F0F0Fu, (cw >> 4) & 0x0F0F0F0Fu, bp, smm);
         }
     } else if (mode == 2) {
 #pragma unroll
@@ -475,7 +488,7 @@ __device__ __forceinline__ void decode_whole_rows(const Cursor &c, const Rows<D,
                 (cw & 3u) | (((cw >> 4) & 3u) << 8) | (((cw >> 8) & 3u) << 16) | (((cw >> 12) & 3u) << 24);
             const uint32_t hi = ((cw >> 2) & 3u) | (((cw >> 6) & 3u) << 8) | (((cw >> 10) & 3u) << 16) |
                                 (((cw >> 14) & 3u) << 24);
-            dst[dg] = octet_row<D>(R, dg, lo, hi, bp);
+            dst[dg] = octet_row<D>(R, dg, lo, hi, bp, smm);
         }
     } else if (mode == 3) {
         // 3-bit codes: octet dg's 24 bits are bytes [3dg, 3dg + 3) of the
@@ -486,7 +499,7 @@ __device__ __forceinline__ void decode_whole_rows(const Cursor &c, const Rows<D,
             const uint32_t w = __builtin_amdgcn_alignbyte(code_dword3<D>(R, q + (b > 1 ? 1 : 0)),
                                                           code_dword3<D>(R, q), uint32_t(b));
             const uint32_t x = (w & 0x3Fu) | ((w << 2) & 0x3F00u) | ((w << 4) & 0x3F0000u) | ((w << 6) & 0x3F000000u);
-            dst[dg] = octet_row<D>(R, dg, x & 0x07070707u, (x >> 3) & 0x07070707u, bp);
+            dst[dg] = octet_row<D>(R, dg, x & 0x07070707u, (x >> 3) & 0x07070707u, bp, smm);
         }
     } else {
         // raw rows: register i holds piece raw_start + i of the rows loaded
@@ -508,7 +521,8 @@ __device__ __forceinline__ void decode_whole_rows(const Cursor &c, const Rows<D,
 // Lanes >= rows (past the chunk's end) then store -0 in every channel of
 // their row (wanted for V; harmless for K).
 template <int D>
-__device__ __forceinline__ void decode_pieces(const Cursor &c, Rows<D, false> &R, uint8_t *tile, int rows) {
+__device__ __forceinline__ void decode_pieces(const Cursor &c, Rows<D, false> &R, uint8_t *tile, int rows,
+                                              uint32_t smm) {
     constexpr int NP = Shape<D>::kPieces, RS = Shape<D>::kPieceRows, TS = Shape<D>::kTileStride;
     // At head_dim 256 the coded pieces go in two passes of eight, the last
     // eight registers moved into the first eight in between: one copy of each
@@ -538,8 +552,8 @@ __device__ __forceinline__ void decode_pieces(const Cursor &c, Rows<D, false> &R
                 for (int k = 0; k < PP; ++k) {
                     const uint32_t c0 = R.c[k].x, c1 = R.c[k].y;
                     uint4 *o = reinterpret_cast<uint4 *>(dst + RS * k * TS);
-                    o[0] = octet(R.s[k], 0, c0 & 0x0F0F0F0Fu, (c0 >> 4) & 0x0F0F0F0Fu, bp);
-                    o[1] = octet(R.s[k], 1, c1 & 0x0F0F0F0Fu, (c1 >> 4) & 0x0F0F0F0Fu, bp);
+                    o[0] = octet(R.s[k], 0, c0 & 0x0F0F0F0Fu, (c0 >> 4) & 0x0F0F0F0Fu, bp, smm);
+                    o[1] = octet(R.s[k], 1, c1 & 0x0F0F0F0Fu, (c1 >> 4) & 0x0F0F0F0Fu, bp, smm);
                 }
             } else if (mode == 2) {
 #pragma unroll
@@ -553,7 +567,7 @@ __device__ __forceinline__ void decode_pieces(const Cursor &c, Rows<D, false> &R
                                             (((cw >> 12) & 3u) << 24);
                         const uint32_t hi = ((cw >> 2) & 3u) | (((cw >> 6) & 3u) << 8) | (((cw >> 10) & 3u) << 16) |
                                             (((cw >> 14) & 3u) << 24);
-                        o[h] = octet(R.s[k], h, lo, hi, bp);
+                        o[h] = octet(R.s[k], h, lo, hi, bp, smm);
                     }
                 }
             } else {
@@ -568,7 +582,7 @@ __device__ __forceinline__ void decode_pieces(const Cursor &c, Rows<D, false> &R
                             h == 0 ? __builtin_amdgcn_alignbyte(R.c[k].y, R.c[k].x, 2u) : R.c[k].y >> 8;
                         const uint32_t x =
                             (w & 0x3Fu) | ((w << 2) & 0x3F00u) | ((w << 4) & 0x3F0000u) | ((w << 6) & 0x3F000000u);
-                        o[h] = octet(R.s[k], h, x & 0x07070707u, (x >> 3) & 0x07070707u, bp);
+                        o[h] = octet(R.s[k], h, x & 0x07070707u, (x >> 3) & 0x07070707u, bp, smm);
                     }
                 }
             }
@@ -599,9 +613,9 @@ __device__ __forceinline__ void decode_pieces(const Cursor &c, Rows<D, false> &R
 // pair words that base_pairs wrote (whole rows only).
 template <int D>
 __device__ __forceinline__ void decode_rows(const Cursor &c, Rows<D> &R, const uint32_t *bp, uint8_t *tile,
-                                            int rows) {
-    if constexpr (kWholeRows<D>) decode_whole_rows<D>(c, R, bp, tile, rows);
-    else decode_pieces<D>(c, R, tile, rows);
+                                            int rows, uint32_t smm) {
+    if constexpr (kWholeRows<D>) decode_whole_rows<D>(c, R, bp, tile, rows, smm);
+    else decode_pieces<D>(c, R, tile, rows, smm);
 }
 
 // ---- AVX-512 BF16 order ------------------------------------------------------
@@ -670,6 +684,15 @@ __device__ __forceinline__ bool patch_escapes(Cursor &c, int r0, int n, uint8_t 
 __device__ __forceinline__ void wave_sync() {
     asm volatile("" ::: "memory");
     __builtin_amdgcn_wave_barrier();
+}
+
+// max(a, b) as one v_max_f32 (IEEE maxNum: a NaN operand gives the other).
+// The inputs are arithmetic results, DPP maxima of them or -inf, never
+// signalling NaNs, so fmaxf's quieting of each operand is not needed.
+__device__ __forceinline__ float max_f32(float a, float b) {
+    float r;
+    asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+    return r;
 }
 
 __device__ __forceinline__ float lo_f32(uint32_t w) { return __uint_as_float(w << 16); }
@@ -1129,6 +1152,9 @@ void attn_wave_kernel(const HeadDev *__restrict__ heads, const WorkItem *__restr
 #pragma unroll
     for (int g = 0; g < G; ++g) msc[g] = -__builtin_inff();
     float lvec = 0.0f; // lane g < G holds l of query row g
+    // rows whose maximum moved in the previous chunk (their row of aT holds
+    // alphas other than 1); every row at the start, when aT is unwritten
+    uint32_t prevmv = (1u << G) - 1u;
 
     Cursor kc{}, vc{};
     typename RegsOf<XKV, D>::T RK, RV;
@@ -1221,7 +1247,7 @@ void attn_wave_kernel(const HeadDev *__restrict__ heads, const WorkItem *__restr
             } else {
                 flush = ORDER == 1;
             }
-            decode_rows<D>(kc, RK, S.bp, S.tile, n);
+            decode_rows<D>(kc, RK, S.bp, S.tile, n, sm_mask_vgpr());
             wave_sync();
             flush |= patch_escapes<D, ORDER == 1>(kc, t - kc.t0, n, S.tile, klow);
         } else {
@@ -1264,30 +1290,58 @@ void attn_wave_kernel(const HeadDev *__restrict__ heads, const WorkItem *__restr
         // DPP prefix maximum (seeded with each row's maximum so far, held in
         // scalar registers), e = exp(s - m) for every token and row, and, for
         // the rows where some token of the chunk moves the maximum,
-        // alpha = exp(m_prev - m) (rows without such a token keep 1). Tokens
-        // past the chunk's end get e = 0 and alpha = 1.
+        // alpha = exp(m_prev - m). Tokens past the chunk's end get e = 0 and
+        // alpha = 1. A row moves in this chunk exactly when one of its valid
+        // tokens scores above its running maximum (a NaN score never moves
+        // it); the other rows keep their maximum and alpha = 1, whose row of
+        // aT is only written again when the previous chunk moved it. The
+        // exponentials run in batches of up to four rows: every row's
+        // reduction and table read, then every row's polynomial, so that the
+        // table reads are in flight together.
         const uint64_t nmask = n >= kChunk ? ~0ull : ((1ull << n) - 1ull);
         float mi[G];
         uint64_t amask = 0;
 #pragma unroll
         for (int g = 0; g < G; ++g) mi[g] = s[g];
         wave_scan_max_rows<G>(mi);
-        // row by row, each row's values stored as soon as they are made (few
-        // registers live beside the V rows in flight)
+        uint32_t rowmv = 0;
 #pragma unroll
-        for (int g = 0; g < G; ++g) {
-            const float m = fmaxf(mi[g], msc[g]);
-            const float dg = wave_shift_up(m, msc[g]) - m;
-            // alpha != 1 exactly when m_prev - m is not zero (NaN included)
-            const uint64_t rmask = __ballot(!(dg == 0.0f)) & nmask;
-            amask |= rmask;
-            const float e = kvexp_expf_nonpos_nb(s[g] - m, tab);
-            S.eT[g][ln] = ln < n ? e : 0.0f;
-            float al = 1.0f;
-            if (rmask != 0) al = ln < n ? kvexp_expf_nonpos_nb(dg, tab) : 1.0f;
-            S.aT[g][ln] = al;
-            msc[g] = readlane_f32(m, n - 1);
+        for (int g = 0; g < G; ++g) rowmv |= (__ballot(s[g] > msc[g]) & nmask) != 0 ? 1u << g : 0u;
+        rowmv = __builtin_amdgcn_readfirstlane(rowmv);
+#pragma unroll
+        for (int g0 = 0; g0 < G; g0 += 4) {
+            constexpr int B = 4;
+            float m[B], x[B];
+            double kd[B], rr[B];
+            uint64_t tb[B];
+#pragma unroll
+            for (int b = 0; b < B; ++b) {
+                if (g0 + b >= G) break;
+                const int g = g0 + b;
+                m[b] = max_f32(mi[g], msc[g]);
+                x[b] = s[g] - m[b];
+                kvexp_expf_reduce(x[b], kd[b], rr[b]);
+                tb[b] = tab[uint32_t(__double_as_longlong(kd[b])) & 31u];
+            }
+#pragma unroll
+            for (int b = 0; b < B; ++b) {
+                if (g0 + b >= G) break;
+                const int g = g0 + b;
+                const float e = kvexp_expf_finish(kd[b], rr[b], tb[b]);
+                // glibc's expf gives +0 below -0x1.9fe368p6 (the core does not)
+                S.eT[g][ln] = (ln < n && !(x[b] < -0x1.9fe368p6f)) ? e : 0.0f;
+                if ((rowmv >> g) & 1u) {
+                    const float dg = wave_shift_up(m[b], msc[g]) - m[b];
+                    // alpha != 1 exactly when m_prev - m is not zero (NaN included)
+                    amask |= __ballot(!(dg == 0.0f)) & nmask;
+                    S.aT[g][ln] = ln < n ? kvexp_expf_nonpos_nb(dg, tab) : 1.0f;
+                    msc[g] = readlane_f32(m[b], n - 1);
+                } else if ((prevmv >> g) & 1u) {
+                    S.aT[g][ln] = 1.0f;
+                }
+            }
         }
+        prevmv = rowmv;
         wave_sync();
 
         stamp(3); // softmax coefficients in LDS
@@ -1319,7 +1373,7 @@ void attn_wave_kernel(const HeadDev *__restrict__ heads, const WorkItem *__restr
                     wave_sync();
                 }
             }
-            decode_rows<D>(vc, RV, S.bp, S.tile, n);
+            decode_rows<D>(vc, RV, S.bp, S.tile, n, sm_mask_vgpr());
             wave_sync();
             stamp(5); // V rows decoded
             patch_escapes<D>(vc, t - vc.t0, n, S.tile);

@@ -175,8 +175,55 @@ __device__ static inline __attribute__((always_inline)) float kvexp_expf_core_fa
         : "v"(kd), "v"(tb), "v"(r), "s"(c0), "v"(c1), "s"(c2));
     return yf;
 }
+
+/* kvexp_expf_core_fast in two halves, so that a caller evaluating several
+ * exponentials can issue all their table reads before the first is needed:
+ * kvexp_expf_reduce gives kd (the table index in the low bits of its bit
+ * pattern) and r; kvexp_expf_finish takes them and the table entry
+ * tb = tab[bits(kd) & 31]. The same operations in the same order. */
+__device__ static inline __attribute__((always_inline)) void kvexp_expf_reduce(float x, double &kd, double &r) {
+    double xd;
+    const double c = KVEXP_EXP_INVLN2N, sh = KVEXP_EXP_SHIFT, nsh = -KVEXP_EXP_SHIFT;
+    asm("v_cvt_f64_f32 %0, %3\n\t"
+        "v_fma_f64 %1, %4, %0, %5\n\t"
+        "v_add_f64 %2, %1, %6\n\t"
+        "v_fma_f64 %2, %4, %0, -%2"
+        : "=&v"(xd), "=&v"(kd), "=&v"(r)
+        : "v"(x), "s"(c), "v"(sh), "s"(nsh));
+}
+__device__ static inline __attribute__((always_inline)) float kvexp_expf_finish(double kd, double r, uint64_t tb) {
+    const double c0 = KVEXP_EXP_C0, c1 = KVEXP_EXP_C1, c2 = KVEXP_EXP_C2;
+    double s, r2, p, y;
+    float yf;
+    asm("v_lshlrev_b64 %0, 47, %5\n\t"
+        "v_lshl_add_u64 %0, %0, 0, %6\n\t"
+        "v_mul_f64 %1, %7, %7\n\t"
+        "v_fma_f64 %2, %8, %7, %9\n\t"
+        "v_fma_f64 %3, %10, %7, 1.0\n\t"
+        "v_fma_f64 %3, %2, %1, %3\n\t"
+        "v_mul_f64 %3, %3, %0\n\t"
+        "v_cvt_f32_f64 %4, %3"
+        : "=&v"(s), "=&v"(r2), "=&v"(p), "=&v"(y), "=v"(yf)
+        : "v"(kd), "v"(tb), "v"(r), "s"(c0), "v"(c1), "s"(c2));
+    return yf;
+}
 #else
 #define kvexp_expf_core_fast kvexp_expf_core_tab
+#if defined(__HIPCC__)
+/* Portable forms of the two halves (host pass; other expf forms). */
+__device__ static inline void kvexp_expf_reduce(float x, double &kd, double &r) {
+    const double xd = (double)x;
+    kd = KVEXP_FMA64(KVEXP_EXP_INVLN2N, xd, KVEXP_EXP_SHIFT);
+    r = KVEXP_FMA64(KVEXP_EXP_INVLN2N, xd, -(kd - KVEXP_EXP_SHIFT));
+}
+__device__ static inline float kvexp_expf_finish(double kd, double r, uint64_t tb) {
+    const double s = kvexp_f64_from(tb + (kvexp_f64_bits(kd) << 47));
+    const double p = KVEXP_FMA64(KVEXP_EXP_C0, r, KVEXP_EXP_C1);
+    double y = KVEXP_FMA64(KVEXP_EXP_C2, r, 1.0);
+    y = KVEXP_FMA64(p, r * r, y);
+    return (float)(y * s);
+}
+#endif
 #endif
 
 /* kvexp_expf_tab_nb for arguments that are not positive (x <= 0, -0, -inf)
