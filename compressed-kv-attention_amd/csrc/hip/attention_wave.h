@@ -105,7 +105,7 @@ struct Shape {
     static constexpr int kRowRegs = kSmRegs + D / 32; // + its 4-bit codes: what a coded row needs
     static constexpr int kHalves = D / 64;          // channels per lane in the fold (lane, lane + 64, ...)
     static constexpr int kWaves = D == 64 ? 4 : (D == 128 ? 2 : 1); // waves per workgroup (LDS: see WaveLds)
-    static constexpr int kMergeBatch = 128 / kHalves; // split slots whose loads are in flight together in the merge
+    static constexpr int kMergeBatch = D == 256 ? 32 : 64; // splits per merge batch (one per lane; their rows in flight together)
 };
 
 // Per-wave LDS. The tile holds the chunk's K rows (row t: the D BF16 of
@@ -221,22 +221,28 @@ __device__ __forceinline__ void enter_block(Cursor &c, const BlockDesc *d, int t
 }
 
 // The block's base exponents (see Cursor: one 4-byte load) and its next
-// kEscWindow escape records (four per lane per 16-byte load). Every lane
-// loads, from an
-// always valid address (a records array ends with kEscPad spare records),
-// and the call is made on every chunk whether or not the block changed, so
-// the number of loads in flight never depends on the path taken: the
+// kEscWindow escape records (four per lane per 16-byte load). The call is
+// made on every chunk whether or not the block changed, and each load
+// instruction is issued whatever the path (lane 0 always loads, from an
+// always valid address: a records array ends with kEscPad spare records),
+// so the number of loads in flight never depends on the path taken: the
 // compiler's wait counts then stay exact, and a wait for the K rows leaves
-// the V rows in flight. Records at or past n_escape are masked where used.
+// the V rows in flight. Lanes whose four records all lie at or past
+// n_escape do not load (their bytes would be masked where used): a block
+// holds about two dozen escapes on c2, so the window's load reads one or two
+// cache lines instead of sixteen.
 template <int D>
 __device__ __forceinline__ void block_vectors(Cursor &c) {
     const int lane = lane_here();
     constexpr int NP = Shape<D>::kPieces;
     if constexpr (kWholeRows<D>) c.basew = *(g_u16 *)(c.blk + 8 + 2 * (lane & (D / 2 - 1)));
     else c.basew = *(g_u32 *)(c.blk + 8 + 16 * (lane % NP) + 4 * ((lane / NP) & 3));
+    const int left = c.nesc() - c.ecur; // records of the block not yet written
 #pragma unroll
     for (int i = 0; i < kEscLoads<D>; ++i) {
-        const u32x4 r = *(g_u32x4 *)(c.esc + c.ecur + 256 * i + 4 * lane);
+        const int first = 256 * i + 4 * lane;
+        u32x4 r = {0u, 0u, 0u, 0u};
+        if (first < left || lane == 0) r = *(g_u32x4 *)(c.esc + c.ecur + first);
         c.erec[i] = make_uint4(r.x, r.y, r.z, r.w);
     }
 }
@@ -1095,7 +1101,7 @@ void attn_wave_kernel(const HeadDev *__restrict__ heads, const WorkItem *__restr
                       float *__restrict__ ws) {
     constexpr int TS = Shape<D>::kTileStride, H = D / 64;
     __shared__ WgLds<G, D> L;
-    if (threadIdx.x < 32) L.exptab[threadIdx.x] = kvexp_exp2_32_table[threadIdx.x];
+    if (threadIdx.x < 64) kvexp_exp_table_to_lds(L.exptab);
     __syncthreads();
 
     const int lane = lane_id();
@@ -1472,79 +1478,87 @@ void attn_wave_kernel(const HeadDev *__restrict__ heads, const WorkItem *__restr
 }
 
 // Ordered merge of a head's split states (softmax.hpp:16-30 merge_state,
-// left to right in split order), then out = acc * (1/l) and lse = m + log l.
-// One wave per merge item (device head, query row): lane = channel
-// (channels lane + 64 h). A separate launch, so the slots written by the split kernel are
-// visible without fences.
-// One batch of the merge: splits [s0, s0 + cnt) (cnt <= B), every load
-// issued before any use (indices clamped), then folded in split order.
-template <int D, int B>
-__device__ __forceinline__ void merge_batch(const float *slots, int g, int s0, int cnt, const uint64_t *tab,
-                                            float (&a)[D / 64], float &mf, float &lf) {
-    constexpr int H = D / 64, SF = Shape<D>::kSlotFloats;
-    const int lane = lane_id();
-    float ab[B][H];
-#pragma unroll
-    for (int j = 0; j < B; ++j)
-#pragma unroll
-        for (int c = 0; c < H; ++c)
-            ab[j][c] = slots[size_t(s0 + min(j, cnt - 1)) * SF + 2 * kSlotQ + g * D + 64 * c + lane];
-    float ms[(B + 63) / 64], lb[(B + 63) / 64];
-#pragma unroll
-    for (int h = 0; h < (B + 63) / 64; ++h) {
-        const int j = 64 * h + lane;
-        const float *ls = slots + size_t(s0 + min(j, cnt - 1)) * SF;
-        ms[h] = j < cnt ? ls[g] : -__builtin_inff();
-        lb[h] = ls[kSlotQ + g];
-    }
-#pragma unroll
-    for (int h = 0; h < (B + 63) / 64; ++h) {
-        if (64 * h >= cnt) break;
-        // lane = split s0 + 64h + lane: running maximum and the two exponentials
-        const float mm = fmaxf(wave_scan_max(ms[h]), mf);
-        const float mprev = wave_shift_up(mm, mf);
-        const float e1 = kvexp_expf_nonpos_nb(mprev - mm, tab); // scale of the running state
-        const float e2 = kvexp_expf_nonpos_nb(ms[h] - mm, tab); // scale of split s0 + 64h + lane
-        mf = readlane_f32(mm, min(64, cnt - 64 * h) - 1);
-#pragma unroll
-        for (int jj = 0; jj < 64; ++jj) {
-            if (64 * h + jj < cnt) {
-                const float x1 = readlane_f32(e1, jj), x2 = readlane_f32(e2, jj);
-#pragma unroll
-                for (int c = 0; c < H; ++c) a[c] = fmaf(a[c], x1, ab[64 * h + jj][c] * x2);
-                lf = fmaf(lf, x1, readlane_f32(lb[h], jj) * x2);
-            }
-        }
-    }
-}
-
+// left to right in split order; dispatch.cpp:98-103), then out = acc * (1/l)
+// and lse = m + log l. One wave per merge item (device head, query row): lane
+// = channel (channels lane + 64 h) for the accumulators. A separate launch,
+// so the slots written by the split kernel are visible without fences.
+//
+// Splits go in batches of kMergeBatch. In a batch, lane j first loads m and
+// l of split s0 + j, then every lane its channels of the batch's
+// accumulator rows (all loads in flight together). While the rows arrive,
+// lane j computes the running maximum after split s0 + j (a wave scan; the
+// maximum is exact in any grouping), the two exponentials of its merge step
+// (e1 scales the running state, e2 the split) and l_j * e2 (the same product
+// merge_state forms), and stages the three in LDS. The ordered chains then
+// read them four splits at a time (one broadcast LDS read per operand) and
+// take one fused multiply-add per split and channel, as merge_state does.
+// The first batch starts from split 0's state, as dispatch.cpp does.
 template <int D>
 __global__ __launch_bounds__(4 * 64) void wave_merge_kernel(
     const MergeItem *__restrict__ mitems, int n_mitems, float *__restrict__ out_all,
     float *__restrict__ lse_all, const float *__restrict__ ws) {
     constexpr int H = D / 64, B = Shape<D>::kMergeBatch, SF = Shape<D>::kSlotFloats;
+    static_assert(B % 4 == 0 && B <= kWave, "one split per lane, read four at a time");
     __shared__ uint64_t tab[32];
-    if (threadIdx.x < 32) tab[threadIdx.x] = kvexp_exp2_32_table[threadIdx.x];
+    __shared__ float stage[4][3][B]; // per wave: e1, e2 and l * e2 of the batch's splits
+    if (threadIdx.x < 64) kvexp_exp_table_to_lds(tab);
     __syncthreads();
     const int lane = lane_id();
-    const int mi = __builtin_amdgcn_readfirstlane(int(blockIdx.x) * 4 + (int(threadIdx.x) >> 6));
+    const int w = int(threadIdx.x) >> 6;
+    const int mi = __builtin_amdgcn_readfirstlane(int(blockIdx.x) * 4 + w);
     if (mi >= n_mitems) return;
     const MergeItem it = load_scalar(mitems + mi);
     const int g = it.g;
     const float *slots = ws + size_t(it.ws_base) * SF;
     const int n = it.n_splits;
-    float a[H];
-#pragma unroll
-    for (int c = 0; c < H; ++c) a[c] = slots[2 * kSlotQ + g * D + 64 * c + lane];
-    float mf = slots[g];
-    float lf = slots[kSlotQ + g];
-    for (int s0 = 1; s0 < n; s0 += B) {
+    lds_f32 *st = (lds_f32 *)&stage[w][0][0];
+    float a[H] = {};
+    float mf = 0.0f, lf = 0.0f;
+    for (int s0 = 0; s0 < n; s0 += B) {
         const int cnt = min(B, n - s0);
-        // a half-size batch when it covers the rest (fewer clamped loads)
-        if (cnt <= B / 2)
-            merge_batch<D, B / 2>(slots, g, s0, cnt, tab, a, mf, lf);
-        else
-            merge_batch<D, B>(slots, g, s0, cnt, tab, a, mf, lf);
+        const float *ls = slots + size_t(s0 + min(lane, cnt - 1)) * SF;
+        const float ms = lane < cnt ? ls[g] : -__builtin_inff();
+        const float lb = ls[kSlotQ + g];
+        float ab[B][H];
+#pragma unroll
+        for (int j = 0; j < B; ++j)
+#pragma unroll
+            for (int c = 0; c < H; ++c)
+                ab[j][c] = slots[size_t(s0 + min(j, cnt - 1)) * SF + 2 * kSlotQ + g * D + 64 * c + lane];
+        const int j0 = s0 == 0 ? 1 : 0; // split 0 is the starting state
+        if (s0 == 0) mf = readlane_f32(ms, 0);
+        const float mm = fmaxf(wave_scan_max(ms), mf);
+        const float mprev = wave_shift_up(mm, mf);
+        const float e1 = kvexp_expf_nonpos_nb(mprev - mm, tab); // scale of the running state
+        const float e2 = kvexp_expf_nonpos_nb(ms - mm, tab);    // scale of split s0 + lane
+        if (lane < B) {
+            stage[w][0][lane] = e1;
+            stage[w][1][lane] = e2;
+            stage[w][2][lane] = lb * e2;
+        }
+        mf = readlane_f32(mm, cnt - 1);
+        wave_sync();
+        if (s0 == 0) {
+            lf = readlane_f32(lb, 0);
+#pragma unroll
+            for (int c = 0; c < H; ++c) a[c] = ab[0][c];
+        }
+#pragma unroll
+        for (int jq = 0; jq < B; jq += 4) {
+            if (jq >= cnt) continue;
+            const f4 x1 = *reinterpret_cast<lds_f4 *>(st + jq);
+            const f4 x2 = *reinterpret_cast<lds_f4 *>(st + B + jq);
+            const f4 pl = *reinterpret_cast<lds_f4 *>(st + 2 * B + jq);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                if (jq + k >= j0 && jq + k < cnt) {
+#pragma unroll
+                    for (int c = 0; c < H; ++c) a[c] = fmaf(a[c], x1[k], ab[jq + k][c] * x2[k]);
+                    lf = fmaf(lf, x1[k], pl[k]);
+                }
+            }
+        }
+        wave_sync(); // the next batch overwrites the stage
     }
 #pragma unroll
     for (int c = 0; c < H; ++c) out_all[(size_t(it.q_row) + g) * D + 64 * c + lane] = a[c] * (1.0f / lf);

@@ -1234,11 +1234,12 @@ __global__ __launch_bounds__(kThreads) void plan_refresh_kernel(const EscJob *__
 
 // y = expf(x) in the forms the attention kernels evaluate it (all must equal
 // glibc): thread % 3 == 0 the branching special cases with the constant-memory
-// table, 1 the branch-free form with the table copied to LDS, 2 the
-// non-positive form for x <= 0, +0 and NaN (the branch-free form otherwise).
+// table, 1 the branch-free form with the table copied to LDS (as the wave
+// kernels copy it: from immediates), 2 the non-positive form for x <= 0, +0
+// and NaN (the branch-free form otherwise).
 __global__ __launch_bounds__(256) void expf_kernel(const float *__restrict__ x, float *__restrict__ y, size_t n) {
     __shared__ uint64_t tab[32];
-    if (threadIdx.x < 32) tab[threadIdx.x] = kvexp_exp2_32_table[threadIdx.x];
+    if (threadIdx.x < 64) kvexp_exp_table_to_lds(tab);
     __syncthreads();
     const size_t i = size_t(blockIdx.x) * 256u + threadIdx.x;
     if (i >= n) return;

@@ -45,16 +45,40 @@
 #define KVEXP_EXP_TABLE_QUAL static const
 #endif
 
-KVEXP_EXP_TABLE_QUAL uint64_t kvexp_exp2_32_table[32] = {
-    0x3ff0000000000000ull, 0x3fefd9b0d3158574ull, 0x3fefb5586cf9890full, 0x3fef9301d0125b51ull,
-    0x3fef72b83c7d517bull, 0x3fef54873168b9aaull, 0x3fef387a6e756238ull, 0x3fef1e9df51fdee1ull,
-    0x3fef06fe0a31b715ull, 0x3feef1a7373aa9cbull, 0x3feedea64c123422ull, 0x3feece086061892dull,
-    0x3feebfdad5362a27ull, 0x3feeb42b569d4f82ull, 0x3feeab07dd485429ull, 0x3feea47eb03a5585ull,
-    0x3feea09e667f3bcdull, 0x3fee9f75e8ec5f74ull, 0x3feea11473eb0187ull, 0x3feea589994cce13ull,
-    0x3feeace5422aa0dbull, 0x3feeb737b0cdc5e5ull, 0x3feec49182a3f090ull, 0x3feed503b23e255dull,
-    0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,
-    0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull,
-};
+#define KVEXP_EXP2_32_VALUES \
+    0x3ff0000000000000ull, 0x3fefd9b0d3158574ull, 0x3fefb5586cf9890full, 0x3fef9301d0125b51ull, \
+    0x3fef72b83c7d517bull, 0x3fef54873168b9aaull, 0x3fef387a6e756238ull, 0x3fef1e9df51fdee1ull, \
+    0x3fef06fe0a31b715ull, 0x3feef1a7373aa9cbull, 0x3feedea64c123422ull, 0x3feece086061892dull, \
+    0x3feebfdad5362a27ull, 0x3feeb42b569d4f82ull, 0x3feeab07dd485429ull, 0x3feea47eb03a5585ull, \
+    0x3feea09e667f3bcdull, 0x3fee9f75e8ec5f74ull, 0x3feea11473eb0187ull, 0x3feea589994cce13ull, \
+    0x3feeace5422aa0dbull, 0x3feeb737b0cdc5e5ull, 0x3feec49182a3f090ull, 0x3feed503b23e255dull, \
+    0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull, \
+    0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull
+
+KVEXP_EXP_TABLE_QUAL uint64_t kvexp_exp2_32_table[32] = {KVEXP_EXP2_32_VALUES};
+
+#if defined(__HIPCC__)
+/* Lane i < 32 of a wave stores table entry i at dst[i] (a copy in LDS). The
+ * entries come from scalar immediates written into the lanes
+ * (v_writelane_b32), not from a load of the table in global memory, so a
+ * kernel that starts with this copy does not wait one or two memory round
+ * trips (the table's address, then its bytes) before its first own loads.
+ * Call with the whole wave active. */
+template <int K>
+__device__ static inline void kvexp_exp_table_lanes(uint32_t &lo, uint32_t &hi) {
+    constexpr uint64_t t[32] = {KVEXP_EXP2_32_VALUES};
+    asm("v_writelane_b32 %0, %1, %2" : "+v"(lo) : "s"(uint32_t(t[K])), "n"(K));
+    asm("v_writelane_b32 %0, %1, %2" : "+v"(hi) : "s"(uint32_t(t[K] >> 32)), "n"(K));
+    if constexpr (K + 1 < 32) kvexp_exp_table_lanes<K + 1>(lo, hi);
+}
+__device__ static inline void kvexp_exp_table_to_lds(uint64_t *dst) {
+    uint32_t lo = 0, hi = 0;
+    kvexp_exp_table_lanes<0>(lo, hi);
+    const int lane = int(__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)));
+    if (lane < 32) dst[lane] = (uint64_t(hi) << 32) | lo;
+}
+#endif
+
 
 #define KVEXP_EXP_INVLN2N (0x1.71547652b82fep+0 * 32.0)
 #define KVEXP_EXP_SHIFT 0x1.8p+52
