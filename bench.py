@@ -489,27 +489,45 @@ def cpu_baseline_c2(R, np, a, q, ks, vs, kxs, vxs, G, D, S, BT) -> dict:
 
 # The split kernel's other bound: SIMD instruction issue. Per chunk of 64
 # tokens at head_dim 64 and 7 query rows a wave issues 256 FP32 matrix-core
-# products (128 score, 128 fold) and, on c2's containers, 983 other
-# vector-ALU instructions (SQ_INSTS_VALU - SQ_INSTS_MFMA per chunk,
-# profiles/attn_wave_c2_sq_counters.md); measured issue costs 8.4 and 2.5
-# SIMD cycles (measured per instruction on gfx950), which do not overlap. Chunks
-# are spread over the 1,024 SIMDs at the 2.4 GHz peak clock. The ideal time
-# is what the SIMDs would take issuing back to back; achieved / ideal is the
-# fraction of that bound the kernel reaches.
-ISSUE_MFMA_PER_CHUNK, ISSUE_VALU_PER_CHUNK, ISSUE_MFMA_CYC, ISSUE_VALU_CYC = 256, 983, 8.4, 2.5
+# products (128 score, 128 fold) and, on c2's containers, about a thousand
+# other vector-ALU instructions; both counts are read from the committed SQ
+# counter summary (SQ_INSTS_MFMA and SQ_INSTS_VALU - SQ_INSTS_MFMA per
+# chunk). A product keeps the matrix pipe busy 8 cycles
+# (SQ_VALU_MFMA_BUSY_CYCLES / SQ_INSTS_MFMA in the same summary), and a
+# vector instruction takes at least 2.8 cycles of the SIMD's issue at three
+# waves per SIMD (the fast class of a per-instruction throughput probe on
+# gfx950; others take 4.2-4.4); the two kinds do not overlap. Chunks are
+# spread over the 1,024 SIMDs at the 2.4 GHz clock the counters show, so
+# ideal_us is a floor: the time the SIMDs would take issuing back to back.
+ISSUE_MFMA_CYC, ISSUE_VALU_CYC = 8.0, 2.8
 SIMDS, CLOCK_GHZ = 1024, 2.4
+SQ_PROFILE = "attn_wave_c2_sq_counters.md"
+
+
+def profile_value(profile: str, key: str):
+    """A `key: value` line of a committed profile summary (None if absent)."""
+    try:
+        for line in open(os.path.join(ROOT, "profiles", profile)):
+            if line.startswith(key + ":"):
+                return float(line.split(":", 1)[1].strip())
+    except OSError:
+        pass
+    return None
 
 
 def issue_roofline(tokens: int, kernel_us: float, three_bit: bool):
     if three_bit:
         return None  # the vector instruction count was measured on encode_bf16's containers
+    mfma = profile_value(SQ_PROFILE, "mfma_per_chunk")
+    valu = profile_value(SQ_PROFILE, "valu_per_chunk")
+    if mfma is None or valu is None:
+        return None
     chunks = tokens / 64
-    cycles = chunks / SIMDS * (ISSUE_MFMA_PER_CHUNK * ISSUE_MFMA_CYC + ISSUE_VALU_PER_CHUNK * ISSUE_VALU_CYC)
+    cycles = chunks / SIMDS * (mfma * ISSUE_MFMA_CYC + valu * ISSUE_VALU_CYC)
     ideal_us = cycles / (CLOCK_GHZ * 1e3)
     return {"bound": "simd-issue", "ideal_us": round(ideal_us, 2), "achieved_us": round(kernel_us, 2),
-            "frac": round(ideal_us / kernel_us, 4), "mfma_per_chunk": ISSUE_MFMA_PER_CHUNK,
-            "valu_per_chunk": ISSUE_VALU_PER_CHUNK, "mfma_cycles": ISSUE_MFMA_CYC, "valu_cycles": ISSUE_VALU_CYC,
-            "source": "profiles/attn_wave_c2_sq_counters.md"}
+            "frac": round(ideal_us / kernel_us, 4), "mfma_per_chunk": mfma, "valu_per_chunk": valu,
+            "mfma_cycles": ISSUE_MFMA_CYC, "valu_cycles": ISSUE_VALU_CYC, "source": "profiles/" + SQ_PROFILE}
 
 
 def bench_config(a, torch, np, kvexp_amd, synth) -> int:
