@@ -1296,7 +1296,10 @@ void attn_wave_kernel(const HeadDev *__restrict__ heads, const WorkItem *__restr
         // DPP prefix maximum (seeded with each row's maximum so far, held in
         // scalar registers), e = exp(s - m) for every token and row, and, for
         // the rows where some token of the chunk moves the maximum,
-        // alpha = exp(m_prev - m). Tokens past the chunk's end get e = 0 and
+        // alpha = exp(m_prev - m) (softmax.hpp:8-14). A token that moves the
+        // maximum has m = s, so its e is exp(0); a token that does not has
+        // m_prev = m, so its alpha is exp(0): one exponential per token and
+        // row gives both. Tokens past the chunk's end get e = 0 and
         // alpha = 1. A row moves in this chunk exactly when one of its valid
         // tokens scores above its running maximum (a NaN score never moves
         // it); the other rows keep their maximum and alpha = 1, whose row of
@@ -1317,7 +1320,7 @@ void attn_wave_kernel(const HeadDev *__restrict__ heads, const WorkItem *__restr
 #pragma unroll
         for (int g0 = 0; g0 < G; g0 += 4) {
             constexpr int B = 4;
-            float m[B], x[B];
+            float m[B], mp[B], x[B];
             double kd[B], rr[B];
             uint64_t tb[B];
 #pragma unroll
@@ -1325,7 +1328,13 @@ void attn_wave_kernel(const HeadDev *__restrict__ heads, const WorkItem *__restr
                 if (g0 + b >= G) break;
                 const int g = g0 + b;
                 m[b] = max_f32(mi[g], msc[g]);
-                x[b] = s[g] - m[b];
+                // the maximum before this token; the token moves it exactly
+                // when it scores above it, and then m = s
+                mp[b] = wave_shift_up(m[b], msc[g]);
+                // one exponential per token: alpha's argument where the token
+                // moves the maximum (its e is exp(0)), e's elsewhere (its
+                // alpha is exp(0), or NaN where m_prev - m is)
+                x[b] = s[g] > mp[b] ? mp[b] - s[g] : s[g] - m[b];
                 kvexp_expf_reduce(x[b], kd[b], rr[b]);
                 tb[b] = tab[uint32_t(__double_as_longlong(kd[b])) & 31u];
             }
@@ -1333,17 +1342,25 @@ void attn_wave_kernel(const HeadDev *__restrict__ heads, const WorkItem *__restr
             for (int b = 0; b < B; ++b) {
                 if (g0 + b >= G) break;
                 const int g = g0 + b;
-                const float e = kvexp_expf_finish(kd[b], rr[b], tb[b]);
+                float y = kvexp_expf_finish(kd[b], rr[b], tb[b]);
                 // glibc's expf gives +0 below -0x1.9fe368p6 (the core does not)
-                S.eT[g][ln] = (ln < n && !(x[b] < -0x1.9fe368p6f)) ? e : 0.0f;
+                y = x[b] < -0x1.9fe368p6f ? 0.0f : y;
                 if ((rowmv >> g) & 1u) {
-                    const float dg = wave_shift_up(m[b], msc[g]) - m[b];
+                    const float dg = mp[b] - m[b];
                     // alpha != 1 exactly when m_prev - m is not zero (NaN included)
                     amask |= __ballot(!(dg == 0.0f)) & nmask;
-                    S.aT[g][ln] = ln < n ? kvexp_expf_nonpos_nb(dg, tab) : 1.0f;
+                    // a moving token: e = exp(s - m) with s = m, that is exp(0)
+                    // = 1, or NaN where s is infinite (s - m + 1 gives both);
+                    // elsewhere alpha = exp(dg) with dg 0 or NaN (dg + 1)
+                    const bool mv = s[g] > mp[b];
+                    const float e = mv ? (s[g] - m[b]) + 1.0f : y;
+                    const float al = mv ? y : dg + 1.0f;
+                    S.eT[g][ln] = ln < n ? e : 0.0f;
+                    S.aT[g][ln] = ln < n ? al : 1.0f;
                     msc[g] = readlane_f32(m[b], n - 1);
-                } else if ((prevmv >> g) & 1u) {
-                    S.aT[g][ln] = 1.0f;
+                } else {
+                    S.eT[g][ln] = ln < n ? y : 0.0f;
+                    if ((prevmv >> g) & 1u) S.aT[g][ln] = 1.0f;
                 }
             }
         }
