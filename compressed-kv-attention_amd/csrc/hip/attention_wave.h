@@ -1158,9 +1158,6 @@ void attn_wave_kernel(const HeadDev *__restrict__ heads, const WorkItem *__restr
 #pragma unroll
     for (int g = 0; g < G; ++g) msc[g] = -__builtin_inff();
     float lvec = 0.0f; // lane g < G holds l of query row g
-    // rows whose maximum moved in the previous chunk (their row of aT holds
-    // alphas other than 1); every row at the start, when aT is unwritten
-    uint32_t prevmv = (1u << G) - 1u;
 
     Cursor kc{}, vc{};
     typename RegsOf<XKV, D>::T RK, RV;
@@ -1294,29 +1291,23 @@ void attn_wave_kernel(const HeadDev *__restrict__ heads, const WorkItem *__restr
         stamp(2); // scores done
         // 3. softmax coefficients, lane = token: the running maxima by an exact
         // DPP prefix maximum (seeded with each row's maximum so far, held in
-        // scalar registers), e = exp(s - m) for every token and row, and, for
-        // the rows where some token of the chunk moves the maximum,
-        // alpha = exp(m_prev - m) (softmax.hpp:8-14). A token that moves the
-        // maximum has m = s, so its e is exp(0); a token that does not has
-        // m_prev = m, so its alpha is exp(0): one exponential per token and
-        // row gives both. Tokens past the chunk's end get e = 0 and
-        // alpha = 1. A row moves in this chunk exactly when one of its valid
-        // tokens scores above its running maximum (a NaN score never moves
-        // it); the other rows keep their maximum and alpha = 1, whose row of
-        // aT is only written again when the previous chunk moved it. The
-        // exponentials run in batches of up to four rows: every row's
-        // reduction and table read, then every row's polynomial, so that the
-        // table reads are in flight together.
+        // scalar registers), then e = exp(s - m) and alpha = exp(m_prev - m)
+        // for every token and row (softmax.hpp:8-14). A token moves its row's
+        // maximum exactly when it scores above the maximum before it (a NaN
+        // score never does), and then m = s, so its e is exp(0); a token that
+        // does not has m_prev = m, so its alpha is exp(0) (NaN where the
+        // maximum is infinite, as in the reference): one exponential per
+        // token and row gives both, with no branch on the rows. Tokens past
+        // the chunk's end get e = 0 and alpha = 1. The exponentials run in
+        // batches of up to four rows: every row's reduction and table read,
+        // then every row's polynomial, so that the table reads are in flight
+        // together.
         const uint64_t nmask = n >= kChunk ? ~0ull : ((1ull << n) - 1ull);
         float mi[G];
         uint64_t amask = 0;
 #pragma unroll
         for (int g = 0; g < G; ++g) mi[g] = s[g];
         wave_scan_max_rows<G>(mi);
-        uint32_t rowmv = 0;
-#pragma unroll
-        for (int g = 0; g < G; ++g) rowmv |= (__ballot(s[g] > msc[g]) & nmask) != 0 ? 1u << g : 0u;
-        rowmv = __builtin_amdgcn_readfirstlane(rowmv);
 #pragma unroll
         for (int g0 = 0; g0 < G; g0 += 4) {
             constexpr int B = 4;
@@ -1345,26 +1336,20 @@ void attn_wave_kernel(const HeadDev *__restrict__ heads, const WorkItem *__restr
                 float y = kvexp_expf_finish(kd[b], rr[b], tb[b]);
                 // glibc's expf gives +0 below -0x1.9fe368p6 (the core does not)
                 y = x[b] < -0x1.9fe368p6f ? 0.0f : y;
-                if ((rowmv >> g) & 1u) {
-                    const float dg = mp[b] - m[b];
-                    // alpha != 1 exactly when m_prev - m is not zero (NaN included)
-                    amask |= __ballot(!(dg == 0.0f)) & nmask;
-                    // a moving token: e = exp(s - m) with s = m, that is exp(0)
-                    // = 1, or NaN where s is infinite (s - m + 1 gives both);
-                    // elsewhere alpha = exp(dg) with dg 0 or NaN (dg + 1)
-                    const bool mv = s[g] > mp[b];
-                    const float e = mv ? (s[g] - m[b]) + 1.0f : y;
-                    const float al = mv ? y : dg + 1.0f;
-                    S.eT[g][ln] = ln < n ? e : 0.0f;
-                    S.aT[g][ln] = ln < n ? al : 1.0f;
-                    msc[g] = readlane_f32(m[b], n - 1);
-                } else {
-                    S.eT[g][ln] = ln < n ? y : 0.0f;
-                    if ((prevmv >> g) & 1u) S.aT[g][ln] = 1.0f;
-                }
+                const float dg = mp[b] - m[b];
+                // alpha != 1 exactly when m_prev - m is not zero (NaN included)
+                amask |= __ballot(!(dg == 0.0f)) & nmask;
+                // a moving token: e = exp(s - m) with s = m, that is exp(0)
+                // = 1, or NaN where s is infinite (s - m + 1 gives both);
+                // elsewhere alpha = exp(dg) with dg 0 or NaN (dg + 1)
+                const bool mv = s[g] > mp[b];
+                const float e = mv ? (s[g] - m[b]) + 1.0f : y;
+                const float al = mv ? y : dg + 1.0f;
+                S.eT[g][ln] = ln < n ? e : 0.0f;
+                S.aT[g][ln] = ln < n ? al : 1.0f;
+                msc[g] = readlane_f32(m[b], n - 1);
             }
         }
-        prevmv = rowmv;
         wave_sync();
 
         stamp(3); // softmax coefficients in LDS
