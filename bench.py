@@ -714,7 +714,7 @@ def phase_trace(a) -> int:
         kvexp_amd.check(L.kvexp_hip_encode_trace_read(buf.ctypes.data_as(C.c_void_p), buf.size))
         t = buf.reshape(32768, 12)[:nb].astype(np.int64)
         life = t[:, 8] - t[:, 0]
-        names = ["job + ticket", "(none)", "tokens arrive", "histograms", "window bases + mode",
+        names = ["histograms cleared", "(none)", "tokens arrive", "histograms", "window bases + mode",
                  "codes + escape ranks", "look-back", "stores issued"]
         print(f"c2 prefill: {nb} blocks; block life mean {life.mean():.0f} cycles (min {life.min()}, max {life.max()})")
         for i, n in enumerate(names):
@@ -724,9 +724,24 @@ def phase_trace(a) -> int:
         polls = t[:, 9]
         print(f"  look-back waits: {np.mean(polls > 0) * 100:.1f} % of blocks polled again; "
               f"mean {polls.mean():.2f}, max {polls.max()}")
-        b = np.arange(nb) % (S // BT)
-        print(f"  ticket equals blockIdx.x for {np.mean(t[:, 11] == b) * 100:.1f} % of blocks "
-              f"({np.mean(np.abs(t[:, 11] - b) <= 8) * 100:.1f} % within 8)")
+        # the persistent workgroups: blocks per workgroup and how much of the
+        # launch each spends inside its blocks
+        # (a workgroup's blocks run on one CU, whose clock they share)
+        job = np.arange(nb) // (S // BT)
+        wg = job * 65536 + t[:, 11]
+        first, last, busy, count = {}, {}, {}, {}
+        for k, t0, t1, lf in zip(wg, t[:, 0], t[:, 8], life):
+            first[k] = min(first.get(k, t0), t0)
+            last[k] = max(last.get(k, t1), t1)
+            busy[k] = busy.get(k, 0) + lf
+            count[k] = count.get(k, 0) + 1
+        keys = list(busy)
+        span = np.array([last[k] - first[k] for k in keys])
+        frac = np.array([busy[k] for k in keys]) / span
+        cnt = np.array([count[k] for k in keys])
+        print(f"  {int(t[:, 11].max()) + 1} workgroups per job, {len(keys)} in all; blocks per workgroup "
+              f"{cnt.mean():.1f} (min {cnt.min()}, max {cnt.max()}); a workgroup's first-to-last-block span "
+              f"{span.mean():.0f} cycles, {frac.mean() * 100:.1f} % of it inside its blocks")
         return 0
     config = a.config
     if config not in ("c2", "c4"):

@@ -105,7 +105,8 @@ struct Shape {
     static constexpr int kRowRegs = kSmRegs + D / 32; // + its 4-bit codes: what a coded row needs
     static constexpr int kHalves = D / 64;          // channels per lane in the fold (lane, lane + 64, ...)
     static constexpr int kWaves = D == 64 ? 4 : (D == 128 ? 2 : 1); // waves per workgroup (LDS: see WaveLds)
-    static constexpr int kMergeBatch = D == 256 ? 32 : 64; // splits per merge batch (one per lane; their rows in flight together)
+    // splits per merge batch (one per lane; their rows in flight together)
+    static constexpr int kMergeBatch = D == 256 ? 32 : 64;
 };
 
 // Per-wave LDS. The tile holds the chunk's K rows (row t: the D BF16 of

@@ -515,10 +515,17 @@ __global__ __launch_bounds__(kThreads) void append_tail_kernel(const AppendJobDe
 // ------------------------------------------------ encode: one fused pass --
 // Statistics, place and bytes of every block in one launch, reading the
 // tokens once (the three launches above read them twice). The grid is
-// [blocks of the longest job] x [jobs]; a workgroup takes the next block of
-// its job (blockIdx.y) from the job's ticket counter, so every earlier block
-// of the job has already started (workgroups past the job's blocks draw no
-// ticket and return at once); it holds the block's tokens in
+// [P] x [jobs], P workgroups per job, as many as stay resident together (at
+// most the longest job's block count); a workgroup takes its job's
+// (blockIdx.y) blocks one at a time from the job's ticket counter, so every
+// earlier block of the job has already been taken by a running workgroup
+// (which finishes its current block first and then that one). It draws its
+// next ticket as soon as it starts a block and, once the ticket is back
+// (after the histograms), issues the next block's token loads, so that
+// neither round trip stands on a block's path but the first one's. It stops
+// at its first ticket past the job's blocks (the one that draws the job's
+// last ticket, number n_blocks + P - 1, resets the counter). A block: it
+// holds the block's tokens in
 // registers (chunks of 8 elements of one row, 16 bytes, NL chunks per
 // thread), counts each channel's exponents into LDS byte counters, slides the
 // code windows (one (window, channel) pair per thread, so that every wave
@@ -629,6 +636,10 @@ __device__ __forceinline__ EscRanks<NL> fused_escape_ranks(const uint32_t (&v)[E
 // 512 / waves without spilling): 8 with up to four chunk rows per thread.
 template <int NL>
 constexpr int kFusedWaves = NL <= 4 ? 8 : 4;
+// Fewest waves per SIMD the compiler may plan for: one block's tokens in
+// registers beside the next block's (NL 16-byte loads each).
+template <int NL>
+constexpr int kFusedWavesMin = NL <= 2 ? 8 : (NL <= 4 ? 6 : 3);
 
 // Dynamic LDS of the one-pass encoder: the histogram columns, or the
 // largest block (raw: header + 2 bytes per element) staged for its copy,
@@ -642,7 +653,7 @@ __host__ __device__ constexpr size_t fused_lds_bytes(int dim, int bt) {
 // JOBS: the jobs are in device memory (appends); else the one job is a
 // kernel argument (an encode), read from the argument segment.
 template <int NL, bool JOBS>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(kFusedWaves<NL>, kFusedWaves<NL>))) void
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(kFusedWavesMin<NL>, kFusedWaves<NL>))) void
 encode_fused_kernel(const AppendJobDev *__restrict__ jobs, AppendJobDev one, int dim, int bt, int modes,
                     uint64_t *__restrict__ state, uint32_t *__restrict__ tickets, uint32_t epoch,
                     uint32_t *__restrict__ status) {
@@ -651,7 +662,7 @@ encode_fused_kernel(const AppendJobDev *__restrict__ jobs, AppendJobDev one, int
     extern __shared__ uint32_t fz_lds[];
     uint32_t *fz_hist = fz_lds;
     uint8_t *stage = reinterpret_cast<uint8_t *>(fz_lds);
-    __shared__ uint32_t s_ticket;
+    __shared__ uint32_t s_ticket, s_next;
     __shared__ int s_lo[kWaves], s_hi[kWaves], s_esc[kWaves][3];
     __shared__ __align__(16) uint8_t s_base[3][kMaxDim]; // window bases of the 2-, 3- and 4-bit codes
     __shared__ uint16_t s_key[3 * kMaxDim];               // best (coverage, base) of the upper half of each range
@@ -663,342 +674,384 @@ encode_fused_kernel(const AppendJobDev *__restrict__ jobs, AppendJobDev one, int
 #if defined(KVEXP_PHASE_TRACE)
     unsigned long long enc_tr[9];
 #endif
-    KVEXP_ENC_MARK(0);
 
-    // ---- ticket (every workgroup of the job's grid row draws one, so the
-    // one that draws the row's last resets the counter) while the job loads
+    // ---- first ticket while the job loads; every workgroup of the job's
+    // grid row draws tickets until one lies past the job's blocks, so the
+    // job's draws number n_blocks + P, and the one that draws the last
+    // resets the counter
+    const AppendJobDev j = JOBS ? jobs[jx] : one;
+    const uint32_t last_draw = uint32_t(j.nb) + gridDim.x - 1u;
     if (tid == 0) {
         const uint32_t t = atomicAdd(tickets + jx, 1u);
-        if (t == gridDim.x - 1u) atomicExch(tickets + jx, 0u);
+        if (t == last_draw) atomicExch(tickets + jx, 0u);
         s_ticket = t;
     }
-    const AppendJobDev j = JOBS ? jobs[jx] : one;
-#pragma unroll 1
-    for (int i = tid; i < dim * kHistStride; i += kThreads) fz_hist[i] = 0u;
-    __syncthreads();
-    const int b = int(s_ticket);
-    if (b >= j.nb) { // past the job's blocks (or a counter not left at 0: then nothing of the job runs)
-        if (tid == 0 && b >= int(gridDim.x)) atomicOr(status, kStLookback);
-        return;
-    }
-    const int g = j.blk0 + b; // look-back entry of the block
-    KVEXP_ENC_MARK(1);
-    const int n = min(bt, j.seq - b * bt);
-#if defined(KVEXP_PHASE_TRACE)
-    asm volatile("" ::"v"(n));
-#endif
-    KVEXP_ENC_MARK(2);
-    const EncRows src = job_rows(j, b, bt, dim);
-    const int chunks = n * dim / 8, cpr = dim / 8, split = src.split / 8;
-    const float inv_cpr = __builtin_amdgcn_rcpf(float(cpr));
-
-    // ---- the block's tokens into registers; channel histograms
     // first channel of chunk c (8 * (c mod dim / 8); the float quotient is
     // exact to far below its distance from an integer, c < 4096)
+    const int cpr = dim / 8;
+    const float inv_cpr = __builtin_amdgcn_rcpf(float(cpr));
     auto chunk_d0 = [&](int c) {
         const int row = int((float(c) + 0.5f) * inv_cpr);
         return 8 * (c - row * cpr);
     };
-    u32x4_t x[NL];
-    uint32_t pk_lo = 0xFFFFFFFFu, pk_hi = 0u; // exponent fields (bits 14..7 of each half), smallest and largest
+    // the tokens of block bb into registers: chunks of 8 elements of one
+    // row, NL per thread, all loads in flight together (chunks past the
+    // block read chunk 0)
+    auto load_tokens = [&](int bb, u32x4_t (&dst)[NL]) {
+        const EncRows sr = job_rows(j, bb, bt, dim);
+        const int nch = min(bt, j.seq - bb * bt) * dim / 8, spl = sr.split / 8;
 #pragma unroll
-    for (int k = 0; k < NL; ++k) { // all loads in flight together: chunks past the block read chunk 0
-        const int c = k * kThreads + tid < chunks ? k * kThreads + tid : 0;
-        const uint16_t *p = c < split ? src.a + 8 * size_t(c) : src.b + 8 * size_t(c - split);
-        x[k] = *(g_cu32x4 *)(p);
-    }
+        for (int k = 0; k < NL; ++k) {
+            const int c = k * kThreads + tid < nch ? k * kThreads + tid : 0;
+            const uint16_t *p = c < spl ? sr.a + 8 * size_t(c) : sr.b + 8 * size_t(c - spl);
+            dst[k] = *(g_cu32x4 *)(p);
+        }
+    };
+    __syncthreads();
+    u32x4_t x[NL], xn[NL];
+    int b = int(s_ticket);
+    if (b < j.nb) load_tokens(b, x);
+#pragma unroll 1
+    while (true) {
+        // the thread index through an empty asm, so that the addresses made
+        // from it are made again in each block rather than hoisted out of the
+        // loop and held in registers across it
+        const int tid = [] {
+            int t = int(threadIdx.x);
+            asm volatile("" : "+v"(t));
+            return t;
+        }();
+        const int lane = tid & (kWave - 1), w = tid >> 6;
+        if (b >= j.nb) { // past the job's blocks (or a counter not left at 0: then nothing of the job runs)
+            if (tid == 0 && uint32_t(b) > last_draw) atomicOr(status, kStLookback);
+            return;
+        }
+        KVEXP_ENC_MARK(0);
+        // the next ticket, consumed after the histograms
+        uint32_t tn = 0;
+        if (tid == 0) tn = atomicAdd(tickets + jx, 1u);
+#pragma unroll 1
+        for (int i = tid; i < dim * kHistStride; i += kThreads) fz_hist[i] = 0u;
+        __syncthreads();
+        polls = 0;
+        const int g = j.blk0 + b; // look-back entry of the block
+        KVEXP_ENC_MARK(1);
+        const int n = min(bt, j.seq - b * bt);
 #if defined(KVEXP_PHASE_TRACE)
-    asm volatile("" ::"v"(x[NL - 1][0]), "v"(x[0][0]));
+        asm volatile("" ::"v"(n));
 #endif
-    KVEXP_ENC_MARK(3);
-    // Lanes that share a chunk column (the rows of one chunk position) count
-    // their 8 elements in an order rotated by the row (step h takes element
-    // (h + row) % 8), so that the 64 lanes of an LDS add hit different
-    // channel columns rather than 8 lanes one counter.
-#pragma unroll
-    for (int k = 0; k < NL; ++k) {
-        const int c = k * kThreads + tid;
-        if (c < chunks) {
-            const int row = int((float(c) + 0.5f) * inv_cpr);
-            const int rot = row & 7;
-            uint32_t *col = fz_hist + 8 * (c - row * cpr) * kHistStride;
-            // the chunk rotated right by 16 * rot bits: element h of v is element (h + rot) % 8
-            u32x4_t v = x[k];
-            if (rot & 4) v = u32x4_t{v[2], v[3], v[0], v[1]};
-            if (rot & 2) v = u32x4_t{v[1], v[2], v[3], v[0]};
-            if (rot & 1)
-                v = u32x4_t{__builtin_amdgcn_alignbit(v[1], v[0], 16), __builtin_amdgcn_alignbit(v[2], v[1], 16),
-                            __builtin_amdgcn_alignbit(v[3], v[2], 16), __builtin_amdgcn_alignbit(v[0], v[3], 16)};
-#pragma unroll
-            for (int h = 0; h < 8; ++h) {
-                const uint32_t e = (v[h >> 1] >> (16 * (h & 1) + 7)) & 0xFFu;
-                atomicAdd(col + ((h + rot) & 7) * kHistStride + int(e >> 2), 1u << (8u * (e & 3u)));
-            }
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const uint32_t ef = x[k][i] & 0x7F807F80u;
-                pk_lo = min(min(pk_lo, ef & 0xFFFFu), ef >> 16);
-                pk_hi = max(max(pk_hi, ef & 0xFFFFu), ef >> 16);
-            }
-        }
-    }
-    const int e_lo = wave_min_i32(pk_lo == 0xFFFFFFFFu ? 255 : int(pk_lo >> 7));
-    const int e_hi = wave_max_i32(int(pk_hi >> 7));
-    if (lane == 0) {
-        s_lo[w] = e_lo;
-        s_hi[w] = e_hi;
-    }
-    __syncthreads();
-    KVEXP_ENC_MARK(4);
-    int blk_lo = 255, blk_hi = 0;
-#pragma unroll
-    for (int i = 0; i < kWaves; ++i) {
-        blk_lo = min(blk_lo, s_lo[i]);
-        blk_hi = max(blk_hi, s_hi[i]);
-    }
+        KVEXP_ENC_MARK(2);
+        const int chunks = n * dim / 8;
 
-    // ---- best_base of each (window, channel) (codec.cpp:18-35): the most
-    // covered exponents, then the smallest base; bases outside
-    // [blk_lo - width + 1, blk_hi] cover nothing. Each range is split in two
-    // halves taken by different waves (tasks [0, pairs) the lower halves,
-    // [pairs, 2 pairs) the upper); a half's best is the key
-    // coverage * 256 + 255 - base, so the larger key is the better base.
-    const int nwin = (modes & 8) ? 3 : 2;
-    const int pairs = nwin * dim;
-    int key_lo[3] = {0, 0, 0}; // this thread's lower-half results (tasks tid, tid + 256, tid + 512)
-#pragma unroll
-    for (int r = 0; r < 6; ++r) {
-        const int t = tid + r * kThreads;
-        if (t >= 2 * pairs) break;
-        const int half = int(t >= pairs);
-        const int pt = t - half * pairs;
-        const int wi = int(pt >= dim) + int(pt >= 2 * dim);
-        const int d = pt - wi * dim;
-        const int bi = wi == 0 ? 0 : (nwin == 2 ? 2 : wi);
-        const int width = (4 << bi) - 1;
-        const int lo0 = min(max(0, blk_lo - width + 1), 256 - width);
-        const int hi0 = min(blk_hi, 256 - width);
-        const int mid = (lo0 + hi0 + 1) >> 1;
-        const int lo = half ? mid : lo0, hi = half ? hi0 : mid - 1;
-        int key = 0;
-        if (lo <= hi) {
-            const uint8_t *hb = reinterpret_cast<const uint8_t *>(fz_hist + d * kHistStride);
-            int cov = 0;
-            for (int e = lo; e < lo + width; ++e) cov += hb[e];
-            int best = cov, best_b = lo;
-#pragma unroll 4
-            for (int base = lo + 1; base <= hi; ++base) {
-                cov += int(hb[base + width - 1]) - int(hb[base - 1]);
-                if (cov > best) {
-                    best = cov;
-                    best_b = base;
-                }
-            }
-            key = best * 256 + 255 - best_b;
-        }
-        if (half) s_key[pt] = uint16_t(key);
-        else if (r < 3) key_lo[r] = key;
-    }
-    __syncthreads();
-    int esc[3] = {0, 0, 0};
-#pragma unroll
-    for (int r = 0; r < 3; ++r) {
-        const int pt = tid + r * kThreads;
-        if (pt >= pairs) break;
-        const int wi = int(pt >= dim) + int(pt >= 2 * dim);
-        const int d = pt - wi * dim;
-        const int bi = wi == 0 ? 0 : (nwin == 2 ? 2 : wi);
-        const int key = max(key_lo[r], int(s_key[pt]));
-        s_base[bi][d] = uint8_t(255 - (key & 255));
-        esc[bi] += n - (key >> 8);
-    }
-#pragma unroll
-    for (int bi = 0; bi < 3; ++bi) esc[bi] = wave_sum_i32(esc[bi]);
-    if (lane == 0) {
-#pragma unroll
-        for (int bi = 0; bi < 3; ++bi) s_esc[w][bi] = esc[bi];
-    }
-    __syncthreads();
-    int cand[3] = {0, 0, 0};
-#pragma unroll
-    for (int i = 0; i < kWaves; ++i) {
-#pragma unroll
-        for (int bi = 0; bi < 3; ++bi) cand[bi] += s_esc[i][bi];
-    }
-    const EncBlockMeta m = choose_mode(cand, n, dim, modes, nwin);
-    KVEXP_ENC_MARK(5);
-
-    // ---- publish the size
-    if (tid == 0)
-        __hip_atomic_store(state + g, lb_word(epoch, b == 0 ? 2u : 1u, uint64_t(m.bytes)), __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
-
-    // ---- codes and sentinel counts
-    const int mode = m.mode;
-    const uint32_t width = (1u << mode) - 1u;
-    uint32_t cw[NL];
-    uint32_t cnt_pk[EscRanks<NL>::NP] = {}; // sentinels per chunk, 16 bits each
-#pragma unroll
-    for (int k = 0; k < NL; ++k) {
-        cw[k] = 0u;
-        if (mode != 0 && k * kThreads + tid < chunks) {
-            int cnt = 0;
-            const uint2 bb = *reinterpret_cast<const uint2 *>(&s_base[mode - 2][chunk_d0(k * kThreads + tid)]);
-#pragma unroll
-            for (int h = 0; h < 8; ++h) {
-                const uint32_t e = (x[k][h >> 1] >> (16 * (h & 1) + 7)) & 0xFFu;
-                const uint32_t base = ((h < 4 ? bb.x : bb.y) >> (8 * (h & 3))) & 0xFFu;
-                const uint32_t delta = e - base; // wraps when e < base
-                const bool hit = delta < width;
-                cw[k] |= (hit ? delta : width) << (mode * h);
-                cnt += hit ? 0 : 1;
-            }
-            cnt_pk[k / 2] |= uint32_t(cnt) << (16 * (k % 2));
-        }
-    }
-    // the escape ranks; the barrier in it also ends every read of the
-    // histograms, whose LDS now takes the staged block
-    const EscRanks<NL> er = fused_escape_ranks<NL>(cnt_pk, s_scan);
-    KVEXP_ENC_MARK(6);
-
-    // ---- the block's bytes, staged in LDS in their final order
-    if (tid < 8) {
-        const int ne = mode == 0 ? 0 : m.n_escape;
-        const uint32_t hdr[8] = {uint32_t(mode), uint32_t(n), uint32_t(ne & 0xFF), uint32_t(ne >> 8),
-                                 uint32_t(dim & 0xFF), uint32_t(dim >> 8), 0u, 0u};
-        stage[tid] = uint8_t(hdr[tid]);
-    }
-    uint8_t *body = stage + 8;
-    if (mode == 0) {
+        // ---- channel histograms of the block's tokens (in registers)
+        uint32_t pk_lo = 0xFFFFFFFFu, pk_hi = 0u; // exponent fields (bits 14..7 of each half), smallest and largest
+#if defined(KVEXP_PHASE_TRACE)
+        asm volatile("" ::"v"(x[NL - 1][0]), "v"(x[0][0]));
+#endif
+        KVEXP_ENC_MARK(3);
+        // Lanes that share a chunk column (the rows of one chunk position) count
+        // their 8 elements in an order rotated by the row (step h takes element
+        // (h + row) % 8), so that the 64 lanes of an LDS add hit different
+        // channel columns rather than 8 lanes one counter.
 #pragma unroll
         for (int k = 0; k < NL; ++k) {
             const int c = k * kThreads + tid;
-            typedef u32x4_t __attribute__((aligned(8))) u32x4_a8;
-            if (c < chunks) *reinterpret_cast<u32x4_a8 *>(body + 16 * c) = x[k]; // 8 + 16c: 8-byte aligned
-        }
-    } else {
-        if (2 * tid < dim) // dim <= 256 = kThreads: one pair of bases per thread
-            *reinterpret_cast<uint16_t *>(body + 2 * tid) = *reinterpret_cast<const uint16_t *>(&s_base[mode - 2][2 * tid]);
-        uint8_t *sm = body + dim;
-        uint8_t *codes = sm + n * dim;
-        uint8_t *escw = codes + exp_payload_bytes(n, dim, mode);
-#pragma unroll
-        for (int k = 0; k < NL; ++k) {
-            const int c = k * kThreads + tid;
-            if (c >= chunks) continue;
-            // sign and mantissa bytes of the 8 elements: (h >> 8 & 0x80) | (h & 0x7F)
-            uint32_t s4[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const uint32_t mm = x[k][i] & 0x807F807Fu;
-                s4[i] = mm | (mm >> 8); // bytes 0 and 2 hold the two elements' sm bytes
-            }
-            u32x2_t smv;
-            smv.x = __builtin_amdgcn_perm(s4[1], s4[0], 0x06040200u);
-            smv.y = __builtin_amdgcn_perm(s4[3], s4[2], 0x06040200u);
-            *reinterpret_cast<u32x2_t *>(sm + 8 * c) = smv; // 8 + dim + 8c: 8-byte aligned
-            if (mode == 4) {
-                *reinterpret_cast<uint32_t *>(codes + 4 * c) = cw[k];
-            } else if (mode == 2) {
-                *reinterpret_cast<uint16_t *>(codes + 2 * c) = uint16_t(cw[k]);
-            } else {
-                uint8_t *q = codes + 3 * c;
-                q[0] = uint8_t(cw[k]);
-                q[1] = uint8_t(cw[k] >> 8);
-                q[2] = uint8_t(cw[k] >> 16);
-            }
-            if (((cnt_pk[k / 2] >> (16 * (k % 2))) & 0xFFFFu) != 0) {
-                int r = er.rank(k);
+            if (c < chunks) {
+                const int row = int((float(c) + 0.5f) * inv_cpr);
+                const int rot = row & 7;
+                uint32_t *col = fz_hist + 8 * (c - row * cpr) * kHistStride;
+                // the chunk rotated right by 16 * rot bits: element h of v is element (h + rot) % 8
+                u32x4_t v = x[k];
+                if (rot & 4) v = u32x4_t{v[2], v[3], v[0], v[1]};
+                if (rot & 2) v = u32x4_t{v[1], v[2], v[3], v[0]};
+                if (rot & 1)
+                    v = u32x4_t{__builtin_amdgcn_alignbit(v[1], v[0], 16), __builtin_amdgcn_alignbit(v[2], v[1], 16),
+                                __builtin_amdgcn_alignbit(v[3], v[2], 16), __builtin_amdgcn_alignbit(v[0], v[3], 16)};
 #pragma unroll
                 for (int h = 0; h < 8; ++h) {
-                    if (((cw[k] >> (mode * h)) & width) == width) {
-                        if (r < m.n_escape) { // escape words may sit at odd offsets (3-bit codes): bytes
-                            const uint32_t v = x[k][h >> 1] >> (16 * (h & 1));
-                            escw[2 * r] = uint8_t(v);
-                            escw[2 * r + 1] = uint8_t(v >> 8);
+                    const uint32_t e = (v[h >> 1] >> (16 * (h & 1) + 7)) & 0xFFu;
+                    atomicAdd(col + ((h + rot) & 7) * kHistStride + int(e >> 2), 1u << (8u * (e & 3u)));
+                }
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const uint32_t ef = x[k][i] & 0x7F807F80u;
+                    pk_lo = min(min(pk_lo, ef & 0xFFFFu), ef >> 16);
+                    pk_hi = max(max(pk_hi, ef & 0xFFFFu), ef >> 16);
+                }
+            }
+        }
+        const int e_lo = wave_min_i32(pk_lo == 0xFFFFFFFFu ? 255 : int(pk_lo >> 7));
+        const int e_hi = wave_max_i32(int(pk_hi >> 7));
+        if (lane == 0) {
+            s_lo[w] = e_lo;
+            s_hi[w] = e_hi;
+        }
+        if (tid == 0) {
+            if (tn == last_draw) atomicExch(tickets + jx, 0u);
+            s_next = tn;
+        }
+        __syncthreads();
+        KVEXP_ENC_MARK(4);
+        int blk_lo = 255, blk_hi = 0;
+#pragma unroll
+        for (int i = 0; i < kWaves; ++i) {
+            blk_lo = min(blk_lo, s_lo[i]);
+            blk_hi = max(blk_hi, s_hi[i]);
+        }
+        // the next block's tokens, in flight while this block is encoded
+        const int bn = int(s_next);
+        if (bn < j.nb) load_tokens(bn, xn);
+
+        // ---- best_base of each (window, channel) (codec.cpp:18-35): the most
+        // covered exponents, then the smallest base; bases outside
+        // [blk_lo - width + 1, blk_hi] cover nothing. Each range is split in two
+        // halves taken by different waves (tasks [0, pairs) the lower halves,
+        // [pairs, 2 pairs) the upper); a half's best is the key
+        // coverage * 256 + 255 - base, so the larger key is the better base.
+        const int nwin = (modes & 8) ? 3 : 2;
+        const int pairs = nwin * dim;
+        int key_lo[3] = {0, 0, 0}; // this thread's lower-half results (tasks tid, tid + 256, tid + 512)
+#pragma unroll
+        for (int r = 0; r < 6; ++r) {
+            const int t = tid + r * kThreads;
+            if (t >= 2 * pairs) break;
+            const int half = int(t >= pairs);
+            const int pt = t - half * pairs;
+            const int wi = int(pt >= dim) + int(pt >= 2 * dim);
+            const int d = pt - wi * dim;
+            const int bi = wi == 0 ? 0 : (nwin == 2 ? 2 : wi);
+            const int width = (4 << bi) - 1;
+            const int lo0 = min(max(0, blk_lo - width + 1), 256 - width);
+            const int hi0 = min(blk_hi, 256 - width);
+            const int mid = (lo0 + hi0 + 1) >> 1;
+            const int lo = half ? mid : lo0, hi = half ? hi0 : mid - 1;
+            int key = 0;
+            if (lo <= hi) {
+                const uint8_t *hb = reinterpret_cast<const uint8_t *>(fz_hist + d * kHistStride);
+                int cov = 0;
+                for (int e = lo; e < lo + width; ++e) cov += hb[e];
+                int best = cov, best_b = lo;
+#pragma unroll 4
+                for (int base = lo + 1; base <= hi; ++base) {
+                    cov += int(hb[base + width - 1]) - int(hb[base - 1]);
+                    if (cov > best) {
+                        best = cov;
+                        best_b = base;
+                    }
+                }
+                key = best * 256 + 255 - best_b;
+            }
+            if (half) s_key[pt] = uint16_t(key);
+            else if (r < 3) key_lo[r] = key;
+        }
+        __syncthreads();
+        int esc[3] = {0, 0, 0};
+#pragma unroll
+        for (int r = 0; r < 3; ++r) {
+            const int pt = tid + r * kThreads;
+            if (pt >= pairs) break;
+            const int wi = int(pt >= dim) + int(pt >= 2 * dim);
+            const int d = pt - wi * dim;
+            const int bi = wi == 0 ? 0 : (nwin == 2 ? 2 : wi);
+            const int key = max(key_lo[r], int(s_key[pt]));
+            s_base[bi][d] = uint8_t(255 - (key & 255));
+            esc[bi] += n - (key >> 8);
+        }
+#pragma unroll
+        for (int bi = 0; bi < 3; ++bi) esc[bi] = wave_sum_i32(esc[bi]);
+        if (lane == 0) {
+#pragma unroll
+            for (int bi = 0; bi < 3; ++bi) s_esc[w][bi] = esc[bi];
+        }
+        __syncthreads();
+        int cand[3] = {0, 0, 0};
+#pragma unroll
+        for (int i = 0; i < kWaves; ++i) {
+#pragma unroll
+            for (int bi = 0; bi < 3; ++bi) cand[bi] += s_esc[i][bi];
+        }
+        const EncBlockMeta m = choose_mode(cand, n, dim, modes, nwin);
+        KVEXP_ENC_MARK(5);
+
+        // ---- publish the size
+        if (tid == 0)
+            __hip_atomic_store(state + g, lb_word(epoch, b == 0 ? 2u : 1u, uint64_t(m.bytes)), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+
+        // ---- codes and sentinel counts
+        const int mode = m.mode;
+        const uint32_t width = (1u << mode) - 1u;
+        uint32_t cw[NL];
+        uint32_t cnt_pk[EscRanks<NL>::NP] = {}; // sentinels per chunk, 16 bits each
+#pragma unroll
+        for (int k = 0; k < NL; ++k) {
+            cw[k] = 0u;
+            if (mode != 0 && k * kThreads + tid < chunks) {
+                int cnt = 0;
+                const uint2 bb = *reinterpret_cast<const uint2 *>(&s_base[mode - 2][chunk_d0(k * kThreads + tid)]);
+#pragma unroll
+                for (int h = 0; h < 8; ++h) {
+                    const uint32_t e = (x[k][h >> 1] >> (16 * (h & 1) + 7)) & 0xFFu;
+                    const uint32_t base = ((h < 4 ? bb.x : bb.y) >> (8 * (h & 3))) & 0xFFu;
+                    const uint32_t delta = e - base; // wraps when e < base
+                    const bool hit = delta < width;
+                    cw[k] |= (hit ? delta : width) << (mode * h);
+                    cnt += hit ? 0 : 1;
+                }
+                cnt_pk[k / 2] |= uint32_t(cnt) << (16 * (k % 2));
+            }
+        }
+        // the escape ranks; the barrier in it also ends every read of the
+        // histograms, whose LDS now takes the staged block
+        const EscRanks<NL> er = fused_escape_ranks<NL>(cnt_pk, s_scan);
+        KVEXP_ENC_MARK(6);
+
+        // ---- the block's bytes, staged in LDS in their final order
+        if (tid < 8) {
+            const int ne = mode == 0 ? 0 : m.n_escape;
+            const uint32_t hdr[8] = {uint32_t(mode), uint32_t(n), uint32_t(ne & 0xFF), uint32_t(ne >> 8),
+                                     uint32_t(dim & 0xFF), uint32_t(dim >> 8), 0u, 0u};
+            stage[tid] = uint8_t(hdr[tid]);
+        }
+        uint8_t *body = stage + 8;
+        if (mode == 0) {
+#pragma unroll
+            for (int k = 0; k < NL; ++k) {
+                const int c = k * kThreads + tid;
+                typedef u32x4_t __attribute__((aligned(8))) u32x4_a8;
+                if (c < chunks) *reinterpret_cast<u32x4_a8 *>(body + 16 * c) = x[k]; // 8 + 16c: 8-byte aligned
+            }
+        } else {
+            if (2 * tid < dim) // dim <= 256 = kThreads: one pair of bases per thread
+                *reinterpret_cast<uint16_t *>(body + 2 * tid) =
+                    *reinterpret_cast<const uint16_t *>(&s_base[mode - 2][2 * tid]);
+            uint8_t *sm = body + dim;
+            uint8_t *codes = sm + n * dim;
+            uint8_t *escw = codes + exp_payload_bytes(n, dim, mode);
+#pragma unroll
+            for (int k = 0; k < NL; ++k) {
+                const int c = k * kThreads + tid;
+                if (c >= chunks) continue;
+                // sign and mantissa bytes of the 8 elements: (h >> 8 & 0x80) | (h & 0x7F)
+                uint32_t s4[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const uint32_t mm = x[k][i] & 0x807F807Fu;
+                    s4[i] = mm | (mm >> 8); // bytes 0 and 2 hold the two elements' sm bytes
+                }
+                u32x2_t smv;
+                smv.x = __builtin_amdgcn_perm(s4[1], s4[0], 0x06040200u);
+                smv.y = __builtin_amdgcn_perm(s4[3], s4[2], 0x06040200u);
+                *reinterpret_cast<u32x2_t *>(sm + 8 * c) = smv; // 8 + dim + 8c: 8-byte aligned
+                if (mode == 4) {
+                    *reinterpret_cast<uint32_t *>(codes + 4 * c) = cw[k];
+                } else if (mode == 2) {
+                    *reinterpret_cast<uint16_t *>(codes + 2 * c) = uint16_t(cw[k]);
+                } else {
+                    uint8_t *q = codes + 3 * c;
+                    q[0] = uint8_t(cw[k]);
+                    q[1] = uint8_t(cw[k] >> 8);
+                    q[2] = uint8_t(cw[k] >> 16);
+                }
+                if (((cnt_pk[k / 2] >> (16 * (k % 2))) & 0xFFFFu) != 0) {
+                    int r = er.rank(k);
+#pragma unroll
+                    for (int h = 0; h < 8; ++h) {
+                        if (((cw[k] >> (mode * h)) & width) == width) {
+                            if (r < m.n_escape) { // escape words may sit at odd offsets (3-bit codes): bytes
+                                const uint32_t v = x[k][h >> 1] >> (16 * (h & 1));
+                                escw[2 * r] = uint8_t(v);
+                                escw[2 * r + 1] = uint8_t(v >> 8);
+                            }
+                            ++r;
                         }
-                        ++r;
                     }
                 }
             }
         }
-    }
 
-    // ---- wave 0 finds the block's place while the others wait at the barrier
-    if (w == 0) {
-        int64_t excl = 0;
-        if (b > 0) {
-            int pos = g - 1;
-            auto lb_read = [&]() -> uint64_t {
-                const int idx = pos - lane;
-                return idx >= j.blk0 ? __hip_atomic_load(state + idx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                                     : 0u;
-            };
-            uint64_t wv = lb_read();
-            while (true) {
-                const bool in = pos - lane >= j.blk0;
-                const uint32_t kind = in && uint32_t(wv >> 48) == epoch ? uint32_t(wv >> 46) & 3u : 0u;
-                const uint64_t ends = __ballot(in && kind == 2u);
-                const uint64_t open = __ballot(in && kind == 0u);
-                const int fe = ends ? __ffsll((unsigned long long)ends) - 1 : kWave;
-                const int fo = open ? __ffsll((unsigned long long)open) - 1 : kWave;
-                if (fo < fe) { // a nearer block has not published its size yet
-                    if (++polls > kLookbackPolls) {
-                        if (lane == 0) atomicOr(status, kStLookback);
-                        break;
+        // ---- wave 0 finds the block's place while the others wait at the barrier
+        if (w == 0) {
+            int64_t excl = 0;
+            if (b > 0) {
+                int pos = g - 1;
+                auto lb_read = [&]() -> uint64_t {
+                    const int idx = pos - lane;
+                    return idx >= j.blk0 ? __hip_atomic_load(state + idx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                                         : 0u;
+                };
+                uint64_t wv = lb_read();
+                while (true) {
+                    const bool in = pos - lane >= j.blk0;
+                    const uint32_t kind = in && uint32_t(wv >> 48) == epoch ? uint32_t(wv >> 46) & 3u : 0u;
+                    const uint64_t ends = __ballot(in && kind == 2u);
+                    const uint64_t open = __ballot(in && kind == 0u);
+                    const int fe = ends ? __ffsll((unsigned long long)ends) - 1 : kWave;
+                    const int fo = open ? __ffsll((unsigned long long)open) - 1 : kWave;
+                    if (fo < fe) { // a nearer block has not published its size yet
+                        if (++polls > kLookbackPolls) {
+                            if (lane == 0) atomicOr(status, kStLookback);
+                            break;
+                        }
+                        __builtin_amdgcn_s_sleep(2);
+                        wv = lb_read();
+                        continue;
                     }
-                    __builtin_amdgcn_s_sleep(2);
+                    excl += wave_sum_i64(in && lane <= fe ? int64_t(wv & kLbValueMask) : 0);
+                    if (fe < kWave) break;
+                    pos -= kWave;
                     wv = lb_read();
-                    continue;
                 }
-                excl += wave_sum_i64(in && lane <= fe ? int64_t(wv & kLbValueMask) : 0);
-                if (fe < kWave) break;
-                pos -= kWave;
-                wv = lb_read();
+                if (lane == 0)
+                    __hip_atomic_store(state + g, lb_word(epoch, 2u, uint64_t(excl + m.bytes)), __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
             }
-            if (lane == 0)
-                __hip_atomic_store(state + g, lb_word(epoch, 2u, uint64_t(excl + m.bytes)), __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
+            if (lane == 0) s_excl = excl;
         }
-        if (lane == 0) s_excl = excl;
-    }
-    __syncthreads();
-    KVEXP_ENC_MARK(7);
+        __syncthreads();
+        KVEXP_ENC_MARK(7);
 
-    // ---- the staged bytes to the container: 16-byte aligned stores, the
-    // bytes before the first aligned address and after the last one alone
-    const int64_t off = (j.rebase ? j.offs[0] : 0) + s_excl;
-    uint8_t *p = j.out + off;
-    const int nbytes = int(m.bytes);
-    const int head = min(nbytes, int((16u - (uint32_t(reinterpret_cast<uintptr_t>(p)) & 15u)) & 15u));
-    const int n16 = (nbytes - head) >> 4;
-    const int tail0 = head + 16 * n16;
-    for (int i = tid; i < n16; i += kThreads) {
-        typedef const u32x4_t __attribute__((aligned(1))) u32x4_a1;
-        *(__attribute__((address_space(1))) u32x4_t *)(p + head + 16 * i) =
-            *reinterpret_cast<u32x4_a1 *>(stage + head + 16 * i);
-    }
-    if (tid < head) p[tid] = stage[tid];
-    else if (tid >= 16 && tid - 16 < nbytes - tail0) p[tail0 + tid - 16] = stage[tail0 + tid - 16];
-    if (tid == 0) {
-        j.offs[b] = off;
-        j.first[b] = j.tok0 + b * bt;
-        if (b == j.nb - 1) {
-            j.offs[b + 1] = off + m.bytes;
-            j.first[b + 1] = j.tok0 + j.seq;
+        // ---- the staged bytes to the container: 16-byte aligned stores, the
+        // bytes before the first aligned address and after the last one alone
+        const int64_t off = (j.rebase ? j.offs[0] : 0) + s_excl;
+        uint8_t *p = j.out + off;
+        const int nbytes = int(m.bytes);
+        const int head = min(nbytes, int((16u - (uint32_t(reinterpret_cast<uintptr_t>(p)) & 15u)) & 15u));
+        const int n16 = (nbytes - head) >> 4;
+        const int tail0 = head + 16 * n16;
+        for (int i = tid; i < n16; i += kThreads) {
+            typedef const u32x4_t __attribute__((aligned(1))) u32x4_a1;
+            *(__attribute__((address_space(1))) u32x4_t *)(p + head + 16 * i) =
+                *reinterpret_cast<u32x4_a1 *>(stage + head + 16 * i);
         }
-        if (er.sum() != (mode == 0 ? 0 : m.n_escape)) atomicOr(status, kStEscape);
-    }
+        if (tid < head) p[tid] = stage[tid];
+        else if (tid >= 16 && tid - 16 < nbytes - tail0) p[tail0 + tid - 16] = stage[tail0 + tid - 16];
+        if (tid == 0) {
+            j.offs[b] = off;
+            j.first[b] = j.tok0 + b * bt;
+            if (b == j.nb - 1) {
+                j.offs[b + 1] = off + m.bytes;
+                j.first[b + 1] = j.tok0 + j.seq;
+            }
+            if (er.sum() != (mode == 0 ? 0 : m.n_escape)) atomicOr(status, kStEscape);
+        }
 #if defined(KVEXP_PHASE_TRACE)
-    KVEXP_ENC_MARK(8);
-    if (w == 0 && lane == 0 && g < kEncTraceBlocks) {
-        unsigned long long *o = g_enc_trace + size_t(g) * kEncTraceWords;
-        for (int i = 0; i < 9; ++i) o[i] = enc_tr[i];
-        o[9] = polls;
-        o[10] = (unsigned long long)__smid();
-        o[11] = (unsigned long long)blockIdx.x; // the ticket (b) is the block: how often they agree
-    }
+        KVEXP_ENC_MARK(8);
+        if (w == 0 && lane == 0 && g < kEncTraceBlocks) {
+            unsigned long long *o = g_enc_trace + size_t(g) * kEncTraceWords;
+            for (int i = 0; i < 9; ++i) o[i] = enc_tr[i];
+            o[9] = polls;
+            o[10] = (unsigned long long)__smid();
+            o[11] = (unsigned long long)blockIdx.x; // the workgroup that encoded the block
+        }
 #endif
+        // the next block; the barrier at its start also ends every read of this
+        // block's staged bytes before the histograms reuse their LDS
+        b = bn;
+#pragma unroll
+        for (int k = 0; k < NL; ++k) x[k] = xn[k];
+        __syncthreads();
+    }
 }
 
 #if defined(KVEXP_PHASE_TRACE)
@@ -1280,7 +1333,18 @@ hipError_t launch_fused_j(const AppendJobDev *jobs, int n_jobs, const AppendJobD
                             hipFuncAttributeMaxDynamicSharedMemorySize, int(fused_lds_bytes(kMaxDim, 64)));
     if (configured != hipSuccess) return configured;
     const size_t lds = fused_lds_bytes(dim, bt);
-    hipLaunchKernelGGL((encode_fused_kernel<NL, JOBS>), dim3(unsigned(max_job_blocks), unsigned(n_jobs)),
+    // P workgroups per job: as many as are resident together over all jobs
+    // (each loops over its job's blocks), at most the longest job's blocks
+    int dev = 0, cus = 0, per_cu = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e == hipSuccess)
+        e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &per_cu, reinterpret_cast<const void *>(encode_fused_kernel<NL, JOBS>), kThreads, lds);
+    if (e != hipSuccess) return e;
+    const int64_t resident = std::max<int64_t>(1, int64_t(cus) * std::max(per_cu, 1));
+    const int per_job = int(std::max<int64_t>(1, std::min<int64_t>(max_job_blocks, resident / std::max(n_jobs, 1))));
+    hipLaunchKernelGGL((encode_fused_kernel<NL, JOBS>), dim3(unsigned(per_job), unsigned(n_jobs)),
                        dim3(kThreads), lds, s, jobs, one, dim, bt, modes, lb.words, lb.tickets, lb.epoch, status);
     return hipGetLastError();
 }
