@@ -659,7 +659,7 @@ encode_fused_kernel(const AppendJobDev *__restrict__ jobs, AppendJobDev one, int
                     uint32_t *__restrict__ status) {
     // dynamic LDS: the exponent byte counters [dim][kHistStride], then the
     // block's bytes staged for the copy to the container (fused_lds_bytes)
-    extern __shared__ uint32_t fz_lds[];
+    extern __shared__ __align__(16) uint32_t fz_lds[];
     uint32_t *fz_hist = fz_lds;
     uint8_t *stage = reinterpret_cast<uint8_t *>(fz_lds);
     __shared__ uint32_t s_ticket, s_next;
@@ -730,8 +730,10 @@ encode_fused_kernel(const AppendJobDev *__restrict__ jobs, AppendJobDev one, int
         // the next ticket, consumed after the histograms
         uint32_t tn = 0;
         if (tid == 0) tn = atomicAdd(tickets + jx, 1u);
+        // (dim * kHistStride is a multiple of 8: 16-byte stores)
 #pragma unroll 1
-        for (int i = tid; i < dim * kHistStride; i += kThreads) fz_hist[i] = 0u;
+        for (int i = 4 * tid; i < dim * kHistStride; i += 4 * kThreads)
+            *reinterpret_cast<uint4 *>(fz_hist + i) = make_uint4(0u, 0u, 0u, 0u);
         __syncthreads();
         polls = 0;
         const int g = j.blk0 + b; // look-back entry of the block
