@@ -680,7 +680,10 @@ encode_fused_kernel(const AppendJobDev *__restrict__ jobs, AppendJobDev one, int
     // job's draws number n_blocks + P, and the one that draws the last
     // resets the counter
     const AppendJobDev j = JOBS ? jobs[jx] : one;
-    const uint32_t last_draw = uint32_t(j.nb) + gridDim.x - 1u;
+    // a job with no more blocks than workgroups: one ticket each, no
+    // prefetch (the job's draws number P)
+    const bool one_shot = gridDim.x >= uint32_t(j.nb);
+    const uint32_t last_draw = (one_shot ? 0u : uint32_t(j.nb)) + gridDim.x - 1u;
     if (tid == 0) {
         const uint32_t t = atomicAdd(tickets + jx, 1u);
         if (t == last_draw) atomicExch(tickets + jx, 0u);
@@ -728,8 +731,8 @@ encode_fused_kernel(const AppendJobDev *__restrict__ jobs, AppendJobDev one, int
         }
         KVEXP_ENC_MARK(0);
         // the next ticket, consumed after the histograms
-        uint32_t tn = 0;
-        if (tid == 0) tn = atomicAdd(tickets + jx, 1u);
+        uint32_t tn = uint32_t(j.nb);
+        if (tid == 0 && !one_shot) tn = atomicAdd(tickets + jx, 1u);
         // (dim * kHistStride is a multiple of 8: 16-byte stores)
 #pragma unroll 1
         for (int i = 4 * tid; i < dim * kHistStride; i += 4 * kThreads)
@@ -789,7 +792,7 @@ encode_fused_kernel(const AppendJobDev *__restrict__ jobs, AppendJobDev one, int
             s_hi[w] = e_hi;
         }
         if (tid == 0) {
-            if (tn == last_draw) atomicExch(tickets + jx, 0u);
+            if (!one_shot && tn == last_draw) atomicExch(tickets + jx, 0u);
             s_next = tn;
         }
         __syncthreads();
@@ -1047,6 +1050,7 @@ encode_fused_kernel(const AppendJobDev *__restrict__ jobs, AppendJobDev one, int
             o[11] = (unsigned long long)blockIdx.x; // the workgroup that encoded the block
         }
 #endif
+        if (one_shot) return;
         // the next block; the barrier at its start also ends every read of this
         // block's staged bytes before the histograms reuse their LDS
         b = bn;
