@@ -637,9 +637,15 @@ __device__ __forceinline__ EscRanks<NL> fused_escape_ranks(const uint32_t (&v)[E
 template <int NL>
 constexpr int kFusedWaves = NL <= 4 ? 8 : 4;
 // Fewest waves per SIMD the compiler may plan for: one block's tokens in
-// registers beside the next block's (NL 16-byte loads each).
+// registers beside the next block's (NL 16-byte loads each). At NL 8 the
+// budget stays at four (128 registers): three would let a head_dim-128
+// tensor's 1,024 blocks fill only 768 workgroups at once.
 template <int NL>
-constexpr int kFusedWavesMin = NL <= 2 ? 8 : (NL <= 4 ? 6 : 3);
+constexpr int kFusedWavesMin = NL <= 2 ? 8 : (NL <= 4 ? 6 : 4);
+// Whether the next block's tokens are loaded right after the histograms
+// (beside this block's) or only once this block's bytes are staged.
+template <int NL>
+constexpr bool kFusedNextEarly = NL <= 4;
 
 // Dynamic LDS of the one-pass encoder: the histogram columns, or the
 // largest block (raw: header + 2 bytes per element) staged for its copy,
@@ -803,9 +809,13 @@ encode_fused_kernel(const AppendJobDev *__restrict__ jobs, AppendJobDev one, int
             blk_lo = min(blk_lo, s_lo[i]);
             blk_hi = max(blk_hi, s_hi[i]);
         }
-        // the next block's tokens, in flight while this block is encoded
+        // the next block's tokens, in flight while this block is encoded (at
+        // NL 8 once this block's are dead, before the look-back: two sets
+        // would not fit the 128 registers of four waves per SIMD)
         const int bn = int(s_next);
-        if (bn < j.nb) load_tokens(bn, xn);
+        if constexpr (kFusedNextEarly<NL>) {
+            if (bn < j.nb) load_tokens(bn, xn);
+        }
 
         // ---- best_base of each (window, channel) (codec.cpp:18-35): the most
         // covered exponents, then the smallest base; bases outside
@@ -975,6 +985,10 @@ encode_fused_kernel(const AppendJobDev *__restrict__ jobs, AppendJobDev one, int
             }
         }
 
+        if constexpr (!kFusedNextEarly<NL>) {
+            if (bn < j.nb) load_tokens(bn, x);
+        }
+
         // ---- wave 0 finds the block's place while the others wait at the barrier
         if (w == 0) {
             int64_t excl = 0;
@@ -1054,8 +1068,10 @@ encode_fused_kernel(const AppendJobDev *__restrict__ jobs, AppendJobDev one, int
         // the next block; the barrier at its start also ends every read of this
         // block's staged bytes before the histograms reuse their LDS
         b = bn;
+        if constexpr (kFusedNextEarly<NL>) {
 #pragma unroll
-        for (int k = 0; k < NL; ++k) x[k] = xn[k];
+            for (int k = 0; k < NL; ++k) x[k] = xn[k];
+        }
         __syncthreads();
     }
 }

@@ -109,6 +109,44 @@ def test_fused_append_prefill(ctx, oracle):
         assert np.array_equal(c.view().first.cpu().numpy(), first), i
 
 
+def test_fused_looping_workgroups(ctx, oracle):
+    """Jobs with more blocks than workgroups stay resident (a workgroup then
+    encodes several blocks, by ticket, and loads the next block's tokens
+    while it finishes the current one): single encodes at 1, 4 and 8 chunk
+    rows per thread with 1,094 to 1,875 blocks (MI355X keeps at most 1,024
+    workgroups of the head_dim 128 and 256 shapes resident, 1,536 of head_dim
+    64), and one batched append from empty of three head_dim-128 containers
+    of 391 blocks each."""
+    import torch
+
+    rng = np.random.default_rng(12)
+    for dim, block, seq in [(128, 128, 140000), (256, 64, 70010), (64, 128, 240000), (8, 255, 600000)]:
+        kind = "wide" if dim == 256 else "outliers"
+        say("fused encode, looping workgroups", dict(dim=dim, block=block, seq=seq, kind=kind))
+        kv = _data(rng, seq, dim, kind)
+        enc = ctx.encode(to_dev(kv, torch.int16), seq, dim, block)
+        want = oracle.encode(kv, seq, dim, block)
+        assert enc.nbytes == want.size, (dim, block, seq)
+        assert np.array_equal(enc.blob[: enc.nbytes].cpu().numpy(), want), (dim, block, seq)
+        off, first = oracle.block_index(want, dim, seq)
+        assert np.array_equal(enc.offsets.cpu().numpy(), off), (dim, block, seq)
+        assert np.array_equal(enc.first.cpu().numpy(), first), (dim, block, seq)
+
+    dim, block, add = 128, 128, 50000
+    data = [_data(rng, add, dim, kind) for kind in ("outliers", "specials", "wide")]
+    caches = [ctx.cache(dim, add, block) for _ in data]
+    say("fused append, looping workgroups", dict(containers=len(caches), dim=dim, tokens=add))
+    ctx.append_batch(caches, [to_dev(d, torch.int16) for d in data], [add] * len(data), check_errors=True)
+    for i, (c, d) in enumerate(zip(caches, data)):
+        want = oracle.encode(d, add, dim, block)
+        n = c.size()
+        assert n == want.size, i
+        assert np.array_equal(c.blob[:n].cpu().numpy(), want), i
+        off, first = oracle.block_index(want, dim, add)
+        assert np.array_equal(c.view().offsets.cpu().numpy(), off), i
+        assert np.array_equal(c.view().first.cpu().numpy(), first), i
+
+
 def test_fused_epoch_wrap(oracle):
     """A container of 313 blocks, then 65,534 one-block encodes, then another
     container of 313 blocks with other tokens on the same context: the last
