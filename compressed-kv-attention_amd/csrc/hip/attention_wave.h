@@ -23,7 +23,10 @@
 //      escape, and a chunk is cut short where its escapes would not fit);
 //      raw blocks are copied in chunks of at most 48 rows (the registers of
 //      64 coded rows). Every lane issues the same loads on every path, so
-//      the compiler's waits for the K rows leave the V rows in flight;
+//      the compiler's waits for the K rows leave the V rows in flight. At
+//      head_dim 64 in the scalar order (lane = row in the decode as in the
+//      scores), a 4- or 2-bit chunk without escapes skips the tile: its
+//      pairs are decoded straight into the score products (scores_coded);
 //   2. computes the G scores of each token in the reference order: 8 strided
 //      FMA chains over the head's channels, then the
 //      ((l0+l4)+(l1+l5))+((l2+l6)+(l3+l7)) tree. Every fmaf of the chains is
@@ -93,6 +96,10 @@ constexpr int kSlotQ = 8;       // partial-state slot: m[8], l[8], acc[8][head_d
 // c4 (head_dim 128), pieces: 2,726 against 3,323 for whole rows.
 template <int D>
 constexpr bool kWholeRows = D == 64;
+// Whether K rows of a chunk without escapes may skip the tile (whole rows,
+// scalar order: lane = row = token in both the decode and the scores).
+template <int D, int ORDER>
+constexpr bool kDirectK = kWholeRows<D> && ORDER == 0;
 
 // The kernel's sizes for head_dim D (64, 128 or 256).
 template <int D>
@@ -468,6 +475,51 @@ __device__ __forceinline__ void fill_negzero(uint8_t *row) {
     for (int i = 0; i < D / 8; ++i) reinterpret_cast<uint4 *>(row)[i] = make_uint4(z, z, z, z);
 }
 
+// Whole rows: the codes of octet dg (channels 8dg .. 8dg + 7) of the lane's
+// coded row for a block of mode MODE (4, 3 or 2 bits per code), as lo (byte
+// p: code 2p) and hi (byte p: code 2p + 1).
+template <int D, int MODE>
+__device__ __forceinline__ void octet_codes(const Rows<D, true> &R, int dg, uint32_t &lo, uint32_t &hi) {
+    constexpr int SM = Shape<D>::kSmRegs;
+    if constexpr (MODE == 4) {
+        const uint32_t cw = comp(R.r[SM + (dg >> 2)], dg & 3);
+        lo = cw & 0x0F0F0F0Fu;
+        hi = (cw >> 4) & 0x0F0F0F0Fu;
+    } else if constexpr (MODE == 2) {
+        // 16 two-bit codes per dword; octet dg uses 16 bits
+        const uint32_t cw = comp(R.r[SM + (dg >> 3)], (dg >> 1) & 3) >> (16 * (dg & 1));
+        lo = (cw & 3u) | (((cw >> 4) & 3u) << 8) | (((cw >> 8) & 3u) << 16) | (((cw >> 12) & 3u) << 24);
+        hi = ((cw >> 2) & 3u) | (((cw >> 6) & 3u) << 8) | (((cw >> 10) & 3u) << 16) | (((cw >> 14) & 3u) << 24);
+    } else {
+        // 3-bit codes: octet dg's 24 bits are bytes [3dg, 3dg + 3) of the
+        // row's codes; groups of two codes (6 bits) are spread to bytes first
+        const int q = (3 * dg) >> 2, b = (3 * dg) & 3;
+        const uint32_t w = __builtin_amdgcn_alignbyte(code_dword3<D>(R, q + (b > 1 ? 1 : 0)), code_dword3<D>(R, q),
+                                                      uint32_t(b));
+        const uint32_t x = (w & 0x3Fu) | ((w << 2) & 0x3F00u) | ((w << 4) & 0x3F0000u) | ((w << 6) & 0x3F000000u);
+        lo = x & 0x07070707u;
+        hi = (x >> 3) & 0x07070707u;
+    }
+}
+
+// Whole rows: octet dg of the lane's coded row as four BF16 pairs (mode
+// MODE), with the channel pairs' base words in bp (base_pairs).
+template <int D, int MODE>
+__device__ __forceinline__ uint4 coded_octet(const Rows<D, true> &R, int dg, const uint32_t *bp, uint32_t smm) {
+    uint32_t lo, hi;
+    octet_codes<D, MODE>(R, dg, lo, hi);
+    return octet_row<D>(R, dg, lo, hi, bp, smm);
+}
+
+// Whole rows: pair P (channels 8dg + 2P, 8dg + 2P + 1) of octet dg, as
+// octet_row builds it, from the octet's codes and the pair's base word.
+template <int D>
+__device__ __forceinline__ uint32_t coded_pair(const Rows<D, true> &R, int dg, int P, uint32_t lo, uint32_t hi,
+                                               uint32_t bpw, uint32_t smm) {
+    const uint32_t sw = comp(R.r[dg >> 1], (dg & 1) * 2 + (P >> 1));
+    return pair4(sw, 2 * (P & 1), lo, hi, P, bpw, smm);
+}
+
 // Whole rows: decodes the rows held in R into the tile, a coded row into the
 // lane's tile row with the base pair words in bp (base_pairs), raw pieces to
 // their rows. One uniform branch on the mode, then a straight-line body per
@@ -475,39 +527,19 @@ __device__ __forceinline__ void fill_negzero(uint8_t *row) {
 template <int D>
 __device__ __forceinline__ void decode_whole_rows(const Cursor &c, const Rows<D, true> &R, const uint32_t *bp,
                                                   uint8_t *tile, int rows, uint32_t smm) {
-    constexpr int SM = Shape<D>::kSmRegs, RR = Shape<D>::kRowRegs;
+    constexpr int RR = Shape<D>::kRowRegs;
     const int lane = lane_here();
     uint4 *dst = reinterpret_cast<uint4 *>(tile + lane * Shape<D>::kTileStride);
     const int mode = c.mode();
     if (mode == 4) {
 #pragma unroll
-        for (int dg = 0; dg < D / 8; ++dg) {
-            const uint32_t cw = comp(R.r[SM + (dg >> 2)], dg & 3);
-            dst[dg] = octet_row<D>(R, dg, cw & 0x0F0F0F0Fu, (cw >> 4) & 0x0F0F0F0Fu, bp, smm);
-        }
+        for (int dg = 0; dg < D / 8; ++dg) dst[dg] = coded_octet<D, 4>(R, dg, bp, smm);
     } else if (mode == 2) {
 #pragma unroll
-        for (int dg = 0; dg < D / 8; ++dg) {
-            // 16 two-bit codes per dword; octet dg uses 16 bits. Byte p of
-            // lo/hi: codes 2p and 2p+1 of the octet.
-            const uint32_t cw = comp(R.r[SM + (dg >> 3)], (dg >> 1) & 3) >> (16 * (dg & 1));
-            const uint32_t lo =
-                (cw & 3u) | (((cw >> 4) & 3u) << 8) | (((cw >> 8) & 3u) << 16) | (((cw >> 12) & 3u) << 24);
-            const uint32_t hi = ((cw >> 2) & 3u) | (((cw >> 6) & 3u) << 8) | (((cw >> 10) & 3u) << 16) |
-                                (((cw >> 14) & 3u) << 24);
-            dst[dg] = octet_row<D>(R, dg, lo, hi, bp, smm);
-        }
+        for (int dg = 0; dg < D / 8; ++dg) dst[dg] = coded_octet<D, 2>(R, dg, bp, smm);
     } else if (mode == 3) {
-        // 3-bit codes: octet dg's 24 bits are bytes [3dg, 3dg + 3) of the
-        // row's codes; groups of two codes (6 bits) are spread to bytes first
 #pragma unroll
-        for (int dg = 0; dg < D / 8; ++dg) {
-            const int q = (3 * dg) >> 2, b = (3 * dg) & 3;
-            const uint32_t w = __builtin_amdgcn_alignbyte(code_dword3<D>(R, q + (b > 1 ? 1 : 0)),
-                                                          code_dword3<D>(R, q), uint32_t(b));
-            const uint32_t x = (w & 0x3Fu) | ((w << 2) & 0x3F00u) | ((w << 4) & 0x3F0000u) | ((w << 6) & 0x3F000000u);
-            dst[dg] = octet_row<D>(R, dg, x & 0x07070707u, (x >> 3) & 0x07070707u, bp, smm);
-        }
+        for (int dg = 0; dg < D / 8; ++dg) dst[dg] = coded_octet<D, 3>(R, dg, bp, smm);
     } else {
         // raw rows: register i holds piece raw_start + i of the rows loaded
         // (c.lrows >= rows); pieces of rows >= rows are overwritten below
@@ -730,14 +762,16 @@ __device__ __forceinline__ void static_for(F &&f) {
 template <int G>
 constexpr int kGroups = (G + 3) / 4;
 
-// Scores of the lane's tile row (lane = token) for G query rows in the
+// Scores of the lane's K row (lane = token) for G query rows in the
 // scalar/AVX2 order of attention_scalar.cpp:23-29: chain j (j = 0..7) takes
 // channels j, j + 8, ..., j + D - 8 in order, lane[j] = fmaf(q, k, lane[j]),
 // then hsum8's ((l0 + l4) + (l1 + l5)) + ((l2 + l6) + (l3 + l7)). Channel d
 // is one rank-1 product per row group into chain d % 8. qa[rg][d / 16] holds
-// q[4 rg + r][d] at lane 4 (d % 16) + r.
-template <int G, int D>
-__device__ __forceinline__ void scores(const uint8_t *row, const float (&qa)[kGroups<G>][D / 16], float (&s)[G]) {
+// q[4 rg + r][d] at lane 4 (d % 16) + r. octet(dg) gives channels 8dg ..
+// 8dg + 7 of the row as four BF16 pairs (from the tile, or decoded from the
+// coded row in registers).
+template <int G, int D, class Octet>
+__device__ __forceinline__ void scores_of(Octet &&octet, const float (&qa)[kGroups<G>][D / 16], float (&s)[G]) {
     constexpr int NG = kGroups<G>;
     f4 ch[NG][8];
 #pragma unroll
@@ -745,7 +779,7 @@ __device__ __forceinline__ void scores(const uint8_t *row, const float (&qa)[kGr
 #pragma unroll
         for (int j = 0; j < 8; ++j) ch[rg][j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
     static_for<0, D / 8>([&](auto DG) {
-        const uint4 kb = *reinterpret_cast<const uint4 *>(row + 16 * DG);
+        const uint4 kb = octet(int(decltype(DG)::value));
         const float k[8] = {lo_f32(kb.x), hi_f32(kb.x), lo_f32(kb.y), hi_f32(kb.y),
                             lo_f32(kb.z), hi_f32(kb.z), lo_f32(kb.w), hi_f32(kb.w)};
         static_for<0, 8>([&](auto J) {
@@ -770,6 +804,75 @@ __device__ __forceinline__ void scores(const uint8_t *row, const float (&qa)[kGr
         if (4 * rg + 2 < G) s[(4 * rg + 2) % G] = t.z;
         if (4 * rg + 3 < G) s[(4 * rg + 3) % G] = t.w;
     }
+}
+
+// Scores of the lane's tile row (scores_of).
+template <int G, int D>
+__device__ __forceinline__ void scores(const uint8_t *row, const float (&qa)[kGroups<G>][D / 16], float (&s)[G]) {
+    scores_of<G, D>([&](int dg) { return *reinterpret_cast<const uint4 *>(row + 16 * dg); }, qa, s);
+}
+
+// Scores (scores_of's order) of the lane's coded row held in R (whole rows,
+// a block of mode MODE without escapes in the chunk), decoded pair by pair
+// into the products instead of through the tile. Two passes over the row's
+// octets, each over four of the eight chains: chains 0, 1, 4, 5 (pairs 0
+// and 2 of every octet), then 2, 3, 6, 7 (pairs 1 and 3); every chain still
+// takes its channels in order, and hsum8's tree splits into the two passes'
+// sums (l0 + l4) + (l1 + l5) and (l2 + l6) + (l3 + l7). Half the chains are
+// live at a time, which leaves room for the coded row.
+template <int G, int D, int MODE>
+__device__ __forceinline__ void scores_coded(const Rows<D, true> &R, const uint32_t *bp, uint32_t smm,
+                                             const float (&qa)[kGroups<G>][D / 16], float (&s)[G]) {
+    constexpr int NG = kGroups<G>;
+    f4 half[2][NG];
+    static_for<0, 2>([&](auto H) {
+        constexpr int h = decltype(H)::value;
+        // ch[rg][c]: chains 2h, 2h + 1, 4 + 2h, 5 + 2h
+        f4 ch[NG][4];
+#pragma unroll
+        for (int rg = 0; rg < NG; ++rg)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) ch[rg][c] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+        static_for<0, D / 8>([&](auto DG) {
+            constexpr int dg = decltype(DG)::value;
+            uint32_t lo, hi;
+            octet_codes<D, MODE>(R, dg, lo, hi);
+            const uint32_t p0 = coded_pair<D>(R, dg, h, lo, hi, bp[4 * dg + h], smm);
+            const uint32_t p1 = coded_pair<D>(R, dg, 2 + h, lo, hi, bp[4 * dg + 2 + h], smm);
+            const float k[4] = {lo_f32(p0), hi_f32(p0), lo_f32(p1), hi_f32(p1)};
+            static_for<0, 4>([&](auto C) {
+                constexpr int c = decltype(C)::value;
+                constexpr int d = 8 * dg + (c < 2 ? 2 * h + c : 4 + 2 * h + (c - 2));
+#pragma unroll
+                for (int rg = 0; rg < NG; ++rg) ch[rg][c] = mfma_rank1<d % 16>(qa[rg][d / 16], k[c], ch[rg][c]);
+            });
+            // the octet's decode and widenings, then its products: the
+            // scheduler would otherwise decode octets ahead and hold more
+            // registers than three waves per SIMD have (G 5 to 7 spilled)
+            __builtin_amdgcn_sched_group_barrier(0x002, 14, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 4 * NG, 0);
+        });
+#pragma unroll
+        for (int rg = 0; rg < NG; ++rg) half[h][rg] = (ch[rg][0] + ch[rg][2]) + (ch[rg][1] + ch[rg][3]);
+    });
+#pragma unroll
+    for (int rg = 0; rg < NG; ++rg) {
+        const f4 t = half[0][rg] + half[1][rg];
+        if (4 * rg + 0 < G) s[(4 * rg + 0) % G] = t.x;
+        if (4 * rg + 1 < G) s[(4 * rg + 1) % G] = t.y;
+        if (4 * rg + 2 < G) s[(4 * rg + 2) % G] = t.z;
+        if (4 * rg + 3 < G) s[(4 * rg + 3) % G] = t.w;
+    }
+}
+
+// Whether rows [r0, r0 + n) of the cursor's block hold an escape: the
+// block's next escape not yet written (record ecur, the first of lane 0's
+// window) lies before their end.
+template <int D>
+__device__ __forceinline__ bool rows_have_escapes(const Cursor &c, int r0, int n) {
+    if (c.ecur >= c.nesc()) return false;
+    const uint32_t pos = __builtin_amdgcn_readfirstlane(c.erec[0].x) & 0xFFFFu;
+    return pos < uint32_t((r0 + n) * D);
 }
 
 // Scores in the AVX-512 BF16 order (attention_avx512.cpp:21-30,116-124) for a
@@ -1228,7 +1331,7 @@ void attn_wave_kernel(const HeadDev *__restrict__ heads, const WorkItem *__restr
         stamp(0);
         // 1. K rows -> tile (ORDER 1: and whether the chunk needs the flushing
         // score path)
-        bool flush = false;
+        bool flush = false, kdirect = false;
         if constexpr (XKV) {
             if (kc.mode() != 0) {
                 if constexpr (ORDER == 1) {
@@ -1251,9 +1354,16 @@ void attn_wave_kernel(const HeadDev *__restrict__ heads, const WorkItem *__restr
             } else {
                 flush = ORDER == 1;
             }
-            decode_rows<D>(kc, RK, S.bp, S.tile, n, sm_mask_vgpr());
-            wave_sync();
-            flush |= patch_escapes<D, ORDER == 1>(kc, t - kc.t0, n, S.tile, klow);
+            // whole rows in the scalar order: a 4- or 2-bit chunk without
+            // escapes is decoded octet by octet into the score products
+            // below, not into the tile
+            if constexpr (kDirectK<D, ORDER>)
+                kdirect = (kc.mode() == 4 || kc.mode() == 2) && !rows_have_escapes<D>(kc, t - kc.t0, n);
+            if (!kdirect) {
+                decode_rows<D>(kc, RK, S.bp, S.tile, n, sm_mask_vgpr());
+                wave_sync();
+                flush |= patch_escapes<D, ORDER == 1>(kc, t - kc.t0, n, S.tile, klow);
+            }
         } else {
             store_raw<D>(RK, S.tile);
             if constexpr (ORDER == 1) {
@@ -1277,7 +1387,17 @@ void attn_wave_kernel(const HeadDev *__restrict__ heads, const WorkItem *__restr
         // 2. scores, lane = token
         float s[G];
         if constexpr (ORDER == 0) {
-            scores<G, D>(S.tile + ln * TS, qa, s);
+            if constexpr (XKV && kDirectK<D, ORDER>) {
+                if (kdirect) {
+                    const uint32_t smm = sm_mask_vgpr();
+                    if (kc.mode() == 4) scores_coded<G, D, 4>(RK, S.bp, smm, qa, s);
+                    else scores_coded<G, D, 2>(RK, S.bp, smm, qa, s);
+                } else {
+                    scores<G, D>(S.tile + ln * TS, qa, s);
+                }
+            } else {
+                scores<G, D>(S.tile + ln * TS, qa, s);
+            }
         } else if (!flush) {
             scores_dp<G, D>(S.tile + ln * TS, qa, s);
         } else {
