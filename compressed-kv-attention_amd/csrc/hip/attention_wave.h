@@ -1618,7 +1618,7 @@ void attn_wave_kernel(const HeadDev *__restrict__ heads, const WorkItem *__restr
 // The first batch starts from split 0's state, as dispatch.cpp does.
 template <int D>
 __global__ __launch_bounds__(4 * 64) void wave_merge_kernel(
-    const MergeItem *__restrict__ mitems, int n_mitems, float *__restrict__ out_all,
+    const MergeItem *__restrict__ mitems, int n_mitems, MergeItem uni, float *__restrict__ out_all,
     float *__restrict__ lse_all, const float *__restrict__ ws) {
     constexpr int H = D / 64, B = Shape<D>::kMergeBatch, SF = Shape<D>::kSlotFloats;
     static_assert(B % 4 == 0 && B <= kWave, "one split per lane, read four at a time");
@@ -1630,7 +1630,16 @@ __global__ __launch_bounds__(4 * 64) void wave_merge_kernel(
     const int w = int(threadIdx.x) >> 6;
     const int mi = __builtin_amdgcn_readfirstlane(int(blockIdx.x) * 4 + w);
     if (mi >= n_mitems) return;
-    const MergeItem it = load_scalar(mitems + mi);
+    // uni.g > 0: item i is (uni.ws_base + k uni.n_splits, uni.n_splits,
+    // uni.q_row + k uni.g, i - k uni.g) with k = i / uni.g, so the slots'
+    // loads need not wait for the item's
+    MergeItem it;
+    if (uni.g > 0) {
+        const int k = mi / uni.g;
+        it = MergeItem{uni.ws_base + k * uni.n_splits, uni.n_splits, uni.q_row + k * uni.g, mi - k * uni.g};
+    } else {
+        it = load_scalar(mitems + mi);
+    }
     const int g = it.g;
     const float *slots = ws + size_t(it.ws_base) * SF;
     const int n = it.n_splits;

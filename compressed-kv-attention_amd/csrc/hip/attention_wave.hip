@@ -27,19 +27,19 @@ int wave_waves_per_wg(int dim) {
     return dim == 64 ? wave::Shape<64>::kWaves : (dim == 128 ? wave::Shape<128>::kWaves : wave::Shape<256>::kWaves);
 }
 
-hipError_t wave_merge(int dim, const MergeItem *mitems, int n_mitems, float *out, float *lse, const float *ws,
-                      hipStream_t s) {
+hipError_t wave_merge(int dim, const MergeItem *mitems, int n_mitems, const MergeItem &uni, float *out, float *lse,
+                      const float *ws, hipStream_t s) {
     if (n_mitems <= 0) return hipSuccess;
     const int grid = (n_mitems + 3) / 4;
     if (dim == 64)
-        hipLaunchKernelGGL(wave::wave_merge_kernel<64>, dim3(grid), dim3(4 * 64), 0, s, mitems, n_mitems, out, lse,
-                           ws);
+        hipLaunchKernelGGL(wave::wave_merge_kernel<64>, dim3(grid), dim3(4 * 64), 0, s, mitems, n_mitems, uni, out,
+                           lse, ws);
     else if (dim == 128)
-        hipLaunchKernelGGL(wave::wave_merge_kernel<128>, dim3(grid), dim3(4 * 64), 0, s, mitems, n_mitems, out, lse,
-                           ws);
+        hipLaunchKernelGGL(wave::wave_merge_kernel<128>, dim3(grid), dim3(4 * 64), 0, s, mitems, n_mitems, uni, out,
+                           lse, ws);
     else if (dim == 256)
-        hipLaunchKernelGGL(wave::wave_merge_kernel<256>, dim3(grid), dim3(4 * 64), 0, s, mitems, n_mitems, out, lse,
-                           ws);
+        hipLaunchKernelGGL(wave::wave_merge_kernel<256>, dim3(grid), dim3(4 * 64), 0, s, mitems, n_mitems, uni, out,
+                           lse, ws);
     else
         return hipErrorInvalidValue;
     return hipGetLastError();

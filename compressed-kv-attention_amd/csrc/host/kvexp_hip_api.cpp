@@ -48,8 +48,8 @@ bool wave_supports(int dim);
 hipError_t attention_wave(bool xkv, int order, int G, int dim, const HeadDev *heads, const WorkItem *items,
                           int n_items, const kvexp_dev::BlockDesc *desc, const uint16_t *q, float *out, float *lse,
                           float *ws, hipStream_t s);
-hipError_t wave_merge(int dim, const kvexp_dev::MergeItem *mitems, int n_mitems, float *out, float *lse,
-                      const float *ws, hipStream_t s);
+hipError_t wave_merge(int dim, const kvexp_dev::MergeItem *mitems, int n_mitems, const kvexp_dev::MergeItem &uni,
+                      float *out, float *lse, const float *ws, hipStream_t s);
 int wave_waves_per_wg(int dim);
 hipError_t noalloc_scratch_setup(int device, void **ptr);
 void *noalloc_scratch(int device);
@@ -273,6 +273,9 @@ struct kvexp_hip_plan {
     // wave kernel: merge work (head, row), escape records, block descriptors
     DevBuf mitems, esc0, escpos, desc;
     int n_mitems = 0;
+    // the merge items as a pattern when they follow one (g > 0; see
+    // wave_merge_kernel), else g = 0
+    kvexp_dev::MergeItem merge_uni{};
     int n_dev_heads = 0, n_items = 0, n_merge = 0;
     // wave kernel: items sorted by query-row count G; group_start[G] .. group_start[G+1]
     int group_start[10] = {0};
@@ -1095,6 +1098,21 @@ void plan_build(kvexp_hip_plan *p, const kvexp_hip_head *heads, int n_heads, hip
             for (int g = 0; g < d.n_q; ++g) mi.push_back(kvexp_dev::MergeItem{d.ws_base, d.n_splits, d.q_row, g});
         }
         p->n_mitems = int(mi.size());
+        // every merged device head with the same query rows and splits, its
+        // slots and output rows one after another: the kernel then builds
+        // item i from i instead of loading it
+        p->merge_uni = kvexp_dev::MergeItem{};
+        if (!mi.empty()) {
+            const kvexp_dev::MergeItem f = mi[0];
+            const int G = hv[size_t(merge[0])].n_q;
+            bool uni = true;
+            for (size_t i = 0; i < mi.size() && uni; ++i) {
+                const int32_t k = int32_t(i) / G;
+                uni = mi[i].ws_base == f.ws_base + k * f.n_splits && mi[i].n_splits == f.n_splits &&
+                      mi[i].q_row == f.q_row + k * G && mi[i].g == int32_t(i) % G;
+            }
+            if (uni) p->merge_uni = kvexp_dev::MergeItem{f.ws_base, f.n_splits, f.q_row, G};
+        }
         p->mitems = p->alloc(std::max<size_t>(1, mi.size()) * sizeof(kvexp_dev::MergeItem));
         if (!mi.empty())
             HIPX(hipMemcpyAsync(p->mitems.p, mi.data(), mi.size() * sizeof(kvexp_dev::MergeItem),
@@ -1150,6 +1168,7 @@ void swap_built(kvexp_hip_plan &dst, kvexp_hip_plan &src) {
     swap(dst.escpos, src.escpos);
     swap(dst.desc, src.desc);
     swap(dst.n_mitems, src.n_mitems);
+    swap(dst.merge_uni, src.merge_uni);
     swap(dst.n_dev_heads, src.n_dev_heads);
     swap(dst.n_items, src.n_items);
     swap(dst.n_merge, src.n_merge);
@@ -1321,7 +1340,8 @@ int kvexp_hip_attention_run(kvexp_hip_plan *plan, const uint16_t *d_q, float *d_
                                                       plan->ws.as<float>(), s));
             }
             if (ev1) HIPX(hipEventRecord(ev1, s));
-            HIPX(kvexp_launch::wave_merge(plan->dim, plan->mitems.as<kvexp_dev::MergeItem>(), plan->n_mitems, d_out,
+            HIPX(kvexp_launch::wave_merge(plan->dim, plan->mitems.as<kvexp_dev::MergeItem>(), plan->n_mitems,
+                                          plan->merge_uni, d_out,
                                           d_lse, plan->ws.as<float>(), s));
         } else {
             if (ev0) HIPX(hipEventRecord(ev0, s));
