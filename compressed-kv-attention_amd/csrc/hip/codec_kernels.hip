@@ -755,7 +755,11 @@ encode_fused_kernel(const AppendJobDev *__restrict__ jobs, AppendJobDev one, int
         const int chunks = n * dim / 8;
 
         // ---- channel histograms of the block's tokens (in registers)
-        uint32_t pk_lo = 0xFFFFFFFFu, pk_hi = 0u; // exponent fields (bits 14..7 of each half), smallest and largest
+        // exponent fields (bits 14..7 of each BF16) of the thread's elements,
+        // smallest and largest, both halves at once (v_pk_min_u16 /
+        // v_pk_max_u16); 0xFFFF: no element
+        typedef unsigned short u16x2_t __attribute__((ext_vector_type(2)));
+        u16x2_t lo2 = {0xFFFF, 0xFFFF}, hi2 = {0, 0};
 #if defined(KVEXP_PHASE_TRACE)
         asm volatile("" ::"v"(x[NL - 1][0]), "v"(x[0][0]));
 #endif
@@ -785,13 +789,14 @@ encode_fused_kernel(const AppendJobDev *__restrict__ jobs, AppendJobDev one, int
                 }
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    const uint32_t ef = x[k][i] & 0x7F807F80u;
-                    pk_lo = min(min(pk_lo, ef & 0xFFFFu), ef >> 16);
-                    pk_hi = max(max(pk_hi, ef & 0xFFFFu), ef >> 16);
+                    const u16x2_t ef = __builtin_bit_cast(u16x2_t, x[k][i] & 0x7F807F80u);
+                    lo2 = __builtin_elementwise_min(lo2, ef);
+                    hi2 = __builtin_elementwise_max(hi2, ef);
                 }
             }
         }
-        const int e_lo = wave_min_i32(pk_lo == 0xFFFFFFFFu ? 255 : int(pk_lo >> 7));
+        const uint32_t pk_lo = min(uint32_t(lo2.x), uint32_t(lo2.y)), pk_hi = max(uint32_t(hi2.x), uint32_t(hi2.y));
+        const int e_lo = wave_min_i32(pk_lo == 0xFFFFu ? 255 : int(pk_lo >> 7));
         const int e_hi = wave_max_i32(int(pk_hi >> 7));
         if (lane == 0) {
             s_lo[w] = e_lo;
