@@ -96,10 +96,11 @@ constexpr int kSlotQ = 8;       // partial-state slot: m[8], l[8], acc[8][head_d
 // c4 (head_dim 128), pieces: 2,726 against 3,323 for whole rows.
 template <int D>
 constexpr bool kWholeRows = D == 64;
-// Whether K rows of a chunk without escapes may skip the tile (whole rows,
-// scalar order: lane = row = token in both the decode and the scores).
+// Whether K rows of a chunk without escapes may skip the tile (whole rows:
+// lane = row = token in both the decode and the scores; in the AVX-512 BF16
+// order only where the chunk needs no flush).
 template <int D, int ORDER>
-constexpr bool kDirectK = kWholeRows<D> && ORDER == 0;
+constexpr bool kDirectK = kWholeRows<D>;
 
 // The kernel's sizes for head_dim D (64, 128 or 256).
 template <int D>
@@ -884,9 +885,11 @@ __device__ __forceinline__ bool rows_have_escapes(const Cursor &c, int r0, int n
 // (chains 4Q .. 4Q + 3 read octets Q, Q + 4, ...), R quads at a time: two
 // for one row group (eight independent products between dependent ones),
 // one for two row groups (the same, and fewer registers live); each run is
-// reduced to its a_i before the next starts.
-template <int G, int D>
-__device__ __forceinline__ void scores_dp(const uint8_t *row, const float (&qa)[kGroups<G>][D / 16], float (&s)[G]) {
+// reduced to its a_i before the next starts. octet(dg) gives channels 8dg ..
+// 8dg + 7 of the lane's K row as four BF16 pairs (from the tile, or decoded
+// from the coded row in registers); each octet is taken once.
+template <int G, int D, class Octet>
+__device__ __forceinline__ void scores_dp_of(Octet &&octet, const float (&qa)[kGroups<G>][D / 16], float (&s)[G]) {
     constexpr int NG = kGroups<G>;
     // One quad of chains at a time for every row group: at most 4 NG chains
     // live beside the partial sums.
@@ -901,7 +904,7 @@ __device__ __forceinline__ void scores_dp(const uint8_t *row, const float (&qa)[
             for (int j = 0; j < 4; ++j) ch[rg][j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
         static_for<0, D / 32>([&](auto S) {
             constexpr int DG0 = 4 * decltype(S)::value + Q0; // octet of this step
-            const uint4 kb = *reinterpret_cast<const uint4 *>(row + 16 * DG0);
+            const uint4 kb = octet(DG0);
             const uint32_t w[4] = {kb.x, kb.y, kb.z, kb.w};
             static_for<0, 4>([&](auto J) { // odd channel of pair J first
                 constexpr int d = 8 * DG0 + 2 * decltype(J)::value + 1;
@@ -939,6 +942,12 @@ __device__ __forceinline__ void scores_dp(const uint8_t *row, const float (&qa)[
             }
         }
     });
+}
+
+// Scores of the lane's tile row in the AVX-512 BF16 order (scores_dp_of).
+template <int G, int D>
+__device__ __forceinline__ void scores_dp(const uint8_t *row, const float (&qa)[kGroups<G>][D / 16], float (&s)[G]) {
+    scores_dp_of<G, D>([&](int dg) { return *reinterpret_cast<const uint4 *>(row + 16 * dg); }, qa, s);
 }
 
 // The same order on the vector ALU with every flush applied, for chunks the
@@ -1354,11 +1363,11 @@ void attn_wave_kernel(const HeadDev *__restrict__ heads, const WorkItem *__restr
             } else {
                 flush = ORDER == 1;
             }
-            // whole rows in the scalar order: a 4- or 2-bit chunk without
-            // escapes is decoded octet by octet into the score products
-            // below, not into the tile
+            // whole rows: a 4- or 2-bit chunk without escapes (and, in the
+            // AVX-512 order, without a possible flush) is decoded octet by
+            // octet into the score products below, not into the tile
             if constexpr (kDirectK<D, ORDER>)
-                kdirect = (kc.mode() == 4 || kc.mode() == 2) && !rows_have_escapes<D>(kc, t - kc.t0, n);
+                kdirect = (kc.mode() == 4 || kc.mode() == 2) && !flush && !rows_have_escapes<D>(kc, t - kc.t0, n);
             if (!kdirect) {
                 decode_rows<D>(kc, RK, S.bp, S.tile, n, sm_mask_vgpr());
                 wave_sync();
@@ -1399,7 +1408,19 @@ void attn_wave_kernel(const HeadDev *__restrict__ heads, const WorkItem *__restr
                 scores<G, D>(S.tile + ln * TS, qa, s);
             }
         } else if (!flush) {
-            scores_dp<G, D>(S.tile + ln * TS, qa, s);
+            if constexpr (XKV && kDirectK<D, ORDER>) {
+                if (kdirect) {
+                    const uint32_t smm = sm_mask_vgpr();
+                    if (kc.mode() == 4)
+                        scores_dp_of<G, D>([&](int dg) { return coded_octet<D, 4>(RK, dg, S.bp, smm); }, qa, s);
+                    else
+                        scores_dp_of<G, D>([&](int dg) { return coded_octet<D, 2>(RK, dg, S.bp, smm); }, qa, s);
+                } else {
+                    scores_dp<G, D>(S.tile + ln * TS, qa, s);
+                }
+            } else {
+                scores_dp<G, D>(S.tile + ln * TS, qa, s);
+            }
         } else {
             scores_dp_flush<G, D>(S.tile + ln * TS, q_all + size_t(hd.q_row) * D, &S.eT[0][0]);
             wave_sync();
