@@ -24,9 +24,10 @@
 //      raw blocks are copied in chunks of at most 48 rows (the registers of
 //      64 coded rows). Every lane issues the same loads on every path, so
 //      the compiler's waits for the K rows leave the V rows in flight. At
-//      head_dim 64 in the scalar order (lane = row in the decode as in the
-//      scores), a 4- or 2-bit chunk without escapes skips the tile: its
-//      pairs are decoded straight into the score products (scores_coded);
+//      head_dim 64 (lane = row in the decode as in the scores), a 4- or
+//      2-bit chunk without escapes (and, in the AVX-512 order, without a
+//      possible flush) skips the tile: its pairs are decoded straight into
+//      the score products (scores_coded, scores_dp_of);
 //   2. computes the G scores of each token in the reference order: 8 strided
 //      FMA chains over the head's channels, then the
 //      ((l0+l4)+(l1+l5))+((l2+l6)+(l3+l7)) tree. Every fmaf of the chains is
