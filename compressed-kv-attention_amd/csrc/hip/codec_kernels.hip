@@ -848,8 +848,25 @@ encode_fused_kernel(const AppendJobDev *__restrict__ jobs, AppendJobDev one, int
             int key = 0;
             if (lo <= hi) {
                 const uint8_t *hb = reinterpret_cast<const uint8_t *>(fz_hist + d * kHistStride);
+                // the first window's coverage: the byte counters of bins [lo,
+                // lo + width) summed a word (four bins) at a time with
+                // v_sad_u8, the bins outside masked off (lo is the same in
+                // every lane of the wave, so is the loop)
                 int cov = 0;
-                for (int e = lo; e < lo + width; ++e) cov += hb[e];
+                {
+                    const uint32_t *hw = fz_hist + d * kHistStride;
+                    const int w0 = lo >> 2, w1 = (lo + width - 1) >> 2;
+                    const uint32_t m0 = 0xFFFFFFFFu << (8 * (lo & 3));
+                    const uint32_t m1 = 0xFFFFFFFFu >> (8 * (3 - ((lo + width - 1) & 3)));
+                    uint32_t acc = 0;
+                    for (int wi = w0; wi <= w1; ++wi) {
+                        uint32_t m = 0xFFFFFFFFu;
+                        if (wi == w0) m &= m0;
+                        if (wi == w1) m &= m1;
+                        acc = __builtin_amdgcn_sad_u8(hw[wi] & m, 0u, acc);
+                    }
+                    cov = int(acc);
+                }
                 int best = cov, best_b = lo;
 #pragma unroll 4
                 for (int base = lo + 1; base <= hi; ++base) {
