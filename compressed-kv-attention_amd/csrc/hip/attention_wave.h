@@ -69,7 +69,7 @@ namespace wave {
 // by a timestamp taken after an empty asm that reads the loaded register.
 #if defined(KVEXP_PHASE_TRACE)
 constexpr int kTracePhases = 12;
-constexpr int kTraceWaves = 8192, kTraceWords = kTracePhases + 3; // start, end, the phases, CU/SE id
+constexpr int kTraceWaves = 8192, kTraceWords = kTracePhases + 3; // start, end, the phases, CU id | head << 16 | split << 40
 static __device__ unsigned long long g_phase_trace[kTraceWaves * kTraceWords];
 #define KVEXP_TRACE_ON(X, O) ((X) && (O) == 0)
 #else
@@ -1591,7 +1591,9 @@ void attn_wave_kernel(const HeadDev *__restrict__ heads, const WorkItem *__restr
             o[0] = tw0;
             o[1] = __builtin_readcyclecounter();
             for (int i = 0; i < kTracePhases; ++i) o[2 + i] = ph[i];
-            o[kTracePhases + 2] = (unsigned long long)__smid();
+            // the CU, then the split's device head and split number
+            o[kTracePhases + 2] = (unsigned long long)__smid() | ((unsigned long long)wi.head << 16) |
+                                  ((unsigned long long)wi.split << 40);
         }
     }
 #endif
