@@ -1624,6 +1624,11 @@ void attn_wave_kernel(const HeadDev *__restrict__ heads, const WorkItem *__restr
         for (int h = 0; h < H; ++h) slot[2 * kSlotQ + g * D + 64 * h + lane] = acc[g / 4][h][g % 4];
 }
 
+// Waves (merge items) per workgroup of the merge kernel: one, so that a
+// launch's few hundred items spread over every CU (c2: 336 items; 4.97 us
+// per launch against 5.25 with four waves per workgroup on 84 CUs).
+constexpr int kMergeWaves = 1;
+
 // Ordered merge of a head's split states (softmax.hpp:16-30 merge_state,
 // left to right in split order; dispatch.cpp:98-103), then out = acc * (1/l)
 // and lse = m + log l. One wave per merge item (device head, query row): lane
@@ -1641,18 +1646,18 @@ void attn_wave_kernel(const HeadDev *__restrict__ heads, const WorkItem *__restr
 // take one fused multiply-add per split and channel, as merge_state does.
 // The first batch starts from split 0's state, as dispatch.cpp does.
 template <int D>
-__global__ __launch_bounds__(4 * 64) void wave_merge_kernel(
+__global__ __launch_bounds__(kMergeWaves * 64) void wave_merge_kernel(
     const MergeItem *__restrict__ mitems, int n_mitems, MergeItem uni, float *__restrict__ out_all,
     float *__restrict__ lse_all, const float *__restrict__ ws) {
     constexpr int H = D / 64, B = Shape<D>::kMergeBatch, SF = Shape<D>::kSlotFloats;
     static_assert(B % 4 == 0 && B <= kWave, "one split per lane, read four at a time");
     __shared__ uint64_t tab[32];
-    __shared__ float stage[4][3][B]; // per wave: e1, e2 and l * e2 of the batch's splits
+    __shared__ float stage[kMergeWaves][3][B]; // per wave: e1, e2 and l * e2 of the batch's splits
     if (threadIdx.x < 64) kvexp_exp_table_to_lds(tab);
     __syncthreads();
     const int lane = lane_id();
     const int w = int(threadIdx.x) >> 6;
-    const int mi = __builtin_amdgcn_readfirstlane(int(blockIdx.x) * 4 + w);
+    const int mi = __builtin_amdgcn_readfirstlane(int(blockIdx.x) * kMergeWaves + w);
     if (mi >= n_mitems) return;
     // uni.g > 0: item i is (uni.ws_base + k uni.n_splits, uni.n_splits,
     // uni.q_row + k uni.g, i - k uni.g) with k = i / uni.g, so the slots'

@@ -30,15 +30,15 @@ int wave_waves_per_wg(int dim) {
 hipError_t wave_merge(int dim, const MergeItem *mitems, int n_mitems, const MergeItem &uni, float *out, float *lse,
                       const float *ws, hipStream_t s) {
     if (n_mitems <= 0) return hipSuccess;
-    const int grid = (n_mitems + 3) / 4;
+    const int grid = (n_mitems + wave::kMergeWaves - 1) / wave::kMergeWaves;
     if (dim == 64)
-        hipLaunchKernelGGL(wave::wave_merge_kernel<64>, dim3(grid), dim3(4 * 64), 0, s, mitems, n_mitems, uni, out,
+        hipLaunchKernelGGL(wave::wave_merge_kernel<64>, dim3(grid), dim3(wave::kMergeWaves * 64), 0, s, mitems, n_mitems, uni, out,
                            lse, ws);
     else if (dim == 128)
-        hipLaunchKernelGGL(wave::wave_merge_kernel<128>, dim3(grid), dim3(4 * 64), 0, s, mitems, n_mitems, uni, out,
+        hipLaunchKernelGGL(wave::wave_merge_kernel<128>, dim3(grid), dim3(wave::kMergeWaves * 64), 0, s, mitems, n_mitems, uni, out,
                            lse, ws);
     else if (dim == 256)
-        hipLaunchKernelGGL(wave::wave_merge_kernel<256>, dim3(grid), dim3(4 * 64), 0, s, mitems, n_mitems, uni, out,
+        hipLaunchKernelGGL(wave::wave_merge_kernel<256>, dim3(grid), dim3(wave::kMergeWaves * 64), 0, s, mitems, n_mitems, uni, out,
                            lse, ws);
     else
         return hipErrorInvalidValue;
