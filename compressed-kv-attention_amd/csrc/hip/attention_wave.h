@@ -1210,7 +1210,7 @@ constexpr int kWaveOcc = D == 256 ? 1 : (D == 64 && XKV && G < 8 ? 3 : 2);
 template <int G, int D, bool XKV, int ORDER>
 __global__ __launch_bounds__(Shape<D>::kWaves * 64) __attribute__((amdgpu_waves_per_eu(kWaveOcc<G, D, XKV, ORDER>)))
 void attn_wave_kernel(const HeadDev *__restrict__ heads, const WorkItem *__restrict__ items, int n_items,
-                      const BlockDesc *__restrict__ desc,
+                      int wpg, const BlockDesc *__restrict__ desc,
                       const uint16_t *__restrict__ q_all, float *__restrict__ out_all, float *__restrict__ lse_all,
                       float *__restrict__ ws) {
     constexpr int TS = Shape<D>::kTileStride, H = D / 64;
@@ -1220,7 +1220,7 @@ void attn_wave_kernel(const HeadDev *__restrict__ heads, const WorkItem *__restr
 
     const int lane = lane_id();
     const int w = int(threadIdx.x) >> 6;
-    const int item = __builtin_amdgcn_readfirstlane(int(blockIdx.x) * Shape<D>::kWaves + w);
+    const int item = __builtin_amdgcn_readfirstlane(int(blockIdx.x) * wpg + w);
     if (item >= n_items) return;
     WaveLds<G, D> &S = L.w[w];
     const uint64_t *tab = L.exptab;
@@ -1733,28 +1733,32 @@ namespace kvexp_launch {
 using namespace kvexp_dev;
 
 template <int G, int D, bool XKV, int ORDER>
-static hipError_t launch_wave_g(const HeadDev *heads, const WorkItem *items, int n_items, const BlockDesc *desc,
-                                const uint16_t *q, float *out, float *lse, float *ws, hipStream_t s) {
-    constexpr int W = wave::Shape<D>::kWaves;
+static hipError_t launch_wave_g(const HeadDev *heads, const WorkItem *items, int n_items, int wpg,
+                                const BlockDesc *desc, const uint16_t *q, float *out, float *lse, float *ws,
+                                hipStream_t s) {
+    // wpg waves (work items) per workgroup: the kernel's count, or fewer
+    // (1) where a launch has no more items than CUs, so they spread over as
+    // many CUs
+    const int W = wpg >= 1 && wpg <= wave::Shape<D>::kWaves ? wpg : wave::Shape<D>::kWaves;
     const int grid = (n_items + W - 1) / W;
     hipLaunchKernelGGL((wave::attn_wave_kernel<G, D, XKV, ORDER>), dim3(grid), dim3(W * 64), 0, s, heads, items,
-                       n_items, desc, q, out, lse, ws);
+                       n_items, W, desc, q, out, lse, ws);
     return hipGetLastError();
 }
 
 template <int D, bool XKV, int ORDER>
-static hipError_t launch_wave_x(int G, const HeadDev *heads, const WorkItem *items, int n_items,
+static hipError_t launch_wave_x(int G, const HeadDev *heads, const WorkItem *items, int n_items, int wpg,
                                 const BlockDesc *desc, const uint16_t *q, float *out, float *lse, float *ws,
                                 hipStream_t s) {
     switch (G) {
-    case 1: return launch_wave_g<1, D, XKV, ORDER>(heads, items, n_items, desc, q, out, lse, ws, s);
-    case 2: return launch_wave_g<2, D, XKV, ORDER>(heads, items, n_items, desc, q, out, lse, ws, s);
-    case 3: return launch_wave_g<3, D, XKV, ORDER>(heads, items, n_items, desc, q, out, lse, ws, s);
-    case 4: return launch_wave_g<4, D, XKV, ORDER>(heads, items, n_items, desc, q, out, lse, ws, s);
-    case 5: return launch_wave_g<5, D, XKV, ORDER>(heads, items, n_items, desc, q, out, lse, ws, s);
-    case 6: return launch_wave_g<6, D, XKV, ORDER>(heads, items, n_items, desc, q, out, lse, ws, s);
-    case 7: return launch_wave_g<7, D, XKV, ORDER>(heads, items, n_items, desc, q, out, lse, ws, s);
-    case 8: return launch_wave_g<8, D, XKV, ORDER>(heads, items, n_items, desc, q, out, lse, ws, s);
+    case 1: return launch_wave_g<1, D, XKV, ORDER>(heads, items, n_items, wpg, desc, q, out, lse, ws, s);
+    case 2: return launch_wave_g<2, D, XKV, ORDER>(heads, items, n_items, wpg, desc, q, out, lse, ws, s);
+    case 3: return launch_wave_g<3, D, XKV, ORDER>(heads, items, n_items, wpg, desc, q, out, lse, ws, s);
+    case 4: return launch_wave_g<4, D, XKV, ORDER>(heads, items, n_items, wpg, desc, q, out, lse, ws, s);
+    case 5: return launch_wave_g<5, D, XKV, ORDER>(heads, items, n_items, wpg, desc, q, out, lse, ws, s);
+    case 6: return launch_wave_g<6, D, XKV, ORDER>(heads, items, n_items, wpg, desc, q, out, lse, ws, s);
+    case 7: return launch_wave_g<7, D, XKV, ORDER>(heads, items, n_items, wpg, desc, q, out, lse, ws, s);
+    case 8: return launch_wave_g<8, D, XKV, ORDER>(heads, items, n_items, wpg, desc, q, out, lse, ws, s);
     default: return hipErrorInvalidValue;
     }
 }
@@ -1775,10 +1779,10 @@ static hipError_t launch_wave_x(int G, const HeadDev *heads, const WorkItem *ite
 #endif
 #define KVEXP_WAVE_UNIT(D, O)                                                                                        \
     hipError_t attention_wave_d##D##_o##O(bool xkv, int G, const HeadDev *heads, const WorkItem *items,             \
-                                         int n_items, const BlockDesc *desc, const uint16_t *q, float *out,        \
-                                         float *lse, float *ws, hipStream_t s) {                                   \
-        return xkv ? launch_wave_x<D, true, O>(G, heads, items, n_items, desc, q, out, lse, ws, s)                  \
-                   : launch_wave_x<D, false, O>(G, heads, items, n_items, desc, q, out, lse, ws, s);                \
+                                         int n_items, int wpg, const BlockDesc *desc, const uint16_t *q,           \
+                                         float *out, float *lse, float *ws, hipStream_t s) {                       \
+        return xkv ? launch_wave_x<D, true, O>(G, heads, items, n_items, wpg, desc, q, out, lse, ws, s)             \
+                   : launch_wave_x<D, false, O>(G, heads, items, n_items, wpg, desc, q, out, lse, ws, s);           \
     }                                                                                                                \
     KVEXP_WAVE_TRACE_READER(D, O)
 

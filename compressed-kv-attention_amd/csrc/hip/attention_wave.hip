@@ -8,8 +8,8 @@ using namespace kvexp_dev;
 
 #define KVEXP_WAVE_DECL(D, O)                                                                                        \
     hipError_t attention_wave_d##D##_o##O(bool xkv, int G, const HeadDev *heads, const WorkItem *items,             \
-                                         int n_items, const BlockDesc *desc, const uint16_t *q, float *out,        \
-                                         float *lse, float *ws, hipStream_t s);
+                                         int n_items, int wpg, const BlockDesc *desc, const uint16_t *q,           \
+                                         float *out, float *lse, float *ws, hipStream_t s);
 KVEXP_WAVE_DECL(64, 0)
 KVEXP_WAVE_DECL(64, 1)
 KVEXP_WAVE_DECL(128, 0)
@@ -46,14 +46,14 @@ hipError_t wave_merge(int dim, const MergeItem *mitems, int n_mitems, const Merg
 }
 
 hipError_t attention_wave(bool xkv, int order, int G, int dim, const HeadDev *heads, const WorkItem *items,
-                          int n_items, const BlockDesc *desc, const uint16_t *q, float *out, float *lse, float *ws,
-                          hipStream_t s) {
+                          int n_items, int wpg, const BlockDesc *desc, const uint16_t *q, float *out, float *lse,
+                          float *ws, hipStream_t s) {
     if (n_items <= 0) return hipSuccess;
     if (order != 0 && order != 1) return hipErrorInvalidValue;
 #define KVEXP_WAVE_CASE(D)                                                                                           \
     if (dim == D)                                                                                                    \
-        return order == 0 ? attention_wave_d##D##_o0(xkv, G, heads, items, n_items, desc, q, out, lse, ws, s)        \
-                          : attention_wave_d##D##_o1(xkv, G, heads, items, n_items, desc, q, out, lse, ws, s);
+        return order == 0 ? attention_wave_d##D##_o0(xkv, G, heads, items, n_items, wpg, desc, q, out, lse, ws, s)   \
+                          : attention_wave_d##D##_o1(xkv, G, heads, items, n_items, wpg, desc, q, out, lse, ws, s);
     KVEXP_WAVE_CASE(64)
     KVEXP_WAVE_CASE(128)
     KVEXP_WAVE_CASE(256)

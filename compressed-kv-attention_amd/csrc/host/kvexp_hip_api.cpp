@@ -46,8 +46,8 @@ hipError_t plan_refresh(const kvexp_dev::EscJob *jobs, int n_jobs, HeadDev *head
                         int n_items, int per_head, uint32_t *status, hipStream_t s);
 bool wave_supports(int dim);
 hipError_t attention_wave(bool xkv, int order, int G, int dim, const HeadDev *heads, const WorkItem *items,
-                          int n_items, const kvexp_dev::BlockDesc *desc, const uint16_t *q, float *out, float *lse,
-                          float *ws, hipStream_t s);
+                          int n_items, int wpg, const kvexp_dev::BlockDesc *desc, const uint16_t *q, float *out,
+                          float *lse, float *ws, hipStream_t s);
 hipError_t wave_merge(int dim, const kvexp_dev::MergeItem *mitems, int n_mitems, const kvexp_dev::MergeItem &uni,
                       float *out, float *lse, const float *ws, hipStream_t s);
 int wave_waves_per_wg(int dim);
@@ -1334,8 +1334,11 @@ int kvexp_hip_attention_run(kvexp_hip_plan *plan, const uint16_t *d_q, float *d_
             for (int G = 1; G <= 8; ++G) {
                 const int b = plan->group_start[G], e = plan->group_start[G + 1];
                 if (e > b)
+                    // a group with no more items than CUs: one wave per
+                    // workgroup, so that its items spread over as many CUs
                     HIPX(kvexp_launch::attention_wave(plan->xkv, plan->order, G, plan->dim, plan->heads.as<HeadDev>(),
                                                       plan->items.as<WorkItem>() + b, e - b,
+                                                      e - b <= plan->ctx->cu_count ? 1 : 0,
                                                       plan->desc.as<kvexp_dev::BlockDesc>(), d_q, d_out, d_lse,
                                                       plan->ws.as<float>(), s));
             }
