@@ -1335,10 +1335,12 @@ int kvexp_hip_attention_run(kvexp_hip_plan *plan, const uint16_t *d_q, float *d_
                 const int b = plan->group_start[G], e = plan->group_start[G + 1];
                 if (e > b)
                     // a group with no more items than CUs: one wave per
-                    // workgroup, so that its items spread over as many CUs
+                    // workgroup, up to twice as many: two, so that its items
+                    // spread over every CU (else the kernel's own count)
                     HIPX(kvexp_launch::attention_wave(plan->xkv, plan->order, G, plan->dim, plan->heads.as<HeadDev>(),
                                                       plan->items.as<WorkItem>() + b, e - b,
-                                                      e - b <= plan->ctx->cu_count ? 1 : 0,
+                                                      e - b <= plan->ctx->cu_count ? 1
+                                                      : e - b <= 2 * plan->ctx->cu_count ? 2 : 0,
                                                       plan->desc.as<kvexp_dev::BlockDesc>(), d_q, d_out, d_lse,
                                                       plan->ws.as<float>(), s));
             }

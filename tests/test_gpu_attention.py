@@ -140,6 +140,29 @@ def test_many_heads_variable_length(ctx, oracle):
     assert np.allclose(lse_raw, lse_want, rtol=1e-6, atol=1e-6)
 
 
+def test_wave_launch_shapes(ctx, oracle):
+    """Plans of at most as many split waves as the GPU has CUs (one wave per
+    workgroup), of up to twice as many (two) and of more (the kernel's four
+    at head_dim 64): the same bits as the oracle in each."""
+    import torch
+
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    rng = np.random.default_rng(91)
+    dim, n_q, block, seq, splits = 64, 7, 128, 512, 4
+    for n_items in (cus // 2, cus + 4 * 8, 2 * cus + 4 * 8):
+        n_heads = n_items // splits
+        heads = [dict(k=random_kv(rng, seq, dim, spread_lo=-6, spread_hi=4, outliers=2),
+                      v=random_kv(rng, seq, dim, sigma=0.5), seq=seq, splits=splits) for _ in range(n_heads)]
+        q = random_kv(rng, n_heads * n_q, dim)
+        say("launch shape", dict(items=n_heads * splits, cus=cus))
+        want = oracle.attention_heads("scalar", q, [dict(k=h["k"], v=h["v"], seq=seq, threads=splits) for h in heads],
+                                      n_q=n_q, dim=dim, split=block)
+        raw = run_gpu(ctx, 0, q, heads, n_q, dim, block, False)
+        xkv = run_gpu(ctx, 0, q, heads, n_q, dim, block, True)
+        assert bits_equal(raw, xkv)
+        assert bits_equal(xkv, want)
+
+
 def _escape_heavy_kv(rng, seq, dim, frac, narrow=False):
     """K with a fraction `frac` of elements pushed 2^8..2^14 away from their
     channel's exponent window, so that coded blocks carry many escapes
