@@ -736,6 +736,27 @@ __device__ __forceinline__ float max_f32(float a, float b) {
     return r;
 }
 
+// a in the lanes whose bit of m is set, b in the others: v_cndmask_b32 with
+// the lane mask in a scalar register pair. The compiler's own selects take
+// one condition in VCC, and that form (VOP2, reading VCC) issues at about a
+// quarter of the rate of this one on gfx950.
+__device__ __forceinline__ float lane_select(uint64_t m, float a, float b) {
+    float r;
+    asm("v_cndmask_b32_e64 %0, %1, %2, %3" : "=v"(r) : "v"(b), "v"(a), "s"(m));
+    return r;
+}
+// lane_select(m, a, 0) and lane_select(m, a, 1), the constant inline
+__device__ __forceinline__ float lane_select_or0(uint64_t m, float a) {
+    float r;
+    asm("v_cndmask_b32_e64 %0, 0, %1, %2" : "=v"(r) : "v"(a), "s"(m));
+    return r;
+}
+__device__ __forceinline__ float lane_select_or1(uint64_t m, float a) {
+    float r;
+    asm("v_cndmask_b32_e64 %0, 1.0, %1, %2" : "=v"(r) : "v"(a), "s"(m));
+    return r;
+}
+
 __device__ __forceinline__ float lo_f32(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float hi_f32(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
 
@@ -1468,7 +1489,7 @@ void attn_wave_kernel(const HeadDev *__restrict__ heads, const WorkItem *__restr
                 // one exponential per token: alpha's argument where the token
                 // moves the maximum (its e is exp(0)), e's elsewhere (its
                 // alpha is exp(0), or NaN where m_prev - m is)
-                x[b] = s[g] > mp[b] ? mp[b] - s[g] : s[g] - m[b];
+                x[b] = lane_select(__ballot(s[g] > mp[b]), mp[b] - s[g], s[g] - m[b]);
                 kvexp_expf_reduce(x[b], kd[b], rr[b]);
                 tb[b] = tab[uint32_t(__double_as_longlong(kd[b])) & 31u];
             }
@@ -1478,18 +1499,18 @@ void attn_wave_kernel(const HeadDev *__restrict__ heads, const WorkItem *__restr
                 const int g = g0 + b;
                 float y = kvexp_expf_finish(kd[b], rr[b], tb[b]);
                 // glibc's expf gives +0 below -0x1.9fe368p6 (the core does not)
-                y = x[b] < -0x1.9fe368p6f ? 0.0f : y;
+                y = lane_select_or0(__ballot(!(x[b] < -0x1.9fe368p6f)), y);
                 const float dg = mp[b] - m[b];
                 // alpha != 1 exactly when m_prev - m is not zero (NaN included)
                 amask |= __ballot(!(dg == 0.0f)) & nmask;
                 // a moving token: e = exp(s - m) with s = m, that is exp(0)
                 // = 1, or NaN where s is infinite (s - m + 1 gives both);
                 // elsewhere alpha = exp(dg) with dg 0 or NaN (dg + 1)
-                const bool mv = s[g] > mp[b];
-                const float e = mv ? (s[g] - m[b]) + 1.0f : y;
-                const float al = mv ? y : dg + 1.0f;
-                S.eT[g][ln] = ln < n ? e : 0.0f;
-                S.aT[g][ln] = ln < n ? al : 1.0f;
+                const uint64_t mv = __ballot(s[g] > mp[b]); // the lanes whose token moves the maximum
+                const float e = lane_select(mv, (s[g] - m[b]) + 1.0f, y);
+                const float al = lane_select(mv, y, dg + 1.0f);
+                S.eT[g][ln] = lane_select_or0(nmask, e); // lanes ln < n
+                S.aT[g][ln] = lane_select_or1(nmask, al);
                 msc[g] = readlane_f32(m[b], n - 1);
             }
         }
