@@ -1109,17 +1109,19 @@ __device__ __forceinline__ void fold_token(const WaveLds<G, D> &S, lds_f32 *eb, 
 // four tokens issues its vector work (V widening, the l chain) and then its
 // eight products: a product right after a vector instruction, or the reverse,
 // stalls the SIMD, so few switches between the two pay.
-// Group J (tokens 16 J .. 16 J + 15) of the fold with a runtime token index,
+// Group J (tokens 16 J .. 16 J + 15) of the fold with a runtime quad index,
 // for a group where some token moves a running maximum at head_dim 256: there
 // the unrolled form (32 accumulator scalings per token, through the matrix
 // registers) would put the chunk loop far beyond the instruction cache. The
-// same operations in the same order as fold_token: the A operand of token
-// 16 J + b (e of the group's rows, lanes 4b .. 4b + 3 of ea[rg][J]) is moved
-// to lanes 0 .. 3 by ds_bpermute and taken from block 0; V (by channel from
-// the tile), e and alpha are read per token. Then the next group's operands
-// are requested as the unrolled fold would have left them.
+// same operations in the same order as fold_token, four tokens per pass:
+// V of the quad by load_tr, e and alpha of the quad as 16-byte reads, every
+// row's alpha of a token that moves a maximum read one token ahead, and the
+// quad's A operands (e of the group's rows, lanes 16 q .. 16 q + 15 of
+// ea[rg][J]) moved to lanes 0 .. 15 by one ds_bpermute, so that token u of
+// the quad is block u. Then the next group's operands are requested as the
+// unrolled fold would have left them.
 template <int G, int D, int J>
-__device__ __forceinline__ void fold_group_dyn(const WaveLds<G, D> &S, lds_f32 *eb, lds_f32 *ab, const uint16_t *vb,
+__device__ __forceinline__ void fold_group_dyn(const WaveLds<G, D> &S, lds_f32 *eb, lds_f32 *ab,
                                                const uint8_t *trb, const uint32_t (&am)[2],
                                                const float (&ea)[kGroups<G>][4], FoldIn<D / 64> &in,
                                                f4 (&acc)[kGroups<G>][D / 64], float &lvec) {
@@ -1127,29 +1129,51 @@ __device__ __forceinline__ void fold_group_dyn(const WaveLds<G, D> &S, lds_f32 *
     const int lane = lane_id();
     const uint32_t mw = am[J / 2];
 #pragma unroll 1
-    for (int b = 0; b < 16; ++b) {
-        const int T = 16 * J + b;
-        float v[H];
+    for (int q = 0; q < 4; ++q) {
+        const int T0 = 16 * J + 4 * q;
+        uint2 vq[H];
 #pragma unroll
-        for (int h = 0; h < H; ++h) v[h] = __uint_as_float(uint32_t(vb[T * (TS / 2) + 64 * h]) << 16);
-        const float el = eb[T], al = ab[T];
-        if ((mw >> (T % 32)) & 1u) {
+        for (int h = 0; h < H; ++h) vq[h] = load_tr(trb + T0 * TS + 128 * h);
+        const f4 e4 = *reinterpret_cast<lds_f4 *>(eb + T0);
+        const f4 a4 = *reinterpret_cast<lds_f4 *>(ab + T0);
+        float a[NG];
+#pragma unroll
+        for (int rg = 0; rg < NG; ++rg)
+            a[rg] = __int_as_float(__builtin_amdgcn_ds_bpermute(4 * (lane + 16 * q), __float_as_int(ea[rg][J])));
+        const uint32_t qb = (mw >> (T0 % 32)) & 15u; // the quad's tokens that move a maximum
+        // every row's alpha of the token (read one token ahead)
+        float an[G];
+        if (qb & 1u) {
+#pragma unroll
+            for (int g = 0; g < G; ++g) an[g] = S.aT[g][T0];
+        }
+        static_for<0, 4>([&](auto U) {
+            constexpr int u = decltype(U)::value;
             float av[G];
 #pragma unroll
-            for (int g = 0; g < G; ++g) av[g] = S.aT[g][T];
+            for (int g = 0; g < G; ++g) av[g] = an[g];
+            if constexpr (u < 3) {
+                if ((qb >> (u + 1)) & 1u) {
 #pragma unroll
-            for (int g = 0; g < G; ++g)
+                    for (int g = 0; g < G; ++g) an[g] = S.aT[g][T0 + u + 1];
+                }
+            }
+            float v[H];
 #pragma unroll
-                for (int h = 0; h < H; ++h) acc[g / 4][h][g % 4] *= av[g];
-        }
-        lvec = fmaf(lvec, al, el);
-        asm volatile("" : "+v"(lvec));
+            for (int h = 0; h < H; ++h) v[h] = quad_f32<u>(vq[h]);
+            if ((qb >> u) & 1u) {
 #pragma unroll
-        for (int rg = 0; rg < NG; ++rg) {
-            const float a = __int_as_float(__builtin_amdgcn_ds_bpermute(4 * (4 * b + (lane & 3)), __float_as_int(ea[rg][J])));
+                for (int g = 0; g < G; ++g)
 #pragma unroll
-            for (int h = 0; h < H; ++h) acc[rg][h] = mfma_rank1<0>(a, v[h], acc[rg][h]);
-        }
+                    for (int h = 0; h < H; ++h) acc[g / 4][h][g % 4] *= av[g];
+            }
+            lvec = fmaf(lvec, a4[u], e4[u]);
+            asm volatile("" : "+v"(lvec));
+#pragma unroll
+            for (int rg = 0; rg < NG; ++rg)
+#pragma unroll
+                for (int h = 0; h < H; ++h) acc[rg][h] = mfma_rank1<u>(a[rg], v[h], acc[rg][h]);
+        });
     }
     constexpr int Q0 = 4 * (J + 1); // the next group's first quad
     if constexpr (4 * Q0 < kChunk) {
@@ -1179,7 +1203,7 @@ __device__ __forceinline__ void fold(const WaveLds<G, D> &S, lds_f32 *eb, lds_f3
                 __builtin_amdgcn_sched_group_barrier(0x008, 4 * NG * H, 0);
             });
         } else if constexpr (D == 256) {
-            fold_group_dyn<G, D, T / GS>(S, eb, ab, vb, trb, am, ea, in, acc, lvec);
+            fold_group_dyn<G, D, T / GS>(S, eb, ab, trb, am, ea, in, acc, lvec);
         } else {
             static_for<0, GS>([&](auto K) {
                 fold_token<G, D, T + decltype(K)::value, true>(S, eb, ab, trb, am, ea, in, a4, acc, lvec);
