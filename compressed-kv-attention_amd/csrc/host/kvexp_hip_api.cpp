@@ -913,12 +913,13 @@ namespace {
 // is busy for the sum of its waves' work and the launch ends with the
 // busiest SIMD. Cost of a split: its tokens plus its K and V escape words
 // (about 1/15 token each, measured on c2: an escape costs ~5.7 SIMD cycles,
-// a token ~85). Items are sorted by cost, cut into workgroup-sized groups,
+// a token ~85; plain BF16 heads: their tokens). Items are sorted by cost,
+// cut into workgroup-sized groups,
 // and the groups are dealt to the workgroup slots tier by tier, in forward
 // order on even tiers and reversed on odd ones, so that each CU receives a
 // mix of heavy and light groups. The merge follows split numbers, not item
 // order, so the results do not depend on it.
-void balance_items(kvexp_hip_plan &p, std::vector<WorkItem> &items, const int32_t *first_all,
+void balance_items(kvexp_hip_plan &p, std::vector<WorkItem> &items, bool xkv, const int32_t *first_all,
                    const std::vector<size_t> &first_at, int n_q, int dim) {
     const int per_head = (n_q + kMaxQPerLaunch - 1) / kMaxQPerLaunch;
     const int wpw = kvexp_launch::wave_waves_per_wg(dim);
@@ -926,7 +927,7 @@ void balance_items(kvexp_hip_plan &p, std::vector<WorkItem> &items, const int32_
     auto cost = [&](const WorkItem &w) {
         const int h = w.head / per_head;
         double c = double(w.tok_end - w.tok_begin);
-        for (int kv = 0; kv < 2; ++kv) {
+        for (int kv = 0; kv < (xkv ? 2 : 0); ++kv) {
             const size_t t = size_t(2 * h + kv);
             const int32_t *f0 = first_all + first_at[t];
             const int nb = p.jobs[t].n_blocks;
@@ -1119,7 +1120,7 @@ void plan_build(kvexp_hip_plan *p, const kvexp_hip_head *heads, int n_heads, hip
                                 hipMemcpyHostToDevice, s));
         if (xkv) {
             build_escape_index(*p, heads, n_heads, n_q, dim, hv, s);
-            balance_items(*p, items, first_all, first_at, n_q, dim);
+            balance_items(*p, items, true, first_all, first_at, n_q, dim);
             // the split's first descriptors as indexes into the plan's array
             // (device head dh belongs to user head dh / per_head)
             const int per_head = (n_q + kMaxQPerLaunch - 1) / kMaxQPerLaunch;
@@ -1128,6 +1129,8 @@ void plan_build(kvexp_hip_plan *p, const kvexp_hip_head *heads, int n_heads, hip
                 w.kdi = int(p->esc_prefix_at[size_t(2 * h)]) + w.kblk;
                 w.vdi = int(p->esc_prefix_at[size_t(2 * h + 1)]) + w.vblk;
             }
+        } else {
+            balance_items(*p, items, false, nullptr, std::vector<size_t>(), n_q, dim);
         }
     }
     p->heads = p->alloc(hv.size() * sizeof(HeadDev));
