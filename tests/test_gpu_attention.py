@@ -220,6 +220,49 @@ def test_wave_kernel_groups_and_escapes(ctx, oracle, dim, backend):
     assert seen_big
 
 
+# Tokens (from a split's first token) whose scores set a new running maximum:
+# for query rows 0-3 (UP) and rows 4-7 (DOWN). Every position of a quad of
+# four tokens, two and four moves in one quad, a move in each group of 16
+# tokens of the second chunk, the first chunk's last token.
+MOVES_UP = [1, 2, 3, 4, 9, 10, 16, 17, 18, 19, 35, 63, 69, 85, 101, 117]
+MOVES_DOWN = [0, 6, 7, 13, 22, 31, 47, 62, 100, 127]
+
+
+@pytest.mark.parametrize("backend", ["scalar", "avx512"])
+@pytest.mark.parametrize("dim", [64, 128, 256])
+def test_wave_fold_chosen_moves(ctx, oracle, dim, backend):
+    """Running maxima that move at chosen tokens of each split's first two
+    chunks (MOVES_UP for query rows 0-3, MOVES_DOWN for rows 4-7: K rows of
+    growing magnitude and one sign among small random ones, queries of one
+    sign per row group), so that the fold's path for tokens that move a
+    maximum (at head_dim 256 the loop over quads of four tokens) meets moves
+    at every position of a quad, several in one quad and none in others;
+    XKV == raw == oracle in both score orders."""
+    rng = np.random.default_rng(9 + dim)
+    n_q, block, seq, splits = 8, 128, 640, 2
+    x = rng.standard_normal((seq, dim)).astype(np.float32) * np.float32(0.05)
+    chosen = sorted([(t, 1.0) for t in MOVES_UP] + [(t, -1.0) for t in MOVES_DOWN])
+    k_th = 0
+    for s0 in (0, 256):  # the two splits' first tokens (5 blocks over 2 splits)
+        for t, sign in chosen:
+            x[s0 + t] = np.float32(sign * (1.0 + 0.05 * k_th))
+            k_th += 1
+    k = bf16_from_f32(x.reshape(-1))
+    v = random_kv(rng, seq, dim)
+    qf = np.abs(rng.standard_normal((n_q, dim)).astype(np.float32)) * np.float32(0.5) + np.float32(0.25)
+    qf[4:] *= -1.0
+    q = bf16_from_f32(qf.reshape(-1))
+    heads = [dict(k=k, v=v, seq=seq, splits=splits, block=block)]
+    say("wave fold, chosen moves", backend, dict(dim=dim, seq=seq, splits=splits))
+    want = oracle.attention_heads(backend, q, [dict(k=k, v=v, seq=seq, threads=splits)], n_q=n_q, dim=dim,
+                                  split=block)
+    raw = run_gpu(ctx, ORDER[backend], q, heads, n_q, dim, block, False)
+    xkv = run_gpu(ctx, ORDER[backend], q, heads, n_q, dim, block, True)
+    assert not np.isnan(want).any()
+    assert bits_equal(raw, xkv)
+    assert bits_equal(raw, want), max_rel_err(raw, want)
+
+
 def _mixed_block_kv(rng, seq, dim, block, kinds):
     """Tokens whose blocks cycle through `kinds`: "raw" (values spread over 60
     binades: the encoder stores the block raw), "coded" (4-bit codes, a few
