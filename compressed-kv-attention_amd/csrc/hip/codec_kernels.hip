@@ -636,16 +636,20 @@ __device__ __forceinline__ EscRanks<NL> fused_escape_ranks(const uint32_t (&v)[E
 // 512 / waves without spilling): 8 with up to four chunk rows per thread.
 template <int NL>
 constexpr int kFusedWaves = NL <= 4 ? 8 : 4;
-// Fewest waves per SIMD the compiler may plan for: one block's tokens in
-// registers beside the next block's (NL 16-byte loads each). At NL 8 the
+// Fewest waves per SIMD the compiler may plan for. Up to two chunk rows per
+// thread, one block's tokens fit in registers beside the next block's (NL
+// 16-byte loads each) at eight waves; at four rows the next block's tokens
+// are loaded only once this block's are dead (kFusedNextEarly), which keeps
+// the kernel at 64 registers and eight waves (eight workgroups per CU: the
+// c2 prefill 2.6 % faster than six with both sets in registers). At NL 8 the
 // budget stays at four (128 registers): three would let a head_dim-128
 // tensor's 1,024 blocks fill only 768 workgroups at once.
 template <int NL>
-constexpr int kFusedWavesMin = NL <= 2 ? 8 : (NL <= 4 ? 6 : 4);
+constexpr int kFusedWavesMin = NL <= 4 ? 8 : 4;
 // Whether the next block's tokens are loaded right after the histograms
 // (beside this block's) or only once this block's bytes are staged.
 template <int NL>
-constexpr bool kFusedNextEarly = NL <= 4;
+constexpr bool kFusedNextEarly = NL <= 2;
 
 // Dynamic LDS of the one-pass encoder: the histogram columns, or the
 // largest block (raw: header + 2 bytes per element) staged for its copy,
